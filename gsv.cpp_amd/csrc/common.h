@@ -1,0 +1,163 @@
+// Internal helpers shared by the gfx950 kernels and the host runtime.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "gsvk.h"
+
+namespace gsvk {
+
+// Thread-local last error (gsvk_last_error()).
+void set_error(const char * fmt, ...) __attribute__((format(printf, 1, 2)));
+const char * get_error();
+
+}  // namespace gsvk
+
+// Return GSVK_ERR_HIP from the enclosing function when a HIP call fails.
+#define GSVK_HIP(call)                                                                        \
+    do {                                                                                      \
+        hipError_t e_ = (call);                                                               \
+        if (e_ != hipSuccess) {                                                               \
+            gsvk::set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__,  \
+                            __LINE__);                                                        \
+            return GSVK_ERR_HIP;                                                              \
+        }                                                                                     \
+    } while (0)
+
+// Return GSVK_ERR_ARG with a message when a condition does not hold.
+#define GSVK_REQUIRE(cond, ...)                                                               \
+    do {                                                                                      \
+        if (!(cond)) {                                                                        \
+            gsvk::set_error(__VA_ARGS__);                                                     \
+            return GSVK_ERR_ARG;                                                              \
+        }                                                                                     \
+    } while (0)
+
+// Propagate a non-zero status.
+#define GSVK_TRY(call)                                                                        \
+    do {                                                                                      \
+        int s_ = (call);                                                                      \
+        if (s_ != GSVK_OK) return s_;                                                         \
+    } while (0)
+
+#define GSVK_LAUNCH_CHECK()                                                                   \
+    do {                                                                                      \
+        hipError_t e_ = hipGetLastError();                                                    \
+        if (e_ != hipSuccess) {                                                               \
+            gsvk::set_error("kernel launch failed: %s (%s:%d)", hipGetErrorString(e_),        \
+                            __FILE__, __LINE__);                                              \
+            return GSVK_ERR_HIP;                                                              \
+        }                                                                                     \
+    } while (0)
+
+namespace gsvk {
+
+constexpr int QK = 32;           // Q8_0 block length
+constexpr int Q8_BLOCK_BYTES = 34;
+
+// ---- device helpers -------------------------------------------------------------------
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+    _Float16 v = __builtin_bit_cast(_Float16, h);
+    return (float) v;
+}
+
+// fp32 -> fp16, round to nearest even (the F16C conversion ggml-cpu uses).
+__device__ __forceinline__ uint16_t f2h(float f) {
+    _Float16 v = (_Float16) f;
+    return __builtin_bit_cast(uint16_t, v);
+}
+
+__device__ __forceinline__ float warp_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+__device__ __forceinline__ float warp_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ double warp_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Q8_0 activation quantisation of one 32-block held as 32 values spread over `lanes` lanes
+// (each lane holds 32/lanes values in v[]). Mirrors ggml-cpu's x86 quantiser: the scale stored
+// is fp16(amax / 127) and the quants are round-half-even(x * (127 / amax)).
+// Returns the fp32 value of the stored fp16 scale.
+template <int PER_LANE>
+__device__ __forceinline__ float q8_quantize_group(const float (&v)[PER_LANE], int8_t (&q)[PER_LANE],
+                                                   int lanes) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; i++) amax = fmaxf(amax, fabsf(v[i]));
+    for (int o = 1; o < lanes; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float d = amax / 127.0f;
+    const float id = (amax != 0.0f) ? 127.0f / amax : 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER_LANE; i++) q[i] = (int8_t) (int) __builtin_rintf(v[i] * id);
+    return h2f(f2h(d));
+}
+
+// Store the 8 quants of values [8*sub, 8*sub+8) of block blk of one row in the sliced layout
+// (qs[j][blk][t] = q[blk*32 + 4j + t]): they are groups j = 2*sub and 2*sub + 1.
+__device__ __forceinline__ void q8_store_sliced(int8_t * row, int nblk, int blk, int sub,
+                                                const int8_t (&q)[8]) {
+    const int lo = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    const int hi = (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((q[7] & 0xff) << 24);
+    *reinterpret_cast<int *>(row + ((int64_t) (2 * sub) * nblk + blk) * 4) = lo;
+    *reinterpret_cast<int *>(row + ((int64_t) (2 * sub + 1) * nblk + blk) * 4) = hi;
+}
+
+// Byte offset of value w (0..31) of block blk in a sliced row.
+__device__ __forceinline__ int64_t q8_sliced_offset(int nblk, int blk, int w) {
+    return ((int64_t) (w >> 2) * nblk + blk) * 4 + (w & 3);
+}
+
+// Epilogue of the Q8_0 GEMV: bias, activation, and optionally the KV-cache append of the K and
+// V rows (rows [kv_row0, kv_row0 + 2*d_model)) as fp16 into caches laid out
+// [B][n_head][lstride][32]; output row m belongs to sequence m / rows_per_seq at cache column
+// *col_ptr + col_add + m % rows_per_seq.
+struct GemvEpilogue {
+    const float * bias;
+    int act;
+    uint16_t * kc;
+    uint16_t * vc;
+    int kv_row0;
+    int d_model;
+    int n_head;
+    int64_t lstride;
+    int rows_per_seq;
+    const int32_t * col_ptr;
+    int col_add;
+};
+
+int launch_q8_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xs,
+                   const float * xd, int64_t m, const GemvEpilogue & epi, float * y,
+                   hipStream_t stream);
+int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, float * xd,
+                       hipStream_t stream);
+int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
+                     hipStream_t stream);
+int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
+                     int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
+                     hipStream_t stream);
+int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
+                    const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
+                    int8_t * xq, float * xd, hipStream_t stream);
+size_t attn_workspace_bytes(int B, int nh, int64_t max_keys);
+int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
+                       int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,
+                       const int32_t * kv_end, int64_t max_keys, float scale, float * out,
+                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream);
+
+}  // namespace gsvk

@@ -1,0 +1,145 @@
+// Dot products of F16 / F32 weight rows with fp32 activation rows (the logits head and the
+// prefill BERT projection), reproducing ggml-cpu's x86 summation order:
+//
+//  MODE 0 — ggml_vec_dot_f16 / ggml_vec_dot_f32 (decode, and any K not a multiple of 8):
+//    4 accumulators of 8 lanes, sum[j][l] = fma(w[32i+8j+l], x[32i+8j+l], sum[j][l]) for every
+//    full step of 32; GGML_F32x8_REDUCE: sum0+=sum2, sum1+=sum3, sum0+=sum1, then
+//    t_i = s_i + s_{i+4} and ((t0+t1) + (t2+t3)); the k % 32 leftovers are fused in order.
+//    GPU: 32 lanes per output row, lane p = 8j + l owns one accumulator; the reduction is the
+//    xor-16, xor-8, xor-4, xor-1, xor-2 butterfly, which performs exactly those additions.
+//  MODE 1 — llamafile tinyBLAS (prefill with >= 2 activation columns, K % 8 == 0):
+//    one accumulator of 8 lanes, a[l] = fma(w[8i+l], x[8i+l], a[l]); hsum
+//    ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) = xor-4, xor-2, xor-1 butterfly over 8 lanes.
+//
+// For F16 weights the activations are first rounded to fp16 (ggml's vec_dot_type for F16).
+#include "common.h"
+
+namespace gsvk {
+
+template <typename WT>
+__device__ __forceinline__ float wload(const WT * p);
+template <>
+__device__ __forceinline__ float wload<float>(const float * p) { return *p; }
+template <>
+__device__ __forceinline__ float wload<uint16_t>(const uint16_t * p) { return h2f(*p); }
+
+__device__ __forceinline__ float xconv(float x, bool x16) { return x16 ? h2f(f2h(x)) : x; }
+
+// MODE 0: 256 threads = 8 rows x 32 lanes; grid (ceil(n/8), ceil(m/MT))
+template <typename WT, int MT>
+__global__ void __launch_bounds__(256) k_fdot_ggml(const WT * __restrict__ W, int n, int k,
+                                                   const float * __restrict__ X, int64_t xs, int m,
+                                                   float * __restrict__ Y, int64_t ys) {
+    const bool x16 = sizeof(WT) == 2;
+    const int p = threadIdx.x & 31;
+    const int row = blockIdx.x * 8 + (threadIdx.x >> 5);
+    const int m0 = blockIdx.y * MT;
+    const int rowc = row < n ? row : n - 1;
+    const WT * wr = W + (int64_t) rowc * k;
+    const int np = k & ~31;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+    for (int i = 0; i < np; i += 32) {
+        const float w = wload<WT>(wr + i + p);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int mm = m0 + t < m ? m0 + t : m - 1;
+            acc[t] = __builtin_fmaf(w, xconv(X[(int64_t) mm * xs + i + p], x16), acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        float v = acc[t];
+        v = v + __shfl_xor(v, 16, 64);
+        v = v + __shfl_xor(v, 8, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        acc[t] = v;
+    }
+    if (p != 0 || row >= n) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int mm = m0 + t;
+        if (mm < m) {
+            float v = acc[t];
+            for (int i = np; i < k; i++)
+                v = __builtin_fmaf(wload<WT>(wr + i), xconv(X[(int64_t) mm * xs + i], x16), v);
+            Y[(int64_t) mm * ys + row] = v;
+        }
+    }
+}
+
+// MODE 1: 256 threads = 32 rows x 8 lanes; grid (ceil(n/32), ceil(m/MT))
+template <typename WT, int MT>
+__global__ void __launch_bounds__(256) k_fdot_tinyblas(const WT * __restrict__ W, int n, int k,
+                                                       const float * __restrict__ X, int64_t xs,
+                                                       int m, float * __restrict__ Y, int64_t ys) {
+    const bool x16 = sizeof(WT) == 2;
+    const int l = threadIdx.x & 7;
+    const int row = blockIdx.x * 32 + (threadIdx.x >> 3);
+    const int m0 = blockIdx.y * MT;
+    const int rowc = row < n ? row : n - 1;
+    const WT * wr = W + (int64_t) rowc * k;
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+    for (int i = 0; i < k; i += 8) {
+        const float w = wload<WT>(wr + i + l);
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int mm = m0 + t < m ? m0 + t : m - 1;
+            acc[t] = __builtin_fmaf(w, xconv(X[(int64_t) mm * xs + i + l], x16), acc[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        float v = acc[t];
+        v = v + __shfl_xor(v, 4, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        acc[t] = v;
+    }
+    if (l != 0 || row >= n) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+        if (m0 + t < m) Y[(int64_t) (m0 + t) * ys + row] = acc[t];
+}
+
+// wtype: 0 = F32, 1 = F16. mode: 0 = ggml vec_dot, 1 = tinyBLAS (falls back to 0 if k % 8).
+int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
+                int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream) {
+    GSVK_REQUIRE(W && X && Y && (wtype == 0 || wtype == 1), "fdot: bad arguments");
+    GSVK_REQUIRE(n > 0 && k > 0 && m > 0 && n < (1 << 30) && k < (1 << 24) && m < (1 << 30) &&
+                     xs >= k && ys >= n,
+                 "fdot: bad shape n=%lld k=%lld m=%lld", (long long) n, (long long) k,
+                 (long long) m);
+    constexpr int MT = 4;
+    if (mode == 1 && k % 8 == 0) {
+        const dim3 grid((unsigned) ((n + 31) / 32), (unsigned) ((m + MT - 1) / MT));
+        if (wtype == 1)
+            hipLaunchKernelGGL((k_fdot_tinyblas<uint16_t, MT>), grid, dim3(256), 0, stream,
+                               (const uint16_t *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+        else
+            hipLaunchKernelGGL((k_fdot_tinyblas<float, MT>), grid, dim3(256), 0, stream,
+                               (const float *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+    } else {
+        const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MT - 1) / MT));
+        if (wtype == 1)
+            hipLaunchKernelGGL((k_fdot_ggml<uint16_t, MT>), grid, dim3(256), 0, stream,
+                               (const uint16_t *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+        else
+            hipLaunchKernelGGL((k_fdot_ggml<float, MT>), grid, dim3(256), 0, stream,
+                               (const float *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+    }
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk
+
+extern "C" int gsvk_op_fdot(const void * w, int wtype, int64_t n, int64_t k, const float * x,
+                            int64_t m, float * y, int mode, void * stream) {
+    return gsvk::launch_fdot(w, wtype, n, k, x, k, m, y, n, mode, (hipStream_t) stream);
+}

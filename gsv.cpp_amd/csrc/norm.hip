@@ -1,0 +1,190 @@
+// Row-wise kernels for gfx950: the fused LayerNorm(x + r + bias) * w + b with optional Q8_0
+// output, the fused add + activation, and the embedding + positional-encoding gather.
+//
+// All of them run one wave (64 lanes) per row; each lane owns chunks of 8 consecutive floats
+// (two 16-byte loads), so four neighbouring lanes hold exactly one Q8_0 block of 32.
+#include "common.h"
+
+namespace gsvk {
+
+// ---------------------------------------------------------------------------------------
+// LayerNorm (PATCH:1533-1584): v = (x + r) + bias; mean and E[v^2] accumulated in double;
+// mean = float(sum / n); var = float(sum2 / n) - mean * mean; inv = 1 / sqrtf(var + eps);
+// y = (v - mean) * inv * w + b. The reference's Linux build (GCC, -mfma, GNU mode) contracts
+// `a - mean*mean` and `t*w + b` into single FMAs; this file is compiled without contraction and
+// writes exactly those two FMAs, so every other operation rounds where the C expression does.
+// ---------------------------------------------------------------------------------------
+
+template <int MAXC>
+__global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
+                                                  const float * __restrict__ r,
+                                                  const float * __restrict__ bias,
+                                                  const float * __restrict__ wb, int rows, int n,
+                                                  float eps, float * __restrict__ y,
+                                                  int8_t * __restrict__ yq,
+                                                  float * __restrict__ yd) {
+    const int row = blockIdx.x;
+    if (row >= rows) return;
+    const int lane = threadIdx.x;
+    const int nchunk = n / 8;
+    const float * xr = x + (int64_t) row * n;
+    const float * rr = r ? r + (int64_t) row * n : nullptr;
+    float v[MAXC][8];
+    double s = 0.0, s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const int ch = lane + 64 * c;
+        if (ch < nchunk) {
+            const int base = ch * 8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                float t = xr[base + i];
+                if (rr) t = t + rr[base + i];
+                if (bias) t = t + bias[base + i];
+                v[c][i] = t;
+                s += (double) t;
+                s2 += (double) t * (double) t;
+            }
+        }
+    }
+    s = warp_sum_d(s);
+    s2 = warp_sum_d(s2);
+    const float mean = (float) (s / (double) n);
+    const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
+    const float inv = 1.0f / __builtin_sqrtf(var + eps);
+    const float * w = wb;
+    const float * b = wb + n;
+    float * yr = y + (int64_t) row * n;
+    const int nblk = n / QK;
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        const int ch = lane + 64 * c;
+        const bool act = ch < nchunk;
+        float o[8];
+        if (act) {
+            const int base = ch * 8;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                o[i] = __builtin_fmaf((v[c][i] - mean) * inv, w[base + i], b[base + i]);
+                yr[base + i] = o[i];
+            }
+        }
+        if (yq && (64 * c) < nchunk) {   // uniform across the wave
+            if (!act) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] = 0.0f;
+            }
+            int8_t q[8];
+            const float d = q8_quantize_group<8>(o, q, 4);
+            if (act) {
+                q8_store_sliced(yq + (int64_t) row * n, nblk, ch >> 2, ch & 3, q);
+                if ((ch & 3) == 0) yd[(int64_t) row * nblk + ch / 4] = d;
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------
+// add + activation (PATCH:1586-1620)
+// ---------------------------------------------------------------------------------------
+
+__device__ __forceinline__ float apply_act(float v, int act) {
+    if (act == 1) return v > 0.0f ? v : 0.0f;
+    if (act == 2) return 0.5f * v * (1.0f + erff(v * 0.70710678118654752440f));
+    if (act == 3) {
+        const float sp = v > 20.0f ? v : log1pf(expf(v));
+        return v * tanhf(sp);
+    }
+    return v;
+}
+
+__global__ void k_add_act(const float * __restrict__ a, const float * __restrict__ b, int64_t n,
+                          int64_t ne0, int act, float * __restrict__ y) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    y[i] = apply_act(a[i] + b[i % ne0], act);
+}
+
+// ---------------------------------------------------------------------------------------
+// embedding + PE (src/gsv_ar.cpp:798-807): x[b] = emb[tok[b]] + alpha * pe[pos], with Q8_0
+// output. One wave per row; d_model must be 512.
+// ---------------------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
+                                                 const float * __restrict__ pe,
+                                                 const int32_t * __restrict__ tok, int vocab,
+                                                 const int32_t * __restrict__ pos_ptr,
+                                                 int pos_add, float alpha, int d,
+                                                 float * __restrict__ x,
+                                                 int8_t * __restrict__ xq,
+                                                 float * __restrict__ xd) {
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x;
+    int t = tok[b];
+    t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
+    const int pos = *pos_ptr + pos_add;
+    const float * er = emb + (int64_t) t * d + lane * 8;
+    const float * pr = pe + (int64_t) pos * d + lane * 8;
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        o[i] = __builtin_fmaf(alpha, pr[i], er[i]);   // emb + alpha * pe, contracted
+        x[(int64_t) b * d + lane * 8 + i] = o[i];
+    }
+    int8_t q[8];
+    const float dq = q8_quantize_group<8>(o, q, 4);
+    q8_store_sliced(xq + (int64_t) b * d, d / QK, lane >> 2, lane & 3, q);
+    if ((lane & 3) == 0) xd[(int64_t) b * (d / QK) + lane / 4] = dq;
+}
+
+int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
+                     int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
+                     hipStream_t stream) {
+    GSVK_REQUIRE(x && wb && y, "layernorm: null pointer");
+    GSVK_REQUIRE(rows >= 0 && rows < (1 << 30) && n > 0 && n % 32 == 0 && n <= 4096,
+                 "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
+                 (long long) rows, (long long) n);
+    GSVK_REQUIRE((yq == nullptr) == (yd == nullptr), "layernorm: yq and yd go together");
+    if (rows == 0) return GSVK_OK;
+    const dim3 grid((unsigned) rows);
+    if (n <= 512)
+        hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+                           (int) n, eps, y, yq, yd);
+    else if (n <= 1024)
+        hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+                           (int) n, eps, y, yq, yd);
+    else
+        hipLaunchKernelGGL(k_layernorm<8>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+                           (int) n, eps, y, yq, yd);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
+                    const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
+                    int8_t * xq, float * xd, hipStream_t stream) {
+    GSVK_REQUIRE(d == 512, "embed_pe: d_model must be 512");
+    hipLaunchKernelGGL(k_embed_pe, dim3((unsigned) B), dim3(64), 0, stream, emb, pe, tok, vocab,
+                       pos_ptr, pos_add, alpha, d, x, xq, xd);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk
+
+extern "C" int gsvk_op_layernorm(const float * x, const float * r, const float * bias,
+                                 const float * wb, int64_t rows, int64_t n, float eps, float * y,
+                                 int8_t * yq, float * yd, void * stream) {
+    return gsvk::launch_layernorm(x, r, bias, wb, rows, n, eps, y, yq, yd, (hipStream_t) stream);
+}
+
+extern "C" int gsvk_op_add_act(const float * a, const float * b, int64_t n, int64_t ne0, int act,
+                               float * y, void * stream) {
+    GSVK_REQUIRE(a && b && y && n >= 0 && ne0 > 0 && act >= 0 && act <= 3,
+                 "gsvk_op_add_act: bad arguments");
+    if (n == 0) return GSVK_OK;
+    hipLaunchKernelGGL(gsvk::k_add_act, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0,
+                       (hipStream_t) stream, a, b, n, ne0, act, y);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}

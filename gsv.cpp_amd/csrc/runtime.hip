@@ -1,0 +1,995 @@
+// Host runtime of the gfx950 AR decoder: GGUF load and device upload (src/gsv_ar.cpp:490-705),
+// resident fp16 KV cache (:94-147), device-side prefill (:186-293), the decode step (:380-467)
+// captured as one HIP graph together with the device sampler, and the generate loop (:719-824).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdlib>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "common.h"
+#include "gguf.h"
+#include "sampler.h"
+
+namespace gsvk {
+
+// kernels defined in the other translation units
+int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
+                int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream);
+int launch_build_xy(const float * text_emb, const float * audio_emb, const float * pe,
+                    const int32_t * phones, const int32_t * pad, const int32_t * prompt, int B,
+                    int S, int max_len, int d, float ta, float aa, float * xy, hipStream_t stream);
+int launch_bert_feat(const float * bert, const int64_t * boff, const int32_t * row_b,
+                     const int32_t * row_t, const int32_t * tlen, int bert_dim, int R, float * feat,
+                     hipStream_t stream);
+int launch_add_proj(float * xy, const float * proj, const int32_t * row_b, const int32_t * row_t,
+                    const int32_t * pad, int S, int d, int R, hipStream_t stream);
+int launch_gather_last(const float * in, int B, int S, int d, float * out, hipStream_t stream);
+int launch_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                        int d_model, float scale, float * out, int8_t * oq, float * od,
+                        hipStream_t stream);
+
+constexpr int PE_MAX = 4096;   // Y_PE_MAX, src/gsv_ar.cpp:44
+
+// ---- device allocation helper ------------------------------------------------------------
+
+struct DevArena {
+    std::vector<void *> ptrs;
+    ~DevArena() { release(); }
+    void release() {
+        for (void * p : ptrs) (void) hipFree(p);
+        ptrs.clear();
+    }
+    template <typename T>
+    int alloc(T *& out, size_t count) {
+        out = nullptr;
+        if (count == 0) count = 1;
+        void * p = nullptr;
+        const hipError_t e = hipMalloc(&p, count * sizeof(T));
+        if (e != hipSuccess) {
+            (void) hipGetLastError();
+            set_error("hipMalloc of %zu bytes failed: %s", count * sizeof(T), hipGetErrorString(e));
+            return GSVK_ERR_NOMEM;
+        }
+        ptrs.push_back(p);
+        out = (T *) p;
+        return GSVK_OK;
+    }
+};
+
+struct Lin {
+    int8_t * qs = nullptr;
+    uint16_t * d = nullptr;
+    float * b = nullptr;
+    int n = 0, k = 0;
+};
+
+struct LayerW {
+    Lin qkv, out, f1, f2;
+    float * ln1 = nullptr;   // [w; b]
+    float * ln2 = nullptr;
+};
+
+// Activation buffer: fp32 rows plus their Q8_0 copy (sliced quants + fp32 scales).
+struct Act {
+    float * x = nullptr;
+    int8_t * q = nullptr;
+    float * d = nullptr;
+};
+
+}  // namespace gsvk
+
+using namespace gsvk;
+
+struct gsvk_model {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int verbose = 0;
+    // hparams
+    int D = 512, NH = 16, HD = 32, NL = 24, V = 1025, EOS = 1024, PH = 732, BERT = 1024, FFN = 2048;
+    int head_type = 1;
+    float text_alpha = 1.0f, audio_alpha = 1.0f;
+    // weights
+    DevArena wmem;
+    std::vector<LayerW> L;
+    void * head = nullptr;        // F16/F32 [V][D]
+    Lin head_q8;                  // Q8_0 head
+    float * text_emb = nullptr, * audio_emb = nullptr, * bert_aug = nullptr, * pe = nullptr;
+    uint64_t * rng_jump = nullptr, * rng_adv = nullptr;
+    int rng_chunk = 17;
+    // KV cache
+    DevArena kvmem;
+    uint16_t * kc = nullptr, * vc = nullptr;   // [NL][B][NH][lstride][HD]
+    int kv_B = 0, kv_lmax = 0;
+    int64_t lstride = 0;
+    // decode / state buffers (sized for kv_B)
+    DevArena smem;
+    int s_B = 0, s_hist = 0, s_steps = 0;
+    int64_t s_lstride = 0;
+    Act x, attn, n1, hq;
+    float * qkv = nullptr, * o = nullptr, * h = nullptr, * h2 = nullptr, * logits = nullptr;
+    void * attn_ws = nullptr;
+    int32_t * kv_begin = nullptr, * kv_end = nullptr;
+    int32_t * d_step = nullptr, * hist = nullptr, * ny = nullptr, * fin_step = nullptr,
+            * fin_kind = nullptr, * last_tok = nullptr, * done_counter = nullptr,
+            * n_unfinished = nullptr, * oracle = nullptr, * sampled = nullptr;
+    uint64_t * rng = nullptr;
+    float * probs_dump = nullptr;
+    int32_t * h_pinned = nullptr;   // pinned host word for the unfinished count
+    // sequence state
+    int prompt_len = 0, S = 0, max_len = 0, B = 0, host_step = 0;
+    bool prefilled = false;
+    // graph of one decode step
+    hipGraphExec_t gexec = nullptr;
+    hipGraph_t graph = nullptr;
+    bool use_graph = true;
+
+    ~gsvk_model() {
+        if (gexec) (void) hipGraphExecDestroy(gexec);
+        if (graph) (void) hipGraphDestroy(graph);
+        if (h_pinned) (void) hipHostFree(h_pinned);
+        if (stream) (void) hipStreamDestroy(stream);
+    }
+};
+
+namespace {
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        (void) hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void) hipSetDevice(prev);
+    }
+};
+
+void drop_graph(gsvk_model * m) {
+    if (m->gexec) (void) hipGraphExecDestroy(m->gexec);
+    if (m->graph) (void) hipGraphDestroy(m->graph);
+    m->gexec = nullptr;
+    m->graph = nullptr;
+}
+
+int upload(void * dst, const void * src, size_t bytes, hipStream_t st) {
+    GSVK_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, st));
+    return GSVK_OK;
+}
+
+// Read a Q8_0 [rows][k] tensor and repack it to the device layout.
+int load_q8(gsvk_model * m, const GgufFile & g, const GgufTensor * t, Lin & lin, void * staging,
+            size_t staging_bytes, std::vector<uint8_t> & host) {
+    if (t->type != GGML_Q8_0 || t->ne.size() != 2) {
+        set_error("%s: expected a 2-D Q8_0 tensor (type %u)", t->name.c_str(), t->type);
+        return GSVK_ERR_FORMAT;
+    }
+    lin.k = (int) t->ne[0];
+    lin.n = (int) t->ne[1];
+    if (lin.k % 128 != 0) {
+        set_error("%s: row length %d must be a multiple of 128", t->name.c_str(), lin.k);
+        return GSVK_ERR_FORMAT;
+    }
+    if (t->nbytes > staging_bytes) {
+        set_error("%s: staging buffer too small", t->name.c_str());
+        return GSVK_ERR_FORMAT;
+    }
+    host.resize(t->nbytes);
+    if (!g.read(*t, host.data())) {
+        set_error("read of %s failed", t->name.c_str());
+        return GSVK_ERR_IO;
+    }
+    GSVK_TRY(m->wmem.alloc(lin.qs, (size_t) lin.n * lin.k));
+    GSVK_TRY(m->wmem.alloc(lin.d, (size_t) lin.n * (lin.k / 32)));
+    GSVK_HIP(hipMemcpyAsync(staging, host.data(), t->nbytes, hipMemcpyHostToDevice, m->stream));
+    GSVK_TRY(launch_q8_repack(staging, lin.n, lin.k, lin.qs, lin.d, m->stream));
+    GSVK_HIP(hipStreamSynchronize(m->stream));   // host buffer is reused
+    return GSVK_OK;
+}
+
+int load_f32(gsvk_model * m, const GgufFile & g, const char * name, int64_t expect, float *& dst,
+             std::vector<float> * keep = nullptr) {
+    const GgufTensor * t = g.tensor(name);
+    if (!t) { set_error("missing tensor %s", name); return GSVK_ERR_FORMAT; }
+    if (t->type != GGML_F32) { set_error("%s must be F32 (type %u)", name, t->type); return GSVK_ERR_FORMAT; }
+    int64_t nel = 1;
+    for (int64_t v : t->ne) nel *= v;
+    if (expect >= 0 && nel != expect) {
+        set_error("%s: %lld elements, expected %lld", name, (long long) nel, (long long) expect);
+        return GSVK_ERR_FORMAT;
+    }
+    std::vector<float> host((size_t) nel);
+    if (!g.read(*t, host.data())) { set_error("read of %s failed", name); return GSVK_ERR_IO; }
+    GSVK_TRY(m->wmem.alloc(dst, (size_t) nel));
+    GSVK_HIP(hipMemcpy(dst, host.data(), (size_t) nel * 4, hipMemcpyHostToDevice));
+    if (keep) *keep = std::move(host);
+    return GSVK_OK;
+}
+
+// Resident buffers of the decode step, prefill excluded (sized by B and the KV capacity).
+int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
+    if (m->s_B == B && m->s_hist >= hist_len && m->s_steps >= max_steps && m->s_lstride == m->lstride &&
+        m->x.x)
+        return GSVK_OK;
+    drop_graph(m);
+    m->smem.release();
+    const int D = m->D;
+    auto & a = m->smem;
+    GSVK_TRY(a.alloc(m->x.x, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->x.q, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->x.d, (size_t) B * D / 32));
+    GSVK_TRY(a.alloc(m->attn.x, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->attn.q, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->attn.d, (size_t) B * D / 32));
+    GSVK_TRY(a.alloc(m->n1.x, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->n1.q, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->n1.d, (size_t) B * D / 32));
+    GSVK_TRY(a.alloc(m->hq.q, (size_t) B * m->FFN));
+    GSVK_TRY(a.alloc(m->hq.d, (size_t) B * m->FFN / 32));
+    GSVK_TRY(a.alloc(m->qkv, (size_t) B * 3 * D));
+    GSVK_TRY(a.alloc(m->o, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->h, (size_t) B * m->FFN));
+    GSVK_TRY(a.alloc(m->h2, (size_t) B * D));
+    GSVK_TRY(a.alloc(m->logits, (size_t) B * m->V));
+    char * ws = nullptr;
+    GSVK_TRY(a.alloc(ws, attn_workspace_bytes(B, m->NH, m->lstride)));
+    GSVK_HIP(hipMemset(ws, 0, attn_workspace_bytes(B, m->NH, m->lstride)));
+    m->attn_ws = ws;
+    GSVK_TRY(a.alloc(m->kv_begin, B));
+    GSVK_TRY(a.alloc(m->kv_end, B));
+    GSVK_TRY(a.alloc(m->d_step, 1));
+    GSVK_TRY(a.alloc(m->hist, (size_t) B * hist_len));
+    GSVK_TRY(a.alloc(m->ny, B));
+    GSVK_TRY(a.alloc(m->fin_step, B));
+    GSVK_TRY(a.alloc(m->fin_kind, B));
+    GSVK_TRY(a.alloc(m->last_tok, B));
+    GSVK_TRY(a.alloc(m->done_counter, 1));
+    GSVK_HIP(hipMemset(m->done_counter, 0, sizeof(int32_t)));
+    GSVK_TRY(a.alloc(m->n_unfinished, 1));
+    GSVK_TRY(a.alloc(m->oracle, max_steps));
+    GSVK_TRY(a.alloc(m->sampled, (size_t) max_steps * B));
+    GSVK_TRY(a.alloc(m->rng, B));
+    GSVK_TRY(a.alloc(m->probs_dump, (size_t) max_steps * m->V));
+    m->s_B = B;
+    m->s_hist = hist_len;
+    m->s_steps = max_steps;
+    m->s_lstride = m->lstride;
+    return GSVK_OK;
+}
+
+int alloc_kv(gsvk_model * m, int B, int lmax) {
+    if (m->kc && m->kv_lmax >= lmax && m->kv_B == B) return GSVK_OK;
+    drop_graph(m);
+    m->kvmem.release();
+    m->smem.release();
+    m->s_B = 0;
+    m->kc = m->vc = nullptr;
+    m->kv_B = m->kv_lmax = 0;
+    const size_t per = (size_t) m->NL * B * m->NH * (size_t) (lmax + 1) * m->HD;
+    GSVK_TRY(m->kvmem.alloc(m->kc, per));
+    GSVK_TRY(m->kvmem.alloc(m->vc, per));
+    GSVK_HIP(hipMemsetAsync(m->kc, 0, per * 2, m->stream));
+    GSVK_HIP(hipMemsetAsync(m->vc, 0, per * 2, m->stream));
+    m->kv_B = B;
+    m->kv_lmax = lmax;
+    m->lstride = lmax + 1;
+    return GSVK_OK;
+}
+
+int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
+    if (m->head_type == GGML_Q8_0) {
+        GemvEpilogue epi{};
+        return launch_q8_gemv(m->head_q8.qs, m->head_q8.d, m->V, m->D, x.q, x.d, B, epi, out,
+                              m->stream);
+    }
+    return launch_fdot(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, m->D, x.x, m->D, B, out,
+                       m->V, mode, m->stream);
+}
+
+// One transformer layer after the QKV projection and attention (shared by prefill and decode).
+int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, Act & cur, const Act & attn, float * o,
+               Act & n1, float * h, Act & hq, float * h2) {
+    const int D = m->D, F = m->FFN;
+    GemvEpilogue none{};
+    GSVK_TRY(launch_q8_gemv(w.out.qs, w.out.d, D, D, attn.q, attn.d, R, none, o, m->stream));
+    GSVK_TRY(launch_layernorm(cur.x, o, w.out.b, w.ln1, R, D, 1e-5f, n1.x, n1.q, n1.d, m->stream));
+    GemvEpilogue relu{};
+    relu.bias = w.f1.b;
+    relu.act = 1;
+    GSVK_TRY(launch_q8_gemv(w.f1.qs, w.f1.d, F, D, n1.q, n1.d, R, relu, h, m->stream));
+    GSVK_TRY(launch_q8_quantize(h, R, F, hq.q, hq.d, m->stream));
+    GSVK_TRY(launch_q8_gemv(w.f2.qs, w.f2.d, D, F, hq.q, hq.d, R, none, h2, m->stream));
+    GSVK_TRY(launch_layernorm(n1.x, h2, w.f2.b, w.ln2, R, D, 1e-5f, cur.x, cur.q, cur.d, m->stream));
+    return GSVK_OK;
+}
+
+// Kernels of one decode step at loop index (*d_step - 1): embedding + PE of last_tok, 24
+// layers with the KV append at column S - 1 + *d_step, logits.
+int enqueue_decode_body(gsvk_model * m) {
+    const int B = m->B, D = m->D;
+    GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
+                             m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q, m->x.d,
+                             m->stream));
+    const float scale = 1.0f / std::sqrt((float) m->HD);
+    for (int li = 0; li < m->NL; li++) {
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+        GemvEpilogue qe{};
+        qe.bias = w.qkv.b;
+        qe.kc = m->kc + loff;
+        qe.vc = m->vc + loff;
+        qe.kv_row0 = D;
+        qe.d_model = D;
+        qe.n_head = m->NH;
+        qe.lstride = m->lstride;
+        qe.rows_per_seq = 1;
+        qe.col_ptr = m->d_step;
+        qe.col_add = m->S - 1;
+        GSVK_TRY(launch_q8_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, m->x.q, m->x.d, B, qe, m->qkv, m->stream));
+        GSVK_TRY(launch_attn_decode(m->qkv, 3 * D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
+                                    m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
+                                    m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream));
+        GSVK_TRY(layer_tail(m, w, B, m->x, m->attn, m->o, m->n1, m->h, m->hq, m->h2));
+    }
+    return head_logits(m, m->x, B, 0, m->logits);
+}
+
+}  // namespace
+
+// kv_end[b] = S + step (keys [pad_b, S - 1 + step] inclusive) — written by a tiny kernel so the
+// captured step needs no host update.
+__global__ void k_set_kv_end(int32_t * kv_end, const int32_t * step, int base, int B) {
+    const int b = threadIdx.x + blockIdx.x * blockDim.x;
+    if (b < B) kv_end[b] = base + *step;
+}
+
+namespace {
+
+int enqueue_step_prologue(gsvk_model * m) {
+    hipLaunchKernelGGL(k_set_kv_end, dim3((unsigned) ((m->B + 127) / 128)), dim3(128), 0, m->stream,
+                       m->kv_end, m->d_step, m->S, m->B);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// prefill
+// ---------------------------------------------------------------------------------------
+
+int check_requests(gsvk_model * m, const gsvk_request * reqs, int B) {
+    GSVK_REQUIRE(reqs && B > 0, "no requests");
+    const int P = reqs[0].n_prompt;
+    GSVK_REQUIRE(P >= 0 && P <= PE_MAX, "prompt length %d out of range", P);
+    for (int b = 0; b < B; b++) {
+        const gsvk_request & r = reqs[b];
+        GSVK_REQUIRE(r.n_prompt == P, "request %d: prompt length %d differs from %d (the batch "
+                     "shares one prompt length)", b, r.n_prompt, P);
+        GSVK_REQUIRE(r.n_phones >= 0 && r.n_phones <= PE_MAX, "request %d: %d phones out of range",
+                     b, r.n_phones);
+        GSVK_REQUIRE(r.n_phones == 0 || r.phones, "request %d: null phones", b);
+        GSVK_REQUIRE(P == 0 || r.prompt, "request %d: null prompt", b);
+        for (int t = 0; t < r.n_phones; t++)
+            GSVK_REQUIRE(r.phones[t] >= 0 && r.phones[t] < m->PH, "request %d: phone id %d out of "
+                         "range", b, r.phones[t]);
+        for (int t = 0; t < P; t++)
+            GSVK_REQUIRE(r.prompt[t] >= 0 && r.prompt[t] < m->V, "request %d: prompt code %d out "
+                         "of range", b, r.prompt[t]);
+    }
+    return GSVK_OK;
+}
+
+int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed, float * logits_host,
+               int hist_len, int max_steps) {
+    GSVK_TRY(check_requests(m, reqs, B));
+    const int P = reqs[0].n_prompt;
+    int max_len = 0;
+    for (int b = 0; b < B; b++) max_len = std::max(max_len, reqs[b].n_phones);
+    const int S = max_len + P;
+    GSVK_REQUIRE(S >= 1, "empty input (no phones and no prompt)");
+    const int D = m->D, F = m->FFN, BD = m->BERT;
+    GSVK_TRY(alloc_kv(m, B, std::max(lmax_needed, S + 8)));
+    GSVK_TRY(ensure_state(m, B, std::max(hist_len, P + 1), std::max(max_steps, 1)));
+    m->prompt_len = P;
+    m->S = S;
+    m->max_len = max_len;
+    m->B = B;
+    m->host_step = 0;
+    m->prefilled = false;
+    hipStream_t st = m->stream;
+
+    // host-side packing of the requests
+    std::vector<int32_t> phones((size_t) B * std::max(max_len, 1), 0), pad(B), tlen(B);
+    std::vector<int32_t> row_b, row_t;
+    std::vector<int64_t> boff(B, -1);
+    size_t bert_total = 0;
+    for (int b = 0; b < B; b++) {
+        const gsvk_request & r = reqs[b];
+        pad[b] = max_len - r.n_phones;
+        tlen[b] = r.n_phones;
+        for (int t = 0; t < r.n_phones; t++) {
+            phones[(size_t) b * max_len + pad[b] + t] = r.phones[t];
+            row_b.push_back(b);
+            row_t.push_back(t);
+        }
+        if (r.bert && r.n_phones > 0) {
+            boff[b] = (int64_t) bert_total;
+            bert_total += (size_t) BD * r.n_phones;
+        }
+    }
+    const int R = (int) row_b.size();
+    const int64_t rows = (int64_t) B * S;
+
+    DevArena tmp;
+    int32_t * d_phones, * d_pad, * d_prompt, * d_rowb, * d_rowt, * d_tlen;
+    int64_t * d_boff;
+    float * d_bert = nullptr, * feat = nullptr, * proj = nullptr;
+    GSVK_TRY(tmp.alloc(d_phones, phones.size()));
+    GSVK_TRY(tmp.alloc(d_pad, B));
+    GSVK_TRY(tmp.alloc(d_prompt, std::max(P, 1)));
+    GSVK_TRY(tmp.alloc(d_rowb, std::max(R, 1)));
+    GSVK_TRY(tmp.alloc(d_rowt, std::max(R, 1)));
+    GSVK_TRY(tmp.alloc(d_tlen, B));
+    GSVK_TRY(tmp.alloc(d_boff, B));
+    GSVK_TRY(upload(d_phones, phones.data(), phones.size() * 4, st));
+    GSVK_TRY(upload(d_pad, pad.data(), (size_t) B * 4, st));
+    if (P) GSVK_TRY(upload(d_prompt, reqs[0].prompt, (size_t) P * 4, st));
+    if (R) {
+        GSVK_TRY(upload(d_rowb, row_b.data(), (size_t) R * 4, st));
+        GSVK_TRY(upload(d_rowt, row_t.data(), (size_t) R * 4, st));
+    }
+    GSVK_TRY(upload(d_tlen, tlen.data(), (size_t) B * 4, st));
+    GSVK_TRY(upload(d_boff, boff.data(), (size_t) B * 8, st));
+    if (bert_total) {
+        GSVK_TRY(tmp.alloc(d_bert, bert_total));
+        for (int b = 0; b < B; b++)
+            if (boff[b] >= 0)
+                GSVK_TRY(upload(d_bert + boff[b], reqs[b].bert, (size_t) BD * reqs[b].n_phones * 4, st));
+    }
+    // activations of the prefill rows
+    Act cur, attn, n1, hq;
+    float * qkv, * o, * h, * h2, * last, * lg;
+    GSVK_TRY(tmp.alloc(cur.x, rows * D));
+    GSVK_TRY(tmp.alloc(cur.q, rows * D));
+    GSVK_TRY(tmp.alloc(cur.d, rows * D / 32));
+    GSVK_TRY(tmp.alloc(attn.x, rows * D));
+    GSVK_TRY(tmp.alloc(attn.q, rows * D));
+    GSVK_TRY(tmp.alloc(attn.d, rows * D / 32));
+    GSVK_TRY(tmp.alloc(n1.x, rows * D));
+    GSVK_TRY(tmp.alloc(n1.q, rows * D));
+    GSVK_TRY(tmp.alloc(n1.d, rows * D / 32));
+    GSVK_TRY(tmp.alloc(hq.q, rows * F));
+    GSVK_TRY(tmp.alloc(hq.d, rows * F / 32));
+    GSVK_TRY(tmp.alloc(qkv, rows * 3 * D));
+    GSVK_TRY(tmp.alloc(o, rows * D));
+    GSVK_TRY(tmp.alloc(h, rows * F));
+    GSVK_TRY(tmp.alloc(h2, rows * D));
+    GSVK_TRY(tmp.alloc(last, (size_t) B * D));
+    GSVK_TRY(tmp.alloc(lg, (size_t) B * m->V));
+
+    // inputs: xy, then + bert_aug . [feat; 1] on the text rows
+    GSVK_TRY(launch_build_xy(m->text_emb, m->audio_emb, m->pe, d_phones, d_pad, d_prompt, B, S,
+                             max_len, D, m->text_alpha, m->audio_alpha, cur.x, st));
+    if (R) {
+        GSVK_TRY(tmp.alloc(feat, (size_t) R * (BD + 1)));
+        GSVK_TRY(tmp.alloc(proj, (size_t) R * D));
+        GSVK_TRY(launch_bert_feat(d_bert ? d_bert : cur.x, d_boff, d_rowb, d_rowt, d_tlen, BD, R,
+                                  feat, st));
+        GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R, proj, D, 0, st));
+        GSVK_TRY(launch_add_proj(cur.x, proj, d_rowb, d_rowt, d_pad, S, D, R, st));
+    }
+    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st));
+    int32_t * zero = nullptr;
+    GSVK_TRY(tmp.alloc(zero, 1));
+    GSVK_HIP(hipMemsetAsync(zero, 0, 4, st));
+    const float scale = 1.0f / std::sqrt((float) m->HD);
+    for (int li = 0; li < m->NL; li++) {
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+        GemvEpilogue qe{};
+        qe.bias = w.qkv.b;
+        qe.kc = m->kc + loff;
+        qe.vc = m->vc + loff;
+        qe.kv_row0 = D;
+        qe.d_model = D;
+        qe.n_head = m->NH;
+        qe.lstride = m->lstride;
+        qe.rows_per_seq = S;
+        qe.col_ptr = zero;
+        qe.col_add = 0;
+        GSVK_TRY(launch_q8_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, cur.q, cur.d, rows, qe, qkv, st));
+        GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
+                                     attn.d, st));
+        GSVK_TRY(layer_tail(m, w, rows, cur, attn, o, n1, h, hq, h2));
+    }
+    GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
+    Act lastq;
+    lastq.x = last;
+    if (m->head_type == GGML_Q8_0) {
+        GSVK_TRY(tmp.alloc(lastq.q, (size_t) B * D));
+        GSVK_TRY(tmp.alloc(lastq.d, (size_t) B * D / 32));
+        GSVK_TRY(launch_q8_quantize(last, B, D, lastq.q, lastq.d, st));
+    }
+    // llamafile's tinyBLAS handles the head when the prefill has >= 2 columns
+    GSVK_TRY(head_logits(m, lastq, B, S >= 2 ? 1 : 0, lg));
+    GSVK_HIP(hipMemcpyAsync(m->logits, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToDevice, st));
+    GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));
+    if (logits_host)
+        GSVK_HIP(hipMemcpyAsync(logits_host, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+    m->prefilled = true;
+    return GSVK_OK;
+}
+
+}  // namespace
+
+// ===========================================================================================
+// C ABI
+// ===========================================================================================
+
+extern "C" int gsvk_device_count(int * n) {
+    GSVK_REQUIRE(n, "null pointer");
+    int c = 0;
+    if (hipGetDeviceCount(&c) != hipSuccess) {
+        (void) hipGetLastError();
+        c = 0;
+    }
+    *n = c;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_parse_device(const char * s, int * device) {
+    GSVK_REQUIRE(device, "null pointer");
+    const std::string d = s ? s : "";
+    *device = 0;
+    if (d == "cpu" || d == "CPU" || d == "CPUExecutionProvider") {
+        set_error("device '%s': this build runs on HIP devices only", d.c_str());
+        return GSVK_ERR_NODEV;
+    }
+    if (d.empty()) return GSVK_OK;
+    const size_t colon = d.rfind(':');
+    if (colon != std::string::npos) {
+        *device = std::atoi(d.c_str() + colon + 1);
+        return GSVK_OK;
+    }
+    if (d.find_first_not_of("0123456789") == std::string::npos) {
+        *device = std::atoi(d.c_str());
+        return GSVK_OK;
+    }
+    static const char * names[] = {"gpu", "GPU", "hip", "HIP", "rocm", "ROCm", "vulkan", "Vulkan",
+                                   "cuda", "CUDA"};
+    for (const char * nm : names)
+        if (d == nm) return GSVK_OK;
+    set_error("device '%s' not recognised", d.c_str());
+    return GSVK_ERR_NODEV;
+}
+
+extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_model ** out) {
+    GSVK_REQUIRE(path && out, "null argument");
+    *out = nullptr;
+    int ndev = 0;
+    gsvk_device_count(&ndev);
+    if (device < 0 || device >= ndev) {
+        set_error("HIP device %d not found (%d visible)", device, ndev);
+        return GSVK_ERR_NODEV;
+    }
+    DeviceGuard guard(device);
+    std::unique_ptr<gsvk_model> m(new gsvk_model());
+    m->device = device;
+    m->verbose = verbose;
+    GSVK_HIP(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+    if (getenv("GSVK_NO_GRAPH")) m->use_graph = false;
+    GgufFile g;
+    std::string err;
+    if (!g.open(path, err)) { set_error("%s", err.c_str()); return GSVK_ERR_IO; }
+    uint32_t v;
+    if (g.get_u32("ar.hidden_dim", v)) m->D = (int) v;
+    if (g.get_u32("ar.head", v)) m->NH = (int) v;
+    if (g.get_u32("ar.n_layer", v)) m->NL = (int) v;
+    if (g.get_u32("ar.vocab_size", v)) m->V = (int) v;
+    if (g.get_u32("ar.phoneme_vocab_size", v)) m->PH = (int) v;
+    if (g.get_u32("ar.eos", v)) m->EOS = (int) v;
+    GSVK_REQUIRE(m->NH > 0 && m->D % m->NH == 0, "bad hparams");
+    m->HD = m->D / m->NH;
+    if (m->HD != 32 || m->D != 512) {
+        set_error("unsupported shape d_model=%d head_dim=%d (this build: 512 / 32)", m->D, m->HD);
+        return GSVK_ERR_FORMAT;
+    }
+    GSVK_REQUIRE(m->V > 0 && m->V <= 2048 && m->EOS >= 0 && m->EOS < m->V && m->NL > 0 &&
+                     m->NL <= 256 && m->PH > 0,
+                 "bad hparams V=%d EOS=%d NL=%d", m->V, m->EOS, m->NL);
+    // staging buffer for the largest Q8_0 tensor
+    size_t staging_bytes = 0;
+    for (const auto & t : g.tensors()) staging_bytes = std::max<size_t>(staging_bytes, t.nbytes);
+    DevArena stage;
+    uint8_t * staging = nullptr;
+    GSVK_TRY(stage.alloc(staging, staging_bytes));
+    std::vector<uint8_t> host;
+    m->L.resize(m->NL);
+    char nm[128];
+    for (int li = 0; li < m->NL; li++) {
+        LayerW & w = m->L[li];
+        struct { const char * suffix; Lin * lin; int expect_n, expect_k; } q8s[] = {
+            {"qkv_w", &w.qkv, 3 * m->D, m->D}, {"out_w", &w.out, m->D, m->D},
+            {"ffn1_w", &w.f1, -1, m->D}, {"ffn2_w", &w.f2, m->D, -1}};
+        for (auto & q : q8s) {
+            snprintf(nm, sizeof nm, "transformer.block%d.%s", li, q.suffix);
+            const GgufTensor * t = g.tensor(nm);
+            if (!t) { set_error("missing tensor %s", nm); return GSVK_ERR_FORMAT; }
+            GSVK_TRY(load_q8(m.get(), g, t, *q.lin, staging, staging_bytes, host));
+            if ((q.expect_n >= 0 && q.lin->n != q.expect_n) || (q.expect_k >= 0 && q.lin->k != q.expect_k)) {
+                set_error("%s: shape [%d, %d] does not match the model", nm, q.lin->n, q.lin->k);
+                return GSVK_ERR_FORMAT;
+            }
+        }
+        if (li == 0) m->FFN = w.f1.n;
+        if (w.f1.n != m->FFN || w.f2.k != m->FFN) { set_error("layer %d: inconsistent FFN size", li); return GSVK_ERR_FORMAT; }
+        struct { const char * suffix; float ** dst; int64_t n; } f32s[] = {
+            {"qkv_b", &w.qkv.b, 3 * m->D}, {"out_b", &w.out.b, m->D}, {"ffn1_b", &w.f1.b, m->FFN},
+            {"ffn2_b", &w.f2.b, m->D}};
+        for (auto & f : f32s) {
+            snprintf(nm, sizeof nm, "transformer.block%d.%s", li, f.suffix);
+            GSVK_TRY(load_f32(m.get(), g, nm, f.n, *f.dst));
+        }
+        // LayerNorm [w; b] packs (src/gsv_ar.cpp:599-626)
+        std::vector<float> wv, bv, pack(2 * (size_t) m->D);
+        float * tmpd = nullptr;
+        for (int which = 0; which < 2; which++) {
+            snprintf(nm, sizeof nm, "transformer.block%d.norm%d_w", li, which + 1);
+            GSVK_TRY(load_f32(m.get(), g, nm, m->D, tmpd, &wv));
+            snprintf(nm, sizeof nm, "transformer.block%d.norm%d_b", li, which + 1);
+            GSVK_TRY(load_f32(m.get(), g, nm, m->D, tmpd, &bv));
+            std::copy(wv.begin(), wv.end(), pack.begin());
+            std::copy(bv.begin(), bv.end(), pack.begin() + m->D);
+            float *& dst = which == 0 ? w.ln1 : w.ln2;
+            GSVK_TRY(m->wmem.alloc(dst, pack.size()));
+            GSVK_HIP(hipMemcpy(dst, pack.data(), pack.size() * 4, hipMemcpyHostToDevice));
+        }
+    }
+    // head (any of F32 / F16 / Q8_0)
+    {
+        const GgufTensor * t = g.tensor("ar.predict");
+        if (!t) { set_error("missing tensor ar.predict"); return GSVK_ERR_FORMAT; }
+        if (t->ne.size() != 2 || t->ne[0] != m->D || t->ne[1] != m->V) {
+            set_error("ar.predict: shape does not match d_model x vocab");
+            return GSVK_ERR_FORMAT;
+        }
+        m->head_type = (int) t->type;
+        if (t->type == GGML_Q8_0) {
+            GSVK_TRY(load_q8(m.get(), g, t, m->head_q8, staging, staging_bytes, host));
+        } else if (t->type == GGML_F16 || t->type == GGML_F32) {
+            host.resize(t->nbytes);
+            if (!g.read(*t, host.data())) { set_error("read of ar.predict failed"); return GSVK_ERR_IO; }
+            uint8_t * d = nullptr;
+            GSVK_TRY(m->wmem.alloc(d, t->nbytes));
+            GSVK_HIP(hipMemcpy(d, host.data(), t->nbytes, hipMemcpyHostToDevice));
+            m->head = d;
+        } else {
+            set_error("ar.predict: unsupported type %u", t->type);
+            return GSVK_ERR_FORMAT;
+        }
+    }
+    // embeddings and BERT projection must be F32 (src/gsv_ar.cpp:632-637)
+    GSVK_TRY(load_f32(m.get(), g, "ar.text_emb", (int64_t) m->PH * m->D, m->text_emb));
+    GSVK_TRY(load_f32(m.get(), g, "ar.audio_emb", (int64_t) m->V * m->D, m->audio_emb));
+    {
+        std::vector<float> wv, bv;
+        float * tmpd = nullptr;
+        GSVK_TRY(load_f32(m.get(), g, "ar.bert_proj", (int64_t) m->D * m->BERT, tmpd, &wv));
+        GSVK_TRY(load_f32(m.get(), g, "ar.bert_proj_b", m->D, tmpd, &bv));
+        // bert_aug [D][BERT+1] = [W | b] (src/gsv_ar.cpp:647-656)
+        std::vector<float> aug((size_t) m->D * (m->BERT + 1));
+        for (int d = 0; d < m->D; d++) {
+            std::copy(wv.begin() + (size_t) d * m->BERT, wv.begin() + (size_t) (d + 1) * m->BERT,
+                      aug.begin() + (size_t) d * (m->BERT + 1));
+            aug[(size_t) d * (m->BERT + 1) + m->BERT] = bv[d];
+        }
+        GSVK_TRY(m->wmem.alloc(m->bert_aug, aug.size()));
+        GSVK_HIP(hipMemcpy(m->bert_aug, aug.data(), aug.size() * 4, hipMemcpyHostToDevice));
+    }
+    {
+        std::vector<float> a1, a2;
+        float * tmpd = nullptr;
+        GSVK_TRY(load_f32(m.get(), g, "ar.text_pe_alpha", 1, tmpd, &a1));
+        GSVK_TRY(load_f32(m.get(), g, "ar.audio_pe_alpha", 1, tmpd, &a2));
+        m->text_alpha = a1[0];
+        m->audio_alpha = a2[0];
+    }
+    // PE table (impl::mk_pe, src/gsv_ar.cpp:173-181), same float expressions, host libm
+    {
+        std::vector<float> pe((size_t) PE_MAX * m->D);
+        for (int pos = 0; pos < PE_MAX; pos++)
+            for (int i = 0; i < m->D; i += 2) {
+                const float div = std::exp((float) i * -(std::log(10000.0f) / (float) m->D));
+                pe[(size_t) pos * m->D + i] = std::sin((float) pos * div);
+                pe[(size_t) pos * m->D + i + 1] = std::cos((float) pos * div);
+            }
+        GSVK_TRY(m->wmem.alloc(m->pe, pe.size()));
+        GSVK_HIP(hipMemcpy(m->pe, pe.data(), pe.size() * 4, hipMemcpyHostToDevice));
+    }
+    // xorshift64* jump tables for this vocabulary
+    {
+        m->rng_chunk = (m->V + 63) / 64;
+        std::vector<uint64_t> jump(64 * 64), adv(64);
+        rng_tables(m->V, m->rng_chunk, jump.data(), adv.data());
+        GSVK_TRY(m->wmem.alloc(m->rng_jump, jump.size()));
+        GSVK_TRY(m->wmem.alloc(m->rng_adv, adv.size()));
+        GSVK_HIP(hipMemcpy(m->rng_jump, jump.data(), jump.size() * 8, hipMemcpyHostToDevice));
+        GSVK_HIP(hipMemcpy(m->rng_adv, adv.data(), adv.size() * 8, hipMemcpyHostToDevice));
+    }
+    GSVK_HIP(hipHostMalloc((void **) &m->h_pinned, 64, hipHostMallocDefault));
+    GSVK_HIP(hipStreamSynchronize(m->stream));
+    if (verbose)
+        fprintf(stderr, "[gsvk] loaded %s on HIP device %d: D=%d heads=%d layers=%d vocab=%d EOS=%d "
+                        "ffn=%d head=%s\n", path, device, m->D, m->NH, m->NL, m->V, m->EOS, m->FFN,
+                m->head_type == 0 ? "F32" : m->head_type == 1 ? "F16" : "Q8_0");
+    *out = m.release();
+    return GSVK_OK;
+}
+
+extern "C" void gsvk_model_free(gsvk_model * m) {
+    if (!m) return;
+    DeviceGuard guard(m->device);
+    (void) hipStreamSynchronize(m->stream);
+    delete m;
+}
+
+extern "C" int gsvk_model_get_info(const gsvk_model * m, gsvk_model_info * info) {
+    GSVK_REQUIRE(m && info, "null argument");
+    info->d_model = m->D;
+    info->n_head = m->NH;
+    info->head_dim = m->HD;
+    info->n_layer = m->NL;
+    info->vocab = m->V;
+    info->eos = m->EOS;
+    info->phone_vocab = m->PH;
+    info->bert_dim = m->BERT;
+    info->ffn_dim = m->FFN;
+    info->head_type = m->head_type;
+    info->text_alpha = m->text_alpha;
+    info->audio_alpha = m->audio_alpha;
+    info->prompt_len = m->prompt_len;
+    info->kv_batch = m->kv_B;
+    info->kv_lmax = m->kv_lmax;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_kv_alloc(gsvk_model * m, int B, int lmax) {
+    GSVK_REQUIRE(m && B > 0 && lmax > 0, "bad arguments");
+    DeviceGuard guard(m->device);
+    return alloc_kv(m, B, lmax);
+}
+
+extern "C" int gsvk_release_cache(gsvk_model * m) {
+    GSVK_REQUIRE(m, "null model");
+    DeviceGuard guard(m->device);
+    GSVK_HIP(hipStreamSynchronize(m->stream));
+    drop_graph(m);
+    m->smem.release();
+    m->s_B = 0;
+    m->kvmem.release();
+    m->kc = m->vc = nullptr;
+    m->kv_B = m->kv_lmax = 0;
+    m->prefilled = false;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits) {
+    GSVK_REQUIRE(m && logits, "null argument");
+    if (B == 0) return GSVK_OK;
+    DeviceGuard guard(m->device);
+    int max_len = 0;
+    for (int b = 0; b < B; b++) max_len = std::max(max_len, reqs[b].n_phones);
+    return do_prefill(m, reqs, B, max_len + (B > 0 ? reqs[0].n_prompt : 0) + 8, logits, 0, 1);
+}
+
+extern "C" int gsvk_prefill(gsvk_model * m, const gsvk_request * reqs, int B, float * logits,
+                            int * S_out) {
+    GSVK_REQUIRE(m, "null model");
+    DeviceGuard guard(m->device);
+    int max_len = 0;
+    for (int b = 0; b < B && reqs; b++) max_len = std::max(max_len, reqs[b].n_phones);
+    const int S = max_len + (B > 0 && reqs ? reqs[0].n_prompt : 0);
+    // keep an existing larger cache of the same batch (src/gsv_ar.cpp:95)
+    const int lmax = (m->kc && m->kv_B == B) ? std::max(m->kv_lmax, S + 8) : S + 8;
+    GSVK_TRY(do_prefill(m, reqs, B, lmax, logits, 0, 1));
+    if (S_out) *S_out = m->S;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float * logits) {
+    GSVK_REQUIRE(m && last_tok, "null argument");
+    if (!m->prefilled) { set_error("decode_step before prefill"); return GSVK_ERR_STATE; }
+    DeviceGuard guard(m->device);
+    const int B = m->B;
+    if (m->S + m->host_step >= m->kv_lmax + 1 || m->prompt_len + m->host_step >= PE_MAX) {
+        set_error("decode_step: KV cache or positional table full (step %d)", m->host_step);
+        return GSVK_ERR_STATE;
+    }
+    for (int b = 0; b < B; b++)
+        GSVK_REQUIRE(last_tok[b] >= 0 && last_tok[b] < m->V, "token %d out of range", last_tok[b]);
+    hipStream_t st = m->stream;
+    const int32_t step1 = m->host_step + 1;
+    GSVK_TRY(upload(m->last_tok, last_tok, (size_t) B * 4, st));
+    GSVK_TRY(upload(m->d_step, &step1, 4, st));
+    GSVK_HIP(hipStreamSynchronize(st));   // the host values above live on this stack frame
+    GSVK_TRY(enqueue_step_prologue(m));
+    GSVK_TRY(enqueue_decode_body(m));
+    if (logits) GSVK_HIP(hipMemcpyAsync(logits, m->logits, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+    m->host_step++;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_kv_read(gsvk_model * m, int layer, uint16_t * k_out, uint16_t * v_out) {
+    GSVK_REQUIRE(m && m->kc && layer >= 0 && layer < m->NL, "bad arguments");
+    DeviceGuard guard(m->device);
+    const size_t per = (size_t) m->kv_B * m->NH * m->lstride * m->HD;
+    if (k_out) GSVK_HIP(hipMemcpyAsync(k_out, m->kc + per * layer, per * 2, hipMemcpyDeviceToHost, m->stream));
+    if (v_out) GSVK_HIP(hipMemcpyAsync(v_out, m->vc + per * layer, per * 2, hipMemcpyDeviceToHost, m->stream));
+    GSVK_HIP(hipStreamSynchronize(m->stream));
+    return GSVK_OK;
+}
+
+
+extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
+                             const gsvk_sampler_cfg * cfg, uint64_t seed_base, int early_stop_num,
+                             int max_steps, const int32_t * oracle, int n_oracle,
+                             const uint64_t * seeds, unsigned flags, gsvk_gen_out * out) {
+    GSVK_REQUIRE(m && cfg && out, "null argument");
+    if (B == 0) return GSVK_OK;
+    GSVK_REQUIRE(reqs && B > 0 && max_steps >= 0, "bad arguments");
+    GSVK_REQUIRE(out->tokens && out->tok_len && out->lens, "null output buffers");
+    DeviceGuard guard(m->device);
+    const int P = reqs[0].n_prompt;
+    GSVK_REQUIRE(out->tok_stride >= P + max_steps, "tok_stride %d < prompt + max_steps (%d)",
+                 out->tok_stride, P + max_steps);
+    GSVK_REQUIRE(P + max_steps <= PE_MAX, "prompt_len + max_steps = %d exceeds the positional "
+                 "table (%d)", P + max_steps, PE_MAX);
+    GSVK_REQUIRE(!oracle || n_oracle >= 0, "bad oracle length");
+    int max_len = 0;
+    for (int b = 0; b < B; b++) max_len = std::max(max_len, reqs[b].n_phones);
+    const int S = max_len + P;
+    const int hist_len = P + max_steps;
+    const auto t_pf = std::chrono::steady_clock::now();
+    GSVK_TRY(do_prefill(m, reqs, B, S + max_steps + 8, nullptr, hist_len, max_steps));
+    out->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_pf).count();
+    hipStream_t st = m->stream;
+    std::vector<int32_t> pad(B);
+    for (int b = 0; b < B; b++) pad[b] = max_len - reqs[b].n_phones;
+    // host state -> device
+    std::vector<int32_t> hist((size_t) B * hist_len, 0), ny(B, P), fin(B, -1), kind(B, -1), last(B, 0);
+    std::vector<uint64_t> rng(B);
+    for (int b = 0; b < B; b++) {
+        if (P) std::copy(reqs[b].prompt, reqs[b].prompt + P, hist.begin() + (size_t) b * hist_len);
+        last[b] = P ? reqs[b].prompt[P - 1] : 0;
+        const uint64_t sd = seeds ? seeds[b] : seed_base + 0x9E3779B9ull * (uint64_t) b;
+        rng[b] = sd ? sd : 1;   // gsv_rng: seed 0 -> 1
+    }
+    const int32_t zero = 0;
+    GSVK_TRY(upload(m->hist, hist.data(), hist.size() * 4, st));
+    GSVK_TRY(upload(m->ny, ny.data(), (size_t) B * 4, st));
+    GSVK_TRY(upload(m->fin_step, fin.data(), (size_t) B * 4, st));
+    GSVK_TRY(upload(m->fin_kind, kind.data(), (size_t) B * 4, st));
+    GSVK_TRY(upload(m->last_tok, last.data(), (size_t) B * 4, st));
+    GSVK_TRY(upload(m->rng, rng.data(), (size_t) B * 8, st));
+    GSVK_TRY(upload(m->d_step, &zero, 4, st));
+    GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));
+    if (oracle && n_oracle > 0)
+        GSVK_TRY(upload(m->oracle, oracle, (size_t) std::min(n_oracle, max_steps) * 4, st));
+    GSVK_HIP(hipMemsetAsync(m->sampled, 0xff, (size_t) std::max(max_steps, 1) * B * 4, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+
+    // one step = sampler (loop index idx) + decode at idx; the graph is replayed max_steps times
+    SampleArgs sa{};
+    sa.logits = m->logits;
+    sa.V = m->V;
+    sa.eos = m->EOS;
+    sa.B = B;
+    sa.P = P;
+    sa.hist = m->hist;
+    sa.hist_stride = hist_len;
+    sa.ny = m->ny;
+    sa.fin_step = m->fin_step;
+    sa.fin_kind = m->fin_kind;
+    sa.rng = m->rng;
+    sa.jump = m->rng_jump;
+    sa.adv = m->rng_adv;
+    sa.chunk = m->rng_chunk;
+    sa.top_k = cfg->top_k;
+    sa.top_p = cfg->top_p;
+    sa.temperature = cfg->temperature;
+    sa.rep = cfg->repetition_penalty;
+    sa.oracle = (oracle && n_oracle > 0) ? m->oracle : nullptr;
+    sa.n_oracle = std::min(n_oracle, max_steps);
+    sa.step = m->d_step;
+    sa.flags = (flags & GSVK_GEN_EOS_MASK_ALL) ? 1u : 0u;
+    sa.last_tok = m->last_tok;
+    sa.probs_dump = (flags & GSVK_GEN_PROB_DUMP) ? m->probs_dump : nullptr;
+    sa.sampled_dump = m->sampled;
+    sa.max_steps = max_steps;
+    sa.done_counter = m->done_counter;
+    sa.n_unfinished = m->n_unfinished;
+    sa.early_stop = early_stop_num;
+    auto enqueue_step = [&]() -> int {
+        GSVK_TRY(launch_sample(sa, st));
+        GSVK_TRY(enqueue_step_prologue(m));
+        GSVK_TRY(enqueue_decode_body(m));
+        return GSVK_OK;
+    };
+    drop_graph(m);
+    if (m->use_graph && max_steps > 1) {
+        GSVK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        const int rc = enqueue_step();
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc != GSVK_OK) { if (g) (void) hipGraphDestroy(g); return rc; }
+        GSVK_HIP(e);
+        m->graph = g;
+        GSVK_HIP(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+    }
+    const int check_every = 8;
+    int steps_run = 0;
+    GSVK_HIP(hipStreamSynchronize(st));
+    const auto t_dec = std::chrono::steady_clock::now();
+    for (int idx = 0; idx < max_steps; idx++) {
+        if (m->gexec) GSVK_HIP(hipGraphLaunch(m->gexec, st));
+        else GSVK_TRY(enqueue_step());
+        steps_run++;
+        if (out->progress) out->progress(out->progress_user, idx);
+        if ((idx + 1) % check_every == 0 || idx + 1 == max_steps) {
+            GSVK_HIP(hipMemcpyAsync(m->h_pinned, m->n_unfinished, 4, hipMemcpyDeviceToHost, st));
+            GSVK_HIP(hipStreamSynchronize(st));
+            if (*m->h_pinned == 0) break;
+        }
+    }
+    GSVK_HIP(hipStreamSynchronize(st));
+    out->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_dec).count();
+    // results
+    GSVK_HIP(hipMemcpy(hist.data(), m->hist, hist.size() * 4, hipMemcpyDeviceToHost));
+    GSVK_HIP(hipMemcpy(ny.data(), m->ny, (size_t) B * 4, hipMemcpyDeviceToHost));
+    GSVK_HIP(hipMemcpy(fin.data(), m->fin_step, (size_t) B * 4, hipMemcpyDeviceToHost));
+    GSVK_HIP(hipMemcpy(kind.data(), m->fin_kind, (size_t) B * 4, hipMemcpyDeviceToHost));
+    struct Fin { int step, kind, b; };
+    std::vector<Fin> order;
+    int last_fin = -1;
+    bool all = true;
+    for (int b = 0; b < B; b++) {
+        const int nb = ny[b];
+        std::copy(hist.begin() + (size_t) b * hist_len, hist.begin() + (size_t) b * hist_len + nb,
+                  out->tokens + (size_t) b * out->tok_stride);
+        if (fin[b] >= 0) {
+            out->tok_len[b] = nb - 1;   // minus the stopping token
+            order.push_back({fin[b], kind[b], b});
+            last_fin = std::max(last_fin, fin[b]);
+        } else {
+            out->tok_len[b] = nb;
+            order.push_back({max_steps, 2, b});
+            all = false;
+        }
+    }
+    std::stable_sort(order.begin(), order.end(), [](const Fin & x, const Fin & y) {
+        return x.step != y.step ? x.step < y.step : (x.kind != y.kind ? x.kind < y.kind : x.b < y.b);
+    });
+    for (int i = 0; i < B; i++) {
+        out->lens[i] = order[i].step;
+        if (out->finish_seq) out->finish_seq[i] = order[i].b;
+    }
+    out->n_steps = all ? last_fin + 1 : max_steps;
+    if ((flags & GSVK_GEN_PROB_DUMP) && out->probs0 && out->n_steps > 0)
+        GSVK_HIP(hipMemcpy(out->probs0, m->probs_dump, (size_t) out->n_steps * m->V * 4,
+                           hipMemcpyDeviceToHost));
+    (void) steps_run;
+    return GSVK_OK;
+}
+
+// Sampled-token dump of the last generate ([n_steps][B], -1 where a sequence had finished).
+extern "C" int gsvk_last_sampled(gsvk_model * m, int n_steps, int32_t * out) {
+    GSVK_REQUIRE(m && out && n_steps >= 0 && n_steps <= m->s_steps, "bad arguments");
+    DeviceGuard guard(m->device);
+    if (n_steps == 0) return GSVK_OK;
+    GSVK_HIP(hipMemcpy(out, m->sampled, (size_t) n_steps * m->s_B * 4, hipMemcpyDeviceToHost));
+    return GSVK_OK;
+}

@@ -1,0 +1,41 @@
+// Device sampler interface (sampler.hip).
+#pragma once
+
+#include "common.h"
+
+namespace gsvk {
+
+struct SampleArgs {
+    const float * logits;      // [B][V]
+    int V, eos, B, P;
+    int32_t * hist;            // [B][hist_stride] prompt + generated tokens
+    int hist_stride;
+    int32_t * ny;              // [B] tokens in hist
+    int32_t * fin_step;        // [B] -1 while running
+    int32_t * fin_kind;        // [B] 0 EOS, 1 early stop
+    uint64_t * rng;            // [B] xorshift64* state
+    const uint64_t * jump;     // [64][64] columns of A^(chunk*t + 1)
+    const uint64_t * adv;      // [64] columns of A^V
+    int chunk;                 // draws per lane of wave 0
+    int top_k;
+    float top_p, temperature, rep;
+    const int32_t * oracle;    // teacher forcing tokens or null
+    int n_oracle;
+    int32_t * step;            // device loop index
+    unsigned flags;            // bit0: mask EOS at every step
+    int32_t * last_tok;        // [B]
+    float * probs_dump;        // [max_steps][V] for sequence 0, or null
+    int32_t * sampled_dump;    // [max_steps][B] sampler choice before the oracle, or null
+    int max_steps;
+    int32_t * done_counter;    // zero between calls
+    int32_t * n_unfinished;    // written by the last workgroup
+    int early_stop;            // -1 = off
+};
+
+int launch_sample(const SampleArgs & a, hipStream_t stream);
+
+// jump: [64][64] columns of A^(chunk*t + 1) for t < 64; adv: [64] columns of A^V, where A is
+// the GF(2) matrix of one xorshift64* state update.
+void rng_tables(int V, int chunk, uint64_t * jump, uint64_t * adv);
+
+}  // namespace gsvk

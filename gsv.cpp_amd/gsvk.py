@@ -1,0 +1,293 @@
+"""Python binding of the gfx950 AR decoder C ABI (include/gsvk.h) over ctypes.
+
+This is the host-side mirror of the reference's ``gsv_ar`` interface for Python callers, tests
+and benchmarks. It loads ``gsv.cpp_amd/lib/libgsvk.so`` (built by ``gsv.cpp_amd/build.py``) and
+raises if the library is missing: there is no fallback path. Device ops take torch tensors
+(torch is only the device-memory and stream plumbing) and pass raw pointers to the kernels.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libgsvk.so")
+
+GSVK_GEN_EOS_MASK_ALL = 1
+GSVK_GEN_PROB_DUMP = 2
+
+# every entry point declared in include/gsvk.h
+EXPORTS = [
+    "gsvk_last_error", "gsvk_device_count", "gsvk_parse_device", "gsvk_model_load", "gsvk_model_free",
+    "gsvk_model_get_info", "gsvk_generate", "gsvk_first_logits", "gsvk_release_cache", "gsvk_kv_alloc",
+    "gsvk_prefill", "gsvk_decode_step", "gsvk_kv_read", "gsvk_last_sampled", "gsvk_op_q8_dequant",
+    "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
+    "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode",
+]
+
+
+class GsvkError(RuntimeError):
+    pass
+
+
+class Request(C.Structure):
+    _fields_ = [("phones", C.c_void_p), ("n_phones", C.c_int32), ("bert", C.c_void_p),
+                ("prompt", C.c_void_p), ("n_prompt", C.c_int32)]
+
+
+class SamplerCfg(C.Structure):
+    _fields_ = [("top_k", C.c_int), ("top_p", C.c_float), ("temperature", C.c_float),
+                ("repetition_penalty", C.c_float)]
+
+
+PROGRESS_FN = C.CFUNCTYPE(None, C.c_void_p, C.c_int)
+
+
+class GenOut(C.Structure):
+    _fields_ = [("tokens", C.c_void_p), ("tok_stride", C.c_int32), ("tok_len", C.c_void_p),
+                ("lens", C.c_void_p), ("finish_seq", C.c_void_p), ("probs0", C.c_void_p),
+                ("n_steps", C.c_int32), ("progress", PROGRESS_FN), ("progress_user", C.c_void_p),
+                ("prefill_ms", C.c_double), ("decode_ms", C.c_double)]
+
+
+class ModelInfo(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_head", C.c_int), ("head_dim", C.c_int), ("n_layer", C.c_int),
+                ("vocab", C.c_int), ("eos", C.c_int), ("phone_vocab", C.c_int), ("bert_dim", C.c_int),
+                ("ffn_dim", C.c_int), ("head_type", C.c_int), ("text_alpha", C.c_float),
+                ("audio_alpha", C.c_float), ("prompt_len", C.c_int), ("kv_batch", C.c_int),
+                ("kv_lmax", C.c_int)]
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libgsvk.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise GsvkError(f"{LIB_PATH} not found: build it with python gsv.cpp_amd/build.py")
+        L = C.CDLL(LIB_PATH)
+        vp, i64, i32, f32 = C.c_void_p, C.c_int64, C.c_int, C.c_float
+        L.gsvk_last_error.restype = C.c_char_p
+        L.gsvk_device_count.argtypes = [C.POINTER(C.c_int)]
+        L.gsvk_parse_device.argtypes = [C.c_char_p, C.POINTER(C.c_int)]
+        L.gsvk_model_load.argtypes = [C.c_char_p, i32, i32, C.POINTER(vp)]
+        L.gsvk_model_free.argtypes = [vp]
+        L.gsvk_model_free.restype = None
+        L.gsvk_model_get_info.argtypes = [vp, C.POINTER(ModelInfo)]
+        L.gsvk_generate.argtypes = [vp, C.POINTER(Request), i32, C.POINTER(SamplerCfg), C.c_uint64, i32,
+                                    i32, vp, i32, vp, C.c_uint, C.POINTER(GenOut)]
+        L.gsvk_first_logits.argtypes = [vp, C.POINTER(Request), i32, vp]
+        L.gsvk_release_cache.argtypes = [vp]
+        L.gsvk_kv_alloc.argtypes = [vp, i32, i32]
+        L.gsvk_prefill.argtypes = [vp, C.POINTER(Request), i32, vp, C.POINTER(C.c_int)]
+        L.gsvk_decode_step.argtypes = [vp, vp, vp]
+        L.gsvk_kv_read.argtypes = [vp, i32, vp, vp]
+        L.gsvk_last_sampled.argtypes = [vp, i32, vp]
+        L.gsvk_op_q8_dequant.argtypes = [vp, i64, vp, vp]
+        L.gsvk_op_q8_repack.argtypes = [vp, i64, i64, vp, vp, vp]
+        L.gsvk_op_q8_quantize.argtypes = [vp, i64, i64, vp, vp, vp]
+        L.gsvk_op_q8_gemv.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
+        L.gsvk_op_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, f32, vp, vp, vp, vp]
+        L.gsvk_op_add_act.argtypes = [vp, vp, i64, i64, i32, vp, vp]
+        L.gsvk_op_fdot.argtypes = [vp, i32, i64, i64, vp, i64, vp, i32, vp]
+        L.gsvk_attn_workspace_bytes.argtypes = [i32, i32, i64]
+        L.gsvk_attn_workspace_bytes.restype = C.c_size_t
+        L.gsvk_op_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i64, vp, vp, i64, f32, vp, vp, vp,
+                                          vp, vp, vp]
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().gsvk_last_error().decode(errors="replace")
+
+
+def check(rc: int, what: str = "gsvk call"):
+    if rc != 0:
+        raise GsvkError(f"{what} failed ({rc}): {last_error()}")
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    check(lib().gsvk_device_count(C.byref(n)))
+    return n.value
+
+
+def parse_device(s: str) -> int:
+    d = C.c_int(0)
+    check(lib().gsvk_parse_device(s.encode(), C.byref(d)), "parse_device")
+    return d.value
+
+
+# ---- device ops on torch tensors ------------------------------------------------------------
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is not None:
+        return C.c_void_p(stream)
+    import torch
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def op_q8_dequant(blocks, out, stream=None):
+    check(lib().gsvk_op_q8_dequant(_p(blocks), blocks.numel() // 34, _p(out), _stream(stream)), "q8_dequant")
+
+
+def op_q8_repack(blocks, rows, k, qs, d, stream=None):
+    check(lib().gsvk_op_q8_repack(_p(blocks), rows, k, _p(qs), _p(d), _stream(stream)), "q8_repack")
+
+
+def op_q8_quantize(x, xq, xd, stream=None):
+    rows, k = x.shape
+    check(lib().gsvk_op_q8_quantize(_p(x), rows, k, _p(xq), _p(xd), _stream(stream)), "q8_quantize")
+
+
+def op_q8_gemv(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
+    check(lib().gsvk_op_q8_gemv(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y),
+                                _stream(stream)), "q8_gemv")
+
+
+def op_layernorm(x, r, bias, wb, eps, y, yq=None, yd=None, stream=None):
+    rows, n = x.shape
+    check(lib().gsvk_op_layernorm(_p(x), _p(r), _p(bias), _p(wb), rows, n, eps, _p(y), _p(yq), _p(yd),
+                                  _stream(stream)), "layernorm")
+
+
+def op_add_act(a, b, act, y, stream=None):
+    check(lib().gsvk_op_add_act(_p(a), _p(b), a.numel(), b.numel(), act, _p(y), _stream(stream)), "add_act")
+
+
+def op_fdot(w, wtype, x, y, mode, stream=None):
+    n, k = w.shape
+    check(lib().gsvk_op_fdot(_p(w), wtype, n, k, _p(x), x.shape[0], _p(y), mode, _stream(stream)), "fdot")
+
+
+def attn_workspace_bytes(B, nh, max_keys) -> int:
+    return int(lib().gsvk_attn_workspace_bytes(B, nh, max_keys))
+
+
+def op_attn_decode(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, oq=None, od=None, ws=None,
+                   stream=None):
+    B, nh, hd = q.shape
+    lstride = k.shape[2]
+    check(lib().gsvk_op_attn_decode(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin), _p(kv_end),
+                                    max_keys, scale, _p(out), _p(out16), _p(oq), _p(od), _p(ws),
+                                    _stream(stream)), "attn_decode")
+
+
+# ---- model ----------------------------------------------------------------------------------
+
+def _requests(reqs):
+    arr = (Request * len(reqs))()
+    keep = []
+    for i, r in enumerate(reqs):
+        ph = np.ascontiguousarray(r["phones"], np.int32)
+        pr = np.ascontiguousarray(r["prompt"], np.int32)
+        be = None if r.get("bert") is None else np.ascontiguousarray(r["bert"], np.float32)
+        keep += [ph, pr, be]
+        arr[i].phones = ph.ctypes.data if ph.size else None
+        arr[i].n_phones = ph.size
+        arr[i].bert = None if be is None else be.ctypes.data
+        arr[i].prompt = pr.ctypes.data if pr.size else None
+        arr[i].n_prompt = pr.size
+    return arr, keep
+
+
+class Model:
+    """A loaded AR model on one HIP device (mirror of the reference's gsv_ar)."""
+
+    def __init__(self, path: str, device: int = 0, verbose: bool = False):
+        h = C.c_void_p()
+        check(lib().gsvk_model_load(path.encode(), device, int(verbose), C.byref(h)), "model_load")
+        self.h = h
+        self.info = self._info()
+
+    def _info(self):
+        info = ModelInfo()
+        check(lib().gsvk_model_get_info(self.h, C.byref(info)), "model_get_info")
+        return info
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().gsvk_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def V(self):
+        return self.info.vocab
+
+    def first_logits(self, reqs):
+        arr, keep = _requests(reqs)
+        out = np.zeros((len(reqs), self.V), np.float32)
+        check(lib().gsvk_first_logits(self.h, arr, len(reqs), out.ctypes.data), "first_logits")
+        return out
+
+    def prefill(self, reqs):
+        arr, keep = _requests(reqs)
+        out = np.zeros((len(reqs), self.V), np.float32)
+        S = C.c_int(0)
+        check(lib().gsvk_prefill(self.h, arr, len(reqs), out.ctypes.data, C.byref(S)), "prefill")
+        return out, S.value
+
+    def decode_step(self, last_tok):
+        last_tok = np.ascontiguousarray(last_tok, np.int32)
+        out = np.zeros((last_tok.size, self.V), np.float32)
+        check(lib().gsvk_decode_step(self.h, last_tok.ctypes.data, out.ctypes.data), "decode_step")
+        return out
+
+    def kv_read(self, layer):
+        info = self._info()
+        shape = (info.kv_batch, info.n_head, info.kv_lmax + 1, info.head_dim)
+        k = np.zeros(shape, np.uint16)
+        v = np.zeros(shape, np.uint16)
+        check(lib().gsvk_kv_read(self.h, layer, k.ctypes.data, v.ctypes.data), "kv_read")
+        return k, v
+
+    def release_cache(self):
+        check(lib().gsvk_release_cache(self.h), "release_cache")
+
+    def generate(self, reqs, sampler=(15, 1.0, 1.0, 1.35), seed_base=0, early_stop=-1, max_steps=1500,
+                 oracle=None, seeds=None, flags=0, want_sampled=False, want_probs0=False):
+        B = len(reqs)
+        arr, keep = _requests(reqs)
+        P = len(reqs[0]["prompt"])
+        stride = P + max_steps
+        tokens = np.zeros((B, stride), np.int32)
+        tok_len = np.zeros(B, np.int32)
+        lens = np.zeros(B, np.int32)
+        fin = np.zeros(B, np.int32)
+        probs0 = np.zeros((max(max_steps, 1), self.V), np.float32) if want_probs0 else None
+        out = GenOut(tokens.ctypes.data, stride, tok_len.ctypes.data, lens.ctypes.data, fin.ctypes.data,
+                     None if probs0 is None else probs0.ctypes.data, 0, PROGRESS_FN(0), None, 0.0, 0.0)
+        cfg = SamplerCfg(*sampler)
+        orc = None if oracle is None else np.ascontiguousarray(oracle, np.int32)
+        sd = None if seeds is None else np.ascontiguousarray(seeds, np.uint64)
+        if want_probs0:
+            flags |= GSVK_GEN_PROB_DUMP
+        check(lib().gsvk_generate(self.h, arr, B, C.byref(cfg), seed_base, early_stop, max_steps,
+                                  None if orc is None else orc.ctypes.data, 0 if orc is None else orc.size,
+                                  None if sd is None else sd.ctypes.data, flags, C.byref(out)), "generate")
+        n = out.n_steps
+        res = {"tokens": [tokens[b, :tok_len[b]].copy() for b in range(B)], "lens": lens.copy(),
+               "finish_seq": fin.copy(), "n_steps": n, "prefill_ms": out.prefill_ms,
+               "decode_ms": out.decode_ms}
+        if want_sampled:
+            s = np.zeros((max(n, 1), B), np.int32)
+            check(lib().gsvk_last_sampled(self.h, n, s.ctypes.data), "last_sampled")
+            res["sampled"] = s[:n]
+        if want_probs0:
+            res["probs0"] = probs0[:n]
+        return res

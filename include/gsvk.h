@@ -1,0 +1,230 @@
+/*
+ * gsvk.h — C ABI of the MI355X (gfx950) AR / text-to-semantic decoder.
+ *
+ * This is the thin layer between the C++ host code (the gsv_ar class, include/gsv_ar.h) and the
+ * hand-written HIP kernels. Every entry point takes plain pointers and sizes, returns an int
+ * status (GSVK_OK == 0) and never exits the process. gsvk_last_error() gives the message of the
+ * last failure on the calling thread.
+ *
+ * Two groups of entry points:
+ *
+ *  1. Model runtime (gsvk_model_*, gsvk_generate, gsvk_first_logits, gsvk_kv_*): the work that the
+ *     reference does in src/gsv_ar.cpp through ggml graphs. Host buffers stay caller-owned,
+ *     device buffers stay model-owned. One model = one HIP device + one HIP stream; a model is
+ *     not thread-safe (callers serialise on it, as the reference's callers do).
+ *
+ *  2. Device ops (gsvk_op_*): one kernel launch each, on caller-owned DEVICE memory and a caller
+ *     stream (hipStream_t passed as void*, NULL = default stream). They are the same kernels the
+ *     runtime uses, exposed so that each can be checked and timed alone.
+ *
+ * Conventions: fp16 values are passed as uint16_t bit patterns; Q8_0 "blocks" are the GGUF block
+ * layout (34 bytes: fp16 scale d, then 32 int8 quants). On the device Q8_0 rows use the "sliced"
+ * layout: quants qs[row][j][blk][t] = q[row][32*blk + 4*j + t] (j < 8, t < 4) and scales
+ * d[row][blk] (fp16 for weights, fp32 for activations); slice j of a row is what lane j of
+ * ggml-cpu's 8-lane x86 dot accumulates, so the device reproduces its summation order.
+ */
+#ifndef GSVK_H
+#define GSVK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---- */
+#define GSVK_OK          0
+#define GSVK_ERR_ARG     1   /* invalid argument or shape */
+#define GSVK_ERR_HIP     2   /* a HIP runtime call failed */
+#define GSVK_ERR_IO      3   /* file open / read failed */
+#define GSVK_ERR_FORMAT  4   /* GGUF content missing or of an unsupported type */
+#define GSVK_ERR_NOMEM   5   /* device or host allocation failed */
+#define GSVK_ERR_STATE   6   /* call out of order (e.g. decode before prefill) */
+#define GSVK_ERR_NODEV   7   /* no usable HIP device */
+
+/* Message of the last failed call on this thread ("" if none). */
+const char * gsvk_last_error(void);
+
+/* Number of visible HIP devices (0 when none). */
+int gsvk_device_count(int * n);
+
+/* Parse a device string with the reference's syntax (src/gsv_device.h:19-37) extended for HIP:
+ * "", "gpu", "hip", "rocm", "vulkan", "cuda" -> device 0; "gpu:N", "hip:N", "N" -> device N.
+ * "cpu" is rejected (this build has no CPU path): returns GSVK_ERR_NODEV. */
+int gsvk_parse_device(const char * s, int * device);
+
+/* ======================================================================================
+ * 1. Model runtime
+ * ====================================================================================== */
+
+typedef struct gsvk_model gsvk_model;
+
+typedef struct gsvk_model_info {
+    int d_model;        /* ar.hidden_dim (512) */
+    int n_head;         /* ar.head (16) */
+    int head_dim;       /* d_model / n_head (32) */
+    int n_layer;        /* ar.n_layer (24) */
+    int vocab;          /* ar.vocab_size (1025) */
+    int eos;            /* ar.eos (1024) */
+    int phone_vocab;    /* ar.phoneme_vocab_size (732) */
+    int bert_dim;       /* 1024 */
+    int ffn_dim;        /* rows of ffn1_w (2048) */
+    int head_type;      /* GGML type of ar.predict: 0 F32, 1 F16, 8 Q8_0 */
+    float text_alpha;   /* ar.text_pe_alpha */
+    float audio_alpha;  /* ar.audio_pe_alpha */
+    int prompt_len;     /* prompt length seen by the last generate / first_logits (0 = none) */
+    int kv_batch;       /* batch of the resident KV cache (0 = none) */
+    int kv_lmax;        /* key slots per sequence of the resident KV cache */
+} gsvk_model_info;
+
+/* Load a gsv AR GGUF (tools/export_gguf/convert_ar.py contract) onto HIP device `device`.
+ * Replaces gsv_ar::load (src/gsv_ar.cpp:490-705). */
+int gsvk_model_load(const char * gguf_path, int device, int verbose, gsvk_model ** out);
+void gsvk_model_free(gsvk_model * m);
+int gsvk_model_get_info(const gsvk_model * m, gsvk_model_info * info);
+
+/* One request: replaces gsv_ar_request (src/gsv_ar.h:13-17).
+ * bert is [bert_dim][n_phones] row-major (bert[k*n_phones + t]); NULL means all zero. */
+typedef struct gsvk_request {
+    const int32_t * phones;
+    int32_t         n_phones;
+    const float   * bert;
+    const int32_t * prompt;
+    int32_t         n_prompt;
+} gsvk_request;
+
+/* Sampler settings: same fields and meaning as gsv_sampler_cfg (src/gsv_sampler.h:18-23). */
+typedef struct gsvk_sampler_cfg {
+    int   top_k;
+    float top_p;
+    float temperature;
+    float repetition_penalty;
+} gsvk_sampler_cfg;
+
+/* gsvk_generate flags */
+#define GSVK_GEN_EOS_MASK_ALL  1u  /* mask EOS at every step (benchmarks: fixed-length runs) */
+#define GSVK_GEN_PROB_DUMP     2u  /* write sequence 0's per-step probabilities to out->probs0 */
+
+/* Output buffers, all caller-owned host memory.
+ *  tokens     : [B][tok_stride] int32; row b receives prompt + generated tokens minus the
+ *               stopping token (gsv_ar_result.tokens semantics, src/gsv_ar.cpp:782, 790, 813)
+ *  tok_len    : [B] number of valid entries of each tokens row
+ *  lens       : [B] generated-token counts in FINISH order (gsv_ar_result.lens, :783, 791, 814)
+ *  finish_seq : [B] optional (may be NULL): the sequence index of each lens entry
+ *  probs0     : optional [max_steps][vocab] (GSVK_GEN_PROB_DUMP), sequence 0's probabilities
+ *  n_steps    : number of decode-loop iterations that ran */
+typedef struct gsvk_gen_out {
+    int32_t * tokens;
+    int32_t   tok_stride;
+    int32_t * tok_len;
+    int32_t * lens;
+    int32_t * finish_seq;
+    float   * probs0;
+    int32_t   n_steps;
+    /* optional progress callback, called once per decode-loop iteration launched
+     * (gsvprog::tick in the reference, src/gsv_ar.cpp:761-763) */
+    void   (*progress)(void * user, int step);
+    void    * progress_user;
+    /* wall-clock split measured by the runtime, stream-synchronised on both sides */
+    double    prefill_ms;
+    double    decode_ms;
+} gsvk_gen_out;
+
+/* Full batched generation: replaces gsv_ar::generate (src/gsv_ar.cpp:719-824).
+ * oracle (teacher forcing) may be NULL; seeds may be NULL (then seed_base + 0x9E3779B9*b). */
+int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_sampler_cfg * cfg,
+                  uint64_t seed_base, int early_stop_num, int max_steps,
+                  const int32_t * oracle, int n_oracle, const uint64_t * seeds, unsigned flags,
+                  gsvk_gen_out * out);
+
+/* Prefill only, last-position logits [B][vocab]: replaces gsv_ar::first_logits (:707-717). */
+int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out);
+
+/* Free the resident KV cache: replaces gsv_ar::release_cache (:826). */
+int gsvk_release_cache(gsvk_model * m);
+
+/* ---- step-level entry points (the lockstep loop of gsv_ar::generate, split for callers that
+ *      drive it themselves: schedulers, tests, benchmarks) ---- */
+
+/* Allocate (or reuse) the resident KV cache for B sequences of up to lmax positions
+ * (src/gsv_ar.cpp:94-118). K and V are fp16 [n_layer][B][n_head][lmax+1][head_dim]. */
+int gsvk_kv_alloc(gsvk_model * m, int B, int lmax);
+
+/* Prefill B requests (src/gsv_ar.cpp:186-293): builds inputs on the device, runs all layers,
+ * fills the KV cache for positions [0, S) and returns last-position logits [B][vocab] (may be
+ * NULL). *S_out receives S = max(n_phones) + n_prompt. Resets the decode position to S. */
+int gsvk_prefill(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out, int * S_out);
+
+/* One decode step (src/gsv_ar.cpp:798-809 + 380-467): embeds last_tok[b] at PE position
+ * prompt_len + step, appends K/V at column S + step, and returns logits [B][vocab] (may be NULL).
+ * step advances by one per call. */
+int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float * logits_out);
+
+/* Copy the device KV cache of layer `layer` to host fp16 buffers, each [B][n_head][lmax+1][hd]
+ * (for checking the write/gather indexing). */
+int gsvk_kv_read(gsvk_model * m, int layer, uint16_t * k_out, uint16_t * v_out);
+
+/* Sampler choices of the last gsvk_generate before teacher forcing replaced them:
+ * [n_steps][B], -1 where a sequence had already finished (greedy-token checks). */
+int gsvk_last_sampled(gsvk_model * m, int n_steps, int32_t * out);
+
+/* ======================================================================================
+ * 2. Device ops (device pointers, caller stream)
+ * ====================================================================================== */
+
+/* GGUF Q8_0 blocks -> fp32 (w = fp32(d) * q). nblocks blocks, out has 32*nblocks floats. */
+int gsvk_op_q8_dequant(const void * blocks, int64_t nblocks, float * out, void * stream);
+
+/* GGUF Q8_0 blocks [rows][k/32] -> sliced layout qs [rows][k] int8 + d [rows][k/32] fp16. */
+int gsvk_op_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
+                      void * stream);
+
+/* Activation quantisation of fp32 rows [rows][k] to Q8_0 exactly as ggml-cpu's x86 quantiser:
+ * per 32-block amax, d = fp16(amax/127), q = round-half-even(x * (127/amax)).
+ * xq receives the quants in the sliced layout, xd fp32(d) per block ([rows][k/32]). */
+int gsvk_op_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xq, float * xd,
+                        void * stream);
+
+/* y[m][n] = W[n] . x[m] on Q8_0 rows in the sliced layout, ggml-cpu's x86 order: per lane j,
+ * acc_j = fma(fp32(wd[n][blk]) * xd[m][blk], dot4_i8(group j of blk), acc_j) over the blocks,
+ * then ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)); (+ bias[n] if bias) then act (0 none, 1 relu).
+ * k % 128 == 0. */
+int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k,
+                    const int8_t * xq, const float * xd, int64_t m, const float * bias, int act,
+                    float * y, void * stream);
+
+/* Fused LayerNorm (PATCH ggml_compute_forward_layernorm_affine):
+ * v = x + r + bias; y = (v - mean) / sqrt(var + eps) * wb[0:n] + wb[n:2n], sums in double.
+ * r and bias may be NULL. If yq/yd are given, y is also quantised to Q8_0 (n % 32 == 0). */
+int gsvk_op_layernorm(const float * x, const float * r, const float * bias, const float * wb,
+                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
+                      void * stream);
+
+/* Fused add + activation (PATCH ggml_compute_forward_add_act): y = act(a + b[i % ne0]),
+ * act 0 none, 1 relu, 2 gelu(erf), 3 mish. */
+int gsvk_op_add_act(const float * a, const float * b, int64_t n, int64_t ne0, int act, float * y,
+                    void * stream);
+
+/* Dot products of F16 (wtype 1) or F32 (wtype 0) weight rows W [n][k] with fp32 rows x [m][k]:
+ * y[m][n], in ggml-cpu's x86 summation order (mode 0: ggml_vec_dot_f16/_f32, 4x8 lanes;
+ * mode 1: tinyBLAS, 8 lanes, k % 8 == 0). F16 weights take fp16-rounded activations. */
+int gsvk_op_fdot(const void * w, int wtype, int64_t n, int64_t k, const float * x, int64_t m,
+                 float * y, int mode, void * stream);
+
+/* Single-query attention over a per-sequence fp16 KV cache (decode; ggml_flash_attn_ext with
+ * one query row). q fp32 [B][nh][hd]; K/V fp16 [B][nh][lstride][hd]; valid keys of sequence b
+ * are [kv_begin[b], kv_end[b]) (device int32 arrays). out fp32 [B][nh*hd] (head-major).
+ * If oq/od are given the output is also quantised to Q8_0 (one block per head, hd == 32).
+ * ws: device workspace of gsvk_attn_workspace_bytes() bytes. hd must be 32. */
+size_t gsvk_attn_workspace_bytes(int B, int nh, int64_t max_keys);
+int gsvk_op_attn_decode(const float * q, const uint16_t * k, const uint16_t * v, int B, int nh,
+                        int hd, int64_t lstride, const int32_t * kv_begin, const int32_t * kv_end,
+                        int64_t max_keys, float scale, float * out, uint16_t * out_f16,
+                        int8_t * oq, float * od, void * ws, void * stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSVK_H */

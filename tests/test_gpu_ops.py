@@ -1,0 +1,278 @@
+"""Parity of each HIP kernel with the oracle on the same seeded inputs (through the C ABI).
+
+Bars: bit-exact for Q8_0 dequantisation, repacking, activation quantisation, the Q8_0 GEMV/GEMM
+(the device reproduces ggml-cpu's x86 summation order), the F16/F32 head dots and the
+LayerNorm; attention within 2e-3 relative (max |diff| / max |ref|), fp32 accumulation over an
+fp16 cache.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import synth_model as sm
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, torch):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def unslice(qs: np.ndarray, k: int) -> np.ndarray:
+    """sliced [rows][8][nblk][4] -> natural [rows][k] int8"""
+    rows = qs.size // k
+    return qs.reshape(rows, 8, k // 32, 4).transpose(0, 2, 1, 3).reshape(rows, k)
+
+
+def blocks_to_split(blocks: np.ndarray, rows: int, k: int):
+    b = blocks.reshape(rows, k // 32, 34)
+    d = b[:, :, 0:2].copy().view(np.uint16)[:, :, 0]
+    q = b[:, :, 2:].view(np.int8).reshape(rows, k)
+    return q, d
+
+
+def _special_rows(rng, k):
+    x = rng.standard_normal((6, k)).astype(np.float32)
+    x[0, :32] = 0.0                                     # all-zero block: d = 0, q = 0
+    x[1, :32] = -0.0                                    # negative zeros
+    x[2, :32] = np.linspace(-1, 1, 32)                  # +-amax extremes -> +-127
+    x[3, :32] = 0.5                                     # constant block
+    x[4, :32] = np.float32(1e-30)                       # subnormal-range scale
+    x[5, :32] = (np.arange(32) - 15.5).astype(np.float32) / 127.0 * 4  # exact .5 ties at id=127/amax
+    return x
+
+
+def test_q8_dequant_bitexact(gpu):
+    import torch
+    rng = np.random.default_rng(1)
+    x = np.concatenate([_special_rows(rng, 512), rng.standard_normal((64, 512)).astype(np.float32) * 0.02])
+    blocks = sm.q8_quantize_ref(x).ravel()
+    out = torch.zeros(x.size, dtype=torch.float32, device="cuda")
+    gpu.op_q8_dequant(_dev(blocks, torch), out)
+    torch.cuda.synchronize()
+    ref = O.q8_dequant(blocks)
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+
+
+def test_q8_repack_bitexact(gpu):
+    import torch
+    rng = np.random.default_rng(2)
+    rows, k = 40, 2048
+    blocks = sm.q8_quantize_ref(rng.standard_normal((rows, k)).astype(np.float32) * 0.02).ravel()
+    qs = torch.zeros(rows * k, dtype=torch.int8, device="cuda")
+    d = torch.zeros(rows * k // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(blocks, torch), rows, k, qs, d)
+    torch.cuda.synchronize()
+    q_ref, d_ref = blocks_to_split(blocks, rows, k)
+    assert np.array_equal(unslice(qs.cpu().numpy(), k), q_ref)
+    assert np.array_equal(d.cpu().numpy().view(np.uint16).reshape(rows, -1), d_ref)
+
+
+@pytest.mark.parametrize("k", [512, 2048])
+def test_q8_quantize_bitexact(gpu, k):
+    import torch
+    rng = np.random.default_rng(3 + k)
+    x = np.concatenate([_special_rows(rng, k), rng.standard_normal((97, k)).astype(np.float32) * 3.0])
+    rows = x.shape[0]
+    xq = torch.zeros(rows * k, dtype=torch.int8, device="cuda")
+    xd = torch.zeros(rows * k // 32, dtype=torch.float32, device="cuda")
+    gpu.op_q8_quantize(_dev(x, torch), xq, xd)
+    torch.cuda.synchronize()
+    ref = O.q8_quantize_x86(x)
+    q_ref, d_ref = blocks_to_split(ref, rows, k)
+    assert np.array_equal(unslice(xq.cpu().numpy(), k), q_ref)
+    d_ref32 = d_ref.view(np.float16).astype(np.float32)
+    assert np.array_equal(xd.cpu().numpy().reshape(rows, -1).view(np.uint32), d_ref32.view(np.uint32))
+
+
+@pytest.mark.parametrize("n,k", [(1536, 512), (512, 512), (2048, 512), (512, 2048)])
+@pytest.mark.parametrize("m", [1, 4, 16, 37, 64, 300])
+def test_q8_gemv_bitexact(gpu, n, k, m):
+    import torch
+    rng = np.random.default_rng(n * 7 + k + m)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    X[0, :64] = 0.0
+    wb = sm.q8_quantize_ref(W).ravel()
+    wq = torch.zeros(n * k, dtype=torch.int8, device="cuda")
+    wd = torch.zeros(n * k // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(wb, torch), n, k, wq, wd)
+    xq = torch.zeros(m * k, dtype=torch.int8, device="cuda")
+    xd = torch.zeros(m * k // 32, dtype=torch.float32, device="cuda")
+    gpu.op_q8_quantize(_dev(X, torch), xq, xd)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemv(wq, wd, n, k, xq, xd, m, None, 0, y)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.02
+    y2 = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemv(wq, wd, n, k, xq, xd, m, _dev(bias, torch), 1, y2)
+    torch.cuda.synchronize()
+    ref = O.q8_matmul(wb, n, k, X)
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), \
+        f"max |diff| {np.abs(got - ref).max():.3e}, mismatches {(got != ref).sum()}"
+    ref2 = np.maximum(ref + bias[None, :], 0.0).astype(np.float32)
+    assert np.array_equal(y2.cpu().numpy(), ref2)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 512), (16, 512), (333, 512), (8, 1024)])
+def test_layernorm(gpu, rows, n):
+    import torch
+    rng = np.random.default_rng(rows + n)
+    x = rng.standard_normal((rows, n)).astype(np.float32) * 2 + 0.3
+    r = rng.standard_normal((rows, n)).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.1
+    wb = np.concatenate([1 + 0.1 * rng.standard_normal(n), 0.1 * rng.standard_normal(n)]).astype(np.float32)
+    y = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    yq = torch.zeros(rows * n, dtype=torch.int8, device="cuda")
+    yd = torch.zeros(rows * n // 32, dtype=torch.float32, device="cuda")
+    gpu.op_layernorm(_dev(x, torch), _dev(r, torch), _dev(bias, torch), _dev(wb, torch), 1e-5, y, yq, yd)
+    y0 = torch.zeros((rows, n), dtype=torch.float32, device="cuda")
+    gpu.op_layernorm(_dev(x, torch), None, None, _dev(wb, torch), 1e-5, y0)
+    torch.cuda.synchronize()
+    ref = O.layernorm(x, r, bias, wb)
+    got = y.cpu().numpy()
+    # sums are in double on both sides (only their order differs): equal to the bit
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max {np.abs(got - ref).max():.3e}"
+    assert np.array_equal(y0.cpu().numpy(), O.layernorm(x, None, None, wb))
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(ref), rows, n)
+    assert np.array_equal(unslice(yq.cpu().numpy(), n), q_ref)
+    assert np.array_equal(yd.cpu().numpy().reshape(rows, -1), d_ref.view(np.float16).astype(np.float32))
+
+
+def _ref_act(v, act):
+    import math
+    v = v.astype(np.float64)
+    if act == 1:
+        return np.maximum(v, 0)
+    if act == 2:
+        return 0.5 * v * (1 + np.vectorize(math.erf)(v / math.sqrt(2)))
+    if act == 3:
+        return v * np.tanh(np.log1p(np.exp(v)))
+    return v
+
+
+@pytest.mark.parametrize("act", [0, 1, 2, 3])
+def test_add_act_reference_fixture(gpu, act):
+    """tests/test_add_act.cpp:66-101: a[i] = 0.02*((i*37 % 101) - 50) + 0.5, b[i] =
+    0.01*((i*13 % 29) - 14), NE0 = 64, NR = 7; tolerance 2e-3 (5e-3 for GELU)."""
+    import torch
+    NE0, NR = 64, 7
+    i = np.arange(NE0 * NR)
+    a = (0.02 * ((i * 37 % 101) - 50) + 0.5).astype(np.float32)
+    j = np.arange(NE0)
+    b = (0.01 * ((j * 13) % 29 - 14)).astype(np.float32)
+    y = torch.zeros(NE0 * NR, dtype=torch.float32, device="cuda")
+    gpu.op_add_act(_dev(a, torch), _dev(b, torch), act, y)
+    torch.cuda.synchronize()
+    ref = _ref_act((a.reshape(NR, NE0) + b).ravel(), act)
+    tol = 5e-3 if act == 2 else 2e-3
+    assert np.abs(y.cpu().numpy() - ref).max() <= tol
+    if act in (0, 1):
+        assert np.array_equal(y.cpu().numpy(), O.add_act(a, b, act))
+
+
+@pytest.mark.parametrize("wtype", [0, 1])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_fdot_head_bitexact(gpu, wtype, mode):
+    import torch
+    rng = np.random.default_rng(10 + wtype * 2 + mode)
+    n, k, m = 1025, 512, 5
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    if wtype == 1:
+        W16 = W.astype(np.float16).view(np.uint16)
+        gpu.op_fdot(_dev(W16, torch), 1, _dev(X, torch), y, mode)
+        ref = O.f16_matmul(W16, X, mode)
+    else:
+        gpu.op_fdot(_dev(W, torch), 0, _dev(X, torch), y, mode)
+        ref = O.f32_matmul(W, X, mode)
+    torch.cuda.synchronize()
+    got = y.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max {np.abs(got - ref).max():.3e}"
+
+
+def test_fdot_bert_projection_bitexact(gpu):
+    """K = 1025 (bert_aug = [W | b]): ggml_vec_dot_f32 with a fused leftover."""
+    import torch
+    rng = np.random.default_rng(20)
+    W = rng.standard_normal((512, 1025)).astype(np.float32) * 0.02
+    X = rng.uniform(-1, 1, (9, 1025)).astype(np.float32)
+    X[:, 1024] = 1.0
+    y = torch.zeros((9, 512), dtype=torch.float32, device="cuda")
+    gpu.op_fdot(_dev(W, torch), 0, _dev(X, torch), y, 0)
+    torch.cuda.synchronize()
+    ref = O.f32_matmul(W, X, 0)
+    assert np.array_equal(y.cpu().numpy(), ref)
+
+
+def _attn_case(rng, B, nh, lstride, begins, ends):
+    q = rng.standard_normal((B, nh, 32)).astype(np.float32)
+    k = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16).view(np.uint16)
+    return q, k, v, np.asarray(begins, np.int32), np.asarray(ends, np.int32)
+
+
+def _run_attn(gpu, torch, q, k, v, kb, ke, max_keys, quant=False):
+    B, nh, _ = q.shape
+    scale = np.float32(1.0) / np.sqrt(np.float32(32.0))
+    out = torch.zeros((B, nh * 32), dtype=torch.float32, device="cuda")
+    ws = torch.zeros(gpu.attn_workspace_bytes(B, nh, max_keys), dtype=torch.uint8, device="cuda")
+    oq = torch.zeros(B * nh * 32, dtype=torch.int8, device="cuda") if quant else None
+    od = torch.zeros(B * nh, dtype=torch.float32, device="cuda") if quant else None
+    args = [_dev(q, torch), _dev(k, torch), _dev(v, torch), _dev(kb, torch), _dev(ke, torch), max_keys,
+            float(scale), out]
+    gpu.op_attn_decode(*args, oq=oq, od=od, ws=ws)
+    torch.cuda.synchronize()
+    first = out.cpu().numpy().copy()
+    gpu.op_attn_decode(*args, oq=oq, od=od, ws=ws)       # counters must have been reset
+    torch.cuda.synchronize()
+    assert np.array_equal(first, out.cpu().numpy())
+    return first, scale, (None if not quant else (oq.cpu().numpy(), od.cpu().numpy()))
+
+
+def test_attn_decode_parity(gpu):
+    import torch
+    rng = np.random.default_rng(30)
+    B, nh, lstride = 12, 16, 1100
+    begins = rng.integers(0, 200, B)
+    ends = np.minimum(lstride, begins + rng.integers(1, 900, B))
+    begins[0], ends[0] = 0, 1           # one key: output = that V row
+    begins[1], ends[1] = 5, 5 + 256     # exactly one chunk
+    begins[2], ends[2] = 3, 3 + 257     # one key into the second chunk
+    begins[3], ends[3] = 0, lstride     # the whole cache
+    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, begins, ends)
+    got, scale, qd = _run_attn(gpu, torch, q, k, v, kb, ke, lstride, quant=True)
+    ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    assert rel <= 2e-3, rel
+    assert rel <= 1e-5, rel   # fp32 accumulation over the same fp16 data: far inside the bar
+    v0 = v[0, :, 0, :].view(np.float16).astype(np.float32).reshape(-1)
+    assert np.allclose(got[0], v0, rtol=0, atol=1e-6)
+    # the Q8_0 copy is the x86 quantisation of the fp32 output (one block per head)
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(got), B, nh * 32)
+    assert np.array_equal(unslice(qd[0], nh * 32), q_ref)
+
+
+def test_attn_decode_empty_and_constant(gpu):
+    import torch
+    rng = np.random.default_rng(31)
+    B, nh, lstride = 3, 4, 600
+    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, [7, 0, 10], [7, 600, 530])
+    v[1] = np.float16(0.75).view(np.uint16)               # constant V -> output = V
+    got, _, _ = _run_attn(gpu, torch, q, k, v, kb, ke, lstride)
+    assert np.all(got[0] == 0.0)                          # no valid key -> 0 (ggml: S == 0)
+    assert np.allclose(got[1], 0.75, rtol=0, atol=1e-6)
+
+
+def test_attn_decode_microbench_shape(gpu):
+    """The decode-attention microkernel configuration at reduced batch: 16 heads x 32,
+    KV lengths uniform 256-2048, one query per sequence."""
+    import torch
+    rng = np.random.default_rng(32)
+    B, nh, lstride = 16, 16, 2048
+    L = rng.integers(256, 2049, B)
+    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, np.zeros(B), L)
+    got, scale, _ = _run_attn(gpu, torch, q, k, v, kb, ke, lstride)
+    ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-3
