@@ -1,0 +1,244 @@
+#!/usr/bin/env python3
+"""AR decode throughput of the MI355X (gfx950) text-to-semantic decoder on one GPU.
+
+Workload (the batched-decode configuration the metric is quoted on): the GPT-SoVITS t2s-shaped
+decoder (24 layers, d_model 512, 16 heads x 32, FFN 2048, Q8_0 projections, F16 head, synthetic
+weights from a fixed seed), batch 16, prompt lengths uniform in [100, 400] (phones = length - 64,
+64 shared semantic prompt codes), fp16 KV cache, top-k 15 / top-p 1.0 / temperature 1.0 sampling
+with per-sequence xorshift64* seeds, EOS masked so that every sequence decodes all steps.
+
+A "step" is one decode iteration of the whole batch (sampler + 24 layers + head, one HIP graph
+launch). The timed region covers exactly --steps steps with the inputs and the prompt's KV cache
+resident on the device (the prefill runs before it and is reported separately).
+
+    python bench.py [--gpus 1] [--steps 500] [--warmup 16] [--no-cpu]
+
+Prints one JSON line. The roofline object times the dominant decode kernel alone with HIP events
+on the stream it runs on, rotating through buffers larger than the 256 MB MALL; cpu_baseline
+times the oracle (the CPU restatement of the reference path) on this host's cores on a bounded
+sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (os.path.join(ROOT, "gsv.cpp_amd"), os.path.join(ROOT, "oracle")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+SEED = 0x6A5E0002
+N_LAYER, D, NH, HD, FFN, V = 24, 512, 16, 32, 2048, 1025
+
+
+def workload_requests(B=16, seed=SEED):
+    import synth_model as sm
+    rng = np.random.Generator(np.random.PCG64(seed))
+    P_b = rng.integers(100, 401, B)
+    reqs = sm.synth_requests(seed, B, 64, P_b - 64)
+    return reqs
+
+
+def decode_bytes_per_step(reqs, step_kv):
+    """Algorithmic HBM bytes of one decode step: Q8_0 weights + biases/LN + F16 head + the valid
+    fp16 K/V rows read by attention + the new K/V rows written."""
+    w = N_LAYER * (3 * D * D + D * D + 2 * FFN * D) // 32 * 34
+    small = N_LAYER * (3 * D + D + FFN + D + 4 * D) * 4
+    head = V * D * 2
+    T = np.array([len(r["phones"]) for r in reqs])
+    P = len(reqs[0]["prompt"])
+    valid = T + P + step_kv + 1                       # keys [pad_b, S + step] per sequence
+    kv_read = int(valid.sum()) * N_LAYER * 2 * D * 2
+    kv_write = len(reqs) * N_LAYER * 2 * D * 2
+    return w + small + head + kv_read + kv_write
+
+
+def time_events(fn, iters, torch):
+    """Average duration of fn(i) for i < iters: the launches are captured in one graph (so host
+    launch cost is not measured) and the replay is timed with HIP events on its stream."""
+    fn(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for i in range(iters):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(st)
+    g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def kernel_roofline(gsvk, torch, reqs, steps):
+    """Time the decode-step kernels alone at the mid-run shape of the workload."""
+    B = len(reqs)
+    T = np.array([len(r["phones"]) for r in reqs])
+    P = len(reqs[0]["prompt"])
+    max_len = int(T.max())
+    S = max_len + P
+    lstride = S + steps + 8 + 1
+    mid = steps // 2
+    kv_begin = torch.tensor(max_len - T, dtype=torch.int32, device="cuda")
+    kv_end = torch.full((B,), S + mid + 1, dtype=torch.int32, device="cuda")
+    nkeys = int((S + mid + 1 - (max_len - T)).sum())
+    res = {}
+    # attention: rotate over the 24 per-layer caches (24 x 29.8 MB > MALL)
+    rot = N_LAYER
+    kc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda")
+    vc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda")
+    q = torch.randn((B, NH, HD), dtype=torch.float32, device="cuda")
+    out = torch.zeros((B, NH * HD), dtype=torch.float32, device="cuda")
+    oq = torch.zeros(B * D, dtype=torch.int8, device="cuda")
+    od = torch.zeros(B * NH, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(gsvk.attn_workspace_bytes(B, NH, lstride), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / np.sqrt(32.0)
+
+    def attn(i):
+        gsvk.op_attn_decode(q, kc[i % rot], vc[i % rot], kv_begin, kv_end, lstride, scale, out, oq=oq,
+                            od=od, ws=ws)
+    ms = time_events(attn, 240, torch)
+    ab = nkeys * NH * 2 * HD * 2
+    res["attn_decode"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER}
+    del kc, vc
+    # Q8_0 GEMVs at batch B (the decoder's fused kernel): rotate over 96 weight copies (> MALL).
+    # QKV and FFN1 run with their LayerNorm input stage, out and FFN2 read Q8_0 rows.
+    xq = torch.randint(-127, 128, (B * FFN,), dtype=torch.int8, device="cuda")
+    xd = torch.rand((B * FFN // 32,), dtype=torch.float32, device="cuda") * 0.01
+    xres = torch.randn((B, D), dtype=torch.float32, device="cuda")
+    xr = torch.randn((B, D), dtype=torch.float32, device="cuda")
+    wb = torch.cat([torch.ones(D), torch.zeros(D)]).cuda()
+    for name, n, k, ln in (("gemv_qkv", 3 * D, D, True), ("gemv_out", D, D, False), ("gemv_ffn1", FFN, D, True),
+                           ("gemv_ffn2", D, FFN, False)):
+        copies = 96
+        wq = torch.randint(-127, 128, (copies, n * k), dtype=torch.int8, device="cuda")
+        wd = (torch.rand((copies, n * k // 32), device="cuda") * 0.001).half().view(torch.int16)
+        y = torch.zeros((B, n), dtype=torch.float32, device="cuda")
+
+        def gemv(i, wq=wq, wd=wd, n=n, k=k, y=y, ln=ln):
+            if ln:
+                gsvk.op_ln_gemv(wq[i % copies], wd[i % copies], n, xres, xr, None, wb, None, 0, y)
+            else:
+                gsvk.op_q8_gemv(wq[i % copies], wd[i % copies], n, k, xq, xd, B, None, 0, y)
+        ms = time_events(gemv, 480, torch)
+        b = n * k // 32 * 34
+        res[name] = {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": N_LAYER}
+        del wq, wd
+    return res
+
+
+def cpu_baseline(reqs, steps):
+    import oracle
+    import synth_model as sm
+    nthreads = oracle.nthreads_default()
+    path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
+    m = oracle.Model(path)
+    try:
+        r = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=steps, seeds=list(range(1, len(reqs) + 1)),
+                       flags=oracle.ORC_EOS_MASK_ALL, nthreads=nthreads)
+    finally:
+        m.close()
+    tok_s = len(reqs) * steps / (r["decode_ms"] / 1e3)
+    return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": nthreads, "kind": "port",
+            "sample": f"batch {len(reqs)}, same requests, prefill ({r['prefill_ms'] / 1e3:.1f} s, untimed) then "
+                      f"{steps} decode steps timed; F32 KV cache, OpenMP over {nthreads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this decoder runs each batch on a single MI355X and has no "
+              f"multi-GPU path (--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import gsvk
+    import synth_model as sm
+
+    assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
+    g = gsvk.Model(path, device=0)
+    cfg = (15, 1.0, 1.0, 1.35)
+    flags = gsvk.GSVK_GEN_EOS_MASK_ALL
+
+    def run(B, steps, warmup):
+        reqs = workload_requests(B)
+        seeds = list(range(1, B + 1))
+        if warmup:
+            g.generate(reqs, sampler=cfg, max_steps=warmup, seeds=seeds, flags=flags)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        r = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=flags)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        assert r["n_steps"] == steps and all(len(t) == len(reqs[0]["prompt"]) + steps for t in r["tokens"])
+        return reqs, r, wall
+
+    reqs, r, wall = run(args.batch, args.steps, args.warmup)
+    B = args.batch
+    dec_s = r["decode_ms"] / 1e3
+    tok_s = B * args.steps / dec_s
+    ms_step = r["decode_ms"] / args.steps
+    step_bytes = np.mean([decode_bytes_per_step(reqs, s) for s in range(0, args.steps, max(1, args.steps // 16))])
+    extra = {"prefill_ms": round(r["prefill_ms"], 2), "wall_s_incl_prefill": round(wall, 3),
+             "step_bytes_mb": round(step_bytes / 1e6, 1),
+             "step_hbm_frac": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
+    for bb, st in ((1, 300), (64, 200)):
+        _, rb, _ = run(bb, st, 8)
+        extra[f"tok_s_b{bb}"] = round(bb * st / (rb["decode_ms"] / 1e3), 1)
+        extra[f"ms_per_step_b{bb}"] = round(rb["decode_ms"] / st, 4)
+    g.close()
+
+    roof = None
+    if not args.no_kernels:
+        kr = kernel_roofline(gsvk, torch, reqs, args.steps)
+        extra["kernels"] = {k: {"us": round(v["ms"] * 1e3, 2), "GBs": round(v["gbs"], 1),
+                                "frac": round(v["gbs"] / HBM_PEAK_GBS, 4)} for k, v in kr.items()}
+        dom = max(kr, key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
+        d = kr[dom]
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "bytes_per_launch": int(d["bytes"]), "us_per_launch": round(d["ms"] * 1e3, 3)}
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(reqs, args.cpu_steps)
+
+    line = {
+        "metric": "AR decode tokens/sec at batch 1/16/64; attn+Q8_0 GEMV % of HBM roofline",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 int8 dot, fp32 accumulate, fp16 KV",
+        "data": "synthetic (random-init weights from a fixed seed, seeded requests)",
+        "config": {"workload": "batched AR decode, 24-layer t2s decoder (d512, 16x32 heads, FFN 2048, "
+                               "Q8_0), batch 16, prompt lengths U[100,400], 500 steps, top-k 15 sampling",
+                   "batch": B, "decode_steps": args.steps, "prompt_codes": 64,
+                   "kv": "fp16", "parallelism": "single GPU"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

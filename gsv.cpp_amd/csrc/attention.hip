@@ -1,25 +1,27 @@
 // Single-query (decode) attention over a per-sequence fp16 KV cache, for gfx950.
 //
-// Work decomposition: split-K over the key axis. Workgroup (chunk, head, seq) owns up to
-// ATT_CHUNK consecutive valid keys of one (seq, head). Inside a workgroup each wave takes 64
-// keys as 4 passes of 16: lane = (key slot ks = lane/4, quarter qd = lane%4); a lane loads the
-// 16-byte quarter [8qd, 8qd+8) of a 64-byte fp16 K row, so one wave-wide load reads 1 KiB of
-// contiguous cache. Scores are completed with two lane shuffles, the chunk's softmax is local
-// (max, then exp and V accumulation in fp32), and chunks are merged by the last workgroup of
-// each (seq, head) to finish (a device-scope counter), so one launch does the whole op.
+// Work decomposition: workgroup (split, head, seq) of 4 waves. The valid keys [begin, end) of a
+// (seq, head) are cut in blocks of 64; split s owns a contiguous run of blocks (nsplit is 1
+// unless batch x heads is small and the rows long, see attn_nsplit). Wave w of a workgroup takes blocks w, w+4, ... of its run.
+// Inside a block, lane = (key slot ks = lane/4, quarter qd = lane%4) reads the 16-byte quarter
+// [8qd, 8qd+8) of 4 K rows and 4 V rows (all 8 loads issued before any use, and the next block's
+// loads issued before this block's arithmetic); one wave-wide load covers 1 KiB of contiguous
+// cache. Each wave keeps an online softmax (running max per block, exp2 of log2e-scaled scores);
+// the 4 waves merge through LDS, and the splits of one (seq, head), if more than one, are merged
+// by the last workgroup to finish (device-scope counter), so one launch does the whole op.
 //
-// Numerics follow ggml_flash_attn_ext on one query row: s = (q . k) * scale over the valid keys,
-// softmax, times V, output divided by the sum (multiplied by its reciprocal), fp32 throughout.
+// Numerics: softmax(q.k * scale) . V over the valid keys with fp32 accumulation; the output is
+// divided by the sum (multiplied by its reciprocal), as ggml_flash_attn_ext does.
 #include "common.h"
 
 namespace gsvk {
 
-constexpr int ATT_CHUNK = 256;
 constexpr int ATT_HD = 32;
+constexpr int ATT_BLK = 64;            // keys per block
 constexpr int ATT_PART = ATT_HD + 2;   // m, l, o[32]
+constexpr float LOG2E = 1.4426950408889634f;
 
-__device__ __forceinline__ void load_h8(const uint16_t * p, float (&f)[8]) {
-    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+__device__ __forceinline__ void h8_to_f(const uint4 & u, float (&f)[8]) {
     const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -59,13 +61,33 @@ __device__ __forceinline__ void attn_store_out(float val, int lane, int64_t bh, 
     }
 }
 
+struct KV8 {
+    uint4 k[4], v[4];
+};
+
+__device__ __forceinline__ void load_block(const uint16_t * __restrict__ kb,
+                                           const uint16_t * __restrict__ vb, int key0, int end,
+                                           int ks, KV8 & r) {
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        const int key = key0 + p * 16 + ks;
+        if (key < end) {
+            r.k[p] = *reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
+            r.v[p] = *reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+        } else {
+            r.k[p] = make_uint4(0, 0, 0, 0);
+            r.v[p] = make_uint4(0, 0, 0, 0);
+        }
+    }
+}
+
 __global__ void __launch_bounds__(256) k_attn_decode(
     const float * __restrict__ q, int64_t q_stride, const uint16_t * __restrict__ kc,
     const uint16_t * __restrict__ vc, int nh, int64_t lstride, const int32_t * __restrict__ kv_begin,
-    const int32_t * __restrict__ kv_end, int maxch, float scale, float * __restrict__ out,
+    const int32_t * __restrict__ kv_end, int nsplit, float scale_log2, float * __restrict__ out,
     uint16_t * __restrict__ out16, int8_t * __restrict__ oq, float * __restrict__ od,
     float * __restrict__ part, int32_t * __restrict__ counters) {
-    const int chunk = blockIdx.x;
+    const int split = blockIdx.x;
     const int h = blockIdx.y;
     const int b = blockIdx.z;
     // clamp to the buffer so that a bad range can never read outside the cache
@@ -73,10 +95,11 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     int end = kv_end[b];
     beg = beg < 0 ? 0 : beg;
     end = end > (int) lstride ? (int) lstride : end;
-    if (end - beg > maxch * ATT_CHUNK) end = beg + maxch * ATT_CHUNK;
     const int nkeys = end > beg ? end - beg : 0;
-    const int nch = (nkeys + ATT_CHUNK - 1) / ATT_CHUNK;
-    if (chunk >= (nch > 0 ? nch : 1)) return;
+    const int nblk = (nkeys + ATT_BLK - 1) / ATT_BLK;
+    const int bps = (nblk + nsplit - 1) / nsplit;               // blocks per split
+    const int nact = bps > 0 ? (nblk + bps - 1) / bps : 0;      // splits with work
+    if (split >= (nact > 0 ? nact : 1)) return;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -85,7 +108,7 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     const int qd = lane & 3;
     const int64_t bh = (int64_t) b * nh + h;
 
-    __shared__ float s_max[4];
+    __shared__ float s_m[4];
     __shared__ float s_l[4];
     __shared__ float s_o[4][ATT_HD];
 
@@ -104,47 +127,58 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     }
     const uint16_t * kb = kc + bh * lstride * ATT_HD + qd * 8;
     const uint16_t * vb = vc + bh * lstride * ATT_HD + qd * 8;
-    const int c0 = beg + chunk * ATT_CHUNK + wave * 64;
+    const int blk0 = split * bps;
+    const int blk1 = min(nblk, blk0 + bps);
 
-    float s[4];
-    bool ok[4];
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const int key = c0 + p * 16 + ks;
-        ok[p] = key < end;
-        float dot = 0.0f;
-        if (ok[p]) {
-            float kf[8];
-            load_h8(kb + (int64_t) key * ATT_HD, kf);
-#pragma unroll
-            for (int i = 0; i < 8; i++) dot = __builtin_fmaf(qv[i], kf[i], dot);
-        }
-        dot += __shfl_xor(dot, 1, 64);
-        dot += __shfl_xor(dot, 2, 64);
-        s[p] = ok[p] ? dot * scale : -INFINITY;
-    }
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    mx = warp_max(mx);
-    if (lane == 0) s_max[wave] = mx;
-    __syncthreads();
-    const float m = fmaxf(fmaxf(s_max[0], s_max[1]), fmaxf(s_max[2], s_max[3]));
-
-    float l = 0.0f;
+    float m = -INFINITY, l = 0.0f;
     float o[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = 0.0f;
+
+    int blk = blk0 + wave;
+    KV8 cur;
+    if (blk < blk1) load_block(kb, vb, beg + blk * ATT_BLK, end, ks, cur);
+    while (blk < blk1) {
+        const int nxt = blk + 4;
+        KV8 pre;
+        if (nxt < blk1) load_block(kb, vb, beg + nxt * ATT_BLK, end, ks, pre);
+        const int key0 = beg + blk * ATT_BLK;
+        float s[4];
 #pragma unroll
-    for (int p = 0; p < 4; p++) {
-        if (ok[p]) {
-            const int key = c0 + p * 16 + ks;
-            const float pr = expf(s[p] - m);
+        for (int p = 0; p < 4; p++) {
+            float kf[8];
+            h8_to_f(cur.k[p], kf);
+            float dot = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) dot = __builtin_fmaf(qv[i], kf[i], dot);
+            dot += __shfl_xor(dot, 1, 64);
+            dot += __shfl_xor(dot, 2, 64);
+            s[p] = (key0 + p * 16 + ks < end) ? dot * scale_log2 : -INFINITY;
+        }
+        float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+        bm = fmaxf(bm, __shfl_xor(bm, 4, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 8, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+        const float mn = fmaxf(m, bm);                    // finite: each block has a valid key
+        const float f = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first block (m = -inf)
+        l *= f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] *= f;
+        m = mn;
+#pragma unroll
+        for (int p = 0; p < 4; p++) {
+            const float pr = __builtin_amdgcn_exp2f(s[p] - m);   // masked keys: exp2(-inf) = 0
             float vf[8];
-            load_h8(vb + (int64_t) key * ATT_HD, vf);
+            h8_to_f(cur.v[p], vf);
             l += pr;
 #pragma unroll
             for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(pr, vf[i], o[i]);
         }
+        cur = pre;
+        blk = nxt;
     }
+    // reduce the 16 key slots of the wave (m is uniform across the wave)
 #pragma unroll
     for (int off = 4; off < 64; off <<= 1) {
         l += __shfl_xor(l, off, 64);
@@ -154,56 +188,86 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     if (lane < 4) {
 #pragma unroll
         for (int i = 0; i < 8; i++) s_o[wave][lane * 8 + i] = o[i];
-        if (lane == 0) s_l[wave] = l;
+        if (lane == 0) {
+            s_l[wave] = l;
+            s_m[wave] = m;
+        }
     }
     __syncthreads();
     if (wave != 0) return;
 
-    float od_ = 0.0f, lt = 0.0f;
-    if (lane < ATT_HD) od_ = ((s_o[0][lane] + s_o[1][lane]) + s_o[2][lane]) + s_o[3][lane];
-    lt = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
+    // merge the 4 waves (a wave without blocks has m = -inf and weight 0)
+    const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float f = s_m[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w] - M);
+        L = __builtin_fmaf(s_l[w], f, L);
+        if (lane < ATT_HD) O = __builtin_fmaf(s_o[w][lane], f, O);
+    }
 
-    if (nch == 1) {
-        const float inv = 1.0f / lt;
-        attn_store_out(od_ * inv, lane, bh, nh, out, out16, oq, od);
+    if (nact == 1) {
+        attn_store_out(O * (1.0f / L), lane, bh, nh, out, out16, oq, od);
         return;
     }
 
-    // multi-chunk: publish the partial, the last workgroup of this (seq, head) merges
-    float * pp = part + (bh * maxch + chunk) * ATT_PART;
-    if (lane < ATT_HD) st_coherent(pp + 2 + lane, od_);
+    // several splits: publish the partial, the last workgroup of this (seq, head) merges
+    float * pp = part + (bh * nsplit + split) * ATT_PART;
+    if (lane < ATT_HD) st_coherent(pp + 2 + lane, O);
     if (lane == 0) {
-        st_coherent(pp + 0, m);
-        st_coherent(pp + 1, lt);
+        st_coherent(pp + 0, M);
+        st_coherent(pp + 1, L);
     }
     __threadfence();
     int lastflag = 0;
     if (lane == 0) {
         const int prev = __hip_atomic_fetch_add(counters + bh, 1, __ATOMIC_ACQ_REL,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-        lastflag = (prev == nch - 1);
+        lastflag = (prev == nact - 1);
     }
     const int last = __shfl(lastflag, 0, 64);
     if (!last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-
-    float M = -INFINITY;
-    for (int c = 0; c < nch; c++) M = fmaxf(M, ld_coherent(part + (bh * maxch + c) * ATT_PART));
-    float L = 0.0f, O = 0.0f;
-    for (int c = 0; c < nch; c++) {
-        const float * pc = part + (bh * maxch + c) * ATT_PART;
-        const float w = expf(ld_coherent(pc) - M);
-        L = __builtin_fmaf(ld_coherent(pc + 1), w, L);
-        if (lane < ATT_HD) O = __builtin_fmaf(ld_coherent(pc + 2 + lane), w, O);
+    // lane c < nact reads split c's (m, l) in parallel; every lane < 32 reads its o column
+    const float * p0 = part + bh * nsplit * ATT_PART;
+    const float mc = lane < nact ? ld_coherent(p0 + lane * ATT_PART) : -INFINITY;
+    const float lc = lane < nact ? ld_coherent(p0 + lane * ATT_PART + 1) : 0.0f;
+    float Mt = mc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) Mt = fmaxf(Mt, __shfl_xor(Mt, off, 64));
+    const float fc = lane < nact ? __builtin_amdgcn_exp2f(mc - Mt) : 0.0f;
+    float Lt = lc * fc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) Lt += __shfl_xor(Lt, off, 64);
+    float Ot = 0.0f;
+    for (int c = 0; c < nact; c++) {
+        const float w = __shfl(fc, c, 64);
+        if (lane < ATT_HD) Ot = __builtin_fmaf(ld_coherent(p0 + c * ATT_PART + 2 + lane), w, Ot);
     }
-    attn_store_out(O * (1.0f / L), lane, bh, nh, out, out16, oq, od);
+    attn_store_out(Ot * (1.0f / Lt), lane, bh, nh, out, out16, oq, od);
     if (lane == 0)
         __hip_atomic_store(counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Splits per (seq, head). Merging splits needs an agent-scope release per workgroup, which on
+// gfx950 writes back the L2 of the workgroup's XCD; that costs more than it saves unless the
+// launch would otherwise leave most of the chip idle on long rows. So: one workgroup per
+// (seq, head) when there are >= 64 of them or the rows are short, else enough splits of at least
+// 8 blocks (512 keys) to reach ~256 workgroups, at most 64 (the merge reads one split per lane).
+int attn_nsplit(int B, int nh, int64_t max_keys) {
+    const int64_t pairs = (int64_t) B * nh;
+    const int64_t blocks = (max_keys + ATT_BLK - 1) / ATT_BLK;
+    if (pairs >= 64 || blocks < 16) return 1;
+    int64_t ns = (256 + pairs - 1) / pairs;
+    if (ns > blocks / 8) ns = blocks / 8;
+    if (ns > 64) ns = 64;
+    if (ns < 1) ns = 1;
+    return (int) ns;
+}
+
 size_t attn_workspace_bytes(int B, int nh, int64_t max_keys) {
-    const int64_t maxch = (max_keys + ATT_CHUNK - 1) / ATT_CHUNK;
-    const size_t part = (size_t) B * nh * (maxch > 0 ? maxch : 1) * ATT_PART * sizeof(float);
+    const int ns = attn_nsplit(B, nh, max_keys);
+    const size_t part = (size_t) B * nh * ns * ATT_PART * sizeof(float);
     const size_t cnt = (size_t) B * nh * sizeof(int32_t);
     return ((part + 255) / 256) * 256 + cnt;
 }
@@ -211,9 +275,9 @@ size_t attn_workspace_bytes(int B, int nh, int64_t max_keys) {
 // The counter area (the tail of ws) must be zero before the first call; every call leaves it
 // zero again.
 int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
-                       int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin, const int32_t * kv_end,
-                       int64_t max_keys, float scale, float * out, uint16_t * out16, int8_t * oq,
-                       float * od, void * ws, hipStream_t stream) {
+                       int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,
+                       const int32_t * kv_end, int64_t max_keys, float scale, float * out,
+                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream) {
     GSVK_REQUIRE(q && k && v && kv_begin && kv_end && out && ws, "attn_decode: null pointer");
     GSVK_REQUIRE(hd == ATT_HD, "attn_decode: head_dim must be 32 (got %d)", hd);
     GSVK_REQUIRE(q_stride >= (int64_t) nh * hd && q_stride % 4 == 0, "attn_decode: bad q stride");
@@ -222,14 +286,13 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
                  "attn_decode: bad shape B=%d nh=%d lstride=%lld max_keys=%lld", B, nh,
                  (long long) lstride, (long long) max_keys);
     GSVK_REQUIRE((oq == nullptr) == (od == nullptr), "attn_decode: oq and od go together");
-    const int64_t maxch64 = (max_keys + ATT_CHUNK - 1) / ATT_CHUNK;
-    const int maxch = (int) (maxch64 > 0 ? maxch64 : 1);
-    const size_t part_bytes = (size_t) B * nh * maxch * ATT_PART * sizeof(float);
+    const int ns = attn_nsplit(B, nh, max_keys);
+    const size_t part_bytes = (size_t) B * nh * ns * ATT_PART * sizeof(float);
     float * part = (float *) ws;
     int32_t * counters = (int32_t *) ((char *) ws + ((part_bytes + 255) / 256) * 256);
-    hipLaunchKernelGGL(k_attn_decode, dim3((unsigned) maxch, (unsigned) nh, (unsigned) B), dim3(256),
-                       0, stream, q, q_stride, k, v, nh, lstride, kv_begin, kv_end, maxch, scale, out, out16,
-                       oq, od, part, counters);
+    hipLaunchKernelGGL(k_attn_decode, dim3((unsigned) ns, (unsigned) nh, (unsigned) B), dim3(256),
+                       0, stream, q, q_stride, k, v, nh, lstride, kv_begin, kv_end, ns,
+                       scale * LOG2E, out, out16, oq, od, part, counters);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -245,6 +308,6 @@ extern "C" int gsvk_op_attn_decode(const float * q, const uint16_t * k, const ui
                                    const int32_t * kv_end, int64_t max_keys, float scale,
                                    float * out, uint16_t * out_f16, int8_t * oq, float * od,
                                    void * ws, void * stream) {
-    return gsvk::launch_attn_decode(q, (int64_t) nh * hd, k, v, B, nh, hd, lstride, kv_begin, kv_end, max_keys, scale,
-                                    out, out_f16, oq, od, ws, (hipStream_t) stream);
+    return gsvk::launch_attn_decode(q, (int64_t) nh * hd, k, v, B, nh, hd, lstride, kv_begin, kv_end,
+                                    max_keys, scale, out, out_f16, oq, od, ws, (hipStream_t) stream);
 }

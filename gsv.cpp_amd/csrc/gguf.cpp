@@ -77,9 +77,14 @@ GgufFile::~GgufFile() {
     if (f_) fclose(f_);
 }
 
-bool GgufFile::open(const std::string & path, std::string & err) {
+bool GgufFile::open(const std::string & path, std::string & err, bool * io_error) {
+    if (io_error) *io_error = false;
     f_ = fopen(path.c_str(), "rb");
-    if (!f_) { err = "cannot open " + path; return false; }
+    if (!f_) {
+        err = "cannot open " + path;
+        if (io_error) *io_error = true;
+        return false;
+    }
     fseeko(f_, 0, SEEK_END);
     size_ = (uint64_t) ftello(f_);
     fseeko(f_, 0, SEEK_SET);

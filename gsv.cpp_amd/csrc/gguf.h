@@ -28,8 +28,9 @@ struct GgufTensor {
 class GgufFile {
 public:
     ~GgufFile();
-    // Returns false with a message in err on any format problem.
-    bool open(const std::string & path, std::string & err);
+    // Returns false with a message in err on any problem; io_error tells an unreadable file
+    // from a malformed one.
+    bool open(const std::string & path, std::string & err, bool * io_error = nullptr);
     const GgufTensor * tensor(const std::string & name) const;
     bool get_u32(const std::string & key, uint32_t & out) const;
     bool read(const GgufTensor & t, void * dst) const;

@@ -1,0 +1,229 @@
+// Fused decoder-layer GEMV for gfx950: one launch computes the Q8_0 input of a projection and
+// the projection itself.
+//
+//   input stage (per workgroup, for its MT activation rows, into LDS):
+//     IN_Q8  : the rows are already Q8_0 (attention output, FFN1 output)
+//     IN_LN  : v = (res + r) + bias; LayerNorm(v) * w + b (PATCH:1533-1584), then the ggml-cpu
+//              x86 Q8_0 quantisation; workgroups of column 0 also store the fp32 LayerNorm output
+//              (the next residual). Every workgroup computes identical values (same code, same
+//              inputs), so this replaces the separate LayerNorm + quantise launches bit-exactly.
+//     IN_EMB : x = emb[tok] + alpha * PE[pos] (src/gsv_ar.cpp:798-807), quantised likewise;
+//              column-0 workgroups store x and set kv_end for the step.
+//   GEMV stage: the sliced Q8_0 dot in ggml-cpu's x86 order (see q8.hip), 32 output rows per
+//   workgroup (4 waves x 8 rows x 8 slice lanes); the weight loads are issued before the input
+//   stage so their HBM latency overlaps it.
+//   output stage: bias, ReLU, fp32 store of rows < n_store, the K/V append to the fp16 cache, or
+//   (OUT_Q8) the Q8_0 quantisation of each 32-row output block, written sliced.
+#include "common.h"
+#include "layer.h"
+
+namespace gsvk {
+
+constexpr int LG_THREADS = 256;
+constexpr int LG_ROWS = 32;   // output rows per workgroup
+
+// One row of width 512 held by one wave (8 values per lane): LayerNorm as in norm.hip.
+__device__ __forceinline__ void ln_row_wave(const float * __restrict__ res, const float * __restrict__ r,
+                                            const float * __restrict__ bias,
+                                            const float * __restrict__ wb, int lane, float (&o)[8]) {
+    constexpr int n = 512;
+    float v[8];
+    double s = 0.0, s2 = 0.0;
+    const int base = lane * 8;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float t = res[base + i];
+        if (r) t = t + r[base + i];
+        if (bias) t = t + bias[base + i];
+        v[i] = t;
+        s += (double) t;
+        s2 += (double) t * (double) t;
+    }
+    s = warp_sum_d(s);
+    s2 = warp_sum_d(s2);
+    const float mean = (float) (s / (double) n);
+    const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
+    const float inv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf((v[i] - mean) * inv, wb[base + i], wb[n + base + i]);
+}
+
+template <int NB4, int MT>
+__global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __restrict__ ws,
+                                                           const uint16_t * __restrict__ wd, int n,
+                                                           int m, LayerIn in, LayerOut out) {
+    constexpr int K = NB4 * 128;
+    constexpr int NBLK = K / 32;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int r = lane >> 3;
+    const int j = lane & 7;
+    const int row = blockIdx.x * LG_ROWS + wave * 8 + r;
+    const int m0 = blockIdx.y * MT;
+    const bool valid = row < n;
+    const int rowc = valid ? row : n - 1;
+
+    __shared__ __align__(16) int8_t s_x[MT][K];
+    __shared__ __align__(16) float s_d[MT][NBLK];
+    __shared__ float s_out[MT][LG_ROWS];
+
+    // weights first: their HBM latency overlaps the input stage
+    int4 w[NB4];
+    uint2 dh[NB4];
+    {
+        const int4 * wsl = reinterpret_cast<const int4 *>(ws + ((int64_t) rowc * 8 + j) * NBLK * 4);
+        const uint2 * wdr = reinterpret_cast<const uint2 *>(wd + (int64_t) rowc * NBLK);
+#pragma unroll
+        for (int i = 0; i < NB4; i++) {
+            w[i] = wsl[i];
+            dh[i] = wdr[i];
+        }
+    }
+
+    // ---- input stage ----
+    if (in.mode == IN_Q8) {
+        constexpr int CH = K / 16;   // 16-byte chunks per row
+        for (int c = tid; c < MT * CH; c += LG_THREADS) {
+            const int t = c / CH, cc = c % CH;
+            const int mm = min(m0 + t, m - 1);
+            *reinterpret_cast<int4 *>(&s_x[t][cc * 16]) =
+                *reinterpret_cast<const int4 *>(in.xs + (int64_t) mm * K + cc * 16);
+        }
+        for (int c = tid; c < MT * NBLK; c += LG_THREADS) {
+            const int t = c / NBLK, cc = c % NBLK;
+            const int mm = min(m0 + t, m - 1);
+            s_d[t][cc] = in.xd[(int64_t) mm * NBLK + cc];
+        }
+    } else {
+        // K == 512: one wave per activation row
+        for (int t = wave; t < MT; t += LG_THREADS / 64) {
+            const int mm = min(m0 + t, m - 1);
+            float o[8];
+            if (in.mode == IN_LN) {
+                ln_row_wave(in.res + (int64_t) mm * 512, in.r ? in.r + (int64_t) mm * 512 : nullptr,
+                            in.bias, in.wb, lane, o);
+            } else {   // IN_EMB
+                int tk = in.tok[mm];
+                tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
+                const int pos = *in.pos_ptr + in.pos_add;
+                const float * er = in.emb + (int64_t) tk * 512 + lane * 8;
+                const float * pr = in.pe + (int64_t) pos * 512 + lane * 8;
+#pragma unroll
+                for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pr[i], er[i]);
+            }
+            if (blockIdx.x == 0 && m0 + t < m) {
+                if (in.out_x) {
+                    float4 * dst = reinterpret_cast<float4 *>(in.out_x + (int64_t) mm * 512 + lane * 8);
+                    dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+                    dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+                }
+                if (in.kv_end && lane == 0) in.kv_end[mm] = *in.pos_ptr + in.kv_end_add;
+            }
+            int8_t q[8];
+            const float d = q8_quantize_group<8>(o, q, 4);
+            q8_store_sliced(&s_x[t][0], NBLK, lane >> 2, lane & 3, q);
+            if ((lane & 3) == 0) s_d[t][lane >> 2] = d;
+        }
+    }
+    __syncthreads();
+
+    // ---- GEMV stage ----
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NB4; i++) {
+        const float dw0 = h2f((uint16_t) (dh[i].x & 0xffff)), dw1 = h2f((uint16_t) (dh[i].x >> 16));
+        const float dw2 = h2f((uint16_t) (dh[i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[i].y >> 16));
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[t][(j * NBLK + 4 * i) * 4]);
+            const float4 dx = *reinterpret_cast<const float4 *>(&s_d[t][4 * i]);
+            float a = acc[t];
+            a = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w[i].x, xv.x, 0, false), a);
+            a = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w[i].y, xv.y, 0, false), a);
+            a = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w[i].z, xv.z, 0, false), a);
+            a = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w[i].w, xv.w, 0, false), a);
+            acc[t] = a;
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        float v = acc[t];
+        v = v + __shfl_xor(v, 4, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        acc[t] = v;
+    }
+
+    // ---- output stage ----
+    const float bias = (out.bias && valid) ? out.bias[row] : 0.0f;
+    int kvcol0 = 0;
+    if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        const int mm = m0 + t;
+        if ((t & 7) != j) continue;
+        float v = acc[t];
+        if (out.bias) v = v + bias;
+        if (out.act == 1) v = v > 0.0f ? v : 0.0f;
+        if (out.yq) s_out[t][wave * 8 + r] = v;
+        if (!valid || mm >= m) continue;
+        if (out.y && row < out.n_store) out.y[(int64_t) mm * out.y_stride + row] = v;
+        if (out.kc && row >= out.kv_row0) {
+            const int rr = row - out.kv_row0;
+            const int which = rr / out.d_model;
+            const int hd = rr % out.d_model;
+            const int h = hd >> 5, dd = hd & 31;
+            const int b = mm / out.rows_per_seq;
+            const int col = kvcol0 + mm % out.rows_per_seq;
+            uint16_t * cache = which == 0 ? out.kc : out.vc;
+            cache[(((int64_t) b * out.n_head + h) * out.lstride + col) * 32 + dd] = f2h(v);
+        }
+    }
+    if (out.yq) {
+        __syncthreads();
+        // one 32-value block per activation row: block index blockIdx.x of a row of n values
+        for (int t = wave; t < MT; t += LG_THREADS / 64) {
+            const int mm = m0 + t;
+            float v1[1] = {lane < LG_ROWS ? s_out[t][lane] : 0.0f};
+            int8_t q1[1];
+            const float d = q8_quantize_group<1>(v1, q1, 32);
+            if (mm < m && lane < LG_ROWS) {
+                const int nblk_out = n / 32;
+                out.yq[(int64_t) mm * n + q8_sliced_offset(nblk_out, blockIdx.x, lane)] = q1[0];
+                if (lane == 0) out.yd[(int64_t) mm * nblk_out + blockIdx.x] = d;
+            }
+        }
+    }
+}
+
+int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
+                      const LayerIn & in, const LayerOut & out, hipStream_t stream) {
+    GSVK_REQUIRE(ws && wd && n > 0 && m > 0 && n % LG_ROWS == 0 && n < (1 << 30) && m < (1 << 30),
+                 "layer_gemv: bad shape n=%lld m=%lld", (long long) n, (long long) m);
+    GSVK_REQUIRE(k == 512 || k == 2048, "layer_gemv: k must be 512 or 2048 (got %lld)", (long long) k);
+    GSVK_REQUIRE(in.mode == IN_Q8 ? (in.xs && in.xd) : (k == 512), "layer_gemv: bad input mode");
+    GSVK_REQUIRE(in.mode != IN_LN || (in.res && in.wb), "layer_gemv: LayerNorm input needs res and wb");
+    GSVK_REQUIRE(in.mode != IN_EMB || (in.emb && in.pe && in.tok && in.pos_ptr), "layer_gemv: bad embedding input");
+    GSVK_REQUIRE(!out.yq || (out.yd && n % 32 == 0), "layer_gemv: bad quantised output");
+    GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 &&
+                             out.kv_row0 + 2 * out.d_model <= n), "layer_gemv: bad KV epilogue");
+    const unsigned gx = (unsigned) (n / LG_ROWS);
+#define GSVK_LG(NB4, MT)                                                                          \
+    hipLaunchKernelGGL((k_layer_gemv<NB4, MT>), dim3(gx, (unsigned) ((m + MT - 1) / MT)),        \
+                       dim3(LG_THREADS), 0, stream, ws, wd, (int) n, (int) m, in, out)
+    if (k == 512) {
+        if (m <= 32) GSVK_LG(4, 2);
+        else GSVK_LG(4, 4);
+    } else {
+        if (m <= 32) GSVK_LG(16, 1);
+        else GSVK_LG(16, 2);
+    }
+#undef GSVK_LG
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk

@@ -14,6 +14,7 @@
 // 8 lanes combine with the xor-4, xor-2, xor-1 butterfly, which is that reduction order, so the
 // result equals the reference's to the bit.
 #include "common.h"
+#include "layer.h"
 
 namespace gsvk {
 
@@ -77,10 +78,39 @@ __global__ void __launch_bounds__(64) k_q8_quantize(const float * __restrict__ x
 // GEMV / GEMM: y[m][n] = sum_blk fp32(wd[n][blk]) * xd[m][blk] * dot_i8(w[n][blk], x[m][blk])
 //
 // Workgroup = one wave = 8 output rows x 8 slice lanes; grid.y splits the m rows in tiles of
-// MT. Each lane streams its weight slice once per m-tile with 16-byte loads.
+// MT. A lane first issues every load it needs — its whole weight slice and the row's scales
+// (from HBM), then the activation slices and scales of its MT rows (from L2) — and only then runs
+// the FMA chains, so a launch costs about one memory latency. NB4 = nblk/4 is a compile-time
+// constant for the model's two row lengths (512 and 2048); other lengths use the NB4 = 0 loop.
 // ---------------------------------------------------------------------------------------
 
-template <int MT>
+__device__ __forceinline__ float q8_chain4(float a, const int4 & w, const int4 & xv, float dw0,
+                                           float dw1, float dw2, float dw3, const float4 & dx) {
+    a = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w.x, xv.x, 0, false), a);
+    a = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w.y, xv.y, 0, false), a);
+    a = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w.z, xv.z, 0, false), a);
+    a = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w.w, xv.w, 0, false), a);
+    return a;
+}
+
+__device__ __forceinline__ void q8_gemv_epilogue(const GemvEpilogue & epi, int row, int mm, int n,
+                                                 float v, float * __restrict__ y) {
+    if (epi.bias) v = v + epi.bias[row];
+    if (epi.act == 1) v = v > 0.0f ? v : 0.0f;
+    y[(int64_t) mm * n + row] = v;
+    if (epi.kc && row >= epi.kv_row0) {
+        const int rr = row - epi.kv_row0;              // [0, 2*d_model)
+        const int which = rr / epi.d_model;            // 0 = K, 1 = V
+        const int hd = rr % epi.d_model;
+        const int h = hd >> 5, dd = hd & 31;
+        const int b = mm / epi.rows_per_seq;
+        const int col = *epi.col_ptr + epi.col_add + mm % epi.rows_per_seq;
+        uint16_t * cache = which == 0 ? epi.kc : epi.vc;
+        cache[(((int64_t) b * epi.n_head + h) * epi.lstride + col) * 32 + dd] = f2h(v);
+    }
+}
+
+template <int NB4, int MT>
 __global__ void __launch_bounds__(64) k_q8_gemv(const int8_t * __restrict__ ws,
                                                 const uint16_t * __restrict__ wd, int n, int k,
                                                 const int8_t * __restrict__ xs,
@@ -91,34 +121,56 @@ __global__ void __launch_bounds__(64) k_q8_gemv(const int8_t * __restrict__ ws,
     const int j = lane & 7;
     const int row = blockIdx.x * 8 + r;
     const int m0 = blockIdx.y * MT;
-    const int nblk = k >> 5;
+    const int nblk = NB4 > 0 ? NB4 * 4 : k >> 5;
     const bool valid = row < n;
     const int rowc = valid ? row : n - 1;
-    const int * wsl = reinterpret_cast<const int *>(ws + ((int64_t) rowc * 8 + j) * nblk * 4);
-    const uint16_t * wdr = wd + (int64_t) rowc * nblk;
+    const int4 * wsl = reinterpret_cast<const int4 *>(ws + ((int64_t) rowc * 8 + j) * nblk * 4);
+    const uint2 * wdr = reinterpret_cast<const uint2 *>(wd + (int64_t) rowc * nblk);
 
     float acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++) acc[t] = 0.0f;
 
-    for (int b4 = 0; b4 < nblk; b4 += 4) {
-        const int4 w = *reinterpret_cast<const int4 *>(wsl + b4);
-        const uint2 dh = *reinterpret_cast<const uint2 *>(wdr + b4);
-        const float dw0 = h2f((uint16_t) (dh.x & 0xffff)), dw1 = h2f((uint16_t) (dh.x >> 16));
-        const float dw2 = h2f((uint16_t) (dh.y & 0xffff)), dw3 = h2f((uint16_t) (dh.y >> 16));
+    if constexpr (NB4 > 0) {
+        int4 w[NB4];
+        uint2 dh[NB4];
+#pragma unroll
+        for (int i = 0; i < NB4; i++) {
+            w[i] = wsl[i];
+            dh[i] = wdr[i];
+        }
+        int4 xv[MT][NB4];
+        float4 dx[MT][NB4];
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            const int mm = m0 + t;
-            if (mm < m) {
-                const int4 xv = *reinterpret_cast<const int4 *>(
-                    reinterpret_cast<const int *>(xs + ((int64_t) mm * 8 + j) * nblk * 4) + b4);
-                const float4 dx = *reinterpret_cast<const float4 *>(xd + (int64_t) mm * nblk + b4);
-                float a = acc[t];
-                a = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w.x, xv.x, 0, false), a);
-                a = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w.y, xv.y, 0, false), a);
-                a = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w.z, xv.z, 0, false), a);
-                a = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w.w, xv.w, 0, false), a);
-                acc[t] = a;
+            const int mm = m0 + t < m ? m0 + t : m - 1;
+            const int4 * xsl = reinterpret_cast<const int4 *>(xs + ((int64_t) mm * 8 + j) * nblk * 4);
+            const float4 * xdr = reinterpret_cast<const float4 *>(xd + (int64_t) mm * nblk);
+#pragma unroll
+            for (int i = 0; i < NB4; i++) {
+                xv[t][i] = xsl[i];
+                dx[t][i] = xdr[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NB4; i++) {
+            const float dw0 = h2f((uint16_t) (dh[i].x & 0xffff)), dw1 = h2f((uint16_t) (dh[i].x >> 16));
+            const float dw2 = h2f((uint16_t) (dh[i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[i].y >> 16));
+#pragma unroll
+            for (int t = 0; t < MT; t++) acc[t] = q8_chain4(acc[t], w[i], xv[t][i], dw0, dw1, dw2, dw3, dx[t][i]);
+        }
+    } else {
+        for (int i = 0; i < nblk / 4; i++) {
+            const int4 w = wsl[i];
+            const uint2 dh = wdr[i];
+            const float dw0 = h2f((uint16_t) (dh.x & 0xffff)), dw1 = h2f((uint16_t) (dh.x >> 16));
+            const float dw2 = h2f((uint16_t) (dh.y & 0xffff)), dw3 = h2f((uint16_t) (dh.y >> 16));
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int mm = m0 + t < m ? m0 + t : m - 1;
+                const int4 xv = reinterpret_cast<const int4 *>(xs + ((int64_t) mm * 8 + j) * nblk * 4)[i];
+                const float4 dx = reinterpret_cast<const float4 *>(xd + (int64_t) mm * nblk)[i];
+                acc[t] = q8_chain4(acc[t], w, xv, dw0, dw1, dw2, dw3, dx);
             }
         }
     }
@@ -131,28 +183,10 @@ __global__ void __launch_bounds__(64) k_q8_gemv(const int8_t * __restrict__ ws,
         acc[t] = v;
     }
     if (!valid) return;
-    const float bias = epi.bias ? epi.bias[row] : 0.0f;
-    int kvcol0 = 0;
-    if (epi.kc) kvcol0 = *epi.col_ptr + epi.col_add;
 #pragma unroll
     for (int t = 0; t < MT; t++) {
         const int mm = m0 + t;
-        if (mm < m && (t & 7) == j) {
-            float v = acc[t];
-            if (epi.bias) v = v + bias;
-            if (epi.act == 1) v = v > 0.0f ? v : 0.0f;
-            y[(int64_t) mm * n + row] = v;
-            if (epi.kc && row >= epi.kv_row0) {
-                const int rr = row - epi.kv_row0;              // [0, 2*d_model)
-                const int which = rr / epi.d_model;            // 0 = K, 1 = V
-                const int hd = rr % epi.d_model;
-                const int h = hd >> 5, dd = hd & 31;
-                const int b = mm / epi.rows_per_seq;
-                const int col = kvcol0 + mm % epi.rows_per_seq;
-                uint16_t * cache = which == 0 ? epi.kc : epi.vc;
-                cache[(((int64_t) b * epi.n_head + h) * epi.lstride + col) * 32 + dd] = f2h(v);
-            }
-        }
+        if (mm < m && (t & 7) == j) q8_gemv_epilogue(epi, row, mm, n, acc[t], y);
     }
 }
 
@@ -170,15 +204,20 @@ int launch_q8_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
                          epi.kv_row0 >= 0 && epi.kv_row0 + 2 * epi.d_model <= n,
                      "q8_gemv: bad KV epilogue");
     }
-    if (m <= 16) {
-        const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + 3) / 4));
-        hipLaunchKernelGGL(k_q8_gemv<4>, grid, dim3(64), 0, stream, ws, wd, (int) n, (int) k, xs, xd,
-                           (int) m, epi, y);
+    const unsigned gx = (unsigned) ((n + 7) / 8);
+#define GSVK_GEMV(NB4, MT)                                                                          \
+    hipLaunchKernelGGL((k_q8_gemv<NB4, MT>), dim3(gx, (unsigned) ((m + MT - 1) / MT)), dim3(64), 0, \
+                       stream, ws, wd, (int) n, (int) k, xs, xd, (int) m, epi, y)
+    if (k == 512) {
+        if (m <= 16) GSVK_GEMV(4, 2);
+        else GSVK_GEMV(4, 4);
+    } else if (k == 2048) {
+        if (m <= 16) GSVK_GEMV(16, 1);
+        else GSVK_GEMV(16, 2);
     } else {
-        const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + 7) / 8));
-        hipLaunchKernelGGL(k_q8_gemv<8>, grid, dim3(64), 0, stream, ws, wd, (int) n, (int) k, xs, xd,
-                           (int) m, epi, y);
+        GSVK_GEMV(0, 4);
     }
+#undef GSVK_GEMV
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -236,8 +275,46 @@ extern "C" int gsvk_op_q8_quantize(const float * x, int64_t rows, int64_t k, int
 extern "C" int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k,
                                const int8_t * xq, const float * xd, int64_t m, const float * bias,
                                int act, float * y, void * stream) {
+    if ((k == 512 || k == 2048) && n % 32 == 0 && wq && wd && xq && xd) {
+        // the decoder's own fused kernel, input stage reading Q8_0 rows
+        LayerIn in{};
+        in.mode = IN_Q8;
+        in.xs = xq;
+        in.xd = xd;
+        LayerOut out{};
+        out.y = y;
+        out.y_stride = n;
+        out.n_store = (int) n;
+        out.bias = bias;
+        out.act = act;
+        GSVK_REQUIRE(y, "q8_gemv: null pointer");
+        GSVK_REQUIRE(act == 0 || act == 1, "q8_gemv: act must be 0 or 1");
+        return launch_layer_gemv(wq, wd, n, k, m, in, out, (hipStream_t) stream);
+    }
     GemvEpilogue epi{};
     epi.bias = bias;
     epi.act = act;
     return launch_q8_gemv(wq, wd, n, k, xq, xd, m, epi, y, (hipStream_t) stream);
+}
+
+extern "C" int gsvk_op_ln_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, const float * res,
+                               const float * r, const float * ln_bias, const float * wb, int64_t m,
+                               const float * bias, int act, float * y, float * ln_out,
+                               void * stream) {
+    GSVK_REQUIRE(wq && wd && res && wb && y, "ln_gemv: null pointer");
+    GSVK_REQUIRE(act == 0 || act == 1, "ln_gemv: act must be 0 or 1");
+    LayerIn in{};
+    in.mode = IN_LN;
+    in.res = res;
+    in.r = r;
+    in.bias = ln_bias;
+    in.wb = wb;
+    in.out_x = ln_out;
+    LayerOut out{};
+    out.y = y;
+    out.y_stride = n;
+    out.n_store = (int) n;
+    out.bias = bias;
+    out.act = act;
+    return launch_layer_gemv(wq, wd, n, 512, m, in, out, (hipStream_t) stream);
 }

@@ -12,6 +12,7 @@
 
 #include "common.h"
 #include "gguf.h"
+#include "layer.h"
 #include "sampler.h"
 
 namespace gsvk {
@@ -110,7 +111,7 @@ struct gsvk_model {
     int s_B = 0, s_hist = 0, s_steps = 0;
     int64_t s_lstride = 0;
     Act x, attn, n1, hq;
-    float * qkv = nullptr, * o = nullptr, * h = nullptr, * h2 = nullptr, * logits = nullptr;
+    float * qkv = nullptr, * o = nullptr, * h2 = nullptr, * logits = nullptr;
     void * attn_ws = nullptr;
     int32_t * kv_begin = nullptr, * kv_end = nullptr;
     int32_t * d_step = nullptr, * hist = nullptr, * ny = nullptr, * fin_step = nullptr,
@@ -231,7 +232,6 @@ int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
     GSVK_TRY(a.alloc(m->hq.d, (size_t) B * m->FFN / 32));
     GSVK_TRY(a.alloc(m->qkv, (size_t) B * 3 * D));
     GSVK_TRY(a.alloc(m->o, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->h, (size_t) B * m->FFN));
     GSVK_TRY(a.alloc(m->h2, (size_t) B * D));
     GSVK_TRY(a.alloc(m->logits, (size_t) B * m->V));
     char * ws = nullptr;
@@ -289,71 +289,122 @@ int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
                        m->V, mode, m->stream);
 }
 
-// One transformer layer after the QKV projection and attention (shared by prefill and decode).
-int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, Act & cur, const Act & attn, float * o,
-               Act & n1, float * h, Act & hq, float * h2) {
+// The projections of one layer after attention (shared by prefill and decode), with the
+// LayerNorms folded into the input stage of the consuming GEMV:
+//   o  = Wo . attn
+//   n1 = LN1(cur + o + bo)                       (FFN1 input stage; stored to n1x)
+//   hq = Q8_0(relu(W1 . n1 + b1))                (quantised in FFN1's output stage)
+//   h2 = W2 . hq
+// LN2 (cur' = LN2(n1 + h2 + b2)) is the input stage of the next layer's QKV or of final_ln().
+int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
+               float * o, float * n1x, Act & hq, float * h2) {
     const int D = m->D, F = m->FFN;
-    GemvEpilogue none{};
-    GSVK_TRY(launch_q8_gemv(w.out.qs, w.out.d, D, D, attn.q, attn.d, R, none, o, m->stream));
-    GSVK_TRY(launch_layernorm(cur.x, o, w.out.b, w.ln1, R, D, 1e-5f, n1.x, n1.q, n1.d, m->stream));
-    GemvEpilogue relu{};
-    relu.bias = w.f1.b;
-    relu.act = 1;
-    GSVK_TRY(launch_q8_gemv(w.f1.qs, w.f1.d, F, D, n1.q, n1.d, R, relu, h, m->stream));
-    GSVK_TRY(launch_q8_quantize(h, R, F, hq.q, hq.d, m->stream));
-    GSVK_TRY(launch_q8_gemv(w.f2.qs, w.f2.d, D, F, hq.q, hq.d, R, none, h2, m->stream));
-    GSVK_TRY(launch_layernorm(n1.x, h2, w.f2.b, w.ln2, R, D, 1e-5f, cur.x, cur.q, cur.d, m->stream));
+    LayerIn qin{};
+    qin.mode = IN_Q8;
+    qin.xs = attn.q;
+    qin.xd = attn.d;
+    LayerOut oo{};
+    oo.y = o;
+    oo.y_stride = D;
+    oo.n_store = D;
+    GSVK_TRY(launch_layer_gemv(w.out.qs, w.out.d, D, D, R, qin, oo, m->stream));
+    LayerIn lin{};
+    lin.mode = IN_LN;
+    lin.res = cur_x;
+    lin.r = o;
+    lin.bias = w.out.b;
+    lin.wb = w.ln1;
+    lin.out_x = n1x;
+    LayerOut ho{};
+    ho.bias = w.f1.b;
+    ho.act = 1;
+    ho.yq = hq.q;
+    ho.yd = hq.d;
+    GSVK_TRY(launch_layer_gemv(w.f1.qs, w.f1.d, F, D, R, lin, ho, m->stream));
+    LayerIn hin{};
+    hin.mode = IN_Q8;
+    hin.xs = hq.q;
+    hin.xd = hq.d;
+    LayerOut h2o{};
+    h2o.y = h2;
+    h2o.y_stride = D;
+    h2o.n_store = D;
+    GSVK_TRY(launch_layer_gemv(w.f2.qs, w.f2.d, D, F, R, hin, h2o, m->stream));
     return GSVK_OK;
 }
 
-// Kernels of one decode step at loop index (*d_step - 1): embedding + PE of last_tok, 24
-// layers with the KV append at column S - 1 + *d_step, logits.
+// QKV projection output stage: q (and k, v when n_store = 3D) as fp32, plus the K/V append.
+LayerOut qkv_out(gsvk_model * m, const LayerW & w, size_t loff, float * y, int n_store,
+                 int rows_per_seq, const int32_t * col_ptr, int col_add) {
+    LayerOut qo{};
+    qo.y = y;
+    qo.y_stride = n_store;
+    qo.n_store = n_store;
+    qo.bias = w.qkv.b;
+    qo.kc = m->kc + loff;
+    qo.vc = m->vc + loff;
+    qo.kv_row0 = m->D;
+    qo.d_model = m->D;
+    qo.n_head = m->NH;
+    qo.lstride = m->lstride;
+    qo.rows_per_seq = rows_per_seq;
+    qo.col_ptr = col_ptr;
+    qo.col_add = col_add;
+    return qo;
+}
+
+// LN2 of the last layer: x = LN2(n1 + h2 + b2), quantised too when the head is Q8_0.
+int final_ln(gsvk_model * m, int64_t R, const float * n1x, const float * h2, Act & x) {
+    const LayerW & w = m->L[m->NL - 1];
+    const bool q = m->head_type == GGML_Q8_0;
+    return launch_layernorm(n1x, h2, w.f2.b, w.ln2, R, m->D, 1e-5f, x.x, q ? x.q : nullptr,
+                            q ? x.d : nullptr, m->stream);
+}
+
+// Kernels of one decode step at loop index idx = *d_step - 1: the layer-0 QKV embeds last_tok at
+// PE position prompt_len + idx (and sets kv_end = S + idx + 1); every QKV appends K/V at column
+// S + idx; logits of the head.
 int enqueue_decode_body(gsvk_model * m) {
     const int B = m->B, D = m->D;
-    GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
-                             m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q, m->x.d,
-                             m->stream));
     const float scale = 1.0f / std::sqrt((float) m->HD);
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
-        GemvEpilogue qe{};
-        qe.bias = w.qkv.b;
-        qe.kc = m->kc + loff;
-        qe.vc = m->vc + loff;
-        qe.kv_row0 = D;
-        qe.d_model = D;
-        qe.n_head = m->NH;
-        qe.lstride = m->lstride;
-        qe.rows_per_seq = 1;
-        qe.col_ptr = m->d_step;
-        qe.col_add = m->S - 1;
-        GSVK_TRY(launch_q8_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, m->x.q, m->x.d, B, qe, m->qkv, m->stream));
-        GSVK_TRY(launch_attn_decode(m->qkv, 3 * D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
+        LayerIn in{};
+        if (li == 0) {
+            in.mode = IN_EMB;
+            in.emb = m->audio_emb;
+            in.pe = m->pe;
+            in.tok = m->last_tok;
+            in.pos_ptr = m->d_step;
+            in.pos_add = m->prompt_len - 1;
+            in.alpha = m->audio_alpha;
+            in.vocab = m->V;
+            in.kv_end = m->kv_end;
+            in.kv_end_add = m->S;
+        } else {
+            const LayerW & p = m->L[li - 1];
+            in.mode = IN_LN;
+            in.res = m->n1.x;
+            in.r = m->h2;
+            in.bias = p.f2.b;
+            in.wb = p.ln2;
+        }
+        in.out_x = m->x.x;
+        GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, B, in,
+                                   qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
+        GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
                                     m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
                                     m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream));
-        GSVK_TRY(layer_tail(m, w, B, m->x, m->attn, m->o, m->n1, m->h, m->hq, m->h2));
+        GSVK_TRY(layer_tail(m, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2));
     }
+    GSVK_TRY(final_ln(m, B, m->n1.x, m->h2, m->x));
     return head_logits(m, m->x, B, 0, m->logits);
 }
 
 }  // namespace
 
-// kv_end[b] = S + step (keys [pad_b, S - 1 + step] inclusive) — written by a tiny kernel so the
-// captured step needs no host update.
-__global__ void k_set_kv_end(int32_t * kv_end, const int32_t * step, int base, int B) {
-    const int b = threadIdx.x + blockIdx.x * blockDim.x;
-    if (b < B) kv_end[b] = base + *step;
-}
-
 namespace {
-
-int enqueue_step_prologue(gsvk_model * m) {
-    hipLaunchKernelGGL(k_set_kv_end, dim3((unsigned) ((m->B + 127) / 128)), dim3(128), 0, m->stream,
-                       m->kv_end, m->d_step, m->S, m->B);
-    GSVK_LAUNCH_CHECK();
-    return GSVK_OK;
-}
 
 // ---------------------------------------------------------------------------------------
 // prefill
@@ -450,7 +501,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     }
     // activations of the prefill rows
     Act cur, attn, n1, hq;
-    float * qkv, * o, * h, * h2, * last, * lg;
+    float * qkv, * o, * h2, * last, * lg;
     GSVK_TRY(tmp.alloc(cur.x, rows * D));
     GSVK_TRY(tmp.alloc(cur.q, rows * D));
     GSVK_TRY(tmp.alloc(cur.d, rows * D / 32));
@@ -464,7 +515,6 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(tmp.alloc(hq.d, rows * F / 32));
     GSVK_TRY(tmp.alloc(qkv, rows * 3 * D));
     GSVK_TRY(tmp.alloc(o, rows * D));
-    GSVK_TRY(tmp.alloc(h, rows * F));
     GSVK_TRY(tmp.alloc(h2, rows * D));
     GSVK_TRY(tmp.alloc(last, (size_t) B * D));
     GSVK_TRY(tmp.alloc(lg, (size_t) B * m->V));
@@ -488,22 +538,27 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
-        GemvEpilogue qe{};
-        qe.bias = w.qkv.b;
-        qe.kc = m->kc + loff;
-        qe.vc = m->vc + loff;
-        qe.kv_row0 = D;
-        qe.d_model = D;
-        qe.n_head = m->NH;
-        qe.lstride = m->lstride;
-        qe.rows_per_seq = S;
-        qe.col_ptr = zero;
-        qe.col_add = 0;
-        GSVK_TRY(launch_q8_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, cur.q, cur.d, rows, qe, qkv, st));
+        LayerIn in{};
+        if (li == 0) {
+            in.mode = IN_Q8;
+            in.xs = cur.q;
+            in.xd = cur.d;
+        } else {
+            const LayerW & p = m->L[li - 1];
+            in.mode = IN_LN;
+            in.res = n1.x;
+            in.r = h2;
+            in.bias = p.f2.b;
+            in.wb = p.ln2;
+            in.out_x = cur.x;
+        }
+        GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
+                                   qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                      attn.d, st));
-        GSVK_TRY(layer_tail(m, w, rows, cur, attn, o, n1, h, hq, h2));
+        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2));
     }
+    GSVK_TRY(final_ln(m, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
     Act lastq;
     lastq.x = last;
@@ -566,9 +621,88 @@ extern "C" int gsvk_parse_device(const char * s, int * device) {
     return GSVK_ERR_NODEV;
 }
 
+namespace {
+
+struct Hparams {
+    int D = 512, NH = 16, NL = 24, V = 1025, PH = 732, EOS = 1024, FFN = 2048;
+};
+
+// Check the whole tensor contract of tools/export_gguf/convert_ar.py (names, types, shapes) before
+// anything touches the device, so a bad file fails the same way with or without a GPU.
+int validate_gguf(const GgufFile & g, Hparams & hp) {
+    uint32_t v;
+    if (g.get_u32("ar.hidden_dim", v)) hp.D = (int) v;
+    if (g.get_u32("ar.head", v)) hp.NH = (int) v;
+    if (g.get_u32("ar.n_layer", v)) hp.NL = (int) v;
+    if (g.get_u32("ar.vocab_size", v)) hp.V = (int) v;
+    if (g.get_u32("ar.phoneme_vocab_size", v)) hp.PH = (int) v;
+    if (g.get_u32("ar.eos", v)) hp.EOS = (int) v;
+    if (hp.NH <= 0 || hp.D % hp.NH != 0 || hp.D != 512 || hp.D / hp.NH != 32) {
+        set_error("unsupported shape d_model=%d heads=%d (this build: 512 = 16 x 32)", hp.D, hp.NH);
+        return GSVK_ERR_FORMAT;
+    }
+    if (hp.V <= 0 || hp.V > 2048 || hp.EOS < 0 || hp.EOS >= hp.V || hp.NL <= 0 || hp.NL > 256 ||
+        hp.PH <= 0) {
+        set_error("bad hparams vocab=%d eos=%d layers=%d phones=%d", hp.V, hp.EOS, hp.NL, hp.PH);
+        return GSVK_ERR_FORMAT;
+    }
+    auto need = [&](const std::string & name, std::initializer_list<uint32_t> types,
+                    std::initializer_list<int64_t> ne) -> int {
+        const GgufTensor * t = g.tensor(name);
+        if (!t) { set_error("missing tensor %s", name.c_str()); return GSVK_ERR_FORMAT; }
+        bool ok = false;
+        for (uint32_t ty : types) ok |= t->type == ty;
+        if (!ok) { set_error("%s: unsupported type %u", name.c_str(), t->type); return GSVK_ERR_FORMAT; }
+        int64_t nel = 1, want = 1;
+        for (int64_t x : t->ne) nel *= x;
+        for (int64_t x : ne) want *= x;
+        if (nel != want || (ne.size() == 2 && (t->ne.size() < 2 || t->ne[0] != *ne.begin()))) {
+            set_error("%s: shape does not match the model", name.c_str());
+            return GSVK_ERR_FORMAT;
+        }
+        return GSVK_OK;
+    };
+    const GgufTensor * f1 = g.tensor("transformer.block0.ffn1_w");
+    if (f1 && f1->ne.size() == 2) hp.FFN = (int) f1->ne[1];
+    const int D = hp.D, F = hp.FFN;
+    if (F <= 0 || F % 128 != 0) { set_error("ffn size %d must be a multiple of 128", F); return GSVK_ERR_FORMAT; }
+    for (int li = 0; li < hp.NL; li++) {
+        const std::string p = "transformer.block" + std::to_string(li) + ".";
+        GSVK_TRY(need(p + "qkv_w", {GGML_Q8_0}, {D, 3 * D}));
+        GSVK_TRY(need(p + "out_w", {GGML_Q8_0}, {D, D}));
+        GSVK_TRY(need(p + "ffn1_w", {GGML_Q8_0}, {D, F}));
+        GSVK_TRY(need(p + "ffn2_w", {GGML_Q8_0}, {F, D}));
+        GSVK_TRY(need(p + "qkv_b", {GGML_F32}, {3 * D}));
+        GSVK_TRY(need(p + "out_b", {GGML_F32}, {D}));
+        GSVK_TRY(need(p + "ffn1_b", {GGML_F32}, {F}));
+        GSVK_TRY(need(p + "ffn2_b", {GGML_F32}, {D}));
+        for (const char * n : {"norm1_w", "norm1_b", "norm2_w", "norm2_b"}) GSVK_TRY(need(p + n, {GGML_F32}, {D}));
+    }
+    GSVK_TRY(need("ar.predict", {GGML_F32, GGML_F16, GGML_Q8_0}, {D, hp.V}));
+    // host-read tensors must be F32 (src/gsv_ar.cpp:632-637)
+    GSVK_TRY(need("ar.text_emb", {GGML_F32}, {D, hp.PH}));
+    GSVK_TRY(need("ar.audio_emb", {GGML_F32}, {D, hp.V}));
+    GSVK_TRY(need("ar.bert_proj", {GGML_F32}, {1024, D}));
+    GSVK_TRY(need("ar.bert_proj_b", {GGML_F32}, {D}));
+    GSVK_TRY(need("ar.text_pe_alpha", {GGML_F32}, {1}));
+    GSVK_TRY(need("ar.audio_pe_alpha", {GGML_F32}, {1}));
+    return GSVK_OK;
+}
+
+}  // namespace
+
 extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_model ** out) {
     GSVK_REQUIRE(path && out, "null argument");
     *out = nullptr;
+    GgufFile g;
+    std::string err;
+    bool io_error = false;
+    if (!g.open(path, err, &io_error)) {
+        set_error("%s", err.c_str());
+        return io_error ? GSVK_ERR_IO : GSVK_ERR_FORMAT;
+    }
+    Hparams hp;
+    GSVK_TRY(validate_gguf(g, hp));
     int ndev = 0;
     gsvk_device_count(&ndev);
     if (device < 0 || device >= ndev) {
@@ -581,25 +715,14 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
     m->verbose = verbose;
     GSVK_HIP(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     if (getenv("GSVK_NO_GRAPH")) m->use_graph = false;
-    GgufFile g;
-    std::string err;
-    if (!g.open(path, err)) { set_error("%s", err.c_str()); return GSVK_ERR_IO; }
-    uint32_t v;
-    if (g.get_u32("ar.hidden_dim", v)) m->D = (int) v;
-    if (g.get_u32("ar.head", v)) m->NH = (int) v;
-    if (g.get_u32("ar.n_layer", v)) m->NL = (int) v;
-    if (g.get_u32("ar.vocab_size", v)) m->V = (int) v;
-    if (g.get_u32("ar.phoneme_vocab_size", v)) m->PH = (int) v;
-    if (g.get_u32("ar.eos", v)) m->EOS = (int) v;
-    GSVK_REQUIRE(m->NH > 0 && m->D % m->NH == 0, "bad hparams");
+    m->D = hp.D;
+    m->NH = hp.NH;
+    m->NL = hp.NL;
+    m->V = hp.V;
+    m->PH = hp.PH;
+    m->EOS = hp.EOS;
+    m->FFN = hp.FFN;
     m->HD = m->D / m->NH;
-    if (m->HD != 32 || m->D != 512) {
-        set_error("unsupported shape d_model=%d head_dim=%d (this build: 512 / 32)", m->D, m->HD);
-        return GSVK_ERR_FORMAT;
-    }
-    GSVK_REQUIRE(m->V > 0 && m->V <= 2048 && m->EOS >= 0 && m->EOS < m->V && m->NL > 0 &&
-                     m->NL <= 256 && m->PH > 0,
-                 "bad hparams V=%d EOS=%d NL=%d", m->V, m->EOS, m->NL);
     // staging buffer for the largest Q8_0 tensor
     size_t staging_bytes = 0;
     for (const auto & t : g.tensors()) staging_bytes = std::max<size_t>(staging_bytes, t.nbytes);
@@ -815,7 +938,6 @@ extern "C" int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float 
     GSVK_TRY(upload(m->last_tok, last_tok, (size_t) B * 4, st));
     GSVK_TRY(upload(m->d_step, &step1, 4, st));
     GSVK_HIP(hipStreamSynchronize(st));   // the host values above live on this stack frame
-    GSVK_TRY(enqueue_step_prologue(m));
     GSVK_TRY(enqueue_decode_body(m));
     if (logits) GSVK_HIP(hipMemcpyAsync(logits, m->logits, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
     GSVK_HIP(hipStreamSynchronize(st));
@@ -915,7 +1037,6 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     sa.early_stop = early_stop_num;
     auto enqueue_step = [&]() -> int {
         GSVK_TRY(launch_sample(sa, st));
-        GSVK_TRY(enqueue_step_prologue(m));
         GSVK_TRY(enqueue_decode_body(m));
         return GSVK_OK;
     };

@@ -23,6 +23,7 @@ namespace gsvk {
 
 constexpr int SMP_THREADS = 256;
 constexpr int SMP_SORT = 2048;   // >= V
+constexpr int SMP_CH = 32;       // >= ceil(V / 64)
 
 __device__ __forceinline__ uint64_t gf2_apply(const uint64_t * __restrict__ cols, uint64_t s) {
     uint64_t r = 0;
@@ -62,16 +63,6 @@ __device__ void bitonic_sort_desc(float * v, int * idx) {
     __syncthreads();
 }
 
-__device__ __forceinline__ float block_max(float v, float * red) {
-    v = warp_max(v);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float m = red[0];
-    for (int w = 1; w < SMP_THREADS / 64; w++) m = fmaxf(m, red[w]);
-    __syncthreads();
-    return m;
-}
-
 __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -82,7 +73,6 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     __shared__ int cnt[SMP_SORT];
     __shared__ float sv[SMP_SORT];
     __shared__ int si[SMP_SORT];
-    __shared__ float red[SMP_THREADS / 64];
     __shared__ float s_scalar[2];
     __shared__ float s_bestv[1];
     __shared__ int s_besti[1];
@@ -137,55 +127,120 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
         const float temp = a.temperature > 1e-5f ? a.temperature : 1e-5f;
         for (int v = tid; v < V; v += SMP_THREADS) lg[v] = lg[v] / temp;
         __syncthreads();
-        // 4) top-k: pivot = k-th largest value (with multiplicity); values below are masked
-        if (a.top_k > 0 && a.top_k < V) {
+        // 4-6) wave 0 holds the row in registers: lane t owns indices [t*chunk, t*chunk + chunk)
+        // (the same ownership as the RNG chunks of step 6).
+        const bool use_k = a.top_k > 0 && a.top_k < V;
+        if (use_k && a.top_k > 64) {   // large k: pivot from a full stable sort (all threads)
             for (int v = tid; v < SMP_SORT; v += SMP_THREADS) {
                 sv[v] = v < V ? lg[v] : -INFINITY;
                 si[v] = v;
             }
             bitonic_sort_desc(sv, si);
-            const float pivot = sv[a.top_k - 1];
-            for (int v = tid; v < V; v += SMP_THREADS)
-                if (lg[v] < pivot) lg[v] = -INFINITY;
-            __syncthreads();
+            if (tid == 0) s_scalar[1] = sv[a.top_k - 1];
         }
-        // 5) softmax: max, exp, sum in index order in one lane
-        float m = -INFINITY;
-        for (int v = tid; v < V; v += SMP_THREADS) m = fmaxf(m, lg[v]);
-        m = block_max(m, red);
-        for (int v = tid; v < V; v += SMP_THREADS)
-            sv[v] = (lg[v] == -INFINITY) ? 0.0f : (float) exp((double) (lg[v] - m));
+        __syncthreads();
+        const int chunk = a.chunk;
+        const int base = (tid & 63) * chunk;
+        float pv[SMP_CH];
+        int total = 0;
+        if (tid < 64) {
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++) pv[c] = (c < chunk && base + c < V) ? lg[base + c] : -INFINITY;
+            // 4) top-k: pivot = k-th largest value counted with multiplicity; values below it are
+            // masked (ties with the pivot stay)
+            if (use_k) {
+                float pivot;
+                if (a.top_k <= 64) {
+                    float w[SMP_CH];
+#pragma unroll
+                    for (int c = 0; c < SMP_CH; c++) w[c] = pv[c];
+                    pivot = -INFINITY;
+                    for (int r = 0; r < a.top_k; r++) {
+                        float bv = -INFINITY;
+                        int bc = SMP_CH;
+#pragma unroll
+                        for (int c = 0; c < SMP_CH; c++)
+                            if (c < chunk && (w[c] > bv || bc == SMP_CH)) { bv = w[c]; bc = c; }
+                        const int mine = bc < SMP_CH ? base + bc : 0x7fffffff;
+                        float gv = bv;
+                        int gi = mine;
+#pragma unroll
+                        for (int o = 32; o > 0; o >>= 1) {
+                            const float ov = __shfl_xor(gv, o, 64);
+                            const int oi = __shfl_xor(gi, o, 64);
+                            if (ov > gv || (ov == gv && oi < gi)) { gv = ov; gi = oi; }
+                        }
+                        pivot = gv;
+#pragma unroll
+                        for (int c = 0; c < SMP_CH; c++)
+                            if (base + c == gi) w[c] = -INFINITY;   // remove one instance
+                    }
+                } else {
+                    pivot = s_scalar[1];
+                }
+#pragma unroll
+                for (int c = 0; c < SMP_CH; c++)
+                    if (pv[c] < pivot) pv[c] = -INFINITY;
+            }
+            // 5) softmax: max, exp; the sum runs in index order over the non-zero terms only
+            // (adding +0 leaves an fp32 sum unchanged), compacted into LDS in index order
+            float mx = -INFINITY;
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++) mx = fmaxf(mx, pv[c]);
+            mx = warp_max(mx);
+            int cnt = 0;
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++) {
+                pv[c] = (pv[c] == -INFINITY) ? 0.0f : (float) exp((double) (pv[c] - mx));
+                cnt += pv[c] > 0.0f;
+            }
+            int incl = cnt;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                const int t = __shfl_up(incl, o, 64);
+                if ((tid & 63) >= o) incl += t;
+            }
+            total = __shfl(incl, 63, 64);
+            int wpos = incl - cnt;
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++)
+                if (pv[c] > 0.0f) sv[wpos++] = pv[c];
+        }
         __syncthreads();
         if (tid == 0) {
             float sum = 0.0f;
-            for (int v = 0; v < V; v++) sum = sum + sv[v];
+            for (int i = 0; i < total; i++) sum = sum + sv[i];
             s_scalar[0] = 1.0f / sum;
         }
         __syncthreads();
-        const float inv = s_scalar[0];
-        for (int v = tid; v < V; v += SMP_THREADS) sv[v] = sv[v] * inv;
-        __syncthreads();
-        if (b == 0 && a.probs_dump)
-            for (int v = tid; v < V; v += SMP_THREADS) a.probs_dump[(int64_t) idx * V + v] = sv[v];
         // 6) sample: argmax over p > 0 of p / q, q_i = -log(1 - U_i)
         if (tid < 64) {
+            const float inv = s_scalar[0];
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++) pv[c] = pv[c] * inv;
+            if (b == 0 && a.probs_dump) {
+#pragma unroll
+                for (int c = 0; c < SMP_CH; c++)
+                    if (c < chunk && base + c < V) a.probs_dump[(int64_t) idx * V + base + c] = pv[c];
+            }
             const uint64_t s0 = a.rng[b];
-            uint64_t s = gf2_apply(a.jump + (int64_t) tid * 64, s0);
+            uint64_t st = gf2_apply(a.jump + (int64_t) tid * 64, s0);
             float best = -INFINITY;
             int bi = 0x7fffffff;
-            for (int c = 0; c < a.chunk; c++) {
-                const int i = tid * a.chunk + c;
-                if (i >= V) break;
-                const float p = sv[i];
-                float val = 0.0f;
-                if (p > 0.0f) {
-                    const uint64_t x = s * 0x2545F4914F6CDD1Dull;
-                    const float u = (float) ((double) (x >> 40) * (1.0 / 16777216.0));
-                    const float q = -(float) log((double) (1.0f - u));
-                    val = p / q;
+#pragma unroll
+            for (int c = 0; c < SMP_CH; c++) {
+                if (c < chunk && base + c < V) {
+                    const float p = pv[c];
+                    float val = 0.0f;
+                    if (p > 0.0f) {
+                        const uint64_t x = st * 0x2545F4914F6CDD1Dull;
+                        const float u = (float) ((double) (x >> 40) * (1.0 / 16777216.0));
+                        const float q = -(float) log((double) (1.0f - u));
+                        val = p / q;
+                    }
+                    if (val > best) { best = val; bi = base + c; }
+                    st = xs_step(st);
                 }
-                if (val > best) { best = val; bi = i; }
-                s = xs_step(s);
             }
             // first maximum wins: larger value, then smaller index
             for (int o = 32; o > 0; o >>= 1) {
@@ -249,7 +304,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
 }
 
 int launch_sample(const SampleArgs & a, hipStream_t stream) {
-    GSVK_REQUIRE(a.V > 0 && a.V <= SMP_SORT && a.B > 0 && a.chunk * 64 >= a.V,
+    GSVK_REQUIRE(a.V > 0 && a.V <= SMP_SORT && a.B > 0 && a.chunk * 64 >= a.V && a.chunk <= SMP_CH,
                  "sample: vocabulary %d exceeds %d", a.V, SMP_SORT);
     GSVK_REQUIRE(a.top_k < 0 || a.top_k <= SMP_SORT, "sample: bad top_k");
     hipLaunchKernelGGL(k_sample, dim3((unsigned) a.B), dim3(SMP_THREADS), 0, stream, a);

@@ -24,7 +24,7 @@ EXPORTS = [
     "gsvk_model_get_info", "gsvk_generate", "gsvk_first_logits", "gsvk_release_cache", "gsvk_kv_alloc",
     "gsvk_prefill", "gsvk_decode_step", "gsvk_kv_read", "gsvk_last_sampled", "gsvk_op_q8_dequant",
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
-    "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode",
+    "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
 ]
 
 
@@ -92,6 +92,7 @@ def lib():
         L.gsvk_op_q8_quantize.argtypes = [vp, i64, i64, vp, vp, vp]
         L.gsvk_op_q8_gemv.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
         L.gsvk_op_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, f32, vp, vp, vp, vp]
+        L.gsvk_op_ln_gemv.argtypes = [vp, vp, i64, vp, vp, vp, vp, i64, vp, i32, vp, vp, vp]
         L.gsvk_op_add_act.argtypes = [vp, vp, i64, i64, i32, vp, vp]
         L.gsvk_op_fdot.argtypes = [vp, i32, i64, i64, vp, i64, vp, i32, vp]
         L.gsvk_attn_workspace_bytes.argtypes = [i32, i32, i64]
@@ -152,6 +153,12 @@ def op_q8_quantize(x, xq, xd, stream=None):
 def op_q8_gemv(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
     check(lib().gsvk_op_q8_gemv(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y),
                                 _stream(stream)), "q8_gemv")
+
+
+def op_ln_gemv(wq, wd, n, res, r, ln_bias, wb, bias, act, y, ln_out=None, stream=None):
+    m = res.shape[0]
+    check(lib().gsvk_op_ln_gemv(_p(wq), _p(wd), n, _p(res), _p(r), _p(ln_bias), _p(wb), m, _p(bias), act,
+                                _p(y), _p(ln_out), _stream(stream)), "ln_gemv")
 
 
 def op_layernorm(x, r, bias, wb, eps, y, yq=None, yd=None, stream=None):

@@ -194,6 +194,13 @@ int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
                     const int8_t * xq, const float * xd, int64_t m, const float * bias, int act,
                     float * y, void * stream);
 
+/* y = W . Q8_0(LayerNorm((res + r) + ln_bias) * wb[0:512] + wb[512:1024]) (+ bias) then act:
+ * the decoder's fused kernel with its LayerNorm input stage (rows of 512; n % 32 == 0). The
+ * LayerNorm output is also stored to ln_out when given. r, ln_bias, bias may be NULL. */
+int gsvk_op_ln_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, const float * res,
+                    const float * r, const float * ln_bias, const float * wb, int64_t m,
+                    const float * bias, int act, float * y, float * ln_out, void * stream);
+
 /* Fused LayerNorm (PATCH ggml_compute_forward_layernorm_affine):
  * v = x + r + bias; y = (v - mean) / sqrt(var + eps) * wb[0:n] + wb[n:2n], sums in double.
  * r and bias may be NULL. If yq/yd are given, y is also quantised to Q8_0 (n % 32 == 0). */

@@ -114,6 +114,35 @@ def test_q8_gemv_bitexact(gpu, n, k, m):
     assert np.array_equal(y2.cpu().numpy(), ref2)
 
 
+@pytest.mark.parametrize("n", [1536, 2048])
+@pytest.mark.parametrize("m", [1, 16, 41])
+def test_ln_gemv_bitexact(gpu, n, m):
+    """The fused LayerNorm -> Q8_0 -> GEMV kernel equals LayerNorm, x86 quantisation and the
+    Q8_0 dot of the oracle, to the bit."""
+    import torch
+    rng = np.random.default_rng(n + m)
+    k = 512
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    res = rng.standard_normal((m, k)).astype(np.float32)
+    r = rng.standard_normal((m, k)).astype(np.float32) * 0.5
+    lb = rng.standard_normal(k).astype(np.float32) * 0.02
+    wb = np.concatenate([1 + 0.05 * rng.standard_normal(k), 0.05 * rng.standard_normal(k)]).astype(np.float32)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.02
+    wbk = sm.q8_quantize_ref(W).ravel()
+    wq = torch.zeros(n * k, dtype=torch.int8, device="cuda")
+    wd = torch.zeros(n * k // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(wbk, torch), n, k, wq, wd)
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    ln = torch.zeros((m, k), dtype=torch.float32, device="cuda")
+    gpu.op_ln_gemv(wq, wd, n, _dev(res, torch), _dev(r, torch), _dev(lb, torch), _dev(wb, torch),
+                   _dev(bias, torch), 1, y, ln_out=ln)
+    torch.cuda.synchronize()
+    ln_ref = O.layernorm(res, r, lb, wb)
+    assert np.array_equal(ln.cpu().numpy(), ln_ref)
+    ref = np.maximum(O.q8_matmul(wbk, n, k, ln_ref) + bias[None, :], 0.0).astype(np.float32)
+    assert np.array_equal(y.cpu().numpy(), ref)
+
+
 @pytest.mark.parametrize("rows,n", [(1, 512), (16, 512), (333, 512), (8, 1024)])
 def test_layernorm(gpu, rows, n):
     import torch
