@@ -12,7 +12,8 @@ struct LayerIn {
     // IN_Q8: rows already quantised (sliced quants [m][k], fp32 scales [m][k/32])
     const int8_t * xs;
     const float * xd;
-    // IN_LN: LayerNorm((res + r) + bias) * wb[0:512] + wb[512:1024]; r and bias may be null
+    // IN_LN: LayerNorm((res + r) + bias) * wb[0:512] + wb[512:1024]; r and bias may be null.
+    // All rows are 16-byte aligned.
     const float * res;
     const float * r;
     const float * bias;

@@ -22,19 +22,34 @@ namespace gsvk {
 constexpr int LG_THREADS = 256;
 constexpr int LG_ROWS = 32;   // output rows per workgroup
 
-// One row of width 512 held by one wave (8 values per lane): LayerNorm as in norm.hip.
+// read in place of an absent r or bias operand of the LayerNorm input stage
+__device__ __align__(16) const float g_zero_row[512] = {};
+
+// One row of width 512 held by one wave (8 values per lane): LayerNorm as in norm.hip. Every
+// operand is fetched with unconditional 16-byte loads issued before the first use (absent r or
+// bias read a zero row instead of branching), so the stage costs one memory latency.
 __device__ __forceinline__ void ln_row_wave(const float * __restrict__ res, const float * __restrict__ r,
                                             const float * __restrict__ bias,
                                             const float * __restrict__ wb, int lane, float (&o)[8]) {
     constexpr int n = 512;
+    const int base = lane * 8;
+    const float4 * x4 = reinterpret_cast<const float4 *>(res + base);
+    const float4 * r4 = reinterpret_cast<const float4 *>(r + base);
+    const float4 * b4 = reinterpret_cast<const float4 *>(bias + base);
+    const float4 * w4 = reinterpret_cast<const float4 *>(wb + base);
+    const float4 * c4 = reinterpret_cast<const float4 *>(wb + n + base);
+    const float4 xa = x4[0], xb = x4[1], ra = r4[0], rb = r4[1], ba = b4[0], bb = b4[1];
+    const float4 wa = w4[0], wbv = w4[1], ca = c4[0], cb = c4[1];
+    const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+    const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
+    const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
+    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wbv.x, wbv.y, wbv.z, wbv.w};
+    const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
     float v[8];
     double s = 0.0, s2 = 0.0;
-    const int base = lane * 8;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        float t = res[base + i];
-        if (r) t = t + r[base + i];
-        if (bias) t = t + bias[base + i];
+        const float t = (xv[i] + rv[i]) + bv[i];   // x + 0 and + 0 leave x unchanged
         v[i] = t;
         s += (double) t;
         s2 += (double) t * (double) t;
@@ -45,7 +60,7 @@ __device__ __forceinline__ void ln_row_wave(const float * __restrict__ res, cons
     const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
     const float inv = 1.0f / __builtin_sqrtf(var + 1e-5f);
 #pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf((v[i] - mean) * inv, wb[base + i], wb[n + base + i]);
+    for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf((v[i] - mean) * inv, wv[i], cv[i]);
 }
 
 template <int NB4, int MT>
@@ -101,16 +116,19 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
             const int mm = min(m0 + t, m - 1);
             float o[8];
             if (in.mode == IN_LN) {
-                ln_row_wave(in.res + (int64_t) mm * 512, in.r ? in.r + (int64_t) mm * 512 : nullptr,
-                            in.bias, in.wb, lane, o);
+                ln_row_wave(in.res + (int64_t) mm * 512, in.r ? in.r + (int64_t) mm * 512 : g_zero_row,
+                            in.bias ? in.bias : g_zero_row, in.wb, lane, o);
             } else {   // IN_EMB
                 int tk = in.tok[mm];
                 tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
                 const int pos = *in.pos_ptr + in.pos_add;
-                const float * er = in.emb + (int64_t) tk * 512 + lane * 8;
-                const float * pr = in.pe + (int64_t) pos * 512 + lane * 8;
+                const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * 512 + lane * 8);
+                const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) pos * 512 + lane * 8);
+                const float4 e0 = er[0], e1 = er[1], p0 = pr[0], p1 = pr[1];
+                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pr[i], er[i]);
+                for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pv[i], ev[i]);
             }
             if (blockIdx.x == 0 && m0 + t < m) {
                 if (in.out_x) {
@@ -206,6 +224,11 @@ int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t
     GSVK_REQUIRE(k == 512 || k == 2048, "layer_gemv: k must be 512 or 2048 (got %lld)", (long long) k);
     GSVK_REQUIRE(in.mode == IN_Q8 ? (in.xs && in.xd) : (k == 512), "layer_gemv: bad input mode");
     GSVK_REQUIRE(in.mode != IN_LN || (in.res && in.wb), "layer_gemv: LayerNorm input needs res and wb");
+    auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
+    GSVK_REQUIRE(in.mode != IN_LN || (al16(in.res) && al16(in.r) && al16(in.bias) && al16(in.wb)),
+                 "layer_gemv: LayerNorm operands must be 16-byte aligned");
+    GSVK_REQUIRE(in.mode != IN_EMB || (al16(in.emb) && al16(in.pe)),
+                 "layer_gemv: embedding tables must be 16-byte aligned");
     GSVK_REQUIRE(in.mode != IN_EMB || (in.emb && in.pe && in.tok && in.pos_ptr), "layer_gemv: bad embedding input");
     GSVK_REQUIRE(!out.yq || (out.yd && n % 32 == 0), "layer_gemv: bad quantised output");
     GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 &&
