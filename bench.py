@@ -138,6 +138,46 @@ def kernel_roofline(gsvk, torch, reqs, steps):
     return res
 
 
+def attn_microkernel(gsvk, torch, seed=0x6A5E0003, B=64, sets=8):
+    """Decode attention alone: batch 64 x 16 heads x 32, one query per sequence, KV lengths uniform
+    in [256, 2048] from the seed, fp16 K/V ~ N(0,1), fp16 output. Rotates over `sets` K/V buffer
+    sets (8 x 268 MB, > MALL) so that every launch reads HBM."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    L = rng.integers(256, 2049, B)
+    lstride = 2048
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    kc = torch.randn((sets, B, NH, lstride, HD), dtype=torch.float16, device="cuda", generator=g)
+    vc = torch.randn((sets, B, NH, lstride, HD), dtype=torch.float16, device="cuda", generator=g)
+    q = torch.randn((B, NH, HD), dtype=torch.float32, device="cuda", generator=g)
+    kv_begin = torch.zeros(B, dtype=torch.int32, device="cuda")
+    kv_end = torch.tensor(L, dtype=torch.int32, device="cuda")
+    out = torch.zeros((B, NH * HD), dtype=torch.float32, device="cuda")
+    out16 = torch.zeros((B, NH * HD), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(gsvk.attn_workspace_bytes(B, NH, lstride), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / np.sqrt(32.0)
+
+    def attn(i):
+        gsvk.op_attn_decode(q, kc[i % sets], vc[i % sets], kv_begin, kv_end, lstride, scale, out, out16=out16,
+                            ws=ws)
+    ms = time_events(attn, 160, torch)
+    b = int(L.sum()) * NH * 2 * HD * 2
+    del kc, vc
+    return {"us": round(ms * 1e3, 2), "bytes": b, "GBs": round(b / ms / 1e6, 1),
+            "frac": round(b / ms / 1e6 / HBM_PEAK_GBS, 4), "batch": B, "kv_len": "U[256,2048]"}
+
+
+def copy_probe(torch, nbytes=256 << 20):
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE counters give the factor
+    that turns those counters into bytes for the decode kernels."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return nbytes
+
+
 def cpu_baseline(reqs, steps):
     import oracle
     import synth_model as sm
@@ -164,6 +204,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this decoder runs each batch on a single MI355X and has no "
@@ -176,6 +218,14 @@ def main():
     import synth_model as sm
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
+    if args.kernels_only:
+        kr = kernel_roofline(gsvk, torch, workload_requests(args.batch), args.steps)
+        res = {k: {"us": round(v["ms"] * 1e3, 3), "bytes": v["bytes"], "GBs": round(v["gbs"], 1)}
+               for k, v in kr.items()}
+        res["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
+        res["copy_probe_bytes"] = copy_probe(torch)
+        print(json.dumps({"kernels_only": res}))
+        return
     path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
     g = gsvk.Model(path, device=0)
     cfg = (15, 1.0, 1.0, 1.35)
@@ -214,6 +264,7 @@ def main():
         kr = kernel_roofline(gsvk, torch, reqs, args.steps)
         extra["kernels"] = {k: {"us": round(v["ms"] * 1e3, 2), "GBs": round(v["gbs"], 1),
                                 "frac": round(v["gbs"] / HBM_PEAK_GBS, 4)} for k, v in kr.items()}
+        extra["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         dom = max(kr, key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
         d = kr[dom]
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,

@@ -1,13 +1,15 @@
 // Single-query (decode) attention over a per-sequence fp16 KV cache, for gfx950.
 //
-// Work decomposition: workgroup (split, head, seq) of 4 waves. The valid keys [begin, end) of a
-// (seq, head) are cut in blocks of 64; split s owns a contiguous run of blocks (nsplit is 1
-// unless batch x heads is small and the rows long, see attn_nsplit). Wave w of a workgroup takes blocks w, w+4, ... of its run.
+// Work decomposition: workgroup (split, head, seq) of NW waves (4, 8 or 16, see attn_waves: a
+// long row is spread over up to 16 waves so that its blocks are in flight together instead of
+// one after another). The valid keys [begin, end) of a (seq, head) are cut in blocks of 64;
+// split s owns a contiguous run of blocks (nsplit is 1 unless batch x heads is small and the rows
+// long, see attn_nsplit). Wave w of a workgroup takes blocks w, w+NW, ... of its run.
 // Inside a block, lane = (key slot ks = lane/4, quarter qd = lane%4) reads the 16-byte quarter
 // [8qd, 8qd+8) of 4 K rows and 4 V rows (all 8 loads issued before any use, and the next block's
 // loads issued before this block's arithmetic); one wave-wide load covers 1 KiB of contiguous
 // cache. Each wave keeps an online softmax (running max per block, exp2 of log2e-scaled scores);
-// the 4 waves merge through LDS, and the splits of one (seq, head), if more than one, are merged
+// the NW waves merge through LDS, and the splits of one (seq, head), if more than one, are merged
 // by the last workgroup to finish (device-scope counter), so one launch does the whole op.
 //
 // Numerics: softmax(q.k * scale) . V over the valid keys with fp32 accumulation; the output is
@@ -81,7 +83,8 @@ __device__ __forceinline__ void load_block(const uint16_t * __restrict__ kb,
     }
 }
 
-__global__ void __launch_bounds__(256) k_attn_decode(
+template <int NW>
+__global__ void __launch_bounds__(NW * 64) k_attn_decode(
     const float * __restrict__ q, int64_t q_stride, const uint16_t * __restrict__ kc,
     const uint16_t * __restrict__ vc, int nh, int64_t lstride, const int32_t * __restrict__ kv_begin,
     const int32_t * __restrict__ kv_end, int nsplit, float scale_log2, float * __restrict__ out,
@@ -108,9 +111,9 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     const int qd = lane & 3;
     const int64_t bh = (int64_t) b * nh + h;
 
-    __shared__ float s_m[4];
-    __shared__ float s_l[4];
-    __shared__ float s_o[4][ATT_HD];
+    __shared__ float s_m[NW];
+    __shared__ float s_l[NW];
+    __shared__ float s_o[NW][ATT_HD];
 
     if (nkeys == 0) {   // no valid key: ggml returns 0 (S == 0 -> S_inv = 0)
         if (wave == 0) attn_store_out(0.0f, lane, bh, nh, out, out16, oq, od);
@@ -139,7 +142,7 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     KV8 cur;
     if (blk < blk1) load_block(kb, vb, beg + blk * ATT_BLK, end, ks, cur);
     while (blk < blk1) {
-        const int nxt = blk + 4;
+        const int nxt = blk + NW;
         KV8 pre;
         if (nxt < blk1) load_block(kb, vb, beg + nxt * ATT_BLK, end, ks, pre);
         const int key0 = beg + blk * ATT_BLK;
@@ -196,11 +199,13 @@ __global__ void __launch_bounds__(256) k_attn_decode(
     __syncthreads();
     if (wave != 0) return;
 
-    // merge the 4 waves (a wave without blocks has m = -inf and weight 0)
-    const float M = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
+    // merge the NW waves (a wave without blocks has m = -inf and weight 0)
+    float M = s_m[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) M = fmaxf(M, s_m[w]);
     float L = 0.0f, O = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
+    for (int w = 0; w < NW; w++) {
         const float f = s_m[w] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w] - M);
         L = __builtin_fmaf(s_l[w], f, L);
         if (lane < ATT_HD) O = __builtin_fmaf(s_o[w][lane], f, O);
@@ -249,17 +254,28 @@ __global__ void __launch_bounds__(256) k_attn_decode(
         __hip_atomic_store(counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Waves per workgroup: enough to take every block of the longest row at once (4..16), halved
+// while the grid would hold more than 8192 waves (32 per CU, the resident limit of 256 CUs).
+int attn_waves(int B, int nh, int64_t max_keys) {
+    const int64_t pairs = (int64_t) B * nh;
+    const int64_t blocks = (max_keys + ATT_BLK - 1) / ATT_BLK;
+    int nw = 4;
+    while (nw < 16 && nw < blocks) nw *= 2;
+    while (nw > 4 && pairs * nw > 8192) nw /= 2;
+    return nw;
+}
+
 // Splits per (seq, head). Merging splits needs an agent-scope release per workgroup, which on
 // gfx950 writes back the L2 of the workgroup's XCD; that costs more than it saves unless the
 // launch would otherwise leave most of the chip idle on long rows. So: one workgroup per
 // (seq, head) when there are >= 64 of them or the rows are short, else enough splits of at least
-// 8 blocks (512 keys) to reach ~256 workgroups, at most 64 (the merge reads one split per lane).
+// 16 blocks (1024 keys) to reach ~256 workgroups, at most 64 (the merge reads one split per lane).
 int attn_nsplit(int B, int nh, int64_t max_keys) {
     const int64_t pairs = (int64_t) B * nh;
     const int64_t blocks = (max_keys + ATT_BLK - 1) / ATT_BLK;
-    if (pairs >= 64 || blocks < 16) return 1;
+    if (pairs >= 64 || blocks < 32) return 1;
     int64_t ns = (256 + pairs - 1) / pairs;
-    if (ns > blocks / 8) ns = blocks / 8;
+    if (ns > blocks / 16) ns = blocks / 16;
     if (ns > 64) ns = 64;
     if (ns < 1) ns = 1;
     return (int) ns;
@@ -290,9 +306,16 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
     const size_t part_bytes = (size_t) B * nh * ns * ATT_PART * sizeof(float);
     float * part = (float *) ws;
     int32_t * counters = (int32_t *) ((char *) ws + ((part_bytes + 255) / 256) * 256);
-    hipLaunchKernelGGL(k_attn_decode, dim3((unsigned) ns, (unsigned) nh, (unsigned) B), dim3(256),
-                       0, stream, q, q_stride, k, v, nh, lstride, kv_begin, kv_end, ns,
-                       scale * LOG2E, out, out16, oq, od, part, counters);
+    const dim3 grid((unsigned) ns, (unsigned) nh, (unsigned) B);
+    const int nw = attn_waves(B, nh, max_keys);
+#define GSVK_ATTN_LAUNCH(W)                                                                      \
+    hipLaunchKernelGGL(k_attn_decode<W>, grid, dim3(W * 64), 0, stream, q, q_stride, k, v, nh,    \
+                       lstride, kv_begin, kv_end, ns, scale * LOG2E, out, out16, oq, od, part,   \
+                       counters)
+    if (nw == 16) GSVK_ATTN_LAUNCH(16);
+    else if (nw == 8) GSVK_ATTN_LAUNCH(8);
+    else GSVK_ATTN_LAUNCH(4);
+#undef GSVK_ATTN_LAUNCH
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -283,6 +283,30 @@ def test_attn_decode_parity(gpu):
     assert np.array_equal(unslice(qd[0], nh * 32), q_ref)
 
 
+@pytest.mark.parametrize("B,nh,lstride,what", [
+    (8, 16, 200, "4 waves per workgroup (rows of at most 4 blocks)"),
+    (4, 16, 400, "8 waves per workgroup"),
+    (80, 16, 1000, "4 waves per workgroup (1280 (seq, head) pairs cap the grid)"),
+    (40, 16, 1000, "8 waves per workgroup (640 pairs)"),
+    (2, 4, 4096, "16 waves per workgroup, 4 splits merged by the last workgroup"),
+    (1, 16, 3000, "16 waves per workgroup, 2 splits"),
+])
+def test_attn_decode_launch_shapes(gpu, B, nh, lstride, what):
+    import torch
+    rng = np.random.default_rng(33 + B)
+    begins = rng.integers(0, lstride // 4, B)
+    ends = np.minimum(lstride, begins + rng.integers(1, lstride, B))
+    ends[-1] = lstride                    # one row reaches the end of the buffer
+    if B > 2:
+        ends[0] = begins[0]               # and one is empty
+    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, begins, ends)
+    got, scale, _ = _run_attn(gpu, torch, q, k, v, kb, ke, lstride)
+    ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-5, what
+    if B > 2:
+        assert np.all(got[0] == 0.0)
+
+
 def test_attn_decode_empty_and_constant(gpu):
     import torch
     rng = np.random.default_rng(31)
