@@ -178,6 +178,21 @@ def copy_probe(torch, nbytes=256 << 20):
     return nbytes
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` at the workload shape, from the committed counter summary
+    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --kernels-only`, each scaled
+    by what the counter reads for a 256 MiB copy), or None when no summary holds it."""
+    path = os.path.join(ROOT, "profiles", "attn_decode_gemv_b16_kernels_hbm.md")
+    key = {"attn_decode": "attn_decode_b16"}.get(kernel)
+    if key is None or not os.path.exists(path):
+        return None
+    for line in open(path):
+        f = line.split()
+        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == key:
+            return int(f[2])
+    return None
+
+
 def cpu_baseline(reqs, steps):
     import oracle
     import synth_model as sm
@@ -203,7 +218,7 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=500)
     ap.add_argument("--kernels-only", action="store_true",
                     help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
@@ -268,7 +283,7 @@ def main():
         dom = max(kr, key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
         d = kr[dom]
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
                 "bytes_per_launch": int(d["bytes"]), "us_per_launch": round(d["ms"] * 1e3, 3)}
     cpu = None
     if not args.no_cpu:

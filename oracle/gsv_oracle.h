@@ -16,6 +16,28 @@
  * Floating-point convention: the reference's Linux build is GCC -O3 -mavx2 -mfma in GNU mode,
  * which contracts a*b + c into one FMA; this file is compiled with -ffp-contract=off and writes
  * those FMAs explicitly (fmaf) where the reference source has an a*b + c expression.
+ *
+ * What pins each function (tests/test_oracle_pins.py), i.e. what checks it against something
+ * other than its own formula:
+ *   orc_q8_quantize_ref, orc_q8_dequant   known-answer blocks (zero block, +-127 extremes,
+ *                                         negative zero); closed form of the 34-byte block
+ *   orc_q8_quantize_x86                   known answers incl. exact ties (half to even), fp16 d
+ *   orc_q8_dot, orc_q8_matmul             exact integer block sums, fp64 within 1e-6, and the
+ *                                         lane-by-lane scalar restatement
+ *   orc_f16_matmul, orc_f32_matmul        fp64 within the bound of fp32 summation
+ *   orc_layernorm                         closed forms (constant row -> b, arithmetic ramp)
+ *   orc_add_act                           the reference's fixture (tests/test_add_act.cpp:66-98)
+ *   orc_attn_row, orc_attn_decode_f16     fp64 brute force; one key -> that V row; constant V
+ *   orc_logits_to_probs, orc_rng_*,       golden vectors written by the reference's own
+ *   orc_sample, orc_argmax_probs_over_q   src/gsv_sampler.cpp compiled from source
+ *   orc_pe_table                          fp64 closed form
+ *   orc_generate, orc_prefill_kv,         left-padding invariance, text/semantic mask
+ *   orc_first_logits                      properties, EOS / early-stop / oracle-token traces
+ * Parity unpinned: the ORDER of ggml-cpu's floating-point arithmetic (the x86 activation
+ * rounding mode, the 8-lane Q8_0 and F16 dot orders, flash_attn_ext's online-softmax order and
+ * expf) lives in llama.cpp f0c41e01, which is not under the reference tree, and no reference
+ * test or fixture holds its outputs. The values above are pinned to fp64; the exact rounding
+ * sequence follows the published ggml-cpu source as restated here and is unpinned.
  */
 #ifndef GSV_ORACLE_H
 #define GSV_ORACLE_H
