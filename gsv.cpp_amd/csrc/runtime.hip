@@ -835,7 +835,7 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
     // xorshift64* jump tables for this vocabulary
     {
         m->rng_chunk = (m->V + 63) / 64;
-        std::vector<uint64_t> jump(64 * 64), adv(64);
+        std::vector<uint64_t> jump(RNG_JUMP_WORDS), adv(RNG_ADV_WORDS);
         rng_tables(m->V, m->rng_chunk, jump.data(), adv.data());
         GSVK_TRY(m->wmem.alloc(m->rng_jump, jump.size()));
         GSVK_TRY(m->wmem.alloc(m->rng_adv, adv.size()));
@@ -1030,6 +1030,8 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     sa.flags = (flags & GSVK_GEN_EOS_MASK_ALL) ? 1u : 0u;
     sa.last_tok = m->last_tok;
     sa.probs_dump = (flags & GSVK_GEN_PROB_DUMP) ? m->probs_dump : nullptr;
+    sa.probs_per_row = 0;
+    sa.tok_out = nullptr;
     sa.sampled_dump = m->sampled;
     sa.max_steps = max_steps;
     sa.done_counter = m->done_counter;

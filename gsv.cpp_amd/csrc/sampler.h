@@ -10,21 +10,24 @@ struct SampleArgs {
     int V, eos, B, P;
     int32_t * hist;            // [B][hist_stride] prompt + generated tokens
     int hist_stride;
-    int32_t * ny;              // [B] tokens in hist
-    int32_t * fin_step;        // [B] -1 while running
+    int32_t * ny;              // [B] tokens in hist (null = no history)
+    int32_t * fin_step;        // [B] -1 while running (null with step == null)
     int32_t * fin_kind;        // [B] 0 EOS, 1 early stop
     uint64_t * rng;            // [B] xorshift64* state
-    const uint64_t * jump;     // [64][64] columns of A^(chunk*t + 1)
-    const uint64_t * adv;      // [64] columns of A^V
+    const uint64_t * jump;     // [8][256][64] byte tables of A^(chunk*t + 1), see rng_tables
+    const uint64_t * adv;      // [8][256] byte tables of A^V
     int chunk;                 // draws per lane of wave 0
     int top_k;
     float top_p, temperature, rep;
     const int32_t * oracle;    // teacher forcing tokens or null
     int n_oracle;
-    int32_t * step;            // device loop index
+    int32_t * step;            // device loop index; null = one sampling call without loop
+                               // state (no EOS mask, no history append, no bookkeeping)
     unsigned flags;            // bit0: mask EOS at every step
     int32_t * last_tok;        // [B]
-    float * probs_dump;        // [max_steps][V] for sequence 0, or null
+    float * probs_dump;        // [max_steps][V] for sequence 0 (probs_per_row: [B][V]), or null
+    int probs_per_row;
+    int32_t * tok_out;         // [B] sampled token (before any oracle override), or null
     int32_t * sampled_dump;    // [max_steps][B] sampler choice before the oracle, or null
     int max_steps;
     int32_t * done_counter;    // zero between calls
@@ -34,8 +37,12 @@ struct SampleArgs {
 
 int launch_sample(const SampleArgs & a, hipStream_t stream);
 
-// jump: [64][64] columns of A^(chunk*t + 1) for t < 64; adv: [64] columns of A^V, where A is
-// the GF(2) matrix of one xorshift64* state update.
+// A is the GF(2) matrix of one xorshift64* state update. jump (RNG_JUMP_WORDS): entry
+// [p][v][t] = A^(chunk*t + 1) applied to the state whose only non-zero byte is v at byte p, so
+// that A^(chunk*t + 1) s = XOR over p of jump[p][byte p of s][t]; adv (RNG_ADV_WORDS): [p][v],
+// the same for A^V.
+constexpr int RNG_JUMP_WORDS = 8 * 256 * 64;
+constexpr int RNG_ADV_WORDS = 8 * 256;
 void rng_tables(int V, int chunk, uint64_t * jump, uint64_t * adv);
 
 }  // namespace gsvk

@@ -10,9 +10,12 @@
 //
 // The sequential parts (the softmax sum, the top-p cumulative sum) run in one lane in index
 // order, as in the reference, so the sums round identically. The RNG stream is jumped ahead:
-// xorshift64* is linear over GF(2), so the state after n steps is A^n s; lane t of wave 0 starts
-// at draw chunk*t from a precomputed matrix and steps sequentially through its chunk.
+// xorshift64* is linear over GF(2), so the state after n steps is A^n s. Lane t of wave 0 starts
+// at draw chunk*t: M s for the precomputed M = A^(chunk*t + 1) is the XOR over the 8 bytes of s
+// of a table entry (M applied to that byte), 8 loads; it then steps sequentially through its
+// chunk. The next step's state A^V s comes from the same kind of table.
 #include <array>
+#include <vector>
 
 #include "common.h"
 #include "sampler.h"
@@ -25,11 +28,35 @@ constexpr int SMP_THREADS = 256;
 constexpr int SMP_SORT = 2048;   // >= V
 constexpr int SMP_CH = 32;       // >= ceil(V / 64)
 
-__device__ __forceinline__ uint64_t gf2_apply(const uint64_t * __restrict__ cols, uint64_t s) {
-    uint64_t r = 0;
-#pragma unroll 8
-    for (int i = 0; i < 64; i++) r ^= cols[i] & (0ull - ((s >> i) & 1ull));
-    return r;
+// Largest of a uint32 over the 64 lanes (DPP rotations within rows, then the row results).
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x128, 0xf, 0xf, false));
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x124, 0xf, 0xf, false));
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x122, 0xf, 0xf, false));
+    v = max(v, (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, 0x121, 0xf, 0xf, false));
+    const uint32_t a = max((uint32_t) __builtin_amdgcn_readlane((int) v, 0), (uint32_t) __builtin_amdgcn_readlane((int) v, 16));
+    const uint32_t b = max((uint32_t) __builtin_amdgcn_readlane((int) v, 32), (uint32_t) __builtin_amdgcn_readlane((int) v, 48));
+    return max(a, b);
+}
+
+// The k-th largest (1 <= k <= 64, counted with multiplicity) of one uint32 per lane: the largest
+// v with #{lanes u : u >= v} >= k.
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
+    int ge = 0;
+#pragma unroll
+    for (int j = 0; j < 64; j++) ge += (uint32_t) __builtin_amdgcn_readlane((int) v, j) >= v;
+    return wave_max_u32(ge >= k ? v : 0u);
+}
+
+// Sum of an int over the 64 lanes, returned to every lane: rotations within each row of 16
+// lanes (DPP row_ror 8, 4, 2, 1), then the four row totals read as scalars.
+__device__ __forceinline__ int wave_sum_i32(int v) {
+    v += __builtin_amdgcn_update_dpp(0, v, 0x128, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x124, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x122, 0xf, 0xf, false);
+    v += __builtin_amdgcn_update_dpp(0, v, 0x121, 0xf, 0xf, false);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) +
+           __builtin_amdgcn_readlane(v, 32) + __builtin_amdgcn_readlane(v, 48);
 }
 
 __device__ __forceinline__ uint64_t xs_step(uint64_t s) {
@@ -37,6 +64,15 @@ __device__ __forceinline__ uint64_t xs_step(uint64_t s) {
     s ^= s << 25;
     s ^= s >> 27;
     return s;
+}
+
+// order-preserving map of a float to uint32 (larger float -> larger key) and back
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
 // a precedes b in a stable descending sort
@@ -67,31 +103,58 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int V = a.V;
-    const int idx = *a.step;
 
     __shared__ float lg[SMP_SORT];
     __shared__ int cnt[SMP_SORT];
-    __shared__ float sv[SMP_SORT];
+    __shared__ __align__(16) float sv[SMP_SORT];
     __shared__ int si[SMP_SORT];
+    __shared__ float su[SMP_SORT];
     __shared__ float s_scalar[2];
     __shared__ float s_bestv[1];
     __shared__ int s_besti[1];
 
-    const bool running = a.fin_step[b] < 0 && idx < a.max_steps;
-    if (running) {
-        for (int v = tid; v < V; v += SMP_THREADS) {
-            lg[v] = a.logits[(int64_t) b * V + v];
-            cnt[v] = 0;
+    // every load that does not depend on another is issued here, before the first use: the
+    // loop index, this row's state, its logits, the jump matrices and the advance columns
+    const int idx = a.step ? *a.step : 11;   // no loop state: past the EOS-mask window
+    const int fin = a.fin_step ? a.fin_step[b] : -1;
+    const int n_hist = a.ny ? a.ny[b] : 0;
+    const uint64_t s0 = a.rng[b];
+    uint64_t st0 = 0, s_next = 0;   // wave 0: this lane's first draw state; A^V s0
+    if (tid < 64) {
+#pragma unroll
+        for (int p = 0; p < 8; p++) {
+            const int byte = (int) ((s0 >> (8 * p)) & 255u);
+            st0 ^= a.jump[((int64_t) (p * 256 + byte)) * 64 + tid];
+            s_next ^= a.adv[p * 256 + byte];
         }
-        __syncthreads();
-        if (tid == 0 && (idx < 11 || (a.flags & 1u))) lg[a.eos] = -INFINITY;
+    }
+    // the repetition-penalty window: the last <= 4096 tokens, at most 16 per thread
+    constexpr int HW = 4096 / SMP_THREADS;
+    const int np = a.rep != 1.0f ? (n_hist < 4096 ? n_hist : 4096) : 0;
+    int htok[HW];
+    {
+        const int32_t * h = a.hist + (int64_t) b * a.hist_stride + (n_hist - np);
+#pragma unroll
+        for (int r = 0; r < HW; r++) {
+            const int i = tid + r * SMP_THREADS;
+            htok[r] = i < np ? h[i] : -1;
+        }
+    }
+    for (int v = tid; v < V; v += SMP_THREADS) {
+        lg[v] = a.logits[(int64_t) b * V + v];
+        cnt[v] = 0;
+    }
+    asm volatile("" ::"v"(st0), "v"(s_next));   // the table loads complete here, not at first use
+    __syncthreads();
+
+    const bool running = fin < 0 && idx < a.max_steps;
+    if (running) {
+        if (tid == 0 && a.step && (idx < 11 || (a.flags & 1u))) lg[a.eos] = -INFINITY;
         // 1) repetition penalty, once per occurrence in the window
-        if (a.rep != 1.0f) {
-            const int n = a.ny[b];
-            const int np = n < 4096 ? n : 4096;
-            const int32_t * h = a.hist + (int64_t) b * a.hist_stride + (n - np);
-            for (int i = tid; i < np; i += SMP_THREADS) {
-                const int t = h[i];
+        if (np > 0) {
+#pragma unroll
+            for (int r = 0; r < HW; r++) {
+                const int t = htok[r];
                 if (t >= 0 && t < V) atomicAdd(&cnt[t], 1);
             }
             __syncthreads();
@@ -127,120 +190,149 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
         const float temp = a.temperature > 1e-5f ? a.temperature : 1e-5f;
         for (int v = tid; v < V; v += SMP_THREADS) lg[v] = lg[v] / temp;
         __syncthreads();
-        // 4-6) wave 0 holds the row in registers: lane t owns indices [t*chunk, t*chunk + chunk)
-        // (the same ownership as the RNG chunks of step 6).
-        const bool use_k = a.top_k > 0 && a.top_k < V;
-        if (use_k && a.top_k > 64) {   // large k: pivot from a full stable sort (all threads)
-            for (int v = tid; v < SMP_SORT; v += SMP_THREADS) {
-                sv[v] = v < V ? lg[v] : -INFINITY;
-                si[v] = v;
-            }
-            bitonic_sort_desc(sv, si);
-            if (tid == 0) s_scalar[1] = sv[a.top_k - 1];
-        }
-        __syncthreads();
-        const int chunk = a.chunk;
-        const int base = (tid & 63) * chunk;
-        float pv[SMP_CH];
-        int total = 0;
+        // 4-6) wave 0: lane t owns indices [t*chunk, t*chunk + chunk), the same ownership as the
+        // RNG chunks, so index order is (lane, slot) order
         if (tid < 64) {
+            const int chunk = a.chunk;
+            const int lane = tid;
+            const int base = lane * chunk;
+            float pv[SMP_CH];
+            uint32_t key[SMP_CH];
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++) pv[c] = (c < chunk && base + c < V) ? lg[base + c] : -INFINITY;
-            // 4) top-k: pivot = k-th largest value counted with multiplicity; values below it are
-            // masked (ties with the pivot stay)
-            if (use_k) {
-                float pivot;
-                if (a.top_k <= 64) {
-                    float w[SMP_CH];
+            for (int c = 0; c < SMP_CH; c++) {
+                const bool ok = c < chunk && base + c < V;
+                pv[c] = ok ? lg[base + c] : -INFINITY;
+                key[c] = ok ? order_key(pv[c]) : 0u;   // below every value, -inf included
+            }
+            // 4) top-k: pivot = the top_k-th largest value counted with multiplicity (what
+            // nth_element leaves at position k-1), found exactly by a radix select over the
+            // order-preserving key, most significant bit first; values below it are masked,
+            // ties with it stay
+            if (a.top_k > 0 && a.top_k < V) {
+                const int k = a.top_k;
+                bool found = false;
+                uint32_t prefix = 0u;
+                if (k <= 64) {
+                    // T = k-th largest of the 64 lane maxima: at least k values are >= T, so the
+                    // pivot is >= T and the k largest values all lie in {key >= T}. When that set
+                    // fits in one wave, its k-th largest (one sort) is the pivot.
+                    uint32_t lmax = 0u;
 #pragma unroll
-                    for (int c = 0; c < SMP_CH; c++) w[c] = pv[c];
-                    pivot = -INFINITY;
-                    for (int r = 0; r < a.top_k; r++) {
-                        float bv = -INFINITY;
-                        int bc = SMP_CH;
+                    for (int c = 0; c < SMP_CH; c++) lmax = key[c] > lmax ? key[c] : lmax;
+                    const uint32_t T = wave_kth_largest(lmax, k);
+                    int cmine = 0, cbelow = 0, ctotal = 0;
+                    int cpos[SMP_CH];
 #pragma unroll
-                        for (int c = 0; c < SMP_CH; c++)
-                            if (c < chunk && (w[c] > bv || bc == SMP_CH)) { bv = w[c]; bc = c; }
-                        const int mine = bc < SMP_CH ? base + bc : 0x7fffffff;
-                        float gv = bv;
-                        int gi = mine;
-#pragma unroll
-                        for (int o = 32; o > 0; o >>= 1) {
-                            const float ov = __shfl_xor(gv, o, 64);
-                            const int oi = __shfl_xor(gi, o, 64);
-                            if (ov > gv || (ov == gv && oi < gi)) { gv = ov; gi = oi; }
-                        }
-                        pivot = gv;
-#pragma unroll
-                        for (int c = 0; c < SMP_CH; c++)
-                            if (base + c == gi) w[c] = -INFINITY;   // remove one instance
+                    for (int c = 0; c < SMP_CH; c++) {
+                        const bool in = key[c] >= T && key[c] != 0u;
+                        const uint64_t m = __ballot(in);
+                        cbelow += __popcll(m & ((1ull << lane) - 1ull));
+                        ctotal += __popcll(m);
+                        cpos[c] = in ? cmine : -1;
+                        cmine += in;
                     }
-                } else {
-                    pivot = s_scalar[1];
+                    if (ctotal <= 64) {
+                        uint32_t * cand = reinterpret_cast<uint32_t *>(si);
+                        cand[lane] = 0u;
+                        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                        for (int c = 0; c < SMP_CH; c++)
+                            if (cpos[c] >= 0) cand[cbelow + cpos[c]] = key[c];
+                        __builtin_amdgcn_wave_barrier();
+                        prefix = wave_kth_largest(cand[lane], k);
+                        found = true;
+                    }
                 }
+                int rem = k;
+                for (int bit = 31; bit >= 0 && !found; bit--) {
+                    const uint32_t sel = (bit == 31 ? 0u : (0xffffffffu << (bit + 1))) | (1u << bit);
+                    const uint32_t want = prefix | (1u << bit);
+                    int c1 = 0;
+#pragma unroll
+                    for (int c = 0; c < SMP_CH; c++) c1 += (key[c] & sel) == want;
+                    c1 = wave_sum_i32(c1);
+                    if (c1 >= rem) prefix = want;
+                    else rem -= c1;
+                }
+                const float pivot = key_value(prefix);
 #pragma unroll
                 for (int c = 0; c < SMP_CH; c++)
                     if (pv[c] < pivot) pv[c] = -INFINITY;
             }
-            // 5) softmax: max, exp; the sum runs in index order over the non-zero terms only
-            // (adding +0 leaves an fp32 sum unchanged), compacted into LDS in index order
+            // 5) softmax over the survivors. They are compacted into LDS in index order (position
+            // = survivors in lower lanes + survivors in lower slots of this lane), so exp runs
+            // once per survivor and the sum runs in index order over the non-zero terms only
+            // (adding +0 leaves an fp32 sum unchanged).
             float mx = -INFINITY;
 #pragma unroll
             for (int c = 0; c < SMP_CH; c++) mx = fmaxf(mx, pv[c]);
             mx = warp_max(mx);
-            int cnt = 0;
+            const uint64_t lt_mask = (1ull << lane) - 1ull;
+            int below = 0, total = 0, mine = 0;
+            int pos[SMP_CH];
 #pragma unroll
             for (int c = 0; c < SMP_CH; c++) {
-                pv[c] = (pv[c] == -INFINITY) ? 0.0f : (float) exp((double) (pv[c] - mx));
-                cnt += pv[c] > 0.0f;
+                const bool sv_c = pv[c] != -INFINITY;
+                const uint64_t m = __ballot(sv_c);
+                below += __popcll(m & lt_mask);
+                total += __popcll(m);
+                pos[c] = sv_c ? mine : -1;
+                mine += sv_c;
             }
-            int incl = cnt;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int t = __shfl_up(incl, o, 64);
-                if ((tid & 63) >= o) incl += t;
-            }
-            total = __shfl(incl, 63, 64);
-            int wpos = incl - cnt;
 #pragma unroll
             for (int c = 0; c < SMP_CH; c++)
-                if (pv[c] > 0.0f) sv[wpos++] = pv[c];
-        }
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int i = 0; i < total; i++) sum = sum + sv[i];
-            s_scalar[0] = 1.0f / sum;
-        }
-        __syncthreads();
-        // 6) sample: argmax over p > 0 of p / q, q_i = -log(1 - U_i)
-        if (tid < 64) {
-            const float inv = s_scalar[0];
-#pragma unroll
-            for (int c = 0; c < SMP_CH; c++) pv[c] = pv[c] * inv;
-            if (b == 0 && a.probs_dump) {
-#pragma unroll
-                for (int c = 0; c < SMP_CH; c++)
-                    if (c < chunk && base + c < V) a.probs_dump[(int64_t) idx * V + base + c] = pv[c];
+                if (pos[c] >= 0) {
+                    pos[c] += below;
+                    sv[pos[c]] = pv[c];
+                    si[pos[c]] = base + c;
+                }
+            __builtin_amdgcn_wave_barrier();
+            for (int jx = lane; jx < total; jx += 64) sv[jx] = (float) exp((double) (sv[jx] - mx));
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) {   // sequential, in index order; four terms per LDS read
+                float sum = 0.0f;
+                int jx = 0;
+                for (; jx + 4 <= total; jx += 4) {
+                    const float4 t4 = *reinterpret_cast<const float4 *>(&sv[jx]);
+                    sum = sum + t4.x;
+                    sum = sum + t4.y;
+                    sum = sum + t4.z;
+                    sum = sum + t4.w;
+                }
+                for (; jx < total; jx++) sum = sum + sv[jx];
+                s_scalar[0] = 1.0f / sum;
             }
-            const uint64_t s0 = a.rng[b];
-            uint64_t st = gf2_apply(a.jump + (int64_t) tid * 64, s0);
-            float best = -INFINITY;
-            int bi = 0x7fffffff;
+            __builtin_amdgcn_wave_barrier();
+            const float inv = s_scalar[0];
+            for (int jx = lane; jx < total; jx += 64) sv[jx] = sv[jx] * inv;
+            // 6) sample: argmax over p > 0 of p / q, q_i = -log(1 - U_i), U_i the draw of index i.
+            // Each lane walks its chunk of the stream and keeps the draws of its survivors.
+            uint64_t st = st0;
 #pragma unroll
             for (int c = 0; c < SMP_CH; c++) {
                 if (c < chunk && base + c < V) {
-                    const float p = pv[c];
-                    float val = 0.0f;
-                    if (p > 0.0f) {
+                    if (pos[c] >= 0) {
                         const uint64_t x = st * 0x2545F4914F6CDD1Dull;
-                        const float u = (float) ((double) (x >> 40) * (1.0 / 16777216.0));
-                        const float q = -(float) log((double) (1.0f - u));
-                        val = p / q;
+                        su[pos[c]] = (float) ((double) (x >> 40) * (1.0 / 16777216.0));
                     }
-                    if (val > best) { best = val; bi = base + c; }
                     st = xs_step(st);
                 }
+            }
+            __builtin_amdgcn_wave_barrier();
+            float* dump = nullptr;
+            if (a.probs_dump) dump = a.probs_per_row ? a.probs_dump + (int64_t) b * V
+                                                     : (b == 0 ? a.probs_dump + (int64_t) idx * V : nullptr);
+            if (dump) {
+#pragma unroll
+                for (int c = 0; c < SMP_CH; c++)
+                    if (c < chunk && base + c < V) dump[base + c] = pos[c] >= 0 ? sv[pos[c]] : 0.0f;
+            }
+            float best = -INFINITY;
+            int bi = 0x7fffffff;
+            for (int jx = lane; jx < total; jx += 64) {   // increasing index within the lane
+                const float p = sv[jx];
+                const float val = p > 0.0f ? p / -(float) log((double) (1.0f - su[jx])) : 0.0f;
+                if (val > best) { best = val; bi = si[jx]; }
             }
             // first maximum wins: larger value, then smaller index
             for (int o = 32; o > 0; o >>= 1) {
@@ -248,28 +340,32 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                 const int oi = __shfl_xor(bi, o, 64);
                 if (ob > best || (ob == best && oi < bi)) { best = ob; bi = oi; }
             }
-            if (tid == 0) {
+            if (lane == 0) {
                 s_besti[0] = bi;
                 s_bestv[0] = best;
-                a.rng[b] = gf2_apply(a.adv, s0);
+                a.rng[b] = s_next;
             }
         }
         __syncthreads();
         if (tid == 0) {
             int tok = s_besti[0];
-            if (tok < 0 || tok >= V) tok = 0;   // all values were 0: the first index wins
-            if (a.sampled_dump) a.sampled_dump[(int64_t) idx * a.B + b] = tok;
-            if (a.oracle && idx < a.n_oracle) tok = a.oracle[idx];
-            const int n = a.ny[b];
-            a.hist[(int64_t) b * a.hist_stride + n] = tok;
-            a.ny[b] = n + 1;
-            a.last_tok[b] = tok;
-            if (tok == a.eos) {
-                a.fin_step[b] = idx;
-                a.fin_kind[b] = 0;
+            if (tok < 0 || tok >= V) tok = 0;   // no value > 0: the first index wins
+            if (a.tok_out) a.tok_out[b] = tok;
+            if (a.step) {
+                if (a.sampled_dump) a.sampled_dump[(int64_t) idx * a.B + b] = tok;
+                if (a.oracle && idx < a.n_oracle) tok = a.oracle[idx];
+                const int n = n_hist;
+                a.hist[(int64_t) b * a.hist_stride + n] = tok;
+                a.ny[b] = n + 1;
+                a.last_tok[b] = tok;
+                if (tok == a.eos) {
+                    a.fin_step[b] = idx;
+                    a.fin_kind[b] = 0;
+                }
             }
         }
     }
+    if (!a.step) return;   // single sampling call: no loop state
     // the last workgroup applies the early-stop rule and advances the loop index
     __syncthreads();
     if (tid == 0) {
@@ -345,18 +441,74 @@ Mat power(const Mat & a, uint64_t n) {
     }
     return r;
 }
+
+// out[p][v] (stride `stride` between v entries) = M applied to byte value v at byte position p
+void byte_table(const Mat & m, uint64_t * out, int64_t stride) {
+    for (int p = 0; p < 8; p++) {
+        uint64_t * row = out + (int64_t) p * 256 * stride;
+        row[0] = 0;
+        for (int v = 1; v < 256; v++) {
+            const int low = __builtin_ctz(v);
+            row[(int64_t) v * stride] = row[(int64_t) (v & (v - 1)) * stride] ^ m[8 * p + low];
+        }
+    }
+}
 }  // namespace
 
-// jump: [64][64] = A^(chunk*t + 1) for t < 64; adv: [64] = A^V
+// jump: [8][256][64], entry (p, v, t) = A^(chunk*t + 1) applied to byte v at byte position p;
+// adv: [8][256], the same for A^V
 void rng_tables(int V, int chunk, uint64_t * jump, uint64_t * adv) {
     Mat A;
     for (int i = 0; i < 64; i++) A[i] = host_step(1ull << i);
-    for (int t = 0; t < 64; t++) {
-        const Mat m = power(A, (uint64_t) chunk * t + 1);
-        for (int i = 0; i < 64; i++) jump[t * 64 + i] = m[i];
-    }
-    const Mat m = power(A, (uint64_t) V);
-    for (int i = 0; i < 64; i++) adv[i] = m[i];
+    for (int t = 0; t < 64; t++) byte_table(power(A, (uint64_t) chunk * t + 1), jump + t, 64);
+    byte_table(power(A, (uint64_t) V), adv, 1);
 }
 
+size_t sample_workspace_bytes() { return (size_t) (RNG_JUMP_WORDS + RNG_ADV_WORDS) * sizeof(uint64_t); }
+
 }  // namespace gsvk
+
+extern "C" size_t gsvk_sample_workspace_bytes(int V) {
+    (void) V;
+    return gsvk::sample_workspace_bytes();
+}
+
+extern "C" int gsvk_op_sample(const float * logits, int B, int V, const int32_t * hist, int hist_stride,
+                              const int32_t * n_hist, const gsvk_sampler_cfg * cfg, uint64_t * rng,
+                              int32_t * tok_out, float * probs_out, void * ws, void * stream) {
+    using namespace gsvk;
+    GSVK_REQUIRE(logits && cfg && rng && tok_out && ws, "sample: null pointer");
+    GSVK_REQUIRE(B > 0 && V > 0 && V <= SMP_SORT, "sample: bad shape B=%d V=%d (V <= %d)", B, V, SMP_SORT);
+    GSVK_REQUIRE((hist == nullptr) == (n_hist == nullptr) && (!hist || hist_stride > 0),
+                 "sample: hist and n_hist go together");
+    GSVK_REQUIRE(((uintptr_t) ws & 7) == 0, "sample: workspace must be 8-byte aligned");
+    const hipStream_t st = (hipStream_t) stream;
+    const int chunk = (V + 63) / 64;
+    std::vector<uint64_t> tab(RNG_JUMP_WORDS + RNG_ADV_WORDS);
+    rng_tables(V, chunk, tab.data(), tab.data() + RNG_JUMP_WORDS);
+    uint64_t * jump = (uint64_t *) ws;
+    GSVK_HIP(hipMemcpyAsync(jump, tab.data(), tab.size() * 8, hipMemcpyHostToDevice, st));
+    SampleArgs a{};
+    a.logits = logits;
+    a.V = V;
+    a.eos = -1;
+    a.B = B;
+    a.hist = const_cast<int32_t *>(hist);
+    a.hist_stride = hist_stride;
+    a.ny = const_cast<int32_t *>(n_hist);
+    a.rng = rng;
+    a.jump = jump;
+    a.adv = jump + RNG_JUMP_WORDS;
+    a.chunk = chunk;
+    a.top_k = cfg->top_k;
+    a.top_p = cfg->top_p;
+    a.temperature = cfg->temperature;
+    a.rep = cfg->repetition_penalty;
+    a.max_steps = 1 << 30;
+    a.probs_dump = probs_out;
+    a.probs_per_row = 1;
+    a.tok_out = tok_out;
+    GSVK_TRY(launch_sample(a, st));
+    GSVK_HIP(hipStreamSynchronize(st));   // the table upload reads host memory
+    return GSVK_OK;
+}

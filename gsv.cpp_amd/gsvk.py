@@ -25,6 +25,7 @@ EXPORTS = [
     "gsvk_prefill", "gsvk_decode_step", "gsvk_kv_read", "gsvk_last_sampled", "gsvk_op_q8_dequant",
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
+    "gsvk_sample_workspace_bytes", "gsvk_op_sample",
 ]
 
 
@@ -99,6 +100,9 @@ def lib():
         L.gsvk_attn_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i64, vp, vp, i64, f32, vp, vp, vp,
                                           vp, vp, vp]
+        L.gsvk_sample_workspace_bytes.argtypes = [i32]
+        L.gsvk_sample_workspace_bytes.restype = C.c_size_t
+        L.gsvk_op_sample.argtypes = [vp, i32, i32, vp, i32, vp, C.POINTER(SamplerCfg), vp, vp, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -187,6 +191,20 @@ def op_attn_decode(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, 
     check(lib().gsvk_op_attn_decode(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin), _p(kv_end),
                                     max_keys, scale, _p(out), _p(out16), _p(oq), _p(od), _p(ws),
                                     _stream(stream)), "attn_decode")
+
+
+def op_sample(logits, cfg, rng, tok_out, hist=None, n_hist=None, probs_out=None, ws=None, stream=None):
+    """One device sampling call for logits [B][V]: cfg = (top_k, top_p, temperature, rep);
+    rng [B] uint64 states (as int64 tensor) advanced in place; hist [B][stride] int32 with n_hist[b]
+    tokens per row."""
+    import torch
+    B, V = logits.shape
+    sc = SamplerCfg(int(cfg[0]), float(cfg[1]), float(cfg[2]), float(cfg[3]))
+    if ws is None:
+        ws = torch.empty(int(lib().gsvk_sample_workspace_bytes(V)), dtype=torch.uint8, device=logits.device)
+    stride = hist.shape[1] if hist is not None else 0
+    check(lib().gsvk_op_sample(_p(logits), B, V, _p(hist), stride, _p(n_hist), C.byref(sc), _p(rng), _p(tok_out),
+                               _p(probs_out), _p(ws), _stream(stream)), "sample")
 
 
 # ---- model ----------------------------------------------------------------------------------

@@ -219,6 +219,17 @@ int gsvk_op_add_act(const float * a, const float * b, int64_t n, int64_t ne0, in
 int gsvk_op_fdot(const void * w, int wtype, int64_t n, int64_t k, const float * x, int64_t m,
                  float * y, int mode, void * stream);
 
+/* One call of the device sampler for B rows: gsv_logits_to_probs followed by gsv_sample with the
+ * row's gsv_rng (src/gsv_sampler.cpp:8-89). Device memory: logits [B][V] (not modified);
+ * hist [B][hist_stride] holding n_hist[b] tokens per row, of which the last <= 4096 are the
+ * repetition-penalty window (both NULL = no history); rng [B] xorshift64* states, advanced by
+ * V draws; tok_out [B]; probs_out [B][V] or NULL. ws: gsvk_sample_workspace_bytes(V) bytes of
+ * device memory. V <= 2048. The call synchronises the stream. */
+size_t gsvk_sample_workspace_bytes(int V);
+int gsvk_op_sample(const float * logits, int B, int V, const int32_t * hist, int hist_stride,
+                   const int32_t * n_hist, const gsvk_sampler_cfg * cfg, uint64_t * rng,
+                   int32_t * tok_out, float * probs_out, void * ws, void * stream);
+
 /* Single-query attention over a per-sequence fp16 KV cache (decode; ggml_flash_attn_ext with
  * one query row). q fp32 [B][nh][hd]; K/V fp16 [B][nh][lstride][hd]; valid keys of sequence b
  * are [kv_begin[b], kv_end[b]) (device int32 arrays). out fp32 [B][nh*hd] (head-major).
