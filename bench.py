@@ -110,8 +110,28 @@ def kernel_roofline(gsvk, torch, reqs, steps):
                             od=od, ws=ws)
     ms = time_events(attn, 240, torch)
     ab = nkeys * NH * 2 * HD * 2
-    res["attn_decode"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER}
-    del kc, vc
+    fused = B <= 32   # the decode path runs QKV + attention as one kernel up to 32 sequences
+    res["attn_decode"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER,
+                          "in_decode": not fused}
+    # the fused QKV projection + attention: head h's QKV weight rows + the same K/V rows; rotates
+    # over 24 weight copies as well
+    wqkv = torch.randint(-127, 128, (rot, 3 * D * D), dtype=torch.int8, device="cuda")
+    wdqkv = (torch.rand((rot, 3 * D * D // 32), device="cuda") * 0.001).half().view(torch.int16)
+    bqkv = torch.randn(3 * D, dtype=torch.float32, device="cuda") * 0.02
+    lres = torch.randn((B, D), dtype=torch.float32, device="cuda")
+    lr = torch.randn((B, D), dtype=torch.float32, device="cuda")
+    lwb = torch.cat([torch.ones(D), torch.zeros(D)]).cuda()
+    col = torch.tensor([S + mid], dtype=torch.int32, device="cuda")
+
+    def qkv_attn(i):
+        gsvk.op_qkv_attn(wqkv[i % rot], wdqkv[i % rot], bqkv, lres, lr, None, lwb, kc[i % rot], vc[i % rot],
+                         kv_begin, col, scale, out, oq=oq, od=od)
+    if gsvk.qkv_attn_supported(B, NH, lstride):
+        ms = time_events(qkv_attn, 240, torch)
+        fb = ab + 3 * D * D // 32 * 34
+        res["qkv_attn"] = {"ms": ms, "bytes": fb, "gbs": fb / ms / 1e6, "launches_per_step": N_LAYER,
+                           "in_decode": fused}
+    del kc, vc, wqkv, wdqkv
     # Q8_0 GEMVs at batch B (the decoder's fused kernel): rotate over 96 weight copies (> MALL).
     # QKV and FFN1 run with their LayerNorm input stage, out and FFN2 read Q8_0 rows.
     xq = torch.randint(-127, 128, (B * FFN,), dtype=torch.int8, device="cuda")
@@ -133,7 +153,8 @@ def kernel_roofline(gsvk, torch, reqs, steps):
                 gsvk.op_q8_gemv(wq[i % copies], wd[i % copies], n, k, xq, xd, B, None, 0, y)
         ms = time_events(gemv, 480, torch)
         b = n * k // 32 * 34
-        res[name] = {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": N_LAYER}
+        res[name] = {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": N_LAYER,
+                     "in_decode": name != "gemv_qkv" or not fused}
         del wq, wd
     return res
 
@@ -183,7 +204,7 @@ def measured_traffic(kernel):
     (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --kernels-only`, each scaled
     by what the counter reads for a 256 MiB copy), or None when no summary holds it."""
     path = os.path.join(ROOT, "profiles", "attn_decode_gemv_b16_kernels_hbm.md")
-    key = {"attn_decode": "attn_decode_b16"}.get(kernel)
+    key = {"attn_decode": "attn_decode_b16", "qkv_attn": "qkv_attn_b16"}.get(kernel)
     if key is None or not os.path.exists(path):
         return None
     for line in open(path):
@@ -235,8 +256,8 @@ def main():
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.kernels_only:
         kr = kernel_roofline(gsvk, torch, workload_requests(args.batch), args.steps)
-        res = {k: {"us": round(v["ms"] * 1e3, 3), "bytes": v["bytes"], "GBs": round(v["gbs"], 1)}
-               for k, v in kr.items()}
+        res = {k: {"us": round(v["ms"] * 1e3, 3), "bytes": v["bytes"], "GBs": round(v["gbs"], 1),
+                   "in_decode": v["in_decode"]} for k, v in kr.items()}
         res["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         res["copy_probe_bytes"] = copy_probe(torch)
         print(json.dumps({"kernels_only": res}))
@@ -268,10 +289,18 @@ def main():
     extra = {"prefill_ms": round(r["prefill_ms"], 2), "wall_s_incl_prefill": round(wall, 3),
              "step_bytes_mb": round(step_bytes / 1e6, 1),
              "step_hbm_frac": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
-    for bb, st in ((1, 300), (64, 200)):
-        _, rb, _ = run(bb, st, 8)
-        extra[f"tok_s_b{bb}"] = round(bb * st / (rb["decode_ms"] / 1e3), 1)
-        extra[f"ms_per_step_b{bb}"] = round(rb["decode_ms"] / st, 4)
+    # batch 1 as the reference's single-sequence case: 128 phones + 64 prompt codes (prefill 192),
+    # 300 greedy steps with EOS masked
+    r1 = sm.synth_requests(0x6A5E0001, 1, 64, [128])
+    g.generate(r1, sampler=(1, 1.0, 1.0, 1.0), max_steps=8, seeds=[1], flags=flags)
+    rb = g.generate(r1, sampler=(1, 1.0, 1.0, 1.0), max_steps=300, seeds=[1], flags=flags)
+    extra["tok_s_b1"] = round(300 / (rb["decode_ms"] / 1e3), 1)
+    extra["ms_per_step_b1"] = round(rb["decode_ms"] / 300, 4)
+    extra["b1_workload"] = "1 sequence, 128 phones + 64 prompt codes, 300 greedy steps"
+    # batch 64: the batch-16 workload's request shape at 64 sequences, 200 steps
+    _, rb, _ = run(64, 200, 8)
+    extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)
+    extra["ms_per_step_b64"] = round(rb["decode_ms"] / 200, 4)
     g.close()
 
     roof = None
@@ -280,7 +309,7 @@ def main():
         extra["kernels"] = {k: {"us": round(v["ms"] * 1e3, 2), "GBs": round(v["gbs"], 1),
                                 "frac": round(v["gbs"] / HBM_PEAK_GBS, 4)} for k, v in kr.items()}
         extra["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
-        dom = max(kr, key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
+        dom = max((k for k in kr if kr[k]["in_decode"]), key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
         d = kr[dom]
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),

@@ -14,74 +14,9 @@
 //
 // Numerics: softmax(q.k * scale) . V over the valid keys with fp32 accumulation; the output is
 // divided by the sum (multiplied by its reciprocal), as ggml_flash_attn_ext does.
-#include "common.h"
+#include "attn_dev.h"
 
 namespace gsvk {
-
-constexpr int ATT_HD = 32;
-constexpr int ATT_BLK = 64;            // keys per block
-constexpr int ATT_PART = ATT_HD + 2;   // m, l, o[32]
-constexpr float LOG2E = 1.4426950408889634f;
-
-__device__ __forceinline__ void h8_to_f(const uint4 & u, float (&f)[8]) {
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        f[2 * i] = h2f((uint16_t) (w[i] & 0xffff));
-        f[2 * i + 1] = h2f((uint16_t) (w[i] >> 16));
-    }
-}
-
-__device__ __forceinline__ float ld_coherent(const float * p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void st_coherent(float * p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Final output of one (seq, head): lanes 0..31 of the calling wave hold one dimension each.
-// The Q8_0 copy is written in the sliced layout of a row of nh*32 values: head h is block h.
-__device__ __forceinline__ void attn_store_out(float val, int lane, int64_t bh, int nh,
-                                               float * __restrict__ out,
-                                               uint16_t * __restrict__ out16,
-                                               int8_t * __restrict__ oq,
-                                               float * __restrict__ od) {
-    if (lane < ATT_HD) {
-        out[bh * ATT_HD + lane] = val;
-        if (out16) out16[bh * ATT_HD + lane] = f2h(val);
-    }
-    if (oq) {
-        float v1[1] = {lane < ATT_HD ? val : 0.0f};
-        int8_t q1[1];
-        const float d = q8_quantize_group<1>(v1, q1, 32);
-        if (lane < ATT_HD) {
-            const int64_t b = bh / nh;
-            const int h = (int) (bh % nh);
-            oq[b * nh * ATT_HD + q8_sliced_offset(nh, h, lane)] = q1[0];
-            if (lane == 0) od[bh] = d;   // block index == b*nh + h
-        }
-    }
-}
-
-struct KV8 {
-    uint4 k[4], v[4];
-};
-
-__device__ __forceinline__ void load_block(const uint16_t * __restrict__ kb,
-                                           const uint16_t * __restrict__ vb, int key0, int end,
-                                           int ks, KV8 & r) {
-#pragma unroll
-    for (int p = 0; p < 4; p++) {
-        const int key = key0 + p * 16 + ks;
-        if (key < end) {
-            r.k[p] = *reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
-            r.v[p] = *reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
-        } else {
-            r.k[p] = make_uint4(0, 0, 0, 0);
-            r.v[p] = make_uint4(0, 0, 0, 0);
-        }
-    }
-}
 
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) k_attn_decode(
@@ -138,56 +73,30 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = 0.0f;
 
-    int blk = blk0 + wave;
+    // the first block of this wave is loaded unconditionally (a wave past the last block loads
+    // that block again, from L2, and does not use it), then each iteration prefetches the next
+    // block before computing the current one: every load count is known to the compiler, so the
+    // waits are exact
+    const int last_key = end - 1;
+    const int nb = blk1 - blk0;
+    int blk = blk0 + (wave < nb ? wave : nb - 1);
     KV8 cur;
-    if (blk < blk1) load_block(kb, vb, beg + blk * ATT_BLK, end, ks, cur);
-    while (blk < blk1) {
-        const int nxt = blk + NW;
-        KV8 pre;
-        if (nxt < blk1) load_block(kb, vb, beg + nxt * ATT_BLK, end, ks, pre);
-        const int key0 = beg + blk * ATT_BLK;
-        float s[4];
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            float kf[8];
-            h8_to_f(cur.k[p], kf);
-            float dot = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) dot = __builtin_fmaf(qv[i], kf[i], dot);
-            dot += __shfl_xor(dot, 1, 64);
-            dot += __shfl_xor(dot, 2, 64);
-            s[p] = (key0 + p * 16 + ks < end) ? dot * scale_log2 : -INFINITY;
+    load_block(kb, vb, beg + blk * ATT_BLK, last_key, ks, cur);
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+    if (wave < nb) {
+        while (blk + NW < blk1) {
+            KV8 pre;
+            load_block(kb, vb, beg + (blk + NW) * ATT_BLK, last_key, ks, pre);
+            attn_block_step<false>(cur, beg + blk * ATT_BLK, end, ks, qv, scale_log2, -1, z4, z4, m, l, o);
+            cur = pre;
+            blk += NW;
         }
-        float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-        bm = fmaxf(bm, __shfl_xor(bm, 4, 64));
-        bm = fmaxf(bm, __shfl_xor(bm, 8, 64));
-        bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-        bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-        const float mn = fmaxf(m, bm);                    // finite: each block has a valid key
-        const float f = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first block (m = -inf)
-        l *= f;
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] *= f;
-        m = mn;
-#pragma unroll
-        for (int p = 0; p < 4; p++) {
-            const float pr = __builtin_amdgcn_exp2f(s[p] - m);   // masked keys: exp2(-inf) = 0
-            float vf[8];
-            h8_to_f(cur.v[p], vf);
-            l += pr;
-#pragma unroll
-            for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(pr, vf[i], o[i]);
-        }
-        cur = pre;
-        blk = nxt;
+        attn_block_step<false>(cur, beg + blk * ATT_BLK, end, ks, qv, scale_log2, -1, z4, z4, m, l, o);
     }
     // reduce the 16 key slots of the wave (m is uniform across the wave)
+    l = slot_sum(l);
 #pragma unroll
-    for (int off = 4; off < 64; off <<= 1) {
-        l += __shfl_xor(l, off, 64);
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] += __shfl_xor(o[i], off, 64);
-    }
+    for (int i = 0; i < 8; i++) o[i] = slot_sum(o[i]);
     if (lane < 4) {
 #pragma unroll
         for (int i = 0; i < 8; i++) s_o[wave][lane * 8 + i] = o[i];

@@ -72,6 +72,58 @@ __device__ __forceinline__ uint16_t f2h(float f) {
     return __builtin_bit_cast(uint16_t, v);
 }
 
+// ---- cross-lane exchanges without LDS traffic (gfx9 DPP and ds_swizzle) ----
+constexpr int DPP_XOR1 = 0xB1;    // quad_perm [1,0,3,2]: lane i <- lane i ^ 1
+constexpr int DPP_XOR2 = 0x4E;    // quad_perm [2,3,0,1]: lane i <- lane i ^ 2
+constexpr int DPP_ROR1 = 0x121;   // row_ror within 16-lane rows
+constexpr int DPP_ROR2 = 0x122;
+constexpr int DPP_ROR4 = 0x124;
+constexpr int DPP_ROR8 = 0x128;   // rotation by 8 of 16 = lane i <- lane i ^ 8
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, __double2loint(v), CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, __double2hiint(v), CTRL, 0xf, 0xf, false);
+    return __hiloint2double(hi, lo);
+}
+// lane i <- lane i ^ 4 / i ^ 16 (ds_swizzle bit mode, within 32 lanes)
+__device__ __forceinline__ float swz_xor4(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
+}
+__device__ __forceinline__ float swz_xor16(float v) {
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x401F));
+}
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), l),
+                            __builtin_amdgcn_readlane(__double2loint(v), l));
+}
+
+// Maximum over the 64 lanes, the same value in every lane (max is exact: order does not matter).
+__device__ __forceinline__ float wave_max_uniform(float v) {
+    v = fmaxf(v, dpp_f<DPP_XOR1>(v));
+    v = fmaxf(v, dpp_f<DPP_XOR2>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR4>(v));
+    v = fmaxf(v, dpp_f<DPP_ROR8>(v));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
+}
+
+// Sum over the 64 lanes, the same value in every lane: each 16-lane row is summed by rotations
+// (8, 4, 2, 1), then the four row totals of lanes 0, 16, 32, 48 as (r0 + r1) + (r2 + r3).
+__device__ __forceinline__ double wave_sum_d_uniform(double v) {
+    v += dpp_d<DPP_ROR8>(v);
+    v += dpp_d<DPP_ROR4>(v);
+    v += dpp_d<DPP_ROR2>(v);
+    v += dpp_d<DPP_ROR1>(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
+
 __device__ __forceinline__ float warp_max(float v) {
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
@@ -100,7 +152,12 @@ __device__ __forceinline__ float q8_quantize_group(const float (&v)[PER_LANE], i
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < PER_LANE; i++) amax = fmaxf(amax, fabsf(v[i]));
-    for (int o = 1; o < lanes; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    if (lanes == 4) {
+        amax = fmaxf(amax, dpp_f<DPP_XOR1>(amax));
+        amax = fmaxf(amax, dpp_f<DPP_XOR2>(amax));
+    } else {
+        for (int o = 1; o < lanes; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    }
     const float d = amax / 127.0f;
     const float id = (amax != 0.0f) ? 127.0f / amax : 0.0f;
 #pragma unroll

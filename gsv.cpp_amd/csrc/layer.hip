@@ -16,52 +16,12 @@
 //   (OUT_Q8) the Q8_0 quantisation of each 32-row output block, written sliced.
 #include "common.h"
 #include "layer.h"
+#include "layer_dev.h"
 
 namespace gsvk {
 
 constexpr int LG_THREADS = 256;
 constexpr int LG_ROWS = 32;   // output rows per workgroup
-
-// read in place of an absent r or bias operand of the LayerNorm input stage
-__device__ __align__(16) const float g_zero_row[512] = {};
-
-// One row of width 512 held by one wave (8 values per lane): LayerNorm as in norm.hip. Every
-// operand is fetched with unconditional 16-byte loads issued before the first use (absent r or
-// bias read a zero row instead of branching), so the stage costs one memory latency.
-__device__ __forceinline__ void ln_row_wave(const float * __restrict__ res, const float * __restrict__ r,
-                                            const float * __restrict__ bias,
-                                            const float * __restrict__ wb, int lane, float (&o)[8]) {
-    constexpr int n = 512;
-    const int base = lane * 8;
-    const float4 * x4 = reinterpret_cast<const float4 *>(res + base);
-    const float4 * r4 = reinterpret_cast<const float4 *>(r + base);
-    const float4 * b4 = reinterpret_cast<const float4 *>(bias + base);
-    const float4 * w4 = reinterpret_cast<const float4 *>(wb + base);
-    const float4 * c4 = reinterpret_cast<const float4 *>(wb + n + base);
-    const float4 xa = x4[0], xb = x4[1], ra = r4[0], rb = r4[1], ba = b4[0], bb = b4[1];
-    const float4 wa = w4[0], wbv = w4[1], ca = c4[0], cb = c4[1];
-    const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-    const float rv[8] = {ra.x, ra.y, ra.z, ra.w, rb.x, rb.y, rb.z, rb.w};
-    const float bv[8] = {ba.x, ba.y, ba.z, ba.w, bb.x, bb.y, bb.z, bb.w};
-    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wbv.x, wbv.y, wbv.z, wbv.w};
-    const float cv[8] = {ca.x, ca.y, ca.z, ca.w, cb.x, cb.y, cb.z, cb.w};
-    float v[8];
-    double s = 0.0, s2 = 0.0;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const float t = (xv[i] + rv[i]) + bv[i];   // x + 0 and + 0 leave x unchanged
-        v[i] = t;
-        s += (double) t;
-        s2 += (double) t * (double) t;
-    }
-    s = warp_sum_d(s);
-    s2 = warp_sum_d(s2);
-    const float mean = (float) (s / (double) n);
-    const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
-    const float inv = 1.0f / __builtin_sqrtf(var + 1e-5f);
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf((v[i] - mean) * inv, wv[i], cv[i]);
-}
 
 template <int NB4, int MT>
 __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __restrict__ ws,

@@ -31,24 +31,45 @@ __global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
     const float * rr = r ? r + (int64_t) row * n : nullptr;
     float v[MAXC][8];
     double s = 0.0, s2 = 0.0;
+    // 16-byte loads, all issued before the first use; the branches are uniform
+    float4 xv[MAXC][2], rv[MAXC][2], bv[MAXC][2];
 #pragma unroll
     for (int c = 0; c < MAXC; c++) {
-        const int ch = lane + 64 * c;
-        if (ch < nchunk) {
-            const int base = ch * 8;
+        const int base = (lane + 64 * c) * 8;
+        const bool act = lane + 64 * c < nchunk;
+        const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        xv[c][0] = act ? *reinterpret_cast<const float4 *>(xr + base) : z;
+        xv[c][1] = act ? *reinterpret_cast<const float4 *>(xr + base + 4) : z;
+        rv[c][0] = rv[c][1] = bv[c][0] = bv[c][1] = z;
+        if (rr && act) {
+            rv[c][0] = *reinterpret_cast<const float4 *>(rr + base);
+            rv[c][1] = *reinterpret_cast<const float4 *>(rr + base + 4);
+        }
+        if (bias && act) {
+            bv[c][0] = *reinterpret_cast<const float4 *>(bias + base);
+            bv[c][1] = *reinterpret_cast<const float4 *>(bias + base + 4);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < MAXC; c++) {
+        if (lane + 64 * c < nchunk) {
+            const float xs[8] = {xv[c][0].x, xv[c][0].y, xv[c][0].z, xv[c][0].w,
+                                 xv[c][1].x, xv[c][1].y, xv[c][1].z, xv[c][1].w};
+            const float rs[8] = {rv[c][0].x, rv[c][0].y, rv[c][0].z, rv[c][0].w,
+                                 rv[c][1].x, rv[c][1].y, rv[c][1].z, rv[c][1].w};
+            const float bs[8] = {bv[c][0].x, bv[c][0].y, bv[c][0].z, bv[c][0].w,
+                                 bv[c][1].x, bv[c][1].y, bv[c][1].z, bv[c][1].w};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                float t = xr[base + i];
-                if (rr) t = t + rr[base + i];
-                if (bias) t = t + bias[base + i];
+                const float t = (xs[i] + rs[i]) + bs[i];   // + 0 leaves the value unchanged
                 v[c][i] = t;
                 s += (double) t;
                 s2 += (double) t * (double) t;
             }
         }
     }
-    s = warp_sum_d(s);
-    s2 = warp_sum_d(s2);
+    s = wave_sum_d_uniform(s);
+    s2 = wave_sum_d_uniform(s2);
     const float mean = (float) (s / (double) n);
     const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
     const float inv = 1.0f / __builtin_sqrtf(var + eps);
@@ -145,6 +166,8 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
                  "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
                  (long long) rows, (long long) n);
     GSVK_REQUIRE((yq == nullptr) == (yd == nullptr), "layernorm: yq and yd go together");
+    auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
+    GSVK_REQUIRE(al16(x) && al16(r) && al16(bias) && al16(wb), "layernorm: operands must be 16-byte aligned");
     if (rows == 0) return GSVK_OK;
     const dim3 grid((unsigned) rows);
     if (n <= 512)

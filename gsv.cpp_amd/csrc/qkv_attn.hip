@@ -1,0 +1,297 @@
+// QKV projection + single-query attention of one decoder layer in one launch, for gfx950.
+//
+// Workgroup (seq b, head h), NW waves (the same NW as the standalone attention, attn_waves):
+//   1. every wave issues the loads of its first block of cached keys [begin, col) (they do not
+//      depend on this step) together with its share of head h's QKV weight rows;
+//   2. wave 0 builds the Q8_0 input row in LDS: LayerNorm((res + r) + bias) (layers > 0) or
+//      emb[tok] + alpha * PE[pos] (layer 0), as the input stages of layer.hip;
+//   3. the 96 rows of head h (q, k, v; rows 32h.., 512+32h.., 1024+32h..) are computed in the
+//      Q8_0 x86 dot order of q8.hip (8 rows per wave, 8 slice lanes per row); q goes to LDS, the
+//      new k and v are rounded to fp16, appended to the cache at column col and kept in LDS;
+//   4. the attention of attention.hip over keys [begin, col] with the preloaded first block;
+//      the key at column col is taken from LDS (the preloaded registers hold the slot's old
+//      contents).
+// The result equals the separate QKV GEMV + k_attn_decode<NW> bit for bit: the same input row,
+// the same per-row dot, the same blocks per wave and the same merge order.
+//
+// head h's workgroups are blockIdx.x = b * nh + h: with nh a multiple of 8 they all run on one
+// XCD, so the 52 KB of weights of head h are read from HBM once per XCD L2.
+#include "attn_dev.h"
+#include "layer.h"
+#include "layer_dev.h"
+#include "qkv_attn.h"
+
+namespace gsvk {
+
+namespace {
+constexpr int QA_K = 512;                // d_model
+constexpr int QA_NBLK = QA_K / 32;
+constexpr int QA_NB4 = QA_K / 128;       // int4 weight loads per slice lane
+constexpr int QA_ROWS = 3 * ATT_HD;      // rows of one head: q, k, v
+}  // namespace
+
+template <int NW, int MODE>
+__global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
+    constexpr int PASSES = (QA_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
+    const int nh = a.n_head;
+    const int bh = blockIdx.x;
+    const int b = __builtin_amdgcn_readfirstlane(bh / nh);   // uniform: scalar registers
+    const int h = bh - b * nh;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int ks = lane >> 2;
+    const int qd = lane & 3;
+    const int rsub = lane >> 3;   // GEMV: row within the wave's 8
+    const int j = lane & 7;       // GEMV: slice lane
+
+    __shared__ __align__(16) int8_t s_x[QA_K];
+    __shared__ __align__(16) float s_d[QA_NBLK];
+    __shared__ __align__(16) float s_q[ATT_HD];
+    __shared__ __align__(16) uint16_t s_kv[2][ATT_HD];
+    __shared__ float s_m[NW];
+    __shared__ float s_l[NW];
+    __shared__ float s_o[NW][ATT_HD];
+
+    // Order of work, chosen so that no wave-dependent branch separates a load from its use (the
+    // compiler then waits exactly; a wait on a load also completes every load issued before it):
+    // the scalars; every wave's weight rows; wave 0's input stage (its loads and arithmetic in
+    // one branch); every wave's first block of keys. The key blocks (the bulk of the bytes) go
+    // last so that the weights and the input row are not queued behind them.
+    const LayerIn & in = a.in;
+    const int col = *a.col_ptr + a.col_add;   // column of this step's key
+    int beg = a.kv_begin[b];
+
+    int4 w[PASSES][QA_NB4];
+    uint2 dh[PASSES][QA_NB4];
+    float rbias[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int rl = (p * NW + wave) * 8 + rsub;
+        const int rlc = rl < QA_ROWS ? rl : QA_ROWS - 1;
+        const int row = (rlc >> 5) * QA_K + h * ATT_HD + (rlc & 31);
+        const int4 * wsl = reinterpret_cast<const int4 *>(a.ws + ((int64_t) row * 8 + j) * QA_NBLK * 4);
+        const uint2 * wdr = reinterpret_cast<const uint2 *>(a.wd + (int64_t) row * QA_NBLK);
+#pragma unroll
+        for (int i = 0; i < QA_NB4; i++) {
+            w[p][i] = wsl[i];
+            dh[p][i] = wdr[i];
+        }
+        rbias[p] = a.bias[row];
+    }
+
+    // 2. the input row, quantised into LDS
+    if (wave == 0) {
+        float o[8];
+        if constexpr (MODE == IN_LN) {
+            ln_row_wave(in.res + (int64_t) b * QA_K, in.r ? in.r + (int64_t) b * QA_K : g_zero_row,
+                        in.bias ? in.bias : g_zero_row, in.wb, lane, o);
+        } else {
+            const int pos = *in.pos_ptr;
+            int tk = in.tok[b];
+            tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
+            const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * QA_K + lane * 8);
+            const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) (pos + in.pos_add) * QA_K +
+                                                                 lane * 8);
+            const float4 e0 = er[0], e1 = er[1], p0 = pr[0], p1 = pr[1];
+            const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+            const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pv[i], ev[i]);
+            if (h == 0 && in.kv_end && lane == 0) in.kv_end[b] = pos + in.kv_end_add;
+        }
+        if (h == 0 && in.out_x) {
+            float4 * dst = reinterpret_cast<float4 *>(in.out_x + (int64_t) b * QA_K + lane * 8);
+            dst[0] = make_float4(o[0], o[1], o[2], o[3]);
+            dst[1] = make_float4(o[4], o[5], o[6], o[7]);
+        }
+        int8_t q[8];
+        const float d = q8_quantize_group<8>(o, q, 4);
+        q8_store_sliced(s_x, QA_NBLK, lane >> 2, lane & 3, q);
+        if ((lane & 3) == 0) s_d[lane >> 2] = d;
+    }
+
+    // 1b. the first block of cached keys, keys < col (the new key is substituted later); a wave
+    // past the last block loads that block again and does not use it
+    const bool col_ok = col >= 0 && col < a.lstride;
+    beg = beg < 0 ? 0 : (beg < a.lstride ? beg : (int) a.lstride - 1);
+    const int end = col + 1;
+    const int nkeys = (col_ok && end > beg) ? end - beg : 0;
+    const int nblk = (nkeys + ATT_BLK - 1) / ATT_BLK;
+    const int64_t pair = (int64_t) b * nh + h;
+    const uint16_t * kb = a.kc + pair * a.lstride * ATT_HD + qd * 8;
+    const uint16_t * vb = a.vc + pair * a.lstride * ATT_HD + qd * 8;
+    int last_old = col > beg ? col - 1 : beg;          // keys past it read this one
+    last_old = last_old < a.lstride ? last_old : (int) a.lstride - 1;
+    int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
+    KV8 cur;
+    load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+    __syncthreads();
+    if (!col_ok) {   // the new key is outside the cache: write nothing to it, output 0
+        if (wave == 0) attn_store_out(0.0f, lane, pair, nh, a.out, nullptr, a.oq, a.od);
+        return;
+    }
+
+    // 3. the 96 rows of head h
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int rl = (p * NW + wave) * 8 + rsub;
+        if ((p * NW + wave) * 8 >= QA_ROWS) break;   // uniform per wave
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < QA_NB4; i++) {
+            const float dw0 = h2f((uint16_t) (dh[p][i].x & 0xffff)), dw1 = h2f((uint16_t) (dh[p][i].x >> 16));
+            const float dw2 = h2f((uint16_t) (dh[p][i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[p][i].y >> 16));
+            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[(j * QA_NBLK + 4 * i) * 4]);
+            const float4 dx = *reinterpret_cast<const float4 *>(&s_d[4 * i]);
+            acc = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w[p][i].x, xv.x, 0, false), acc);
+            acc = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w[p][i].y, xv.y, 0, false), acc);
+            acc = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w[p][i].z, xv.z, 0, false), acc);
+            acc = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w[p][i].w, xv.w, 0, false), acc);
+        }
+        acc = acc + __shfl_xor(acc, 4, 64);
+        acc = acc + __shfl_xor(acc, 2, 64);
+        acc = acc + __shfl_xor(acc, 1, 64);
+        if (j == 0 && rl < QA_ROWS) {
+            const int which = rl >> 5, dd = rl & 31;
+            const float v = acc + rbias[p];
+            if (which == 0) {
+                s_q[dd] = v;
+            } else {
+                const uint16_t hv = f2h(v);
+                s_kv[which - 1][dd] = hv;
+                (which == 1 ? a.kc : a.vc)[(pair * a.lstride + col) * ATT_HD + dd] = hv;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 4. attention over [beg, col]
+    if (nkeys == 0) {   // (col < beg: nothing valid; ggml returns 0)
+        if (wave == 0) attn_store_out(0.0f, lane, pair, nh, a.out, nullptr, a.oq, a.od);
+        return;
+    }
+    float qv[8];
+    {
+        const float4 q0 = *reinterpret_cast<const float4 *>(&s_q[qd * 8]);
+        const float4 q1 = *reinterpret_cast<const float4 *>(&s_q[qd * 8 + 4]);
+        qv[0] = q0.x; qv[1] = q0.y; qv[2] = q0.z; qv[3] = q0.w;
+        qv[4] = q1.x; qv[5] = q1.y; qv[6] = q1.z; qv[7] = q1.w;
+    }
+    const uint4 knew = *reinterpret_cast<const uint4 *>(&s_kv[0][qd * 8]);
+    const uint4 vnew = *reinterpret_cast<const uint4 *>(&s_kv[1][qd * 8]);
+    const float scale_log2 = a.scale_log2;
+
+    float m = -INFINITY, l = 0.0f;
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = 0.0f;
+    if (wave < nblk) {
+        while (blk + NW < nblk) {
+            KV8 pre;
+            load_block(kb, vb, beg + (blk + NW) * ATT_BLK, last_old, ks, pre);
+            attn_block_step<true>(cur, beg + blk * ATT_BLK, end, ks, qv, scale_log2, col, knew, vnew, m, l, o);
+            cur = pre;
+            blk += NW;
+        }
+        attn_block_step<true>(cur, beg + blk * ATT_BLK, end, ks, qv, scale_log2, col, knew, vnew, m, l, o);
+    }
+    l = slot_sum(l);
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = slot_sum(o[i]);
+    if (lane < 4) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s_o[wave][lane * 8 + i] = o[i];
+        if (lane == 0) {
+            s_l[wave] = l;
+            s_m[wave] = m;
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    float M = s_m[0];
+#pragma unroll
+    for (int w2 = 1; w2 < NW; w2++) M = fmaxf(M, s_m[w2]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll
+    for (int w2 = 0; w2 < NW; w2++) {
+        const float f = s_m[w2] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w2] - M);
+        L = __builtin_fmaf(s_l[w2], f, L);
+        if (lane < ATT_HD) O = __builtin_fmaf(s_o[w2][lane], f, O);
+    }
+    attn_store_out(O * (1.0f / L), lane, pair, nh, a.out, nullptr, a.oq, a.od);
+}
+
+bool qkv_attn_supported(int B, int nh, int64_t max_keys) {
+    return attn_nsplit(B, nh, max_keys) == 1;
+}
+
+// Each workgroup reads its head's 52 KB of weights, so the batch multiplies the weight reads
+// (from L2): at 32 sequences and more the tiled QKV GEMV + attention pair is faster.
+bool qkv_attn_preferred(int B, int nh, int64_t max_keys) {
+    return B <= 32 && qkv_attn_supported(B, nh, max_keys);
+}
+
+int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream) {
+    GSVK_REQUIRE(a.ws && a.wd && a.bias && a.kc && a.vc && a.kv_begin && a.col_ptr && a.out,
+                 "qkv_attn: null pointer");
+    GSVK_REQUIRE(a.n_head * ATT_HD == QA_K && B > 0 && a.lstride > 0 && max_keys <= a.lstride,
+                 "qkv_attn: needs 16 heads of 32 (d_model 512)");
+    GSVK_REQUIRE(a.in.mode == IN_LN ? (a.in.res && a.in.wb) : (a.in.mode == IN_EMB && a.in.emb && a.in.pe &&
+                                                                a.in.tok && a.in.pos_ptr),
+                 "qkv_attn: bad input stage");
+    GSVK_REQUIRE((a.oq == nullptr) == (a.od == nullptr), "qkv_attn: oq and od go together");
+    GSVK_REQUIRE(qkv_attn_supported(B, a.n_head, max_keys), "qkv_attn: rows this long need the split path");
+    const int nw = attn_waves(B, a.n_head, max_keys);
+    const dim3 grid((unsigned) ((int64_t) B * a.n_head));
+#define GSVK_QA(W, MODE) hipLaunchKernelGGL((k_qkv_attn<W, MODE>), grid, dim3(W * 64), 0, stream, a)
+    if (a.in.mode == IN_LN) {
+        if (nw == 16) GSVK_QA(16, IN_LN);
+        else if (nw == 8) GSVK_QA(8, IN_LN);
+        else GSVK_QA(4, IN_LN);
+    } else {
+        if (nw == 16) GSVK_QA(16, IN_EMB);
+        else if (nw == 8) GSVK_QA(8, IN_EMB);
+        else GSVK_QA(4, IN_EMB);
+    }
+#undef GSVK_QA
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk
+
+extern "C" int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
+                                const float * r, const float * ln_bias, const float * wb, int B, int nh,
+                                uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                                const int32_t * col, float scale, float * out, int8_t * oq, float * od,
+                                float * ln_out, void * stream) {
+    using namespace gsvk;
+    GSVK_REQUIRE(res && wb, "qkv_attn: null pointer");
+    QkvAttnArgs a{};
+    a.ws = wq;
+    a.wd = wd;
+    a.bias = bias;
+    a.in.mode = IN_LN;
+    a.in.res = res;
+    a.in.r = r;
+    a.in.bias = ln_bias;
+    a.in.wb = wb;
+    a.in.out_x = ln_out;
+    a.kc = k;
+    a.vc = v;
+    a.lstride = lstride;
+    a.kv_begin = kv_begin;
+    a.col_ptr = col;
+    a.col_add = 0;
+    a.n_head = nh;
+    a.scale_log2 = scale * LOG2E;
+    a.out = out;
+    a.oq = oq;
+    a.od = od;
+    return launch_qkv_attn(a, B, lstride, (hipStream_t) stream);
+}
+
+extern "C" int gsvk_qkv_attn_supported(int B, int nh, int64_t max_keys) {
+    return gsvk::qkv_attn_supported(B, nh, max_keys) ? 1 : 0;
+}

@@ -13,6 +13,7 @@
 #include "common.h"
 #include "gguf.h"
 #include "layer.h"
+#include "qkv_attn.h"
 #include "sampler.h"
 
 namespace gsvk {
@@ -391,11 +392,32 @@ int enqueue_decode_body(gsvk_model * m) {
             in.wb = p.ln2;
         }
         in.out_x = m->x.x;
-        GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, B, in,
-                                   qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
-        GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
-                                    m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
-                                    m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream));
+        if (qkv_attn_preferred(B, m->NH, m->lstride)) {
+            // QKV + attention in one launch per layer
+            QkvAttnArgs qa{};
+            qa.ws = w.qkv.qs;
+            qa.wd = w.qkv.d;
+            qa.bias = w.qkv.b;
+            qa.in = in;
+            qa.kc = m->kc + loff;
+            qa.vc = m->vc + loff;
+            qa.lstride = m->lstride;
+            qa.kv_begin = m->kv_begin;
+            qa.col_ptr = m->d_step;
+            qa.col_add = m->S - 1;
+            qa.n_head = m->NH;
+            qa.scale_log2 = scale * 1.4426950408889634f;
+            qa.out = m->attn.x;
+            qa.oq = m->attn.q;
+            qa.od = m->attn.d;
+            GSVK_TRY(launch_qkv_attn(qa, B, m->lstride, m->stream));
+        } else {
+            GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, B, in,
+                                       qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
+            GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
+                                        m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
+                                        m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream));
+        }
         GSVK_TRY(layer_tail(m, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2));
     }
     GSVK_TRY(final_ln(m, B, m->n1.x, m->h2, m->x));

@@ -25,7 +25,8 @@ EXPORTS = [
     "gsvk_prefill", "gsvk_decode_step", "gsvk_kv_read", "gsvk_last_sampled", "gsvk_op_q8_dequant",
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
-    "gsvk_sample_workspace_bytes", "gsvk_op_sample",
+    "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
+    "gsvk_qkv_attn_supported",
 ]
 
 
@@ -100,6 +101,9 @@ def lib():
         L.gsvk_attn_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i64, vp, vp, i64, f32, vp, vp, vp,
                                           vp, vp, vp]
+        L.gsvk_op_qkv_attn.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp, i64, vp, vp, f32, vp, vp,
+                                       vp, vp, vp]
+        L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
         L.gsvk_sample_workspace_bytes.argtypes = [i32]
         L.gsvk_sample_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_sample.argtypes = [vp, i32, i32, vp, i32, vp, C.POINTER(SamplerCfg), vp, vp, vp, vp, vp]
@@ -191,6 +195,19 @@ def op_attn_decode(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, 
     check(lib().gsvk_op_attn_decode(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin), _p(kv_end),
                                     max_keys, scale, _p(out), _p(out16), _p(oq), _p(od), _p(ws),
                                     _stream(stream)), "attn_decode")
+
+
+def qkv_attn_supported(B, nh, max_keys) -> bool:
+    return bool(lib().gsvk_qkv_attn_supported(B, nh, max_keys))
+
+
+def op_qkv_attn(wq, wd, bias, res, r, ln_bias, wb, k, v, kv_begin, col, scale, out, oq=None, od=None,
+                ln_out=None, stream=None):
+    B = res.shape[0]
+    _, nh, lstride, _ = k.shape
+    check(lib().gsvk_op_qkv_attn(_p(wq), _p(wd), _p(bias), _p(res), _p(r), _p(ln_bias), _p(wb), B, nh, _p(k),
+                                 _p(v), lstride, _p(kv_begin), _p(col), scale, _p(out), _p(oq), _p(od),
+                                 _p(ln_out), _stream(stream)), "qkv_attn")
 
 
 def op_sample(logits, cfg, rng, tok_out, hist=None, n_hist=None, probs_out=None, ws=None, stream=None):

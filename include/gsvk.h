@@ -219,6 +219,22 @@ int gsvk_op_add_act(const float * a, const float * b, int64_t n, int64_t ne0, in
 int gsvk_op_fdot(const void * w, int wtype, int64_t n, int64_t k, const float * x, int64_t m,
                  float * y, int mode, void * stream);
 
+/* QKV projection + decode attention of one layer in one launch (the decode path's fused kernel:
+ * the work of src/gsv_ar.cpp:392 (QKV), :398-399 (K/V append) and :404 (flash_attn_ext) for one
+ * new token per sequence). Input row b: LayerNorm((res + r) + ln_bias) with wb = [w; b] (r and
+ * ln_bias may be NULL), quantised to Q8_0; wq/wd: sliced Q8_0 QKV weights [3*512][512]; bias
+ * [3*512]. The new k, v are appended to the fp16 caches k, v [B][nh][lstride][32] at column *col
+ * (device int) and attention runs over keys [kv_begin[b], *col]. out [B][512] fp32; oq/od
+ * optional Q8_0 copy; ln_out optional LayerNorm output [B][512]. nh * 32 must be 512.
+ * Fails (GSVK_ERR_ARG) for shapes whose rows the standalone attention would split. */
+/* 1 when gsvk_op_qkv_attn accepts this shape (the standalone attention would not split rows). */
+int gsvk_qkv_attn_supported(int B, int nh, int64_t max_keys);
+int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
+                     const float * r, const float * ln_bias, const float * wb, int B, int nh,
+                     uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                     const int32_t * col, float scale, float * out, int8_t * oq, float * od,
+                     float * ln_out, void * stream);
+
 /* One call of the device sampler for B rows: gsv_logits_to_probs followed by gsv_sample with the
  * row's gsv_rng (src/gsv_sampler.cpp:8-89). Device memory: logits [B][V] (not modified);
  * hist [B][hist_stride] holding n_hist[b] tokens per row, of which the last <= 4096 are the

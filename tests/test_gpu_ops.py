@@ -329,3 +329,60 @@ def test_attn_decode_microbench_shape(gpu):
     got, scale, _ = _run_attn(gpu, torch, q, k, v, kb, ke, lstride)
     ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-3
+
+
+@pytest.mark.parametrize("B,lstride", [(16, 1000), (3, 300), (40, 200), (64, 700), (1, 64)])
+def test_qkv_attn_fused_equals_separate_kernels(gpu, B, lstride):
+    """The decode path's fused QKV + attention kernel equals the LN-input QKV GEMV, the fp16 K/V
+    append and the standalone decode attention, to the bit (output, Q8_0 copy, cache, LN row)."""
+    import torch
+    rng = np.random.default_rng(4000 + B)
+    D, nh = 512, 16
+    n = 3 * D
+    W = rng.standard_normal((n, D)).astype(np.float32) * 0.02
+    wbk = sm.q8_quantize_ref(W).ravel()
+    wq = torch.zeros(n * D, dtype=torch.int8, device="cuda")
+    wd = torch.zeros(n * D // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(wbk, torch), n, D, wq, wd)
+    bias = _dev(rng.standard_normal(n).astype(np.float32) * 0.02, torch)
+    res = _dev(rng.standard_normal((B, D)).astype(np.float32), torch)
+    r = _dev(rng.standard_normal((B, D)).astype(np.float32) * 0.5, torch)
+    lb = _dev(rng.standard_normal(D).astype(np.float32) * 0.02, torch)
+    wb = _dev(np.concatenate([1 + 0.05 * rng.standard_normal(D), 0.05 * rng.standard_normal(D)]).astype(np.float32),
+              torch)
+    kc = _dev(rng.standard_normal((B, nh, lstride, 32)).astype(np.float16), torch)
+    vc = _dev(rng.standard_normal((B, nh, lstride, 32)).astype(np.float16), torch)
+    col = lstride - 3
+    begins = rng.integers(0, col + 1, B).astype(np.int32)
+    begins[0] = 0
+    if B > 2:
+        begins[1] = col                     # only the new key is valid
+    kb = _dev(begins, torch)
+    col_d = torch.tensor([col], dtype=torch.int32, device="cuda")
+    scale = float(1.0 / np.sqrt(32.0))
+    # fused
+    k1, v1 = kc.clone(), vc.clone()
+    out1 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    oq1 = torch.zeros(B * D, dtype=torch.int8, device="cuda")
+    od1 = torch.zeros(B * nh, dtype=torch.float32, device="cuda")
+    ln1 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_qkv_attn(wq, wd, bias, res, r, lb, wb, k1, v1, kb, col_d, scale, out1, oq=oq1, od=od1, ln_out=ln1)
+    # separate kernels
+    k2, v2 = kc.clone(), vc.clone()
+    qkv = torch.zeros((B, n), dtype=torch.float32, device="cuda")
+    ln2 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_ln_gemv(wq, wd, n, res, r, lb, wb, bias, 0, qkv, ln_out=ln2)
+    k2[:, :, col, :] = qkv[:, D:2 * D].reshape(B, nh, 32).half()
+    v2[:, :, col, :] = qkv[:, 2 * D:].reshape(B, nh, 32).half()
+    out2 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    oq2 = torch.zeros(B * D, dtype=torch.int8, device="cuda")
+    od2 = torch.zeros(B * nh, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(gpu.attn_workspace_bytes(B, nh, lstride), dtype=torch.uint8, device="cuda")
+    ke = torch.full((B,), col + 1, dtype=torch.int32, device="cuda")
+    gpu.op_attn_decode(qkv[:, :D].reshape(B, nh, 32).contiguous(), k2.view(torch.int16), v2.view(torch.int16), kb,
+                       ke, lstride, scale, out2, oq=oq2, od=od2, ws=ws)
+    torch.cuda.synchronize()
+    assert torch.equal(ln1, ln2)
+    assert torch.equal(k1, k2) and torch.equal(v1, v2)
+    assert torch.equal(out1, out2), (out1 - out2).abs().max().item()
+    assert torch.equal(oq1, oq2) and torch.equal(od1, od2)
