@@ -175,6 +175,16 @@ __device__ __forceinline__ void q8_store_sliced(int8_t * row, int nblk, int blk,
     *reinterpret_cast<int *>(row + ((int64_t) (2 * sub + 1) * nblk + blk) * 4) = hi;
 }
 
+// The same with an explicit byte distance between slices (LDS copies of a row pad each slice by
+// 16 bytes, so that the 8 slices a wave reads at once fall in different banks).
+__device__ __forceinline__ void q8_store_sliced_s(int8_t * row, int slice_bytes, int blk, int sub,
+                                                  const int8_t (&q)[8]) {
+    const int lo = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    const int hi = (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((q[7] & 0xff) << 24);
+    *reinterpret_cast<int *>(row + (2 * sub) * slice_bytes + blk * 4) = lo;
+    *reinterpret_cast<int *>(row + (2 * sub + 1) * slice_bytes + blk * 4) = hi;
+}
+
 // Byte offset of value w (0..31) of block blk in a sliced row.
 __device__ __forceinline__ int64_t q8_sliced_offset(int nblk, int blk, int w) {
     return ((int64_t) (w >> 2) * nblk + blk) * 4 + (w & 3);

@@ -23,10 +23,11 @@ namespace gsvk {
 constexpr int LG_THREADS = 256;
 constexpr int LG_ROWS = 32;   // output rows per workgroup
 
-template <int NB4, int MT>
+template <int NB4, int MT, int MODE>
 __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __restrict__ ws,
                                                            const uint16_t * __restrict__ wd, int n,
                                                            int m, LayerIn in, LayerOut out) {
+    static_assert(MODE == IN_Q8 || MT <= LG_THREADS / 64, "one wave per LayerNorm / embedding row");
     constexpr int K = NB4 * 128;
     constexpr int NBLK = K / 32;
     const int tid = threadIdx.x;
@@ -39,11 +40,54 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     const bool valid = row < n;
     const int rowc = valid ? row : n - 1;
 
-    __shared__ __align__(16) int8_t s_x[MT][K];
+    // LDS copy of the sliced input rows, each slice padded by 16 bytes (bank-conflict free reads)
+    constexpr int SLICE_B = NBLK * 4 + 16;
+    __shared__ __align__(16) int8_t s_x[MT][8 * SLICE_B];
     __shared__ __align__(16) float s_d[MT][NBLK];
     __shared__ float s_out[MT][LG_ROWS];
 
-    // weights first: their HBM latency overlaps the input stage
+    // Loads go out in the order their data is needed, each thread issuing a fixed number of them
+    // (indices clamped rather than skipped, so that no wave-dependent branch separates a load
+    // from its use and every wait is exact): the input rows first, then the weights. Waiting for
+    // the input then does not wait for the weights, whose HBM latency overlaps the input stage.
+    constexpr int CH = K / 16;                                      // 16-byte chunks per row
+    constexpr int QN = (MT * CH + LG_THREADS - 1) / LG_THREADS;     // chunks per thread
+    constexpr int DN = (MT * NBLK + LG_THREADS - 1) / LG_THREADS;   // scales per thread
+    constexpr int CPS = NBLK / 4;                                   // 16-byte chunks per slice
+    int4 xq[MODE == IN_Q8 ? QN : 1];
+    float xdv[MODE == IN_Q8 ? DN : 1];
+    LnRow lnr;
+    float4 e0, e1, p0, p1;
+    const int tr = wave < MT ? wave : MT - 1;   // LN / embedding: this wave's row (waves past MT
+    const int mmr = min(m0 + tr, m - 1);        // repeat the last one and discard it)
+    int pos = 0;
+    if constexpr (MODE == IN_Q8) {
+#pragma unroll
+        for (int u = 0; u < QN; u++) {
+            int c = tid + u * LG_THREADS;
+            c = c < MT * CH ? c : MT * CH - 1;
+            const int mm = min(m0 + c / CH, m - 1);
+            xq[u] = *reinterpret_cast<const int4 *>(in.xs + (int64_t) mm * K + (c % CH) * 16);
+        }
+#pragma unroll
+        for (int u = 0; u < DN; u++) {
+            int c = tid + u * LG_THREADS;
+            c = c < MT * NBLK ? c : MT * NBLK - 1;
+            const int mm = min(m0 + c / NBLK, m - 1);
+            xdv[u] = in.xd[(int64_t) mm * NBLK + c % NBLK];
+        }
+    } else if constexpr (MODE == IN_LN) {
+        ln_row_load(in.res + (int64_t) mmr * 512, in.r ? in.r + (int64_t) mmr * 512 : g_zero_row,
+                    in.bias ? in.bias : g_zero_row, in.wb, lane, lnr);
+    } else {   // IN_EMB
+        int tk = in.tok[mmr];
+        tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
+        pos = *in.pos_ptr;
+        const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * 512 + lane * 8);
+        const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) (pos + in.pos_add) * 512 + lane * 8);
+        e0 = er[0]; e1 = er[1]; p0 = pr[0]; p1 = pr[1];
+    }
+    __builtin_amdgcn_sched_barrier(0);   // keep the input loads ahead of the weight loads
     int4 w[NB4];
     uint2 dh[NB4];
     {
@@ -56,52 +100,45 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
         }
     }
 
-    // ---- input stage ----
-    if (in.mode == IN_Q8) {
-        constexpr int CH = K / 16;   // 16-byte chunks per row
-        for (int c = tid; c < MT * CH; c += LG_THREADS) {
-            const int t = c / CH, cc = c % CH;
-            const int mm = min(m0 + t, m - 1);
-            *reinterpret_cast<int4 *>(&s_x[t][cc * 16]) =
-                *reinterpret_cast<const int4 *>(in.xs + (int64_t) mm * K + cc * 16);
+    // ---- input stage: LayerNorm / embedding arithmetic, the Q8_0 rows into LDS ----
+    if constexpr (MODE == IN_Q8) {
+#pragma unroll
+        for (int u = 0; u < QN; u++) {
+            const int c = tid + u * LG_THREADS;
+            if (c < MT * CH) {
+                const int t = c / CH, cc = c % CH;
+                *reinterpret_cast<int4 *>(&s_x[t][(cc / CPS) * SLICE_B + (cc % CPS) * 16]) = xq[u];
+            }
         }
-        for (int c = tid; c < MT * NBLK; c += LG_THREADS) {
-            const int t = c / NBLK, cc = c % NBLK;
-            const int mm = min(m0 + t, m - 1);
-            s_d[t][cc] = in.xd[(int64_t) mm * NBLK + cc];
+#pragma unroll
+        for (int u = 0; u < DN; u++) {
+            const int c = tid + u * LG_THREADS;
+            if (c < MT * NBLK) s_d[c / NBLK][c % NBLK] = xdv[u];
         }
     } else {
-        // K == 512: one wave per activation row
-        for (int t = wave; t < MT; t += LG_THREADS / 64) {
-            const int mm = min(m0 + t, m - 1);
-            float o[8];
-            if (in.mode == IN_LN) {
-                ln_row_wave(in.res + (int64_t) mm * 512, in.r ? in.r + (int64_t) mm * 512 : g_zero_row,
-                            in.bias ? in.bias : g_zero_row, in.wb, lane, o);
-            } else {   // IN_EMB
-                int tk = in.tok[mm];
-                tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
-                const int pos = *in.pos_ptr + in.pos_add;
-                const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * 512 + lane * 8);
-                const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) pos * 512 + lane * 8);
-                const float4 e0 = er[0], e1 = er[1], p0 = pr[0], p1 = pr[1];
-                const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
-                const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
+        float o[8];
+        if constexpr (MODE == IN_LN) {
+            ln_row_compute(lnr, o);
+        } else {
+            const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};
+            const float pv[8] = {p0.x, p0.y, p0.z, p0.w, p1.x, p1.y, p1.z, p1.w};
 #pragma unroll
-                for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pv[i], ev[i]);
-            }
-            if (blockIdx.x == 0 && m0 + t < m) {
+            for (int i = 0; i < 8; i++) o[i] = __builtin_fmaf(in.alpha, pv[i], ev[i]);
+        }
+        if (wave < MT) {
+            if (blockIdx.x == 0 && m0 + tr < m) {
                 if (in.out_x) {
-                    float4 * dst = reinterpret_cast<float4 *>(in.out_x + (int64_t) mm * 512 + lane * 8);
+                    float4 * dst = reinterpret_cast<float4 *>(in.out_x + (int64_t) mmr * 512 + lane * 8);
                     dst[0] = make_float4(o[0], o[1], o[2], o[3]);
                     dst[1] = make_float4(o[4], o[5], o[6], o[7]);
                 }
-                if (in.kv_end && lane == 0) in.kv_end[mm] = *in.pos_ptr + in.kv_end_add;
+                if constexpr (MODE == IN_EMB)
+                    if (in.kv_end && lane == 0) in.kv_end[mmr] = pos + in.kv_end_add;
             }
             int8_t q[8];
             const float d = q8_quantize_group<8>(o, q, 4);
-            q8_store_sliced(&s_x[t][0], NBLK, lane >> 2, lane & 3, q);
-            if ((lane & 3) == 0) s_d[t][lane >> 2] = d;
+            q8_store_sliced_s(&s_x[tr][0], SLICE_B, lane >> 2, lane & 3, q);
+            if ((lane & 3) == 0) s_d[tr][lane >> 2] = d;
         }
     }
     __syncthreads();
@@ -116,7 +153,7 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
         const float dw2 = h2f((uint16_t) (dh[i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[i].y >> 16));
 #pragma unroll
         for (int t = 0; t < MT; t++) {
-            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[t][(j * NBLK + 4 * i) * 4]);
+            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[t][j * SLICE_B + 16 * i]);
             const float4 dx = *reinterpret_cast<const float4 *>(&s_d[t][4 * i]);
             float a = acc[t];
             a = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w[i].x, xv.x, 0, false), a);
@@ -193,16 +230,27 @@ int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t
     GSVK_REQUIRE(!out.yq || (out.yd && n % 32 == 0), "layer_gemv: bad quantised output");
     GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 &&
                              out.kv_row0 + 2 * out.d_model <= n), "layer_gemv: bad KV epilogue");
+    // activation rows per workgroup: the latency of a wave's dot chain grows with the rows it
+    // carries, the weight re-reads (from L2) with the number of row tiles
     const unsigned gx = (unsigned) (n / LG_ROWS);
-#define GSVK_LG(NB4, MT)                                                                          \
-    hipLaunchKernelGGL((k_layer_gemv<NB4, MT>), dim3(gx, (unsigned) ((m + MT - 1) / MT)),        \
+#define GSVK_LG(NB4, MT, MODE)                                                                      \
+    hipLaunchKernelGGL((k_layer_gemv<NB4, MT, MODE>), dim3(gx, (unsigned) ((m + MT - 1) / MT)),     \
                        dim3(LG_THREADS), 0, stream, ws, wd, (int) n, (int) m, in, out)
     if (k == 512) {
-        if (m <= 32) GSVK_LG(4, 2);
-        else GSVK_LG(4, 4);
+        if (in.mode == IN_Q8) {
+            if (m <= 16) GSVK_LG(4, 1, IN_Q8);
+            else if (m <= 64) GSVK_LG(4, 2, IN_Q8);
+            else GSVK_LG(4, 4, IN_Q8);
+        } else if (in.mode == IN_LN) {
+            if (m <= 2) GSVK_LG(4, 2, IN_LN);
+            else GSVK_LG(4, 4, IN_LN);
+        } else {
+            if (m <= 32) GSVK_LG(4, 2, IN_EMB);
+            else GSVK_LG(4, 4, IN_EMB);
+        }
     } else {
-        if (m <= 32) GSVK_LG(16, 1);
-        else GSVK_LG(16, 2);
+        if (m <= 32) GSVK_LG(16, 1, IN_Q8);
+        else GSVK_LG(16, 2, IN_Q8);
     }
 #undef GSVK_LG
     GSVK_LAUNCH_CHECK();

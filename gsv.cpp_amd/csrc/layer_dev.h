@@ -16,17 +16,28 @@ struct LnRow {
     float4 xa, xb, ra, rb, ba, bb, wa, wbv, ca, cb;
 };
 
+// A pointer into device (global) memory, typed so that loads through it are global loads: a
+// pointer chosen between a kernel argument and a __device__ array is otherwise generic, and
+// generic (flat) loads make the compiler wait for every outstanding load before their use.
+typedef float f4v __attribute__((ext_vector_type(4)));
+typedef const f4v __attribute__((address_space(1))) * gf4ptr;
+__device__ __forceinline__ gf4ptr as_global_f4(const float * p) { return (gf4ptr) p; }
+__device__ __forceinline__ float4 ld4(gf4ptr p, int i) {
+    const f4v v = p[i];
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ void ln_row_load(const float * __restrict__ res, const float * __restrict__ r,
                                             const float * __restrict__ bias, const float * __restrict__ wb,
                                             int lane, LnRow & t) {
     const int base = lane * 8;
-    const float4 * x4 = reinterpret_cast<const float4 *>(res + base);
-    const float4 * r4 = reinterpret_cast<const float4 *>(r + base);
-    const float4 * b4 = reinterpret_cast<const float4 *>(bias + base);
-    const float4 * w4 = reinterpret_cast<const float4 *>(wb + base);
-    const float4 * c4 = reinterpret_cast<const float4 *>(wb + 512 + base);
-    t.xa = x4[0]; t.xb = x4[1]; t.ra = r4[0]; t.rb = r4[1]; t.ba = b4[0]; t.bb = b4[1];
-    t.wa = w4[0]; t.wbv = w4[1]; t.ca = c4[0]; t.cb = c4[1];
+    const gf4ptr x4 = as_global_f4(res + base);
+    const gf4ptr r4 = as_global_f4(r + base);
+    const gf4ptr b4 = as_global_f4(bias + base);
+    const gf4ptr w4 = as_global_f4(wb + base);
+    const gf4ptr c4 = as_global_f4(wb + 512 + base);
+    t.xa = ld4(x4, 0); t.xb = ld4(x4, 1); t.ra = ld4(r4, 0); t.rb = ld4(r4, 1); t.ba = ld4(b4, 0);
+    t.bb = ld4(b4, 1); t.wa = ld4(w4, 0); t.wbv = ld4(w4, 1); t.ca = ld4(c4, 0); t.cb = ld4(c4, 1);
 }
 
 __device__ __forceinline__ void ln_row_compute(const LnRow & t, float (&o)[8]) {

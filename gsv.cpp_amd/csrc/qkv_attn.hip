@@ -45,7 +45,8 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     const int rsub = lane >> 3;   // GEMV: row within the wave's 8
     const int j = lane & 7;       // GEMV: slice lane
 
-    __shared__ __align__(16) int8_t s_x[QA_K];
+    constexpr int SLICE_B = QA_NBLK * 4 + 16;   // slices padded by 16 bytes: conflict-free reads
+    __shared__ __align__(16) int8_t s_x[8 * SLICE_B];
     __shared__ __align__(16) float s_d[QA_NBLK];
     __shared__ __align__(16) float s_q[ATT_HD];
     __shared__ __align__(16) uint16_t s_kv[2][ATT_HD];
@@ -107,7 +108,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
         }
         int8_t q[8];
         const float d = q8_quantize_group<8>(o, q, 4);
-        q8_store_sliced(s_x, QA_NBLK, lane >> 2, lane & 3, q);
+        q8_store_sliced_s(s_x, SLICE_B, lane >> 2, lane & 3, q);
         if ((lane & 3) == 0) s_d[lane >> 2] = d;
     }
 
@@ -142,7 +143,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
         for (int i = 0; i < QA_NB4; i++) {
             const float dw0 = h2f((uint16_t) (dh[p][i].x & 0xffff)), dw1 = h2f((uint16_t) (dh[p][i].x >> 16));
             const float dw2 = h2f((uint16_t) (dh[p][i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[p][i].y >> 16));
-            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[(j * QA_NBLK + 4 * i) * 4]);
+            const int4 xv = *reinterpret_cast<const int4 *>(&s_x[j * SLICE_B + 16 * i]);
             const float4 dx = *reinterpret_cast<const float4 *>(&s_d[4 * i]);
             acc = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w[p][i].x, xv.x, 0, false), acc);
             acc = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w[p][i].y, xv.y, 0, false), acc);
