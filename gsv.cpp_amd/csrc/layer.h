@@ -54,6 +54,14 @@ struct LayerOut {
     int col_add;
 };
 
+// Q8_0 x Q8_0 GEMM on the matrix cores (gemm.hip) with the same epilogue options: n % 128 == 0,
+// k in {512, 2048}; the input rows are sliced Q8_0 (xs [m][k], fp32 scales xd [m][k/32]).
+int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
+                   const int8_t * xs, const float * xd, const LayerOut & out, hipStream_t stream);
+
+// Row count from which the projections run on launch_q8_gemm rather than the GEMV.
+constexpr int64_t GEMM_MIN_ROWS = 64;
+
 // n % 32 == 0, k in {512, 2048}; IN_LN and IN_EMB need k == 512.
 int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
                       const LayerIn & in, const LayerOut & out, hipStream_t stream);

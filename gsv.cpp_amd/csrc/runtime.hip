@@ -298,8 +298,29 @@ int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
 //   h2 = W2 . hq
 // LN2 (cur' = LN2(n1 + h2 + b2)) is the input stage of the next layer's QKV or of final_ln().
 int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
-               float * o, float * n1x, Act & hq, float * h2) {
+               float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr) {
     const int D = m->D, F = m->FFN;
+    if (R >= GEMM_MIN_ROWS && n1) {
+        // many rows: the projections on the matrix cores, LN1 as its own launch (with the Q8_0 copy
+        // the FFN1 GEMM reads)
+        LayerOut oo{};
+        oo.y = o;
+        oo.y_stride = D;
+        oo.n_store = D;
+        GSVK_TRY(launch_q8_gemm(w.out.qs, w.out.d, D, D, R, attn.q, attn.d, oo, m->stream));
+        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream));
+        LayerOut ho{};
+        ho.bias = w.f1.b;
+        ho.act = 1;
+        ho.yq = hq.q;
+        ho.yd = hq.d;
+        GSVK_TRY(launch_q8_gemm(w.f1.qs, w.f1.d, F, D, R, n1->q, n1->d, ho, m->stream));
+        LayerOut h2o{};
+        h2o.y = h2;
+        h2o.y_stride = D;
+        h2o.n_store = D;
+        return launch_q8_gemm(w.f2.qs, w.f2.d, D, F, R, hq.q, hq.d, h2o, m->stream);
+    }
     LayerIn qin{};
     qin.mode = IN_Q8;
     qin.xs = attn.q;
@@ -560,25 +581,36 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
-        LayerIn in{};
-        if (li == 0) {
-            in.mode = IN_Q8;
-            in.xs = cur.q;
-            in.xd = cur.d;
+        const bool gemm = rows >= GEMM_MIN_ROWS;
+        if (gemm) {
+            // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
+            if (li > 0) {
+                const LayerW & p = m->L[li - 1];
+                GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st));
+            }
+            GSVK_TRY(launch_q8_gemm(w.qkv.qs, w.qkv.d, 3 * D, D, rows, cur.q, cur.d,
+                                    qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         } else {
-            const LayerW & p = m->L[li - 1];
-            in.mode = IN_LN;
-            in.res = n1.x;
-            in.r = h2;
-            in.bias = p.f2.b;
-            in.wb = p.ln2;
-            in.out_x = cur.x;
+            LayerIn in{};
+            if (li == 0) {
+                in.mode = IN_Q8;
+                in.xs = cur.q;
+                in.xd = cur.d;
+            } else {
+                const LayerW & p = m->L[li - 1];
+                in.mode = IN_LN;
+                in.res = n1.x;
+                in.r = h2;
+                in.bias = p.f2.b;
+                in.wb = p.ln2;
+                in.out_x = cur.x;
+            }
+            GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
+                                       qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         }
-        GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
-                                   qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                      attn.d, st));
-        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2));
+        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2, &n1));
     }
     GSVK_TRY(final_ln(m, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));

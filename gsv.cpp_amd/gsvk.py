@@ -26,7 +26,7 @@ EXPORTS = [
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
     "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
-    "gsvk_qkv_attn_supported",
+    "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm",
 ]
 
 
@@ -104,6 +104,7 @@ def lib():
         L.gsvk_op_qkv_attn.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp, i64, vp, vp, f32, vp, vp,
                                        vp, vp, vp]
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
+        L.gsvk_op_q8_gemm.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
         L.gsvk_sample_workspace_bytes.argtypes = [i32]
         L.gsvk_sample_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_sample.argtypes = [vp, i32, i32, vp, i32, vp, C.POINTER(SamplerCfg), vp, vp, vp, vp, vp]
@@ -161,6 +162,11 @@ def op_q8_quantize(x, xq, xd, stream=None):
 def op_q8_gemv(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
     check(lib().gsvk_op_q8_gemv(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y),
                                 _stream(stream)), "q8_gemv")
+
+
+def op_q8_gemm(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
+    check(lib().gsvk_op_q8_gemm(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y), _stream(stream)),
+          "q8_gemm")
 
 
 def op_ln_gemv(wq, wd, n, res, r, ln_bias, wb, bias, act, y, ln_out=None, stream=None):

@@ -194,6 +194,14 @@ int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
                     const int8_t * xq, const float * xd, int64_t m, const float * bias, int act,
                     float * y, void * stream);
 
+/* Q8_0 x Q8_0 GEMM on the matrix cores (int8 MFMA, one 32-value block per instruction, fp32
+ * per-block scaling): the projections of src/gsv_ar.cpp:244-263 over many rows (prefill, decode
+ * at large batch). Same operands and result as gsvk_op_q8_gemv; the fp32 accumulation runs block
+ * by block instead of in ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must
+ * be a multiple of 128, k 512 or 2048. */
+int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xq,
+                    const float * xd, int64_t m, const float * bias, int act, float * y, void * stream);
+
 /* y = W . Q8_0(LayerNorm((res + r) + ln_bias) * wb[0:512] + wb[512:1024]) (+ bias) then act:
  * the decoder's fused kernel with its LayerNorm input stage (rows of 512; n % 32 == 0). The
  * LayerNorm output is also stored to ln_out when given. r, ln_bias, bias may be NULL. */

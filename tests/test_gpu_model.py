@@ -38,8 +38,9 @@ def test_first_logits_parity(models):
 
 
 def test_left_padding_invariance(models):
+    """(GEMV path: fewer than 64 prefill rows in the batch and alone.)"""
     g, _ = models
-    reqs = _reqs(2, [3, 17, 9])
+    reqs = _reqs(2, [3, 17, 9], P=4)            # S = 21, 63 rows
     batch = g.first_logits(reqs)
     for b in range(3):
         alone = g.first_logits([reqs[b]])
@@ -56,6 +57,32 @@ def test_kv_write_layer0_bitexact(models):
     vd = v_dev[:, :, :S, :].view(np.float16).astype(np.float32)
     assert np.array_equal(kd, k_ref)
     assert np.array_equal(vd, v_ref)
+
+
+def test_prefill_on_matrix_cores(models):
+    """Prefills of 64 rows and more run the projections on the MFMA GEMM (fp32 accumulation per
+    block, not in ggml-cpu's 8-lane order): logits within 2e-3 of the oracle, the layer-0 K/V
+    within one fp16 ulp of the oracle's (the fp32 values differ by rounding, which can move a
+    value across an fp16 rounding boundary), and left padding still changes nothing."""
+    g, o = models
+    reqs = _reqs(11, [70, 100, 64])            # S = 116, 348 rows; alone: >= 80 rows
+    got = g.first_logits(reqs)
+    ref = o.first_logits(reqs)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-3
+    _, S = g.prefill(reqs)
+    k_dev, v_dev = g.kv_read(0)
+    k_ref, v_ref, _ = o.prefill_kv(reqs, 0, flags=O.ORC_KV_F16)
+    for dev, ref16 in ((k_dev, k_ref), (v_dev, v_ref)):
+        d = dev[:, :, :S, :].view(np.float16).astype(np.float32)
+        r = ref16
+        # one fp16 ulp of the value, or (near zero) an fp32 rounding of the largest value
+        ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float32)
+        tol = np.maximum(ulp, 1e-6 * np.abs(r).max())
+        assert np.all(np.abs(d - r) <= tol), np.abs(d - r).max()
+        assert np.mean(d != r) <= 0.01
+    for b in range(3):
+        alone = g.first_logits([reqs[b]])
+        assert np.array_equal(got[b], alone[0]), b
 
 
 def test_kv_append_matches_prefill(models):

@@ -386,3 +386,35 @@ def test_qkv_attn_fused_equals_separate_kernels(gpu, B, lstride):
     assert torch.equal(k1, k2) and torch.equal(v1, v2)
     assert torch.equal(out1, out2), (out1 - out2).abs().max().item()
     assert torch.equal(oq1, oq2) and torch.equal(od1, od2)
+
+
+@pytest.mark.parametrize("n,k", [(1536, 512), (512, 512), (2048, 512), (512, 2048)])
+@pytest.mark.parametrize("m", [1, 16, 100, 300, 1024])
+def test_q8_gemm_matches_oracle(gpu, n, k, m):
+    """The MFMA GEMM computes the same Q8_0 products as ggml-cpu's mul_mat; only the fp32
+    accumulation order differs (per block instead of 8 lanes + hsum): within 2e-6 of the output
+    scale, i.e. a few fp32 ulps."""
+    import torch
+    rng = np.random.default_rng(7000 + n + k + m)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    X[0, :64] = 0.0
+    wb = sm.q8_quantize_ref(W).ravel()
+    wq = torch.zeros(n * k, dtype=torch.int8, device="cuda")
+    wd = torch.zeros(n * k // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(wb, torch), n, k, wq, wd)
+    xq = torch.zeros(m * k, dtype=torch.int8, device="cuda")
+    xd = torch.zeros(m * k // 32, dtype=torch.float32, device="cuda")
+    gpu.op_q8_quantize(_dev(X, torch), xq, xd)
+    bias = rng.standard_normal(n).astype(np.float32) * 0.02
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemm(wq, wd, n, k, xq, xd, m, None, 0, y)
+    y2 = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemm(wq, wd, n, k, xq, xd, m, _dev(bias, torch), 1, y2)
+    torch.cuda.synchronize()
+    ref = O.q8_matmul(wb, n, k, X)
+    got = y.cpu().numpy()
+    scale = np.abs(ref).max()
+    assert np.abs(got - ref).max() <= 2e-6 * scale, np.abs(got - ref).max() / scale
+    ref2 = np.maximum(ref + bias[None, :], 0.0)
+    assert np.abs(y2.cpu().numpy() - ref2).max() <= 2e-6 * scale
