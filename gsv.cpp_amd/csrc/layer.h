@@ -62,6 +62,12 @@ int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
 // Row count from which the projections run on launch_q8_gemm rather than the GEMV.
 constexpr int64_t GEMM_MIN_ROWS = 64;
 
+// Prefill self-attention on the matrix cores (attn_prefill_mfma.hip): qkv rows [B][S][3*d_model],
+// head_dim 32, 16-byte aligned qkv and out; used from GEMM_MIN_ROWS rows on, like the GEMM.
+int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                             int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream);
+inline bool attn_prefill_uses_mfma(int64_t rows) { return rows >= GEMM_MIN_ROWS; }
+
 // n % 32 == 0, k in {512, 2048}; IN_LN and IN_EMB need k == 512.
 int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
                       const LayerIn & in, const LayerOut & out, hipStream_t stream);

@@ -608,8 +608,12 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
                                        qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         }
-        GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
-                                     attn.d, st));
+        if (attn_prefill_uses_mfma(rows))
+            GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
+                                              attn.d, st));
+        else
+            GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
+                                         attn.d, st));
         GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2, &n1));
     }
     GSVK_TRY(final_ln(m, rows, n1.x, h2, cur));

@@ -26,7 +26,7 @@ EXPORTS = [
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
     "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
-    "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm",
+    "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_attn_prefill",
 ]
 
 
@@ -105,6 +105,7 @@ def lib():
                                        vp, vp, vp]
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
         L.gsvk_op_q8_gemm.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
+        L.gsvk_op_attn_prefill.argtypes = [vp, i32, i32, i32, vp, i32, i32, f32, i32, vp, vp, vp, vp]
         L.gsvk_sample_workspace_bytes.argtypes = [i32]
         L.gsvk_sample_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_sample.argtypes = [vp, i32, i32, vp, i32, vp, C.POINTER(SamplerCfg), vp, vp, vp, vp, vp]
@@ -201,6 +202,15 @@ def op_attn_decode(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, 
     check(lib().gsvk_op_attn_decode(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin), _p(kv_end),
                                     max_keys, scale, _p(out), _p(out16), _p(oq), _p(od), _p(ws),
                                     _stream(stream)), "attn_decode")
+
+
+def op_attn_prefill(qkv, max_len, pad, nh, scale, out, oq=None, od=None, path=0, stream=None):
+    """qkv [B][S][3*D] fp32, pad int32 [B] (device); out [B][S][D]; path 0 auto, 1 lane-per-query,
+    2 matrix cores."""
+    B, S, three_d = qkv.shape
+    hd = three_d // 3 // nh
+    check(lib().gsvk_op_attn_prefill(_p(qkv), B, S, max_len, _p(pad), nh, hd, scale, path, _p(out), _p(oq),
+                                     _p(od), _stream(stream)), "attn_prefill")
 
 
 def qkv_attn_supported(B, nh, max_keys) -> bool:

@@ -265,6 +265,16 @@ int gsvk_op_attn_decode(const float * q, const uint16_t * k, const uint16_t * v,
                         int64_t max_keys, float scale, float * out, uint16_t * out_f16,
                         int8_t * oq, float * od, void * ws, void * stream);
 
+/* Prefill self-attention (the flash_attn_ext of src/gsv_ar.cpp:257 over all B*S rows, masks of
+ * src/gsv_ar.cpp:215-223): qkv fp32 [B][S][3*nh*hd] (Q, K, V of head h at h*hd, D + h*hd,
+ * 2*D + h*hd); pad device int32 [B]; query s of sequence b sees keys [pad[b], max_len) when
+ * s < max_len, else [pad[b], s]. out fp32 [B][S][nh*hd]; oq/od (both or neither) its Q8_0 copy
+ * (sliced quants, fp32 scales). path 0 picks the kernel the prefill uses for B*S rows, 1 the
+ * lane-per-query kernel, 2 the matrix-core kernel. hd must be 32; qkv and out 16-byte aligned. */
+int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                         int hd, float scale, int path, float * out, int8_t * oq, float * od,
+                         void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -661,6 +661,33 @@ static inline float kv_round(float x, unsigned flags) {
 }
 
 /* prefill (run_first, src/gsv_ar.cpp:228-293). Returns last-position logits [B][V]. */
+/* prefill self-attention (src/gsv_ar.cpp:215-223 masks, :257 flash_attn_ext): qkv [B][S][3*D]
+ * (Q, K, V of head h at h*hd, D + h*hd, 2*D + h*hd); query qi of sequence b sees keys
+ * [pad[b], max_len) when qi < max_len, else [pad[b], qi]. out [B][S][D]. */
+void orc_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                      int hd, float scale, float * out, int nt) {
+    const int D = nh * hd;
+#pragma omp parallel for num_threads(nt) schedule(dynamic, 1) collapse(2)
+    for (int b = 0; b < B; b++)
+        for (int hh = 0; hh < nh; hh++) {
+            uint8_t * skip = (uint8_t *) malloc((size_t) S);
+            for (int qi = 0; qi < S; qi++) {
+                for (int k = 0; k < S; k++) {
+                    int mk;
+                    if (k < pad[b]) mk = 1;
+                    else if (qi < max_len) mk = (k >= max_len);
+                    else mk = (k > qi);
+                    skip[k] = (uint8_t) mk;
+                }
+                const float * base = qkv + (size_t) b * S * 3 * D;
+                orc_attn_row(base + (size_t) qi * 3 * D + hh * hd, base + D + hh * hd,
+                             base + 2 * D + hh * hd, 3 * D, hd, S, skip, scale,
+                             out + ((size_t) b * S + qi) * D + hh * hd);
+            }
+            free(skip);
+        }
+}
+
 static void prefill(const orc_model * m, const orc_request * reqs, int B, int S, int max_len,
                     cache_t * c, unsigned flags, int nt, float * logits) {
     const int D = m->D, NH = m->NH, HD = m->HD, F = m->FFN, BD = m->BERT;
@@ -700,26 +727,12 @@ static void prefill(const orc_model * m, const orc_request * reqs, int B, int S,
         orc_q8_matmul(L->qkv.q8, 3 * D, D, cur, R, qkv, nt);
         for (int64_t r = 0; r < R; r++)
             for (int i = 0; i < 3 * D; i++) qkv[r * 3 * D + i] = qkv[r * 3 * D + i] + L->qkv.b[i];
-#pragma omp parallel for num_threads(nt) schedule(dynamic, 1) collapse(2)
-        for (int b = 0; b < B; b++)
-            for (int hh = 0; hh < NH; hh++) {
-                const int pad = max_len - reqs[b].n_phones;
-                uint8_t * skip = (uint8_t *) malloc((size_t) S);
-                for (int qi = 0; qi < S; qi++) {
-                    for (int k = 0; k < S; k++) {
-                        int mk;
-                        if (k < pad) mk = 1;
-                        else if (qi < max_len) mk = (k >= max_len);
-                        else mk = (k > qi);
-                        skip[k] = (uint8_t) mk;
-                    }
-                    const float * base = qkv + (size_t) b * S * 3 * D;
-                    orc_attn_row(base + (size_t) qi * 3 * D + hh * HD, base + D + hh * HD,
-                                 base + 2 * D + hh * HD, 3 * D, HD, S, skip, scale,
-                                 attn + ((size_t) b * S + qi) * D + hh * HD);
-                }
-                free(skip);
-            }
+        {
+            int32_t * pads = (int32_t *) malloc(sizeof(int32_t) * (size_t) B);
+            for (int b = 0; b < B; b++) pads[b] = max_len - reqs[b].n_phones;
+            orc_attn_prefill(qkv, B, S, max_len, pads, NH, HD, scale, attn, nt);
+            free(pads);
+        }
         /* KV cache copy of all S positions (:271-275) */
         for (int b = 0; b < B; b++)
             for (int s = 0; s < S; s++)

@@ -92,6 +92,12 @@ void orc_attn_decode_f16(const float * q, const uint16_t * k, const uint16_t * v
                          int hd, int64_t lstride, const int32_t * kv_begin,
                          const int32_t * kv_end, float scale, float * out, int nthreads);
 
+/* prefill self-attention over fp32 qkv rows [B][S][3*nh*hd] with the reference's masks
+ * (src/gsv_ar.cpp:215-223): query qi of sequence b sees keys [pad[b], max_len) when
+ * qi < max_len (text rows), else [pad[b], qi] (causal semantic rows). out [B][S][nh*hd]. */
+void orc_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                      int hd, float scale, float * out, int nthreads);
+
 /* ---- sampler (src/gsv_sampler.cpp) ---- */
 void     orc_logits_to_probs(int top_k, float top_p, float temperature, float rep, float * logits,
                              int V, const int32_t * prev, int n_prev, float * probs);

@@ -69,6 +69,8 @@ def lib():
         L.orc_attn_row.argtypes = [_f32p, _f32p, _f32p, C.c_int64, C.c_int, C.c_int64, C.c_void_p, C.c_float, _f32p]
         L.orc_attn_decode_f16.argtypes = [_f32p, _u16p, _u16p, C.c_int, C.c_int, C.c_int, C.c_int64,
                                           _i32p, _i32p, C.c_float, _f32p, C.c_int]
+        L.orc_attn_prefill.argtypes = [_f32p, C.c_int, C.c_int, C.c_int, _i32p, C.c_int, C.c_int, C.c_float,
+                                       _f32p, C.c_int]
         L.orc_logits_to_probs.argtypes = [C.c_int, C.c_float, C.c_float, C.c_float, _f32p, C.c_int,
                                           C.c_void_p, C.c_int, _f32p]
         L.orc_rng_next.restype = C.c_uint64
@@ -188,6 +190,17 @@ def attn_decode_f16(q, k16, v16, kv_begin, kv_end, scale, nthreads=None):
     lib().orc_attn_decode_f16(q, np.ascontiguousarray(k16), np.ascontiguousarray(v16), B, nh, hd, lstride,
                               np.ascontiguousarray(kv_begin, np.int32), np.ascontiguousarray(kv_end, np.int32),
                               scale, out, nthreads or nthreads_default())
+    return out
+
+
+def attn_prefill(qkv, max_len, pad, nh, scale, nthreads=None):
+    """Prefill self-attention: qkv fp32 [B][S][3*nh*hd]; returns [B][S][nh*hd]."""
+    qkv = np.ascontiguousarray(qkv, np.float32)
+    B, S, three_d = qkv.shape
+    D = three_d // 3
+    out = np.zeros((B, S, D), np.float32)
+    lib().orc_attn_prefill(qkv, B, S, max_len, np.ascontiguousarray(pad, np.int32), nh, D // nh, scale, out,
+                           nthreads or nthreads_default())
     return out
 
 

@@ -418,3 +418,37 @@ def test_q8_gemm_matches_oracle(gpu, n, k, m):
     assert np.abs(got - ref).max() <= 2e-6 * scale, np.abs(got - ref).max() / scale
     ref2 = np.maximum(ref + bias[None, :], 0.0)
     assert np.abs(y2.cpu().numpy() - ref2).max() <= 2e-6 * scale
+
+
+@pytest.mark.parametrize("B,S,max_len,pads,what", [
+    (3, 300, 100, [0, 17, 60], "text + causal semantic rows, left pads, ragged last tile"),
+    (1, 64, 64, [5], "text rows only"),
+    (2, 130, 1, [0, 0], "one text row; every other row causal"),
+    (2, 33, 20, [19, 3], "a one-key text span; 33 rows"),
+    (2, 1024, 300, [0, 123], "long prompt (1024 rows of which 724 semantic)"),
+])
+@pytest.mark.parametrize("path", [1, 2])
+def test_attn_prefill_matches_oracle(gpu, B, S, max_len, pads, what, path):
+    """Both prefill-attention kernels (1: lane per query, 2: matrix cores with fp16 hi + lo
+    operands) against the oracle; the Q8_0 copy is the x86 quantisation of the fp32 output."""
+    import torch
+    nh, D = 16, 512
+    rng = np.random.default_rng(40 + S + path)
+    qkv = rng.standard_normal((B, S, 3 * D)).astype(np.float32)
+    qkv[:, :, :D] *= 2.0            # sharper softmax than unit scores
+    pad = np.array(pads, np.int32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(32)))
+    out = torch.zeros(B * S * D, dtype=torch.float32, device="cuda")
+    oq = torch.zeros(B * S * D, dtype=torch.int8, device="cuda")
+    od = torch.zeros(B * S * D // 32, dtype=torch.float32, device="cuda")
+    gpu.op_attn_prefill(_dev(qkv, torch), max_len, _dev(pad, torch), nh, scale, out, oq, od, path=path)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(B, S, D)
+    ref = O.attn_prefill(qkv, max_len, pad, nh, scale)
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    assert rel <= 2e-3, rel
+    assert rel <= 2e-5, rel   # fp32 (or hi + lo split) products with fp32 accumulation
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(got.reshape(B * S, D)), B * S, D)
+    assert np.array_equal(unslice(oq.cpu().numpy(), D), q_ref)
+    d_ref32 = d_ref.view(np.float16).astype(np.float32)
+    assert np.array_equal(od.cpu().numpy().reshape(B * S, -1).view(np.uint32), d_ref32.view(np.uint32))

@@ -8,7 +8,7 @@ Every function of the oracle is checked against something other than itself:
   * LayerNorm against closed forms (constant row, 1..512) and fp64;
   * add + activation against the reference's own fixture (tests/test_add_act.cpp:66-101);
   * the PE table against fp64 sin/cos;
-  * attention against an fp64 softmax and its invariants;
+  * attention against an fp64 softmax and its invariants, the prefill masks by perturbation;
   * masks and the generate loop against properties of src/gsv_ar.cpp (left padding changes
     nothing, text queries never see semantic keys, causality) and hand-derived traces of the loop.
 """
@@ -259,6 +259,43 @@ def test_attention_row_bruteforce_and_invariants():
     out = np.zeros(32, np.float32)
     lib.orc_attn_row(q, k[:3].copy(), v[:3].copy(), 32, 32, 3, one.ctypes.data, scale, out)
     assert np.array_equal(out, v[1])
+
+
+def test_attention_prefill_masks_by_perturbation():
+    """Prefill attention: every output row is the fp64 softmax over some key set; which set is
+    fixed by perturbing K/V rows and seeing which outputs move (a text query never sees a
+    semantic key or a left-pad key; a semantic query sees itself and nothing after it)."""
+    rng = np.random.default_rng(9)
+    B, S, max_len, nh, hd = 2, 40, 15, 2, 32
+    D = nh * hd
+    pad = np.array([0, 6], np.int32)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(hd)))
+    qkv = rng.standard_normal((B, S, 3 * D)).astype(np.float32)
+    out = O.attn_prefill(qkv, max_len, pad, nh, scale, nthreads=2)
+    # each row equals the fp64 softmax over the key set the perturbations below establish
+    for b in range(B):
+        for s in range(S):
+            keys = np.arange(pad[b], max_len if s < max_len else s + 1)
+            for h in range(nh):
+                q = qkv[b, s, h * hd:(h + 1) * hd]
+                k = qkv[b, keys, D + h * hd:D + (h + 1) * hd]
+                v = qkv[b, keys, 2 * D + h * hd:2 * D + (h + 1) * hd]
+                ref = _attn64(q, k, v, np.zeros(len(keys), bool), scale)
+                assert np.allclose(out[b, s, h * hd:(h + 1) * hd], ref, rtol=0, atol=2e-6)
+    for b in range(B):
+        for j in range(S):
+            p = qkv.copy()
+            p[b, j, D:] = rng.standard_normal(2 * D) * 5
+            o2 = O.attn_prefill(p, max_len, pad, nh, scale, nthreads=2)
+            moved = np.any(o2[b] != out[b], axis=1)
+            assert np.array_equal(o2[1 - b], out[1 - b])
+            if j < pad[b]:
+                expect = np.zeros(S, bool)                           # left pad: seen by nobody
+            elif j < max_len:
+                expect = np.ones(S, bool)                            # text key: seen by all
+            else:
+                expect = np.arange(S) >= j                           # semantic key: itself and later
+            assert np.array_equal(moved, expect), (b, j)
 
 
 # ------------------------------------------------------------------------------- model semantics
