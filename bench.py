@@ -34,6 +34,7 @@ for _p in (os.path.join(ROOT, "gsv.cpp_amd"), os.path.join(ROOT, "oracle")):
 import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
 SEED = 0x6A5E0002
 N_LAYER, D, NH, HD, FFN, V = 24, 512, 16, 32, 2048, 1025
 
@@ -58,6 +59,30 @@ def decode_bytes_per_step(reqs, step_kv):
     kv_read = int(valid.sum()) * N_LAYER * 2 * D * 2
     kv_write = len(reqs) * N_LAYER * 2 * D * 2
     return w + small + head + kv_read + kv_write
+
+
+def prefill_requests(B=16, S=1024, P=256, lo=512, seed=0x6A5E0004, bert=True):
+    """Prefill workload: B sequences of valid length U[lo, S] from the seed (one of them exactly S),
+    each P shared prompt codes after L_b - P phones, so that the padded batch is B x S rows."""
+    import synth_model as sm
+    rng = np.random.Generator(np.random.PCG64(seed))
+    L = rng.integers(lo, S + 1, B)
+    L[0] = S
+    return sm.synth_requests(seed, B, P, L - P, bert=bert)
+
+
+def prefill_flops(reqs):
+    """Algorithmic FLOPs of the prefill over the valid rows: the Q8_0 projections (2 per weight per
+    row) and attention (QK^T and PV, 4 * head_dim per query-key pair over the reference's masks:
+    text rows see the T_b text keys, the semantic row j (0-based) sees T_b + j + 1 keys)."""
+    P = len(reqs[0]["prompt"])
+    proj = 2 * (3 * D * D + D * D + 2 * FFN * D)
+    f = 0
+    for r in reqs:
+        T = len(r["phones"])
+        pairs = T * T + sum(T + j + 1 for j in range(P))
+        f += (T + P) * proj + pairs * NH * 4 * HD
+    return f * N_LAYER
 
 
 def time_events(fn, iters, torch):
@@ -231,6 +256,26 @@ def cpu_baseline(reqs, steps):
                       f"{steps} decode steps timed; F32 KV cache, OpenMP over {nthreads} threads"}
 
 
+def prefill_line(g, torch):
+    """Prefill of batch 16 x 1024 rows (valid lengths U[512, 1024], 256 prompt codes), 24 layers:
+    median wall time of 3 calls after one warm-up, and TFLOP/s over prefill_flops."""
+    pr = prefill_requests()
+    g.first_logits(pr)
+    torch.cuda.synchronize()
+    t = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        g.first_logits(pr)
+        t.append(time.perf_counter() - t0)
+    pf_s = float(np.median(t))
+    fl = prefill_flops(pr)
+    return {"ms": round(pf_s * 1e3, 2), "tflops": round(fl / pf_s / 1e12, 1),
+            "frac_fp16_peak": round(fl / pf_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
+            "algorithmic_tflop": round(fl / 1e12, 3),
+            "workload": "16 x 1024 rows, valid U[512,1024], 256 prompt codes, wall time of the whole "
+                        "prefill call incl. head logits"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,6 +285,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=500)
+    ap.add_argument("--no-b128", action="store_true", help="skip the batch-128 long-context decode line")
+    ap.add_argument("--prefill-only", action="store_true", help="time only the batch-16 x 1024 prefill")
     ap.add_argument("--kernels-only", action="store_true",
                     help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
@@ -264,6 +311,10 @@ def main():
         return
     path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
     g = gsvk.Model(path, device=0)
+    if args.prefill_only:
+        print(json.dumps({"prefill_b16_s1024": prefill_line(g, torch)}))
+        g.close()
+        return
     cfg = (15, 1.0, 1.0, 1.35)
     flags = gsvk.GSVK_GEN_EOS_MASK_ALL
 
@@ -301,6 +352,22 @@ def main():
     _, rb, _ = run(64, 200, 8)
     extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)
     extra["ms_per_step_b64"] = round(rb["decode_ms"] / 200, 4)
+    extra["prefill_b16_s1024"] = prefill_line(g, torch)
+    # high-batch long context: batch 128, KV lengths U[1024, 4096] (64 prompt codes), 256 greedy steps
+    if not args.no_b128:
+        hb = prefill_requests(B=128, S=4096, P=64, lo=1024, seed=0x6A5E0005, bert=False)
+        seeds = list(range(1, 129))
+        g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=4, seeds=seeds, flags=flags)
+        rb = g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=256, seeds=seeds, flags=flags)
+        ms5 = rb["decode_ms"] / 256
+        b5 = np.mean([decode_bytes_per_step(hb, s) for s in range(0, 256, 16)])
+        extra["b128_long"] = {"tok_s": round(128 * 256 / (rb["decode_ms"] / 1e3), 1), "ms_per_step": round(ms5, 4),
+                              "step_bytes_mb": round(b5 / 1e6, 1),
+                              "step_hbm_frac": round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                              "prefill_ms": round(rb["prefill_ms"], 1),
+                              "workload": "128 sequences, KV lengths U[1024,4096] (phones + 64 prompt codes, "
+                                          "no BERT features), 256 greedy steps"}
+        g.release_cache()
     g.close()
 
     roof = None

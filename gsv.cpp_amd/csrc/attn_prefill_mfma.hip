@@ -19,7 +19,8 @@
 //     -> the P^T operand is taken straight from those registers (keys in their native order:
 //        4h..4h+3, 8+4h..8+4h+3 for the first 16, +16 for the second), and the V^T operand is
 //        read from LDS in the same key order, so the product sums over the right keys.
-// The online softmax runs in log2 units (exp2); the output is divided by the final sum.
+// The online softmax runs in log2 units (exp2); the output is divided by the final sum. Key tiles
+// start at the sequence's first valid key, so left padding changes no result bit.
 #include "common.h"
 #include "layer.h"
 
@@ -115,7 +116,8 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const int ke_w = min(key_end(qlast_w), S);            // the wave's last query sees the most keys
     const int qlast_g = min(q0w + PM_Q * PM_WAVES - 1, S - 1);
     const int ke_g = min(key_end(qlast_g), S);
-    const int kt0 = (pb / PM_KT) * PM_KT;
+    // tiles start at the first valid key: a sequence's arithmetic does not depend on its left pad
+    const int kt0 = pb;
 
     // Q^T operand (B): query q, dims 16c + 8*lh + [0, 8), split hi + lo
     v8h qh[2], ql[2];

@@ -44,6 +44,13 @@ def model4_path():
 
 
 @pytest.fixture(scope="session")
+def model24_path():
+    """The 24-layer synthetic model of the benchmark workloads, F16 head."""
+    import synth_model
+    return synth_model.cached_model(FIXTURE_DIR, n_layer=24)
+
+
+@pytest.fixture(scope="session")
 def gpu():
     import torch
     if not torch.cuda.is_available():

@@ -1,0 +1,109 @@
+"""Parity at the workload shapes of the benchmark, with the 24-layer model, through properties
+that hold at any size and an oracle check on the sequence the oracle finishes in seconds.
+
+* Prefill of 16 sequences x 1024 rows (valid lengths U[512, 1024], 256 prompt codes; projections
+  on the int8 matrix cores, attention on the fp16 matrix cores): each sequence prefilled alone
+  gives bit-identical logits (left padding and the rest of the batch change nothing); for the
+  shortest one the layer-0 K/V cache is within one fp16 ulp of the oracle's and the greedy token
+  of the first logits is the oracle's. Over 24 layers the logits themselves drift from the
+  oracle's by about 1e-2 relative: every layer re-quantises its activations to Q8_0, so a single
+  rounding-level difference (the device and host expf differ in the last bit now and then) flips
+  one int8 value, which moves its whole row by ~1e-3 and spreads through attention. The same drift
+  appears with the bit-exact GEMV and the lane-per-query attention, so the bound below (2e-2) is
+  that of the model's re-quantisation, not of the matrix-core kernels, whose own outputs are
+  checked to 2e-3 (in practice ~1e-6) op by op.
+* Decode at batch 128 with KV lengths U[1024, 4096] (27 GB fp16 KV cache): teacher-forced greedy
+  steps; the shortest sequence's sampled tokens equal the oracle's run of that sequence alone,
+  except where the oracle's top two logits are within 2e-3 of each other.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import synth_model as sm
+
+pytestmark = pytest.mark.gpu
+
+
+def _lengths(seed, B, lo, hi):
+    rng = np.random.Generator(np.random.PCG64(seed))
+    L = rng.integers(lo, hi + 1, B)
+    L[0] = hi
+    return L
+
+
+def _penalised_top2(logits, hist, rep=1.35, mask_eos=None):
+    row = logits.astype(np.float32).copy()
+    if mask_eos is not None:
+        row[mask_eos] = -np.inf
+    for t in hist[-4096:]:
+        s = row[t]
+        row[t] = s * np.float32(rep) if s < 0 else s / np.float32(rep)
+    o = np.argsort(-row, kind="stable")
+    return o[0], float(row[o[0]] - row[o[1]]), float(np.abs(row[np.isfinite(row)]).max())
+
+
+def test_prefill_16x1024(gpu, model24_path):
+    P = 256
+    L = _lengths(0x6A5E0004, 16, 512, 1024)
+    reqs = sm.synth_requests(0x6A5E0004, 16, P, L - P)
+    g = gpu.Model(model24_path)
+    try:
+        batch = g.first_logits(reqs)
+        assert np.all(np.isfinite(batch))
+        short = int(np.argmin(L))
+        for b in (0, short, 7):
+            print(f"prefill alone: sequence {b}, {L[b]} rows", flush=True)
+            alone = g.first_logits([reqs[b]])
+            assert np.array_equal(batch[b], alone[0]), b
+    finally:
+        g.close()
+    g = gpu.Model(model24_path)
+    try:
+        _, S = g.prefill([reqs[short]])
+        k_dev, v_dev = g.kv_read(0)
+    finally:
+        g.close()
+    o = O.Model(model24_path)
+    try:
+        ref = o.first_logits([reqs[short]])
+        k_ref, v_ref, _ = o.prefill_kv([reqs[short]], 0, flags=O.ORC_KV_F16)
+    finally:
+        o.close()
+    for dev, r in ((k_dev, k_ref), (v_dev, v_ref)):
+        d = dev[:, :, :S, :].view(np.float16).astype(np.float32)
+        ulp = np.spacing(np.abs(r).astype(np.float16)).astype(np.float32)
+        assert np.all(np.abs(d - r) <= np.maximum(ulp, 1e-6 * np.abs(r).max()))
+        assert np.mean(d != r) <= 0.01
+    assert int(batch[short].argmax()) == int(ref[0].argmax())
+    rel = np.abs(batch[short] - ref[0]).max() / np.abs(ref[0]).max()
+    assert rel <= 2e-2, rel
+
+
+def test_decode_batch128_long_kv(gpu, model24_path):
+    P, steps = 64, 6
+    L = _lengths(0x6A5E0005, 128, 1024, 4096)
+    reqs = sm.synth_requests(0x6A5E0005, 128, P, L - P, bert=False)
+    forced = np.random.default_rng(12).integers(0, 1024, steps).astype(np.int32)
+    greedy = (1, 1.0, 1.0, 1.35)
+    g = gpu.Model(model24_path)
+    try:
+        print("decode: batch 128, KV lengths U[1024, 4096]", flush=True)
+        res = g.generate(reqs, sampler=greedy, max_steps=steps, oracle=forced, flags=1, want_sampled=True)
+        g.release_cache()
+    finally:
+        g.close()
+    assert res["n_steps"] == steps
+    short = int(np.argmin(L))
+    o = O.Model(model24_path)
+    try:
+        ref = o.generate([reqs[short]], sampler=greedy, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+    finally:
+        o.close()
+    assert np.array_equal(res["tokens"][short], ref["tokens"][0])
+    for i in range(steps):
+        if res["sampled"][i, short] != ref["sampled"][i, 0]:
+            hist = np.concatenate([reqs[short]["prompt"], forced[:i]])
+            _, margin, scale = _penalised_top2(ref["logits"][i, 0], hist, mask_eos=1024)
+            assert margin <= 2e-3 * scale, (i, margin, scale)
