@@ -23,7 +23,10 @@ ARCH = "gfx950"
 
 COMMON = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", "-Wall", "-Wno-unused-function",
           "-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
-DEVICE = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+DEVICE = ["--offload-arch=" + ARCH, "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+          # matrix-core results in ordinary VGPRs: the kernels scale or reduce them with vector
+          # instructions right away, and the AGPR form would add a copy per value
+          "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
 
 
 def sources():

@@ -236,19 +236,19 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     for (int g = 0; g < 4; g++)
         *reinterpret_cast<float4 *>(orow + 8 * g + 4 * lh) = make_float4(y[4 * g], y[4 * g + 1], y[4 * g + 2], y[4 * g + 3]);
     if (oq) {
+        // natural order (the out projection's GEMM reads it)
         amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
         const float dd = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
         const int nblk = d_model / 32;
-        int8_t * qrow = oq + row * d_model;
+        int8_t * qrow = oq + row * d_model + h * 32;
 #pragma unroll
         for (int v = 0; v < 16; v += 4) {
-            // dims 8*(v/4) + 4*lh + [0,4): one slice (4 consecutive values) of block h
-            const int j = 2 * (v >> 2) + lh;
+            // dims 8*(v/4) + 4*lh + [0,4) of block h
             int packed = 0;
 #pragma unroll
             for (int t = 0; t < 4; t++) packed |= (((int) __builtin_rintf(y[v + t] * id)) & 0xff) << (8 * t);
-            *reinterpret_cast<int *>(qrow + ((int64_t) j * nblk + h) * 4) = packed;
+            *reinterpret_cast<int *>(qrow + 8 * (v >> 2) + 4 * lh) = packed;
         }
         if (lh == 0) od[row * nblk + h] = h2f(f2h(dd));
     }

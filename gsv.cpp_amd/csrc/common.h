@@ -175,6 +175,14 @@ __device__ __forceinline__ void q8_store_sliced(int8_t * row, int nblk, int blk,
     *reinterpret_cast<int *>(row + ((int64_t) (2 * sub + 1) * nblk + blk) * 4) = hi;
 }
 
+// Store the same 8 quants in natural order (q[blk*32 + 8*sub + i]), the layout of the operands
+// of the matrix-core GEMM (one 4-block chunk of a row = one 128-byte line).
+__device__ __forceinline__ void q8_store_natural(int8_t * row, int blk, int sub, const int8_t (&q)[8]) {
+    const int lo = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    const int hi = (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((q[7] & 0xff) << 24);
+    *reinterpret_cast<int2 *>(row + blk * 32 + sub * 8) = make_int2(lo, hi);
+}
+
 // The same with an explicit byte distance between slices (LDS copies of a row pad each slice by
 // 16 bytes, so that the 8 slices a wave reads at once fall in different banks).
 __device__ __forceinline__ void q8_store_sliced_s(int8_t * row, int slice_bytes, int blk, int sub,
@@ -211,13 +219,15 @@ struct GemvEpilogue {
 int launch_q8_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xs,
                    const float * xd, int64_t m, const GemvEpilogue & epi, float * y,
                    hipStream_t stream);
+// Q8_0 outputs go to the sliced layout (GEMV operands) unless natural is set (GEMM operands).
 int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, float * xd,
-                       hipStream_t stream);
+                       hipStream_t stream, bool natural = false);
+// qn (may be null): the quants in natural order as well, for the GEMM
 int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
-                     hipStream_t stream);
+                     hipStream_t stream, int8_t * qn = nullptr);
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream);
+                     hipStream_t stream, bool natural = false);
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
                     int8_t * xq, float * xd, hipStream_t stream);

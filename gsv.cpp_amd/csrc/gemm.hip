@@ -12,15 +12,16 @@
 //
 // Tiling: workgroup 256 threads = 4 waves, output tile 128 (rows m) x 128 (columns n); wave w
 // owns rows 64*(w/2).. and columns 64*(w%2).., i.e. 2 x 2 MFMA tiles. K is staged through LDS in
-// chunks of 4 blocks (128 values), double buffered: the next chunk's global loads are in flight
-// while the current one is multiplied. Operands arrive in the sliced Q8_0 layout (slice j of a
-// row = bytes 4j..4j+3 of every block); LDS holds them as [row][block][32 bytes in value order],
-// rows padded by 16 bytes so that a wave's 16-byte reads are bank-conflict free. A lane's MFMA
-// operand is one half (16 values) of a block of one row; A and B use the same halves, so the
-// product sums over the block whatever order the hardware assigns to the bytes.
+// chunks of 2 blocks (64 values) by direct global -> LDS loads, double buffered: the next
+// chunk streams in while the current one is multiplied, with no staging registers, and the
+// 35 KB of LDS and <= 168 VGPRs let 3 workgroups share a CU. Operands arrive with their quants
+// in natural order (q[row][k]; scales apart), so a chunk of a row is half a 128-byte line. A
+// lane's MFMA operand is one half (16 values) of a block of one row; A and B use the same halves,
+// so the product sums over the block whatever order the hardware assigns to the bytes.
 //
 // Epilogue (the options of the decoder's GEMV, layer.h LayerOut): bias, ReLU, fp32 store of
-// columns < n_store, the fp16 K/V append, or the Q8_0 quantisation of each 32-column block.
+// columns < n_store, the fp16 K/V append, or the Q8_0 quantisation of each 32-column block (in
+// natural order: the next GEMM reads it).
 #include "common.h"
 #include "layer.h"
 
@@ -30,78 +31,76 @@ namespace {
 constexpr int GM_THREADS = 256;
 constexpr int GM_BM = 128;                 // rows (m) per workgroup
 constexpr int GM_BN = 128;                 // columns (n) per workgroup
-constexpr int GM_KC = 4;                   // blocks per K chunk
-constexpr int GM_ROWB = GM_KC * 32 + 16;   // LDS bytes per row and chunk (padded)
+constexpr int GM_KC = 2;                   // blocks per K chunk
+constexpr int GM_ROWB = GM_KC * 32;        // LDS bytes per row and chunk: 4 slots of 16 bytes
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace
 
+// K chunk buffers, filled by direct global -> LDS loads (no staging registers). A row's chunk is
+// 64 bytes = 4 slots of 16 bytes; piece p of row r sits in slot p ^ (r & 3), so that the 16-byte
+// operand reads of consecutive rows fall in different banks.
 struct GemmLds {
     int8_t a[2][GM_BM * GM_ROWB];
     int8_t b[2][GM_BN * GM_ROWB];
-    float da[2][GM_KC][GM_BM];   // activation scales [block][row]
-    float db[2][GM_KC][GM_BN];   // weight scales (fp16 -> fp32) [block][col]
+    float da[2][GM_BM * GM_KC];      // activation scales [row][block]
+    uint16_t db[2][GM_BN * GM_KC];   // weight scales (fp16) [col][block]
 };
 
-// Global -> registers for one K chunk: each thread loads 4 x 16 bytes of A and of B (one slice
-// of 4 consecutive blocks of one row each) and its share of the scales.
-struct GemmStage {
-    int4 a[4], b[4];
-    float da[2];
-    uint16_t db[2];
+// The chunk buffers during the K loop; half of the fp32 output tile (64 rows, padded by 4 floats)
+// in the epilogue.
+union GemmSmem {
+    GemmLds k;
+    float y[GM_BM / 2][GM_BN + 4];
 };
 
-template <int NBLK>
-__device__ __forceinline__ void gemm_load(const int8_t * __restrict__ xs, const float * __restrict__ xd,
-                                          const int8_t * __restrict__ ws, const uint16_t * __restrict__ wd,
-                                          int m, int m0, int n0, int chunk, int tid, GemmStage & g) {
-    const int blk0 = chunk * GM_KC;
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int idx = tid + u * GM_THREADS;   // 0..1023 = 128 rows x 8 slices
-        const int row = idx >> 3, j = idx & 7;
-        const int mm = min(m0 + row, m - 1);
-        g.a[u] = *reinterpret_cast<const int4 *>(xs + ((int64_t) mm * 8 + j) * NBLK * 4 + blk0 * 4);
-        g.b[u] = *reinterpret_cast<const int4 *>(ws + ((int64_t) (n0 + row) * 8 + j) * NBLK * 4 + blk0 * 4);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int idx = tid + u * GM_THREADS;   // 0..511 = 128 rows x 4 blocks
-        const int row = idx >> 2, bb = idx & 3;
-        const int mm = min(m0 + row, m - 1);
-        g.da[u] = xd[(int64_t) mm * NBLK + blk0 + bb];
-        g.db[u] = wd[(int64_t) (n0 + row) * NBLK + blk0 + bb];
-    }
+__device__ __forceinline__ void lds_dma16(const void * g, void * lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *) lds, 16, 0, 0);
+}
+__device__ __forceinline__ void lds_dma4(const void * g, void * lds) {
+    __builtin_amdgcn_global_load_lds(g, (lds_void *) lds, 4, 0, 0);
 }
 
-__device__ __forceinline__ void gemm_store(GemmLds & s, int buf, int tid, const GemmStage & g) {
-#pragma unroll
-    for (int u = 0; u < 4; u++) {
-        const int idx = tid + u * GM_THREADS;
-        const int row = idx >> 3, j = idx & 7;
-        // g.a[u] holds slice j of blocks 0..3: word q -> block q, bytes 4j..4j+3
-        int * pa = reinterpret_cast<int *>(&s.a[buf][row * GM_ROWB + j * 4]);
-        int * pb = reinterpret_cast<int *>(&s.b[buf][row * GM_ROWB + j * 4]);
-        pa[0] = g.a[u].x; pa[8] = g.a[u].y; pa[16] = g.a[u].z; pa[24] = g.a[u].w;
-        pb[0] = g.b[u].x; pb[8] = g.b[u].y; pb[16] = g.b[u].z; pb[24] = g.b[u].w;
-    }
+// Issue the direct loads of one K chunk into buffer buf. A wave's load instruction writes 64
+// consecutive 16-byte (or 4-byte) LDS slots, lane L the L-th; the global address of each lane is
+// chosen so that the slot receives what the layout above puts there.
+template <int NBLK>
+__device__ __forceinline__ void gemm_issue(const int8_t * __restrict__ xs, const float * __restrict__ xd,
+                                           const int8_t * __restrict__ ws, const uint16_t * __restrict__ wd,
+                                           int m, int m0, int n0, int chunk, int wave, int lane, GemmLds & s,
+                                           int buf) {
+    const int blk0 = chunk * GM_KC;
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-        const int idx = tid + u * GM_THREADS;
-        const int row = idx >> 2, bb = idx & 3;
-        s.da[buf][bb][row] = g.da[u];
-        s.db[buf][bb][row] = h2f(g.db[u]);
+        const int seg = u * 4 + wave;              // 1 KB segment = 16 rows x 4 slots
+        const int r = seg * 16 + (lane >> 2);
+        const int p = (lane & 3) ^ (r & 3);        // the piece that belongs in this slot
+        const int mm = min(m0 + r, m - 1);
+        lds_dma16(xs + (int64_t) mm * NBLK * 32 + blk0 * 32 + p * 16, &s.a[buf][seg * 1024]);
+        lds_dma16(ws + (int64_t) (n0 + r) * NBLK * 32 + blk0 * 32 + p * 16, &s.b[buf][seg * 1024]);
+    }
+    {
+        const int i = wave * 64 + lane;            // 128 rows x 2 blocks
+        const int mm = min(m0 + (i >> 1), m - 1);
+        lds_dma4(xd + (int64_t) mm * NBLK + blk0 + (i & 1), &s.da[buf][wave * 64]);
+    }
+    if (wave < 2) {                                // 128 columns x 2 fp16 scales = 128 x 4 bytes
+        const int col = wave * 64 + lane;
+        lds_dma4(wd + (int64_t) (n0 + col) * NBLK + blk0, &s.db[buf][wave * 128]);
     }
 }
 
 template <int NBLK>
 __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restrict__ ws,
-                                                        const uint16_t * __restrict__ wd, int n, int m,
-                                                        const int8_t * __restrict__ xs,
-                                                        const float * __restrict__ xd, LayerOut out) {
+                                                           const uint16_t * __restrict__ wd, int n, int m,
+                                                           const int8_t * __restrict__ xs,
+                                                           const float * __restrict__ xd, LayerOut out) {
     constexpr int NCH = NBLK / GM_KC;
-    __shared__ __align__(16) GemmLds s;
+    __shared__ __align__(16) GemmSmem sm;
+    GemmLds & s = sm.k;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -112,98 +111,130 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
     const int li = lane & 31;          // MFMA: row of A / column of B held by this lane
     const int lg = lane >> 5;          // MFMA: which half of the block
 
-    float acc[2][2][16];
+    float acc[4][16];                  // tile t = 2 * ta + tb
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int t = 0; t < 4; t++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
-#pragma unroll
-            for (int v = 0; v < 16; v++) acc[a][b][v] = 0.0f;
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
-    GemmStage g;
-    gemm_load<NBLK>(xs, xd, ws, wd, m, m0, n0, 0, tid, g);
-    gemm_store(s, 0, tid, g);
+    gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, 0, wave, lane, s, 0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int ch = 0; ch < NCH; ch++) {
         const int buf = ch & 1;
-        if (ch + 1 < NCH) gemm_load<NBLK>(xs, xd, ws, wd, m, m0, n0, ch + 1, tid, g);
+        // the next chunk streams into the other buffer (last read before the previous barrier)
+        if (ch + 1 < NCH) gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, ch + 1, wave, lane, s, buf ^ 1);
 #pragma unroll 1
         for (int bb = 0; bb < GM_KC; bb++) {
+            // operands: piece 2 * bb + lg (16 values) of the wave's rows / columns
             v4i fa[2], fb[2];
+            float adx[2], bdw[2];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                fa[t] = *reinterpret_cast<const v4i *>(&s.a[buf][(wm + 32 * t + li) * GM_ROWB + bb * 32 + lg * 16]);
-                fb[t] = *reinterpret_cast<const v4i *>(&s.b[buf][(wn + 32 * t + li) * GM_ROWB + bb * 32 + lg * 16]);
+            for (int h = 0; h < 2; h++) {
+                const int ra = wm + 32 * h + li, rb = wn + 32 * h + li;
+                fa[h] = *reinterpret_cast<const v4i *>(&s.a[buf][ra * GM_ROWB + (((2 * bb + lg) ^ (ra & 3)) << 4)]);
+                fb[h] = *reinterpret_cast<const v4i *>(&s.b[buf][rb * GM_ROWB + (((2 * bb + lg) ^ (rb & 3)) << 4)]);
+                // the scale-product MFMA: A = dx of the tile's rows, B = dw of its columns, both in
+                // K slot 0 (lanes 0-31); the second K slot is zero
+                adx[h] = lg == 0 ? s.da[buf][ra * GM_KC + bb] : 0.0f;
+                bdw[h] = lg == 0 ? h2f(s.db[buf][rb * GM_KC + bb]) : 0.0f;
             }
-            float dwv[2];
+            // per tile: the exact integer sum of the block, the fp32 products dx * dw (one
+            // rounding, as a vector multiply), then acc += float(C) * (dx * dw) on the vector ALUs
 #pragma unroll
-            for (int t = 0; t < 2; t++) dwv[t] = s.db[buf][bb][wn + 32 * t + li];
+            for (int t = 0; t < 4; t++) {
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t >> 1], fb[t & 1], v16i{}, 0, 0, 0);
+                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(adx[t >> 1], bdw[t & 1], v16f{}, 0, 0, 0);
 #pragma unroll
-            for (int ta = 0; ta < 2; ta++) {
-                // activation scales of the 16 rows this lane's outputs belong to:
-                // row = 8 * (v / 4) + 4 * lg + v % 4 within the 32-row tile
-                float dxv[16];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const float4 d4 = *reinterpret_cast<const float4 *>(&s.da[buf][bb][wm + 32 * ta + 8 * q + 4 * lg]);
-                    dxv[4 * q + 0] = d4.x; dxv[4 * q + 1] = d4.y; dxv[4 * q + 2] = d4.z; dxv[4 * q + 3] = d4.w;
-                }
-#pragma unroll
-                for (int tb = 0; tb < 2; tb++) {
-                    v16i c = {};
-                    c = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[ta], fb[tb], c, 0, 0, 0);
-#pragma unroll
-                    for (int v = 0; v < 16; v++)
-                        acc[ta][tb][v] = __builtin_fmaf((float) c[v], dxv[v] * dwv[tb], acc[ta][tb][v]);
-                }
+                for (int v = 0; v < 16; v++) acc[t][v] = __builtin_fmaf((float) c[v], sc[v], acc[t][v]);
             }
         }
-        if (ch + 1 < NCH) {
-            gemm_store(s, buf ^ 1, tid, g);   // the other buffer: last read before the previous barrier
-        }
-        __syncthreads();
+        __builtin_amdgcn_s_waitcnt(0);   // the next chunk has landed
+        __syncthreads();                 // and every wave is done with this one
     }
 
-    // ---- epilogue: lane holds column li of each 32x32 tile, rows 8*(v/4) + 4*lg + v%4 ----
+    // ---- epilogue: each half of the 128 x 128 tile goes through LDS so that each thread then
+    // owns a 32-column block of a row: coalesced stores and an in-register Q8_0 quantisation ----
     int kvcol0 = 0;
     if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
+    const int nblk_out = n / 32;
+#pragma unroll 1
+    for (int half = 0; half < 2; half++) {
+        if (half) __syncthreads();       // the first half has been read
+        if (wm == 64 * half) {
 #pragma unroll
-    for (int tb = 0; tb < 2; tb++) {
-        const int col = n0 + wn + 32 * tb + li;
-        const float bias = out.bias ? out.bias[col] : 0.0f;
+            for (int t = 0; t < 4; t++) {
+                const int ta = t >> 1, tb = t & 1;
 #pragma unroll
-        for (int ta = 0; ta < 2; ta++) {
+                for (int v = 0; v < 16; v++)
+                    sm.y[32 * ta + 8 * (v >> 2) + 4 * lg + (v & 3)][wn + 32 * tb + li] = acc[t][v];
+            }
+        }
+        __syncthreads();
+        const int r = tid >> 2, cb = tid & 3;      // 64 rows x 4 blocks of 32 columns
+        const int row = m0 + 64 * half + r;
+        if (row >= m) continue;
+        const int col0 = n0 + 32 * cb;
+        float y[32];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int row = m0 + wm + 32 * ta + 8 * (v >> 2) + 4 * lg + (v & 3);
-                float y = acc[ta][tb][v];
-                if (out.bias) y = y + bias;
-                if (out.act == 1) y = y > 0.0f ? y : 0.0f;
-                if (out.yq) {
-                    // the 32 columns of this block of row `row` are the 32 lanes of this half
-                    float v1[1] = {y};
-                    int8_t q1[1];
-                    const float d = q8_quantize_group<1>(v1, q1, 32);
-                    if (row < m) {
-                        const int nblk_out = n / 32;
-                        const int blk = col >> 5;
-                        out.yq[(int64_t) row * n + q8_sliced_offset(nblk_out, blk, li)] = q1[0];
-                        if (li == 0) out.yd[(int64_t) row * nblk_out + blk] = d;
-                    }
-                }
-                if (row >= m) continue;
-                if (out.y && col < out.n_store) out.y[(int64_t) row * out.y_stride + col] = y;
-                if (out.kc && col >= out.kv_row0) {
-                    const int rr = col - out.kv_row0;
-                    const int which = rr / out.d_model;
-                    const int hd = rr % out.d_model;
-                    const int h = hd >> 5, dd = hd & 31;
-                    const int b = row / out.rows_per_seq;
-                    const int kcol = kvcol0 + row % out.rows_per_seq;
-                    uint16_t * cache = which == 0 ? out.kc : out.vc;
-                    cache[(((int64_t) b * out.n_head + h) * out.lstride + kcol) * 32 + dd] = f2h(y);
-                }
+        for (int j = 0; j < 8; j++) {
+            const float4 f = *reinterpret_cast<const float4 *>(&sm.y[r][32 * cb + 4 * j]);
+            y[4 * j] = f.x; y[4 * j + 1] = f.y; y[4 * j + 2] = f.z; y[4 * j + 3] = f.w;
+        }
+        if (out.bias) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float4 b4 = *reinterpret_cast<const float4 *>(out.bias + col0 + 4 * j);
+                y[4 * j] = y[4 * j] + b4.x; y[4 * j + 1] = y[4 * j + 1] + b4.y;
+                y[4 * j + 2] = y[4 * j + 2] + b4.z; y[4 * j + 3] = y[4 * j + 3] + b4.w;
+            }
+        }
+        if (out.act == 1) {
+#pragma unroll
+            for (int k = 0; k < 32; k++) y[k] = y[k] > 0.0f ? y[k] : 0.0f;
+        }
+        if (out.y && col0 < out.n_store) {
+            float * yr = out.y + (int64_t) row * out.y_stride + col0;
+#pragma unroll
+            for (int j = 0; j < 8; j++)
+                *reinterpret_cast<float4 *>(yr + 4 * j) = make_float4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
+        }
+        if (out.yq) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(y[k]));
+            const float d = amax / 127.0f;
+            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+            const int blk = col0 >> 5;
+            int w[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                w[j] = 0;
+#pragma unroll
+                for (int t = 0; t < 4; t++) w[j] |= (((int) __builtin_rintf(y[4 * j + t] * id)) & 0xff) << (8 * t);
+            }
+            int4 * qr = reinterpret_cast<int4 *>(out.yq + (int64_t) row * n + col0);   // natural order
+            qr[0] = make_int4(w[0], w[1], w[2], w[3]);
+            qr[1] = make_int4(w[4], w[5], w[6], w[7]);
+            out.yd[(int64_t) row * nblk_out + blk] = h2f(f2h(d));
+        }
+        if (out.kc && col0 >= out.kv_row0) {
+            // one 32-column block = one head of K or V
+            const int rr = col0 - out.kv_row0;
+            const int which = rr / out.d_model;
+            const int h = (rr % out.d_model) >> 5;
+            const int b = row / out.rows_per_seq;
+            const int kcol = kvcol0 + row % out.rows_per_seq;
+            uint16_t * cache = (which == 0 ? out.kc : out.vc) + (((int64_t) b * out.n_head + h) * out.lstride + kcol) * 32;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                uint4 w;
+                w.x = (uint32_t) f2h(y[8 * j + 0]) | ((uint32_t) f2h(y[8 * j + 1]) << 16);
+                w.y = (uint32_t) f2h(y[8 * j + 2]) | ((uint32_t) f2h(y[8 * j + 3]) << 16);
+                w.z = (uint32_t) f2h(y[8 * j + 4]) | ((uint32_t) f2h(y[8 * j + 5]) << 16);
+                w.w = (uint32_t) f2h(y[8 * j + 6]) | ((uint32_t) f2h(y[8 * j + 7]) << 16);
+                *reinterpret_cast<uint4 *>(cache + 8 * j) = w;
             }
         }
     }
@@ -219,6 +250,9 @@ int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
     GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 && out.kv_row0 + 2 * out.d_model <= n),
                  "q8_gemm: bad KV epilogue");
     GSVK_REQUIRE(out.act == 0 || out.act == 1, "q8_gemm: act must be 0 or 1");
+    GSVK_REQUIRE(((uintptr_t) out.bias & 15) == 0 && ((uintptr_t) out.y & 15) == 0 && out.y_stride % 4 == 0 &&
+                     ((uintptr_t) out.kc & 15) == 0 && ((uintptr_t) out.vc & 15) == 0,
+                 "q8_gemm: bias, y (and its row stride) and the K/V caches must be 16-byte aligned");
     const dim3 grid((unsigned) (n / GM_BN), (unsigned) ((m + GM_BM - 1) / GM_BM));
     if (k == 512)
         hipLaunchKernelGGL(k_q8_gemm<16>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);

@@ -55,7 +55,9 @@ struct LayerOut {
 };
 
 // Q8_0 x Q8_0 GEMM on the matrix cores (gemm.hip) with the same epilogue options: n % 128 == 0,
-// k in {512, 2048}; the input rows are sliced Q8_0 (xs [m][k], fp32 scales xd [m][k/32]).
+// k in {512, 2048}. Both operands have their quants in natural order (ws [n][k] as in the GGUF
+// blocks, xs [m][k]) with the scales apart (fp16 wd [n][k/32], fp32 xd [m][k/32]); a Q8_0 output
+// (yq) is written in natural order too.
 int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
                    const int8_t * xs, const float * xd, const LayerOut & out, hipStream_t stream);
 

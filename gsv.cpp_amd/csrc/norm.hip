@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
                                                   const float * __restrict__ wb, int rows, int n,
                                                   float eps, float * __restrict__ y,
                                                   int8_t * __restrict__ yq,
-                                                  float * __restrict__ yd) {
+                                                  float * __restrict__ yd, bool natural) {
     const int row = blockIdx.x;
     if (row >= rows) return;
     const int lane = threadIdx.x;
@@ -98,7 +98,10 @@ __global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
             int8_t q[8];
             const float d = q8_quantize_group<8>(o, q, 4);
             if (act) {
-                q8_store_sliced(yq + (int64_t) row * n, nblk, ch >> 2, ch & 3, q);
+                if (natural)
+                    q8_store_natural(yq + (int64_t) row * n, ch >> 2, ch & 3, q);
+                else
+                    q8_store_sliced(yq + (int64_t) row * n, nblk, ch >> 2, ch & 3, q);
                 if ((ch & 3) == 0) yd[(int64_t) row * nblk + ch / 4] = d;
             }
         }
@@ -160,7 +163,7 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
 
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream) {
+                     hipStream_t stream, bool natural) {
     GSVK_REQUIRE(x && wb && y, "layernorm: null pointer");
     GSVK_REQUIRE(rows >= 0 && rows < (1 << 30) && n > 0 && n % 32 == 0 && n <= 4096,
                  "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
@@ -172,13 +175,13 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     const dim3 grid((unsigned) rows);
     if (n <= 512)
         hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd);
+                           (int) n, eps, y, yq, yd, natural);
     else if (n <= 1024)
         hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd);
+                           (int) n, eps, y, yq, yd, natural);
     else
         hipLaunchKernelGGL(k_layernorm<8>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd);
+                           (int) n, eps, y, yq, yd, natural);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -63,7 +63,8 @@ struct DevArena {
 };
 
 struct Lin {
-    int8_t * qs = nullptr;
+    int8_t * qs = nullptr;    // sliced quants (GEMV)
+    int8_t * qn = nullptr;    // the same quants in natural order (GEMM)
     uint16_t * d = nullptr;
     float * b = nullptr;
     int n = 0, k = 0;
@@ -185,9 +186,10 @@ int load_q8(gsvk_model * m, const GgufFile & g, const GgufTensor * t, Lin & lin,
         return GSVK_ERR_IO;
     }
     GSVK_TRY(m->wmem.alloc(lin.qs, (size_t) lin.n * lin.k));
+    GSVK_TRY(m->wmem.alloc(lin.qn, (size_t) lin.n * lin.k));
     GSVK_TRY(m->wmem.alloc(lin.d, (size_t) lin.n * (lin.k / 32)));
     GSVK_HIP(hipMemcpyAsync(staging, host.data(), t->nbytes, hipMemcpyHostToDevice, m->stream));
-    GSVK_TRY(launch_q8_repack(staging, lin.n, lin.k, lin.qs, lin.d, m->stream));
+    GSVK_TRY(launch_q8_repack(staging, lin.n, lin.k, lin.qs, lin.d, m->stream, lin.qn));
     GSVK_HIP(hipStreamSynchronize(m->stream));   // host buffer is reused
     return GSVK_OK;
 }
@@ -307,19 +309,19 @@ int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x,
         oo.y = o;
         oo.y_stride = D;
         oo.n_store = D;
-        GSVK_TRY(launch_q8_gemm(w.out.qs, w.out.d, D, D, R, attn.q, attn.d, oo, m->stream));
-        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream));
+        GSVK_TRY(launch_q8_gemm(w.out.qn, w.out.d, D, D, R, attn.q, attn.d, oo, m->stream));
+        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream, true));
         LayerOut ho{};
         ho.bias = w.f1.b;
         ho.act = 1;
         ho.yq = hq.q;
         ho.yd = hq.d;
-        GSVK_TRY(launch_q8_gemm(w.f1.qs, w.f1.d, F, D, R, n1->q, n1->d, ho, m->stream));
+        GSVK_TRY(launch_q8_gemm(w.f1.qn, w.f1.d, F, D, R, n1->q, n1->d, ho, m->stream));
         LayerOut h2o{};
         h2o.y = h2;
         h2o.y_stride = D;
         h2o.n_store = D;
-        return launch_q8_gemm(w.f2.qs, w.f2.d, D, F, R, hq.q, hq.d, h2o, m->stream);
+        return launch_q8_gemm(w.f2.qn, w.f2.d, D, F, R, hq.q, hq.d, h2o, m->stream);
     }
     LayerIn qin{};
     qin.mode = IN_Q8;
@@ -573,7 +575,8 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R, proj, D, 0, st));
         GSVK_TRY(launch_add_proj(cur.x, proj, d_rowb, d_rowt, d_pad, S, D, R, st));
     }
-    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st));
+    // the layer-0 QKV reads this copy: natural order for the GEMM, sliced for the GEMV
+    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, rows >= GEMM_MIN_ROWS));
     int32_t * zero = nullptr;
     GSVK_TRY(tmp.alloc(zero, 1));
     GSVK_HIP(hipMemsetAsync(zero, 0, 4, st));
@@ -586,9 +589,9 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
             if (li > 0) {
                 const LayerW & p = m->L[li - 1];
-                GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st));
+                GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st, true));
             }
-            GSVK_TRY(launch_q8_gemm(w.qkv.qs, w.qkv.d, 3 * D, D, rows, cur.q, cur.d,
+            GSVK_TRY(launch_q8_gemm(w.qkv.qn, w.qkv.d, 3 * D, D, rows, cur.q, cur.d,
                                     qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         } else {
             LayerIn in{};

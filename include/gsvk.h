@@ -195,10 +195,12 @@ int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
                     float * y, void * stream);
 
 /* Q8_0 x Q8_0 GEMM on the matrix cores (int8 MFMA, one 32-value block per instruction, fp32
- * per-block scaling): the projections of src/gsv_ar.cpp:244-263 over many rows (prefill, decode
- * at large batch). Same operands and result as gsvk_op_q8_gemv; the fp32 accumulation runs block
- * by block instead of in ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must
- * be a multiple of 128, k 512 or 2048. */
+ * per-block scaling): the projections of src/gsv_ar.cpp:244-263 over many rows (prefill). The
+ * same product as gsvk_op_q8_gemv, but both operands have their quants in NATURAL order (wq
+ * [n][k] = the GGUF blocks' quants without the scales, xq [m][k]) with the scales apart (wd fp16
+ * [n][k/32], xd fp32 [m][k/32]); the fp32 accumulation runs block by block instead of in
+ * ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must be a multiple of 128,
+ * k 512 or 2048; bias and y 16-byte aligned. */
 int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xq,
                     const float * xd, int64_t m, const float * bias, int act, float * y, void * stream);
 
@@ -269,8 +271,10 @@ int gsvk_op_attn_decode(const float * q, const uint16_t * k, const uint16_t * v,
  * src/gsv_ar.cpp:215-223): qkv fp32 [B][S][3*nh*hd] (Q, K, V of head h at h*hd, D + h*hd,
  * 2*D + h*hd); pad device int32 [B]; query s of sequence b sees keys [pad[b], max_len) when
  * s < max_len, else [pad[b], s]. out fp32 [B][S][nh*hd]; oq/od (both or neither) its Q8_0 copy
- * (sliced quants, fp32 scales). path 0 picks the kernel the prefill uses for B*S rows, 1 the
- * lane-per-query kernel, 2 the matrix-core kernel. hd must be 32; qkv and out 16-byte aligned. */
+ * (fp32 scales; the quants in the layout of the projection that reads them: sliced from the
+ * lane-per-query kernel, natural order from the matrix-core kernel). path 0 picks the kernel the
+ * prefill uses for B*S rows, 1 the lane-per-query kernel, 2 the matrix-core kernel. hd must be
+ * 32; qkv and out 16-byte aligned. */
 int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                          int hd, float scale, int path, float * out, int8_t * oq, float * od,
                          void * stream);

@@ -393,19 +393,19 @@ def test_qkv_attn_fused_equals_separate_kernels(gpu, B, lstride):
 def test_q8_gemm_matches_oracle(gpu, n, k, m):
     """The MFMA GEMM computes the same Q8_0 products as ggml-cpu's mul_mat; only the fp32
     accumulation order differs (per block instead of 8 lanes + hsum): within 2e-6 of the output
-    scale, i.e. a few fp32 ulps."""
+    scale, i.e. a few fp32 ulps. Its operands carry the quants in natural order."""
     import torch
     rng = np.random.default_rng(7000 + n + k + m)
     W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
     X = rng.standard_normal((m, k)).astype(np.float32)
     X[0, :64] = 0.0
     wb = sm.q8_quantize_ref(W).ravel()
-    wq = torch.zeros(n * k, dtype=torch.int8, device="cuda")
-    wd = torch.zeros(n * k // 32, dtype=torch.int16, device="cuda")
-    gpu.op_q8_repack(_dev(wb, torch), n, k, wq, wd)
-    xq = torch.zeros(m * k, dtype=torch.int8, device="cuda")
-    xd = torch.zeros(m * k // 32, dtype=torch.float32, device="cuda")
-    gpu.op_q8_quantize(_dev(X, torch), xq, xd)
+    wq_n, wd_n = blocks_to_split(wb, n, k)                  # natural-order quants, fp16 scales
+    xq_n, xd_n = blocks_to_split(O.q8_quantize_x86(X), m, k)
+    wq = _dev(wq_n, torch)
+    wd = _dev(wd_n.view(np.int16), torch)
+    xq = _dev(xq_n, torch)
+    xd = _dev(xd_n.view(np.float16).astype(np.float32), torch)
     bias = rng.standard_normal(n).astype(np.float32) * 0.02
     y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
     gpu.op_q8_gemm(wq, wd, n, k, xq, xd, m, None, 0, y)
@@ -449,6 +449,9 @@ def test_attn_prefill_matches_oracle(gpu, B, S, max_len, pads, what, path):
     assert rel <= 2e-3, rel
     assert rel <= 2e-5, rel   # fp32 (or hi + lo split) products with fp32 accumulation
     q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(got.reshape(B * S, D)), B * S, D)
-    assert np.array_equal(unslice(oq.cpu().numpy(), D), q_ref)
+    q_got = oq.cpu().numpy()
+    # quants in the layout of the projection that reads them: sliced (GEMV) or natural (GEMM)
+    q_got = unslice(q_got, D) if path == 1 else q_got.reshape(B * S, D)
+    assert np.array_equal(q_got, q_ref)
     d_ref32 = d_ref.view(np.float16).astype(np.float32)
     assert np.array_equal(od.cpu().numpy().reshape(B * S, -1).view(np.uint32), d_ref32.view(np.uint32))
