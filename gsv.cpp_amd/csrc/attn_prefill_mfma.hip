@@ -49,46 +49,62 @@ struct PmTile {
     int8_t vlo[32 * PM_VROW];
 };
 
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ void split_h(float x, _Float16 & hi, _Float16 & lo) {
     hi = (_Float16) x;
     lo = (_Float16) (x - (float) hi);
 }
+
+// The same split for a pair: hi = fp16(x) (nearest), lo = fp16(x - hi), where x - hi (exact in
+// fp32) comes from one v_fma_mix per value (the fp16 hi times -1 plus the fp32 x, rounded to
+// fp16) instead of a conversion back to fp32 and a subtraction.
+__device__ __forceinline__ void split_pair(float x0, float x1, v2h & hi, v2h & lo) {
+    hi = v2h{(_Float16) x0, (_Float16) x1};
+    uint32_t h = __builtin_bit_cast(uint32_t, hi), r;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+        "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "=&v"(r)
+        : "v"(h), "v"(x0), "v"(x1));
+    lo = __builtin_bit_cast(v2h, r);
+}
 }  // namespace
 
-// One thread's share of a key tile: 4 dims of K and of V of one key (256 threads: 32 keys x 8).
+// One thread's share of a key tile (256 threads): 4 dims of K of one key (thread = 32 keys x 8
+// groups of 4 dims) and 1 dim of V of 4 keys (thread = 32 dims x 8 groups of 4 keys), so that
+// both land in LDS with 8-byte stores: K as [key][dim], V transposed as [dim][key].
 struct PmRegs {
-    float4 k, v;
+    float4 k;
+    float v[4];
 };
 
 // fetch key tile [k0, k0 + 32) of head h (keys past S read key S - 1; they are masked later)
 __device__ __forceinline__ PmRegs pm_fetch(const float * __restrict__ base, int64_t rs, int d_model, int h,
                                            int S, int k0, int tid) {
     const int key = tid >> 3, dq = (tid & 7) * 4;
-    const float * kp = base + (int64_t) min(k0 + key, S - 1) * rs + d_model + h * 32 + dq;
+    const int vd = tid & 31, vk = (tid >> 5) * 4;
     PmRegs r;
-    r.k = *reinterpret_cast<const float4 *>(kp);
-    r.v = *reinterpret_cast<const float4 *>(kp + d_model);
+    r.k = *reinterpret_cast<const float4 *>(base + (int64_t) min(k0 + key, S - 1) * rs + d_model + h * 32 + dq);
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.v[i] = base[(int64_t) min(k0 + vk + i, S - 1) * rs + 2 * d_model + h * 32 + vd];
     return r;
 }
 
-// split the fetched values into fp16 hi + lo and store them: K as [key][dim], V as V^T [dim][key]
+// split the fetched values into fp16 hi + lo and store them
 __device__ __forceinline__ void pm_store(const PmRegs & r, int tid, PmTile & t) {
     const int key = tid >> 3, dq = (tid & 7) * 4;
-    const float kx[4] = {r.k.x, r.k.y, r.k.z, r.k.w};
-    const float vx[4] = {r.v.x, r.v.y, r.v.z, r.v.w};
-    v4h kh, kl;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        _Float16 hi, lo;
-        split_h(kx[i], hi, lo);
-        kh[i] = hi;
-        kl[i] = lo;
-        split_h(vx[i], hi, lo);
-        *reinterpret_cast<_Float16 *>(&t.vhi[(dq + i) * PM_VROW + key * 2]) = hi;
-        *reinterpret_cast<_Float16 *>(&t.vlo[(dq + i) * PM_VROW + key * 2]) = lo;
-    }
+    const int vd = tid & 31, vk = (tid >> 5) * 4;
+    v2h k0h, k0l, k1h, k1l, v0h, v0l, v1h, v1l;
+    split_pair(r.k.x, r.k.y, k0h, k0l);
+    split_pair(r.k.z, r.k.w, k1h, k1l);
+    split_pair(r.v[0], r.v[1], v0h, v0l);
+    split_pair(r.v[2], r.v[3], v1h, v1l);
+    const v4h kh = {k0h[0], k0h[1], k1h[0], k1h[1]}, kl = {k0l[0], k0l[1], k1l[0], k1l[1]};
+    const v4h vh = {v0h[0], v0h[1], v1h[0], v1h[1]}, vl = {v0l[0], v0l[1], v1l[0], v1l[1]};
     *reinterpret_cast<v4h *>(&t.khi[key * PM_KROW + dq * 2]) = kh;
     *reinterpret_cast<v4h *>(&t.klo[key * PM_KROW + dq * 2]) = kl;
+    *reinterpret_cast<v4h *>(&t.vhi[vd * PM_VROW + vk * 2]) = vh;
+    *reinterpret_cast<v4h *>(&t.vlo[vd * PM_VROW + vk * 2]) = vl;
 }
 
 __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
@@ -113,6 +129,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const int qc = min(q, S - 1);
     const int ke = min(key_end(qc), S);
     const int qlast_w = min(qw + PM_Q - 1, S - 1);
+    const int ke_min_w = min(key_end(min(qw, S - 1)), S);   // the wave's first query sees the fewest keys
     const int ke_w = min(key_end(qlast_w), S);            // the wave's last query sees the most keys
     const int qlast_g = min(q0w + PM_Q * PM_WAVES - 1, S - 1);
     const int ke_g = min(key_end(qlast_g), S);
@@ -161,42 +178,61 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
                 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], sc, 0, 0, 0);
                 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], sc, 0, 0, 0);
             }
-            // mask, scale, running max of this query (own 16 keys + lane l^32's 16)
-            float s[16];
-            float rmax = -INFINITY;
-#pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int key = k0 + 8 * (v >> 2) + 4 * lh + (v & 3);
-                const bool valid = key >= pb && key < ke;
-                s[v] = valid ? sc[v] * scale_log2 : -INFINITY;
-                rmax = fmaxf(rmax, s[v]);
-            }
-            rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
-            const float mn = fmaxf(m, rmax);
-            // all keys so far masked: keep zeros (exp2(-inf - -inf) would be NaN)
-            const float f = mn == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
-            float psum = 0.0f;
+            // Softmax step in log2 units. A tile that every query of the wave sees whole (the
+            // usual case: all but the last tile or two of a row) skips the masks; otherwise
+            // invisible keys get -inf.
+            const bool full = k0 + PM_KT <= ke_min_w;   // uniform per wave (tiles start at pb)
             float p[16];
+            float f, psum = 0.0f;
+            if (full) {
+                float rmax = sc[0];
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                p[v] = mn == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s[v] - mn);
-                psum += p[v];
+                for (int v = 1; v < 16; v++) rmax = fmaxf(rmax, sc[v]);
+                rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+                const float mn = fmaxf(m, rmax * scale_log2);
+                f = __builtin_amdgcn_exp2f(m - mn);   // m = -inf before the first tile: f = 0
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    p[v] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, -mn));
+                    psum += p[v];
+                }
+                m = mn;
+            } else {
+                float rmax = -INFINITY;
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    const int key = k0 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    if (!(key >= pb && key < ke)) sc[v] = -INFINITY;
+                    rmax = fmaxf(rmax, sc[v]);
+                }
+                rmax = fmaxf(rmax, __shfl_xor(rmax, 32, 64));
+                const float mn = fmaxf(m, rmax * scale_log2);
+                // all keys so far masked: keep zeros (exp2(-inf - -inf) would be NaN)
+                const bool dead = mn == -INFINITY;
+                f = dead ? 1.0f : __builtin_amdgcn_exp2f(m - mn);
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    p[v] = dead ? 0.0f : __builtin_amdgcn_exp2f(__builtin_fmaf(sc[v], scale_log2, -mn));
+                    psum += p[v];
+                }
+                m = mn;
             }
             psum += __shfl_xor(psum, 32, 64);
             l = l * f + psum;
-            m = mn;
+            if (__any(f != 1.0f)) {   // no running max of the wave moved: nothing to rescale
 #pragma unroll
-            for (int v = 0; v < 16; v++) o[v] *= f;
+                for (int v = 0; v < 16; v++) o[v] *= f;
+            }
             // O^T += V^T . P^T, keys in the register order (two chunks of 16)
 #pragma unroll
             for (int c = 0; c < 2; c++) {
                 v8h ph, pl;
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    _Float16 hi, lo;
-                    split_h(p[8 * c + i], hi, lo);
-                    ph[i] = hi;
-                    pl[i] = lo;
+                for (int i = 0; i < 8; i += 2) {
+                    v2h hi, lo;
+                    split_pair(p[8 * c + i], p[8 * c + i + 1], hi, lo);
+                    ph[i] = hi[0]; ph[i + 1] = hi[1];
+                    pl[i] = lo[0]; pl[i + 1] = lo[1];
                 }
                 // V^T rows: dim li, keys 16c + 4*lh + [0,4) and 16c + 8 + 4*lh + [0,4)
                 const int kA = 16 * c + 4 * lh, kB = 16 * c + 8 + 4 * lh;

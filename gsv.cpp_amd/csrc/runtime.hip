@@ -36,7 +36,7 @@ int launch_attn_prefill(const float * qkv, int B, int S, int max_len, const int3
 
 constexpr int PE_MAX = 4096;   // Y_PE_MAX, src/gsv_ar.cpp:44
 
-// ---- device allocation helper ------------------------------------------------------------
+// ---- device allocation helpers ------------------------------------------------------------
 
 struct DevArena {
     std::vector<void *> ptrs;
@@ -59,6 +59,26 @@ struct DevArena {
         ptrs.push_back(p);
         out = (T *) p;
         return GSVK_OK;
+    }
+};
+
+// Bump allocation from a model-owned pool that is kept between calls; what does not fit is
+// allocated apart (and freed with the arena), and `need` records the size the pool should have so
+// that the next call of the same shape allocates nothing.
+struct PoolArena {
+    char * base = nullptr;
+    size_t cap = 0, off = 0, need = 0;
+    DevArena extra;
+    template <typename T>
+    int alloc(T *& out, size_t count) {
+        const size_t bytes = ((std::max<size_t>(count, 1) * sizeof(T)) + 255) & ~(size_t) 255;
+        need += bytes;
+        if (off + bytes <= cap) {
+            out = (T *) (base + off);
+            off += bytes;
+            return GSVK_OK;
+        }
+        return extra.alloc(out, count);
     }
 };
 
@@ -110,6 +130,9 @@ struct gsvk_model {
     int64_t lstride = 0;
     // decode / state buffers (sized for kv_B)
     DevArena smem;
+    // prefill workspace (activations of all B*S rows), grown to the largest prefill seen
+    void * pf_pool = nullptr;
+    size_t pf_cap = 0;
     int s_B = 0, s_hist = 0, s_steps = 0;
     int64_t s_lstride = 0;
     Act x, attn, n1, hq;
@@ -131,6 +154,7 @@ struct gsvk_model {
     bool use_graph = true;
 
     ~gsvk_model() {
+        if (pf_pool) (void) hipFree(pf_pool);
         if (gexec) (void) hipGraphExecDestroy(gexec);
         if (graph) (void) hipGraphDestroy(graph);
         if (h_pinned) (void) hipHostFree(h_pinned);
@@ -518,7 +542,9 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     const int R = (int) row_b.size();
     const int64_t rows = (int64_t) B * S;
 
-    DevArena tmp;
+    PoolArena tmp;
+    tmp.base = (char *) m->pf_pool;
+    tmp.cap = m->pf_cap;
     int32_t * d_phones, * d_pad, * d_prompt, * d_rowb, * d_rowt, * d_tlen;
     int64_t * d_boff;
     float * d_bert = nullptr, * feat = nullptr, * proj = nullptr;
@@ -635,6 +661,16 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     if (logits_host)
         GSVK_HIP(hipMemcpyAsync(logits_host, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
     GSVK_HIP(hipStreamSynchronize(st));
+    if (tmp.need > m->pf_cap) {
+        // grow the workspace for the next prefill of this size (nothing of it is in use now)
+        if (m->pf_pool) (void) hipFree(m->pf_pool);
+        m->pf_pool = nullptr;
+        m->pf_cap = 0;
+        if (hipMalloc(&m->pf_pool, tmp.need) == hipSuccess)
+            m->pf_cap = tmp.need;
+        else
+            (void) hipGetLastError();   // not an error of this call: the next one allocates apart
+    }
     m->prefilled = true;
     return GSVK_OK;
 }
@@ -953,6 +989,9 @@ extern "C" int gsvk_release_cache(gsvk_model * m) {
     drop_graph(m);
     m->smem.release();
     m->s_B = 0;
+    if (m->pf_pool) (void) hipFree(m->pf_pool);
+    m->pf_pool = nullptr;
+    m->pf_cap = 0;
     m->kvmem.release();
     m->kc = m->vc = nullptr;
     m->kv_B = m->kv_lmax = 0;
