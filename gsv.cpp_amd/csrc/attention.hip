@@ -1,8 +1,8 @@
 // Single-query (decode) attention over a per-sequence fp16 KV cache, for gfx950.
 //
-// Work decomposition: workgroup (split, head, seq) of NW waves (4, 8 or 16, see attn_waves: a
-// long row is spread over up to 16 waves so that its blocks are in flight together instead of
-// one after another). The valid keys [begin, end) of a (seq, head) are cut in blocks of 64;
+// Work decomposition: workgroup (split, head, seq) of NW waves (4 or 8, see attn_waves: a long
+// row is spread over up to 8 waves so that its blocks are in flight together instead of one
+// after another). The valid keys [begin, end) of a (seq, head) are cut in blocks of 64;
 // split s owns a contiguous run of blocks (nsplit is 1 unless batch x heads is small and the rows
 // long, see attn_nsplit). Wave w of a workgroup takes blocks w, w+NW, ... of its run.
 // Inside a block, lane = (key slot ks = lane/4, quarter qd = lane%4) reads the 16-byte quarter
@@ -163,13 +163,15 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
         __hip_atomic_store(counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waves per workgroup: enough to take every block of the longest row at once (4..16), halved
+// Waves per workgroup: enough to take every block of the longest row at once (4..8), halved
 // while the grid would hold more than 8192 waves (32 per CU, the resident limit of 256 CUs).
 int attn_waves(int B, int nh, int64_t max_keys) {
     const int64_t pairs = (int64_t) B * nh;
     const int64_t blocks = (max_keys + ATT_BLK - 1) / ATT_BLK;
+    // at most 8: a workgroup of 16 waves starts later and merges more partials than the extra
+    // parallelism returns (measured at batch 1-16; equal at 64 and 128)
     int nw = 4;
-    while (nw < 16 && nw < blocks) nw *= 2;
+    while (nw < 8 && nw < blocks) nw *= 2;
     while (nw > 4 && pairs * nw > 8192) nw /= 2;
     return nw;
 }
@@ -221,8 +223,7 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
     hipLaunchKernelGGL(k_attn_decode<W>, grid, dim3(W * 64), 0, stream, q, q_stride, k, v, nh,    \
                        lstride, kv_begin, kv_end, ns, scale * LOG2E, out, out16, oq, od, part,   \
                        counters)
-    if (nw == 16) GSVK_ATTN_LAUNCH(16);
-    else if (nw == 8) GSVK_ATTN_LAUNCH(8);
+    if (nw == 8) GSVK_ATTN_LAUNCH(8);
     else GSVK_ATTN_LAUNCH(4);
 #undef GSVK_ATTN_LAUNCH
     GSVK_LAUNCH_CHECK();

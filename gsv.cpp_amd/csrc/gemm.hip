@@ -4,9 +4,10 @@
 //   Y[m][n] = sum_blk  dx[m][blk] * dw[n][blk] * (sum_{k in blk} qx[m][k] * qw[n][k])
 //
 // One v_mfma_i32_32x32x32_i8 covers exactly one 32-value Q8_0 block of a 32x32 output tile, so
-// every block's integer sum is exact; the per-block fp32 scaling is done on the vector ALUs
-// (acc += float(C) * (dx * dw), three operations per output and block: this kernel is bound by
-// them, not by the matrix cores). The fp32 accumulation order (block by block) differs from the
+// every block's integer sum is exact. The scale products dx * dw of the tile come from a second
+// MFMA (an fp16 outer product: both scales are fp16 values, so the fp32 products are exact), and
+// the vector ALUs do the rest, acc += float(C) * (dx * dw): two instructions per output and
+// block, which bound the kernel. The fp32 accumulation order (block by block) differs from the
 // ggml-cpu x86 order (8 lanes, then hsum), so results agree with it to fp32 rounding, not bit
 // for bit; the decode path keeps the bit-exact GEMV.
 //
@@ -32,11 +33,15 @@ constexpr int GM_THREADS = 256;
 constexpr int GM_BM = 128;                 // rows (m) per workgroup
 constexpr int GM_BN = 128;                 // columns (n) per workgroup
 constexpr int GM_KC = 2;                   // blocks per K chunk
-constexpr int GM_ROWB = GM_KC * 32;        // LDS bytes per row and chunk: 4 slots of 16 bytes
+constexpr int GM_NBUF = 2;                 // chunk buffers (a chunk streams in while one is used)
+constexpr int GM_ROWB = GM_KC * 32;        // LDS bytes per row and chunk
+constexpr int GM_SLOTS = GM_ROWB / 16;     // 16-byte slots per row and chunk
+constexpr int GM_SWZ = GM_SLOTS - 1;       // slot swizzle mask
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace
 
@@ -44,10 +49,10 @@ typedef __attribute__((address_space(3))) void lds_void;
 // 64 bytes = 4 slots of 16 bytes; piece p of row r sits in slot p ^ (r & 3), so that the 16-byte
 // operand reads of consecutive rows fall in different banks.
 struct GemmLds {
-    int8_t a[2][GM_BM * GM_ROWB];
-    int8_t b[2][GM_BN * GM_ROWB];
-    float da[2][GM_BM * GM_KC];      // activation scales [row][block]
-    uint16_t db[2][GM_BN * GM_KC];   // weight scales (fp16) [col][block]
+    int8_t a[GM_NBUF][GM_BM * GM_ROWB];
+    int8_t b[GM_NBUF][GM_BN * GM_ROWB];
+    float da[GM_NBUF][GM_BM * GM_KC];      // activation scales [row][block]
+    uint16_t db[GM_NBUF][GM_BN * GM_KC];   // weight scales (fp16) [col][block]
 };
 
 // The chunk buffers during the K loop; half of the fp32 output tile (64 rows, padded by 4 floats)
@@ -63,6 +68,8 @@ __device__ __forceinline__ void lds_dma16(const void * g, void * lds) {
 __device__ __forceinline__ void lds_dma4(const void * g, void * lds) {
     __builtin_amdgcn_global_load_lds(g, (lds_void *) lds, 4, 0, 0);
 }
+// (a direct load places lane L's data at 4 * L for the 1-, 2- and 4-byte forms: the fp16 weight
+// scales travel in pairs)
 
 // Issue the direct loads of one K chunk into buffer buf. A wave's load instruction writes 64
 // consecutive 16-byte (or 4-byte) LDS slots, lane L the L-th; the global address of each lane is
@@ -73,23 +80,28 @@ __device__ __forceinline__ void gemm_issue(const int8_t * __restrict__ xs, const
                                            int m, int m0, int n0, int chunk, int wave, int lane, GemmLds & s,
                                            int buf) {
     const int blk0 = chunk * GM_KC;
+    constexpr int ROWS_PER_SEG = 64 / GM_SLOTS;   // rows covered by one wave instruction (1 KB)
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
-        const int seg = u * 4 + wave;              // 1 KB segment = 16 rows x 4 slots
-        const int r = seg * 16 + (lane >> 2);
-        const int p = (lane & 3) ^ (r & 3);        // the piece that belongs in this slot
+    for (int u = 0; u < GM_KC; u++) {
+        const int seg = u * 4 + wave;
+        const int r = seg * ROWS_PER_SEG + lane / GM_SLOTS;
+        const int p = (lane % GM_SLOTS) ^ (r & GM_SWZ);   // the piece that belongs in this slot
         const int mm = min(m0 + r, m - 1);
         lds_dma16(xs + (int64_t) mm * NBLK * 32 + blk0 * 32 + p * 16, &s.a[buf][seg * 1024]);
         lds_dma16(ws + (int64_t) (n0 + r) * NBLK * 32 + blk0 * 32 + p * 16, &s.b[buf][seg * 1024]);
     }
-    {
-        const int i = wave * 64 + lane;            // 128 rows x 2 blocks
-        const int mm = min(m0 + (i >> 1), m - 1);
-        lds_dma4(xd + (int64_t) mm * NBLK + blk0 + (i & 1), &s.da[buf][wave * 64]);
+#pragma unroll
+    for (int u = 0; u < GM_KC / 2; u++) {          // 128 rows x GM_KC scales, 256 per instruction
+        const int i = u * 256 + wave * 64 + lane;
+        const int mm = min(m0 + i / GM_KC, m - 1);
+        lds_dma4(xd + (int64_t) mm * NBLK + blk0 + i % GM_KC, &s.da[buf][u * 256 + wave * 64]);
     }
-    if (wave < 2) {                                // 128 columns x 2 fp16 scales = 128 x 4 bytes
-        const int col = wave * 64 + lane;
-        lds_dma4(wd + (int64_t) (n0 + col) * NBLK + blk0, &s.db[buf][wave * 128]);
+    // 128 columns x GM_KC fp16 scales, two per 4-byte lane
+    constexpr int DB_LANES = GM_BN * GM_KC / 2;
+    if (wave * 64 < DB_LANES) {
+        const int i = wave * 64 + lane;
+        const int col = i / (GM_KC / 2), pair = i % (GM_KC / 2);
+        lds_dma4(wd + (int64_t) (n0 + col) * NBLK + blk0 + 2 * pair, &s.db[buf][2 * (wave * 64)]);
     }
 }
 
@@ -117,40 +129,49 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
-    gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, 0, wave, lane, s, 0);
+#pragma unroll
+    for (int c = 0; c < GM_NBUF - 1; c++)
+        if (c < NCH) gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, c, wave, lane, s, c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
     for (int ch = 0; ch < NCH; ch++) {
-        const int buf = ch & 1;
-        // the next chunk streams into the other buffer (last read before the previous barrier)
-        if (ch + 1 < NCH) gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, ch + 1, wave, lane, s, buf ^ 1);
+        const int buf = ch % GM_NBUF;
+        // the chunk GM_NBUF - 1 ahead streams into the buffer read before the previous barrier
+        if (ch + GM_NBUF - 1 < NCH)
+            gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, ch + GM_NBUF - 1, wave, lane, s, (ch + GM_NBUF - 1) % GM_NBUF);
 #pragma unroll 1
         for (int bb = 0; bb < GM_KC; bb++) {
             // operands: piece 2 * bb + lg (16 values) of the wave's rows / columns
             v4i fa[2], fb[2];
-            float adx[2], bdw[2];
+            v8h adx[2], bdw[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 const int ra = wm + 32 * h + li, rb = wn + 32 * h + li;
-                fa[h] = *reinterpret_cast<const v4i *>(&s.a[buf][ra * GM_ROWB + (((2 * bb + lg) ^ (ra & 3)) << 4)]);
-                fb[h] = *reinterpret_cast<const v4i *>(&s.b[buf][rb * GM_ROWB + (((2 * bb + lg) ^ (rb & 3)) << 4)]);
-                // the scale-product MFMA: A = dx of the tile's rows, B = dw of its columns, both in
-                // K slot 0 (lanes 0-31); the second K slot is zero
-                adx[h] = lg == 0 ? s.da[buf][ra * GM_KC + bb] : 0.0f;
-                bdw[h] = lg == 0 ? h2f(s.db[buf][rb * GM_KC + bb]) : 0.0f;
+                fa[h] = *reinterpret_cast<const v4i *>(&s.a[buf][ra * GM_ROWB + (((2 * bb + lg) ^ (ra & GM_SWZ)) << 4)]);
+                fb[h] = *reinterpret_cast<const v4i *>(&s.b[buf][rb * GM_ROWB + (((2 * bb + lg) ^ (rb & GM_SWZ)) << 4)]);
+                // the scale-product MFMA: A = dx of the tile's rows, B = dw of its columns, in one
+                // K slot of lanes 0-31, every other slot zero. Both scales are fp16 values (the
+                // activation scale is rounded to fp16 when it is made), so their product is exact
+                // in the fp16 MFMA's fp32 result, as in a vector multiply.
+                adx[h] = v8h{};
+                bdw[h] = v8h{};
+                if (lg == 0) {
+                    adx[h][0] = (_Float16) s.da[buf][ra * GM_KC + bb];
+                    bdw[h][0] = __builtin_bit_cast(_Float16, s.db[buf][rb * GM_KC + bb]);
+                }
             }
-            // per tile: the exact integer sum of the block, the fp32 products dx * dw (one
-            // rounding, as a vector multiply), then acc += float(C) * (dx * dw) on the vector ALUs
+            // per tile: the exact integer sum of the block, the products dx * dw, then
+            // acc += float(C) * (dx * dw) on the vector ALUs
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t >> 1], fb[t & 1], v16i{}, 0, 0, 0);
-                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x2f32(adx[t >> 1], bdw[t & 1], v16f{}, 0, 0, 0);
+                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[t >> 1], bdw[t & 1], v16f{}, 0, 0, 0);
 #pragma unroll
                 for (int v = 0; v < 16; v++) acc[t][v] = __builtin_fmaf((float) c[v], sc[v], acc[t][v]);
             }
         }
-        __builtin_amdgcn_s_waitcnt(0);   // the next chunk has landed
+        __builtin_amdgcn_s_waitcnt(0);   // the chunks issued so far have landed
         __syncthreads();                 // and every wave is done with this one
     }
 

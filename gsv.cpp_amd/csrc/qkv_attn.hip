@@ -56,13 +56,19 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
 
     // Order of work, chosen so that no wave-dependent branch separates a load from its use (the
     // compiler then waits exactly; a wait on a load also completes every load issued before it):
-    // the scalars; every wave's weight rows; wave 0's input stage (its loads and arithmetic in
-    // one branch); every wave's first block of keys. The key blocks (the bulk of the bytes) go
-    // last so that the weights and the input row are not queued behind them.
+    // the scalars; the input row's operands (every wave); every wave's weight rows; wave 0's input
+    // stage arithmetic; every wave's first block of keys. The key blocks (the bulk of the bytes)
+    // go last so that the weights and the input row are not queued behind them.
     const LayerIn & in = a.in;
     const int col = *a.col_ptr + a.col_add;   // column of this step's key
     int beg = a.kv_begin[b];
 
+    // the input row's operands first, in every wave (the same loads in every wave keep the waits
+    // exact; only wave 0 uses them), so that they are not queued behind the weights and keys
+    LnRow lnr;
+    if constexpr (MODE == IN_LN)
+        ln_row_load(in.res + (int64_t) b * QA_K, in.r ? in.r + (int64_t) b * QA_K : g_zero_row,
+                    in.bias ? in.bias : g_zero_row, in.wb, lane, lnr);
     int4 w[PASSES][QA_NB4];
     uint2 dh[PASSES][QA_NB4];
     float rbias[PASSES];
@@ -85,8 +91,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     if (wave == 0) {
         float o[8];
         if constexpr (MODE == IN_LN) {
-            ln_row_wave(in.res + (int64_t) b * QA_K, in.r ? in.r + (int64_t) b * QA_K : g_zero_row,
-                        in.bias ? in.bias : g_zero_row, in.wb, lane, o);
+            ln_row_compute(lnr, o);
         } else {
             const int pos = *in.pos_ptr;
             int tk = in.tok[b];
@@ -247,12 +252,10 @@ int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t 
     const dim3 grid((unsigned) ((int64_t) B * a.n_head));
 #define GSVK_QA(W, MODE) hipLaunchKernelGGL((k_qkv_attn<W, MODE>), grid, dim3(W * 64), 0, stream, a)
     if (a.in.mode == IN_LN) {
-        if (nw == 16) GSVK_QA(16, IN_LN);
-        else if (nw == 8) GSVK_QA(8, IN_LN);
+        if (nw == 8) GSVK_QA(8, IN_LN);
         else GSVK_QA(4, IN_LN);
     } else {
-        if (nw == 16) GSVK_QA(16, IN_EMB);
-        else if (nw == 8) GSVK_QA(8, IN_EMB);
+        if (nw == 8) GSVK_QA(8, IN_EMB);
         else GSVK_QA(4, IN_EMB);
     }
 #undef GSVK_QA

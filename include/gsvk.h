@@ -198,7 +198,8 @@ int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
  * per-block scaling): the projections of src/gsv_ar.cpp:244-263 over many rows (prefill). The
  * same product as gsvk_op_q8_gemv, but both operands have their quants in NATURAL order (wq
  * [n][k] = the GGUF blocks' quants without the scales, xq [m][k]) with the scales apart (wd fp16
- * [n][k/32], xd fp32 [m][k/32]); the fp32 accumulation runs block by block instead of in
+ * [n][k/32], xd fp32 [m][k/32] holding fp16 values, as every Q8_0 scale does); the fp32
+ * accumulation runs block by block instead of in
  * ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must be a multiple of 128,
  * k 512 or 2048; bias and y 16-byte aligned. */
 int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xq,

@@ -288,8 +288,8 @@ def test_attn_decode_parity(gpu):
     (4, 16, 400, "8 waves per workgroup"),
     (80, 16, 1000, "4 waves per workgroup (1280 (seq, head) pairs cap the grid)"),
     (40, 16, 1000, "8 waves per workgroup (640 pairs)"),
-    (2, 4, 4096, "16 waves per workgroup, 4 splits merged by the last workgroup"),
-    (1, 16, 3000, "16 waves per workgroup, 2 splits"),
+    (2, 4, 4096, "8 waves per workgroup, 4 splits merged by the last workgroup"),
+    (1, 16, 3000, "8 waves per workgroup, 2 splits"),
 ])
 def test_attn_decode_launch_shapes(gpu, B, nh, lstride, what):
     import torch
