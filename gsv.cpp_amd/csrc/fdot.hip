@@ -71,6 +71,69 @@ __global__ void __launch_bounds__(256) k_fdot_ggml(const WT * __restrict__ W, in
     }
 }
 
+// MODE 0 with K = 32 * NI known at compile time (the decode head, K = 512): the same arithmetic
+// as k_fdot_ggml, with every load issued up front. The MT activation rows (rounded to fp16 for
+// F16 weights) are staged once per workgroup in LDS with 16-byte loads; each lane loads its NI
+// weights before the first use. 256 threads = 8 rows x 32 lanes; grid (ceil(n/8), ceil(m/MT)).
+template <typename WT, int MT, int NI>
+__global__ void __launch_bounds__(256) k_fdot_ggml_k(const WT * __restrict__ W, int n,
+                                                     const float * __restrict__ X, int64_t xs, int m,
+                                                     float * __restrict__ Y, int64_t ys) {
+    constexpr int K = 32 * NI;
+    const bool x16 = sizeof(WT) == 2;
+    const int tid = threadIdx.x;
+    const int p = tid & 31;
+    const int row = blockIdx.x * 8 + (tid >> 5);
+    const int m0 = blockIdx.y * MT;
+    const int rowc = row < n ? row : n - 1;
+    __shared__ __align__(16) float s_x[MT][K];
+    constexpr int X4 = MT * K / 4;                       // float4 chunks of the MT rows
+    constexpr int XN = (X4 + 255) / 256;
+    float4 xv[XN];
+#pragma unroll
+    for (int u = 0; u < XN; u++) {
+        int c = tid + u * 256;
+        c = c < X4 ? c : X4 - 1;
+        const int mm = min(m0 + c / (K / 4), m - 1);
+        xv[u] = *reinterpret_cast<const float4 *>(X + (int64_t) mm * xs + (c % (K / 4)) * 4);
+    }
+    const WT * wr = W + (int64_t) rowc * K;
+    float w[NI];
+#pragma unroll
+    for (int i = 0; i < NI; i++) w[i] = wload<WT>(wr + 32 * i + p);
+#pragma unroll
+    for (int u = 0; u < XN; u++) {
+        const int c = tid + u * 256;
+        if (c < X4) {
+            float4 v = xv[u];
+            v.x = xconv(v.x, x16); v.y = xconv(v.y, x16); v.z = xconv(v.z, x16); v.w = xconv(v.w, x16);
+            *reinterpret_cast<float4 *>(&s_x[c / (K / 4)][(c % (K / 4)) * 4]) = v;
+        }
+    }
+    __syncthreads();
+    float acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) acc[t] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; i++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc[t] = __builtin_fmaf(w[i], s_x[t][32 * i + p], acc[t]);
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        float v = acc[t];
+        v = v + __shfl_xor(v, 16, 64);
+        v = v + __shfl_xor(v, 8, 64);
+        v = v + __shfl_xor(v, 4, 64);
+        v = v + __shfl_xor(v, 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        acc[t] = v;
+    }
+    if (p != 0 || row >= n) return;
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+        if (m0 + t < m) Y[(int64_t) (m0 + t) * ys + row] = acc[t];
+}
+
 // MODE 1: 256 threads = 32 rows x 8 lanes; grid (ceil(n/32), ceil(m/MT))
 template <typename WT, int MT>
 __global__ void __launch_bounds__(256) k_fdot_tinyblas(const WT * __restrict__ W, int n, int k,
@@ -124,6 +187,15 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
         else
             hipLaunchKernelGGL((k_fdot_tinyblas<float, MT>), grid, dim3(256), 0, stream,
                                (const float *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+    } else if (k == 512 && xs % 4 == 0 && ((uintptr_t) X & 15) == 0) {
+        constexpr int MTK = 8;
+        const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MTK - 1) / MTK));
+        if (wtype == 1)
+            hipLaunchKernelGGL((k_fdot_ggml_k<uint16_t, MTK, 16>), grid, dim3(256), 0, stream,
+                               (const uint16_t *) W, (int) n, X, xs, (int) m, Y, ys);
+        else
+            hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16>), grid, dim3(256), 0, stream,
+                               (const float *) W, (int) n, X, xs, (int) m, Y, ys);
     } else {
         const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MT - 1) / MT));
         if (wtype == 1)
