@@ -3,14 +3,17 @@
 // Work decomposition: workgroup (split, head, seq) of NW waves (4 or 8, see attn_waves: a long
 // row is spread over up to 8 waves so that its blocks are in flight together instead of one
 // after another). The valid keys [begin, end) of a (seq, head) are cut in blocks of 64;
-// split s owns a contiguous run of blocks (nsplit is 1 unless batch x heads is small and the rows
-// long, see attn_nsplit). Wave w of a workgroup takes blocks w, w+NW, ... of its run.
+// split s owns a contiguous run of blocks (see attn_plan: one run per row unless batch x heads is
+// small and the rows long, or many rows are long enough to be cut in fixed chunks so that the
+// launch holds more workgroups than the chip runs at once and rows of unequal length balance).
+// Wave w of a workgroup takes blocks w, w+NW, ... of its run.
 // Inside a block, lane = (key slot ks = lane/4, quarter qd = lane%4) reads the 16-byte quarter
 // [8qd, 8qd+8) of 4 K rows and 4 V rows (all 8 loads issued before any use, and the next block's
 // loads issued before this block's arithmetic); one wave-wide load covers 1 KiB of contiguous
 // cache. Each wave keeps an online softmax (running max per block, exp2 of log2e-scaled scores);
 // the NW waves merge through LDS, and the splits of one (seq, head), if more than one, are merged
-// by the last workgroup to finish (device-scope counter), so one launch does the whole op.
+// by the last workgroup to finish (device-scope counter, few rows) or by k_attn_merge, a second
+// launch (fixed chunks: no device-scope release per workgroup).
 //
 // Numerics: softmax(q.k * scale) . V over the valid keys with fp32 accumulation; the output is
 // divided by the sum (multiplied by its reciprocal), as ggml_flash_attn_ext does.
@@ -18,13 +21,40 @@
 
 namespace gsvk {
 
+constexpr int ATT_MERGE_WAVES = 16;
+
+// Merge of the nact (<= 64) partials (m, l, o[32]) of one (seq, head) by one wave: lane c reads
+// partial c's (m, l), every lane < 32 its o column; output as attn_store_out.
+__device__ __forceinline__ void attn_merge_parts(const float * p0, int nact, int lane, int64_t bh,
+                                                 int nh, float * __restrict__ out,
+                                                 uint16_t * __restrict__ out16,
+                                                 int8_t * __restrict__ oq, float * __restrict__ od,
+                                                 int oq_layout) {
+    const float mc = lane < nact ? ld_coherent(p0 + lane * ATT_PART) : -INFINITY;
+    const float lc = lane < nact ? ld_coherent(p0 + lane * ATT_PART + 1) : 0.0f;
+    float Mt = mc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) Mt = fmaxf(Mt, __shfl_xor(Mt, off, 64));
+    const float fc = lane < nact ? __builtin_amdgcn_exp2f(mc - Mt) : 0.0f;
+    float Lt = lc * fc;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) Lt += __shfl_xor(Lt, off, 64);
+    float Ot = 0.0f;
+    for (int c = 0; c < nact; c++) {
+        const float w = __shfl(fc, c, 64);
+        if (lane < ATT_HD) Ot = __builtin_fmaf(ld_coherent(p0 + c * ATT_PART + 2 + lane), w, Ot);
+    }
+    attn_store_out(Ot * (1.0f / Lt), lane, bh, nh, out, out16, oq, od, oq_layout);
+}
+
 template <int NW>
 __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     const float * __restrict__ q, int64_t q_stride, const uint16_t * __restrict__ kc,
     const uint16_t * __restrict__ vc, int nh, int64_t lstride, const int32_t * __restrict__ kv_begin,
-    const int32_t * __restrict__ kv_end, int nsplit, float scale_log2, float * __restrict__ out,
-    uint16_t * __restrict__ out16, int8_t * __restrict__ oq, float * __restrict__ od,
-    float * __restrict__ part, int32_t * __restrict__ counters) {
+    const int32_t * __restrict__ kv_end, int nsplit, int chunk, float scale_log2,
+    float * __restrict__ out, uint16_t * __restrict__ out16, int8_t * __restrict__ oq,
+    float * __restrict__ od, int oq_layout, float * __restrict__ part,
+    int32_t * __restrict__ counters) {
     const int split = blockIdx.x;
     const int h = blockIdx.y;
     const int b = blockIdx.z;
@@ -35,7 +65,10 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     end = end > (int) lstride ? (int) lstride : end;
     const int nkeys = end > beg ? end - beg : 0;
     const int nblk = (nkeys + ATT_BLK - 1) / ATT_BLK;
-    const int bps = (nblk + nsplit - 1) / nsplit;               // blocks per split
+    // blocks per split: a row longer than the launch planned for (more than nsplit chunks) gets
+    // longer runs, so that no split index reaches nsplit
+    const int even = (nblk + nsplit - 1) / nsplit;
+    const int bps = chunk > even ? chunk : even;
     const int nact = bps > 0 ? (nblk + bps - 1) / bps : 0;      // splits with work
     if (split >= (nact > 0 ? nact : 1)) return;
 
@@ -51,7 +84,7 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     __shared__ float s_o[NW][ATT_HD];
 
     if (nkeys == 0) {   // no valid key: ggml returns 0 (S == 0 -> S_inv = 0)
-        if (wave == 0) attn_store_out(0.0f, lane, bh, nh, out, out16, oq, od);
+        if (wave == 0) attn_store_out(0.0f, lane, bh, nh, out, out16, oq, od, oq_layout);
         return;
     }
 
@@ -121,12 +154,21 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     }
 
     if (nact == 1) {
-        attn_store_out(O * (1.0f / L), lane, bh, nh, out, out16, oq, od);
+        attn_store_out(O * (1.0f / L), lane, bh, nh, out, out16, oq, od, oq_layout);
         return;
     }
 
-    // several splits: publish the partial, the last workgroup of this (seq, head) merges
+    // several splits: publish the partial; k_attn_merge (fixed chunks) or the last workgroup of
+    // this (seq, head) merges
     float * pp = part + (bh * nsplit + split) * ATT_PART;
+    if (chunk > 0) {
+        if (lane < ATT_HD) pp[2 + lane] = O;
+        if (lane == 0) {
+            pp[0] = M;
+            pp[1] = L;
+        }
+        return;
+    }
     if (lane < ATT_HD) st_coherent(pp + 2 + lane, O);
     if (lane == 0) {
         st_coherent(pp + 0, M);
@@ -142,25 +184,34 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     const int last = __shfl(lastflag, 0, 64);
     if (!last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    // lane c < nact reads split c's (m, l) in parallel; every lane < 32 reads its o column
-    const float * p0 = part + bh * nsplit * ATT_PART;
-    const float mc = lane < nact ? ld_coherent(p0 + lane * ATT_PART) : -INFINITY;
-    const float lc = lane < nact ? ld_coherent(p0 + lane * ATT_PART + 1) : 0.0f;
-    float Mt = mc;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) Mt = fmaxf(Mt, __shfl_xor(Mt, off, 64));
-    const float fc = lane < nact ? __builtin_amdgcn_exp2f(mc - Mt) : 0.0f;
-    float Lt = lc * fc;
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) Lt += __shfl_xor(Lt, off, 64);
-    float Ot = 0.0f;
-    for (int c = 0; c < nact; c++) {
-        const float w = __shfl(fc, c, 64);
-        if (lane < ATT_HD) Ot = __builtin_fmaf(ld_coherent(p0 + c * ATT_PART + 2 + lane), w, Ot);
-    }
-    attn_store_out(Ot * (1.0f / Lt), lane, bh, nh, out, out16, oq, od);
+    attn_merge_parts(part + bh * nsplit * ATT_PART, nact, lane, bh, nh, out, out16, oq, od, oq_layout);
     if (lane == 0)
         __hip_atomic_store(counters + bh, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge of the fixed-chunk partials of k_attn_decode: workgroup (head group, seq), one wave per
+// head of a sequence with more than one chunk (a row of one chunk was stored by its workgroup).
+__global__ void __launch_bounds__(ATT_MERGE_WAVES * 64) k_attn_merge(
+    const int32_t * __restrict__ kv_begin, const int32_t * __restrict__ kv_end, int nh,
+    int64_t lstride, int nsplit, int chunk, const float * __restrict__ part,
+    float * __restrict__ out, uint16_t * __restrict__ out16, int8_t * __restrict__ oq,
+    float * __restrict__ od, int oq_layout) {
+    const int h = blockIdx.x * ATT_MERGE_WAVES + (int) (threadIdx.x >> 6);
+    const int b = blockIdx.y;
+    if (h >= nh) return;
+    int beg = kv_begin[b];
+    int end = kv_end[b];
+    beg = beg < 0 ? 0 : beg;
+    end = end > (int) lstride ? (int) lstride : end;
+    const int nkeys = end > beg ? end - beg : 0;
+    const int nblk = (nkeys + ATT_BLK - 1) / ATT_BLK;
+    const int even = (nblk + nsplit - 1) / nsplit;
+    const int bps = chunk > even ? chunk : even;     // as in k_attn_decode
+    const int nact = bps > 0 ? (nblk + bps - 1) / bps : 0;
+    if (nact <= 1) return;
+    const int64_t bh = (int64_t) b * nh + h;
+    attn_merge_parts(part + bh * nsplit * ATT_PART, nact, threadIdx.x & 63, bh, nh, out, out16, oq,
+                     od, oq_layout);
 }
 
 // Waves per workgroup: enough to take every block of the longest row at once (4..8), halved
@@ -176,21 +227,40 @@ int attn_waves(int B, int nh, int64_t max_keys) {
     return nw;
 }
 
-// Splits per (seq, head). Merging splits needs an agent-scope release per workgroup, which on
-// gfx950 writes back the L2 of the workgroup's XCD; that costs more than it saves unless the
-// launch would otherwise leave most of the chip idle on long rows. So: one workgroup per
-// (seq, head) when there are >= 64 of them or the rows are short, else enough splits of at least
-// 16 blocks (1024 keys) to reach ~256 workgroups, at most 64 (the merge reads one split per lane).
-int attn_nsplit(int B, int nh, int64_t max_keys) {
+// Splits per (seq, head). Merging splits through the last workgroup needs an agent-scope release
+// per workgroup, which on gfx950 writes back the L2 of the workgroup's XCD; that costs more than it
+// saves unless the launch would otherwise leave most of the chip idle on long rows. So, with few
+// rows: one workgroup per (seq, head) when the rows are short, else enough splits of at least 16
+// blocks (1024 keys) to reach ~256 workgroups, at most 64 (the merge reads one split per lane).
+// With >= 1024 rows whose longest has >= 48 blocks the workgroups of one (seq, head) per row would
+// all be resident at once, each CU holding a random handful of rows of unequal length: the rows
+// are cut in chunks of ATT_CHUNK blocks instead (more workgroups than the chip holds, taken up as
+// others finish), merged by k_attn_merge. Batch 128 x 16 heads with rows U[1024, 4096]: 129 us
+// of attention per layer -> 121 us + 5 us of merge. Rows of at most 2 chunks lose more to the
+// extra launch than the balance returns (batch 64 x 16 heads, rows U[256, 2048]: 31 -> 37 us).
+constexpr int ATT_CHUNK = 16;
+
+AttnPlan attn_plan(int B, int nh, int64_t max_keys) {
     const int64_t pairs = (int64_t) B * nh;
     const int64_t blocks = (max_keys + ATT_BLK - 1) / ATT_BLK;
-    if (pairs >= 64 || blocks < 32) return 1;
+    AttnPlan p{1, 0};
+    if (pairs >= 1024) {
+        if (blocks >= 3 * ATT_CHUNK) {
+            p.chunk = ATT_CHUNK;
+            p.nsplit = (int) ((blocks + ATT_CHUNK - 1) / ATT_CHUNK);
+        }
+        return p;
+    }
+    if (pairs >= 64 || blocks < 32) return p;
     int64_t ns = (256 + pairs - 1) / pairs;
     if (ns > blocks / 16) ns = blocks / 16;
     if (ns > 64) ns = 64;
     if (ns < 1) ns = 1;
-    return (int) ns;
+    p.nsplit = (int) ns;
+    return p;
 }
+
+int attn_nsplit(int B, int nh, int64_t max_keys) { return attn_plan(B, nh, max_keys).nsplit; }
 
 size_t attn_workspace_bytes(int B, int nh, int64_t max_keys) {
     const int ns = attn_nsplit(B, nh, max_keys);
@@ -204,7 +274,8 @@ size_t attn_workspace_bytes(int B, int nh, int64_t max_keys) {
 int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
                        int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,
                        const int32_t * kv_end, int64_t max_keys, float scale, float * out,
-                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream) {
+                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream,
+                       int oq_layout) {
     GSVK_REQUIRE(q && k && v && kv_begin && kv_end && out && ws, "attn_decode: null pointer");
     GSVK_REQUIRE(hd == ATT_HD, "attn_decode: head_dim must be 32 (got %d)", hd);
     GSVK_REQUIRE(q_stride >= (int64_t) nh * hd && q_stride % 4 == 0, "attn_decode: bad q stride");
@@ -213,7 +284,9 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
                  "attn_decode: bad shape B=%d nh=%d lstride=%lld max_keys=%lld", B, nh,
                  (long long) lstride, (long long) max_keys);
     GSVK_REQUIRE((oq == nullptr) == (od == nullptr), "attn_decode: oq and od go together");
-    const int ns = attn_nsplit(B, nh, max_keys);
+    const AttnPlan plan = attn_plan(B, nh, max_keys);
+    const int ns = plan.nsplit;
+    GSVK_REQUIRE(ns <= 64, "attn_decode: rows too long for the split merge");
     const size_t part_bytes = (size_t) B * nh * ns * ATT_PART * sizeof(float);
     float * part = (float *) ws;
     int32_t * counters = (int32_t *) ((char *) ws + ((part_bytes + 255) / 256) * 256);
@@ -221,12 +294,19 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
     const int nw = attn_waves(B, nh, max_keys);
 #define GSVK_ATTN_LAUNCH(W)                                                                      \
     hipLaunchKernelGGL(k_attn_decode<W>, grid, dim3(W * 64), 0, stream, q, q_stride, k, v, nh,    \
-                       lstride, kv_begin, kv_end, ns, scale * LOG2E, out, out16, oq, od, part,   \
-                       counters)
+                       lstride, kv_begin, kv_end, ns, plan.chunk, scale * LOG2E, out, out16, oq, \
+                       od, oq_layout, part, counters)
     if (nw == 8) GSVK_ATTN_LAUNCH(8);
     else GSVK_ATTN_LAUNCH(4);
 #undef GSVK_ATTN_LAUNCH
     GSVK_LAUNCH_CHECK();
+    if (plan.chunk > 0) {
+        const int hw = nh < ATT_MERGE_WAVES ? nh : ATT_MERGE_WAVES;
+        const dim3 mgrid((unsigned) ((nh + ATT_MERGE_WAVES - 1) / ATT_MERGE_WAVES), (unsigned) B);
+        hipLaunchKernelGGL(k_attn_merge, mgrid, dim3(hw * 64), 0, stream, kv_begin, kv_end, nh,
+                           lstride, ns, plan.chunk, part, out, out16, oq, od, oq_layout);
+        GSVK_LAUNCH_CHECK();
+    }
     return GSVK_OK;
 }
 

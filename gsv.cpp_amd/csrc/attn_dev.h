@@ -27,12 +27,13 @@ __device__ __forceinline__ void st_coherent(float * p, float v) {
 }
 
 // Final output of one (seq, head): lanes 0..31 of the calling wave hold one dimension each.
-// The Q8_0 copy is written in the sliced layout of a row of nh*32 values: head h is block h.
+// The Q8_0 copy of a row of nh*32 values is written in the given layout (Q8Layout: sliced for
+// the GEMV, natural or tiled for the GEMMs); head h is block h.
 __device__ __forceinline__ void attn_store_out(float val, int lane, int64_t bh, int nh,
                                                float * __restrict__ out,
                                                uint16_t * __restrict__ out16,
                                                int8_t * __restrict__ oq,
-                                               float * __restrict__ od) {
+                                               float * __restrict__ od, int layout = Q8_SLICED) {
     if (lane < ATT_HD) {
         out[bh * ATT_HD + lane] = val;
         if (out16) out16[bh * ATT_HD + lane] = f2h(val);
@@ -44,8 +45,14 @@ __device__ __forceinline__ void attn_store_out(float val, int lane, int64_t bh, 
         if (lane < ATT_HD) {
             const int64_t b = bh / nh;
             const int h = (int) (bh % nh);
-            oq[b * nh * ATT_HD + q8_sliced_offset(nh, h, lane)] = q1[0];
-            if (lane == 0) od[bh] = d;   // block index == b*nh + h
+            if (layout == Q8_TILED) {
+                oq[q8_tiled_offset(b, nh, h, lane)] = q1[0];
+                if (lane == 0) od[q8_tiled_scale(b, nh, h)] = d;
+            } else {
+                oq[b * nh * ATT_HD + (layout == Q8_NATURAL ? (int64_t) h * ATT_HD + lane
+                                                            : q8_sliced_offset(nh, h, lane))] = q1[0];
+                if (lane == 0) od[bh] = d;   // block index == b*nh + h
+            }
         }
     }
 }
@@ -135,6 +142,13 @@ __device__ __forceinline__ void attn_block_step(KV8 cur, int key0, int end, int 
 
 // waves per workgroup and splits per (seq, head) of the decode attention (attention.hip)
 int attn_waves(int B, int nh, int64_t max_keys);
+// Split of the rows: nsplit runs per (seq, head), of `chunk` blocks each when chunk > 0 (merged by
+// a second launch), else of ceil(blocks / nsplit) blocks (merged by the last workgroup).
+struct AttnPlan {
+    int nsplit;
+    int chunk;
+};
+AttnPlan attn_plan(int B, int nh, int64_t max_keys);
 int attn_nsplit(int B, int nh, int64_t max_keys);
 
 }  // namespace gsvk

@@ -183,6 +183,50 @@ __device__ __forceinline__ void q8_store_natural(int8_t * row, int blk, int sub,
     *reinterpret_cast<int2 *>(row + blk * 32 + sub * 8) = make_int2(lo, hi);
 }
 
+// Layouts of a Q8_0 matrix [rows][k] whose scales are stored apart from the quants:
+//   Q8_SLICED  quants of row r: group j of every block together, qs[r][j][blk][4] (the GEMV's
+//              operand), scales [r][k/32];
+//   Q8_NATURAL quants [r][k] in order, scales [r][k/32] (the 128 x 128 GEMM's operand);
+//   Q8_TILED   the matrix-core operand order of the small-batch GEMM: for each 32-row tile and
+//              block, 1 KB in which lane L = 32*h + i holds the 16 quants [16h, 16h+16) of
+//              row i of the tile at bytes [16L, 16L+16); scales per (tile, block) as 32
+//              consecutive values (row i at i). Rows are padded to a multiple of 32.
+enum Q8Layout { Q8_SLICED = 0, Q8_NATURAL = 1, Q8_TILED = 2 };
+
+// Byte offset of quant c (0..31) of block blk of row r in a Q8_TILED matrix of nblk blocks per row.
+__device__ __host__ __forceinline__ int64_t q8_tiled_offset(int64_t r, int nblk, int blk, int c) {
+    return (((r >> 5) * nblk + blk) << 10) + ((((c >> 4) << 5) | (int) (r & 31)) << 4) + (c & 15);
+}
+// Index of the scale of block blk of row r in a Q8_TILED matrix.
+__device__ __host__ __forceinline__ int64_t q8_tiled_scale(int64_t r, int nblk, int blk) {
+    return (((r >> 5) * nblk + blk) << 5) + (r & 31);
+}
+
+// Store the 8 quants [8*sub, 8*sub+8) of block blk of row r of a Q8_TILED matrix.
+__device__ __forceinline__ void q8_store_tiled(int8_t * base, int64_t r, int nblk, int blk, int sub,
+                                               const int8_t (&q)[8]) {
+    const int lo = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    const int hi = (q[4] & 0xff) | ((q[5] & 0xff) << 8) | ((q[6] & 0xff) << 16) | ((q[7] & 0xff) << 24);
+    *reinterpret_cast<int2 *>(base + q8_tiled_offset(r, nblk, blk, 8 * sub)) = make_int2(lo, hi);
+}
+
+// Store the 8 quants of values [8*sub, 8*sub+8) of block blk of row r (and the block's scale
+// when store_d) in the given layout (matrix of nblk blocks per row).
+__device__ __forceinline__ void q8_store_row8(int8_t * q, float * qd, int layout, int64_t r, int nblk,
+                                              int blk, int sub, const int8_t (&v)[8], float d,
+                                              bool store_d) {
+    if (layout == Q8_TILED) {
+        q8_store_tiled(q, r, nblk, blk, sub, v);
+        if (store_d) qd[q8_tiled_scale(r, nblk, blk)] = d;
+        return;
+    }
+    if (layout == Q8_NATURAL)
+        q8_store_natural(q + r * nblk * 32, blk, sub, v);
+    else
+        q8_store_sliced(q + r * nblk * 32, nblk, blk, sub, v);
+    if (store_d) qd[r * nblk + blk] = d;
+}
+
 // The same with an explicit byte distance between slices (LDS copies of a row pad each slice by
 // 16 bytes, so that the 8 slices a wave reads at once fall in different banks).
 __device__ __forceinline__ void q8_store_sliced_s(int8_t * row, int slice_bytes, int blk, int sub,
@@ -219,22 +263,27 @@ struct GemvEpilogue {
 int launch_q8_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xs,
                    const float * xd, int64_t m, const GemvEpilogue & epi, float * y,
                    hipStream_t stream);
-// Q8_0 outputs go to the sliced layout (GEMV operands) unless natural is set (GEMM operands).
+// Q8_0 outputs go to the given layout (Q8Layout; the GEMV reads Q8_SLICED, the GEMMs
+// Q8_NATURAL / Q8_TILED).
 int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, float * xd,
-                       hipStream_t stream, bool natural = false);
-// qn (may be null): the quants in natural order as well, for the GEMM
+                       hipStream_t stream, int layout = Q8_SLICED);
+// qn (may be null): the quants in natural order as well; qt/dt (may be null; rows % 32 == 0):
+// quants and scales in the Q8_TILED order
 int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
-                     hipStream_t stream, int8_t * qn = nullptr);
+                     hipStream_t stream, int8_t * qn = nullptr, int8_t * qt = nullptr,
+                     uint16_t * dt = nullptr);
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, bool natural = false);
+                     hipStream_t stream, int layout = Q8_SLICED);
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
-                    int8_t * xq, float * xd, hipStream_t stream);
+                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, hipStream_t stream,
+                    int layout = Q8_SLICED);
 size_t attn_workspace_bytes(int B, int nh, int64_t max_keys);
 int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
                        int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,
                        const int32_t * kv_end, int64_t max_keys, float scale, float * out,
-                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream);
+                       uint16_t * out16, int8_t * oq, float * od, void * ws, hipStream_t stream,
+                       int oq_layout = Q8_SLICED);
 
 }  // namespace gsvk

@@ -261,11 +261,203 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
     }
 }
 
-int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
-                   const int8_t * xs, const float * xd, const LayerOut & out, hipStream_t stream) {
-    GSVK_REQUIRE(ws && wd && xs && xd, "q8_gemm: null pointer");
-    GSVK_REQUIRE(n > 0 && n % GM_BN == 0 && n < (1 << 30) && m > 0 && m < (1 << 30),
-                 "q8_gemm: n must be a multiple of %d (n=%lld m=%lld)", GM_BN, (long long) n, (long long) m);
+// ---- small batches (decode at 64-256 rows): tiles of 32 columns x 32*MT rows ----
+// A 128 x 128 tile leaves most of the chip idle at these sizes (a 512-column projection would
+// be 4 workgroups). Here a workgroup of 4 waves owns 32 columns and 32*MT rows, and the K range
+// is split over its waves (wave w takes blocks [w*NBLK/4, (w+1)*NBLK/4)): each wave computes the
+// whole tile over its quarter with operands loaded from global memory straight into registers
+// (lane (li, lg): 16 values of row/column li, half lg of the block), a group of blocks ahead of
+// its use. The four partial tiles are summed through LDS in wave order, so the result does not
+// depend on timing. Same arithmetic per block as k_q8_gemm.
+constexpr int GS_THREADS = 256;
+constexpr int64_t GS_MAX_ROWS = 256;      // launch_q8_gemm takes this kernel up to this many rows
+
+template <int NBLK, int MT>
+__global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n, int m,
+                                                                const int8_t * __restrict__ xs,
+                                                                const float * __restrict__ xd,
+                                                                bool x_tiled, LayerOut out) {
+    constexpr int NBW = NBLK / 4;                                  // blocks per wave
+    constexpr int G = NBW <= 4 ? NBW : (MT >= 4 ? 2 : 4);          // blocks per load group
+    constexpr int NG = NBW / G;
+    static_assert(NBW % G == 0, "load groups must tile the wave's blocks");
+    __shared__ float red[4][32 * MT][33];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int li = lane & 31;
+    const int lg = lane >> 5;
+    const int n0 = blockIdx.x * 32;
+    const int m0 = blockIdx.y * 32 * MT;
+    const int kb0 = wave * NBW;
+    // operand of block kb: quants at base + kb * step (16 bytes), scale at dbase[kb * dstep]. Tiled:
+    // the (tile, block) kilobyte in lane order (one whole-line wave load); natural: 16 bytes of
+    // row li.
+    const bool w_tiled = w.qt != nullptr;
+    const int8_t * wrow;
+    const uint16_t * wdr;
+    if (w_tiled) {
+        wrow = w.qt + ((int64_t) (n0 >> 5) * NBLK << 10) + lane * 16;
+        wdr = w.dt + ((int64_t) (n0 >> 5) * NBLK << 5) + li;
+    } else {
+        wrow = w.qn + (int64_t) (n0 + li) * NBLK * 32 + lg * 16;
+        wdr = w.dn + (int64_t) (n0 + li) * NBLK;
+    }
+    const int wstep = w_tiled ? 1024 : 32, wdstep = w_tiled ? 32 : 1;
+    const int8_t * xrow[MT];
+    const float * xdr[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++) {
+        if (x_tiled) {                                  // rows are padded to the tile
+            const int64_t tile = (m0 >> 5) + t;
+            xrow[t] = xs + ((tile * NBLK) << 10) + lane * 16;
+            xdr[t] = xd + ((tile * NBLK) << 5) + li;
+        } else {
+            const int mm = min(m0 + 32 * t + li, m - 1);   // rows past m repeat the last one (unused)
+            xrow[t] = xs + (int64_t) mm * NBLK * 32 + lg * 16;
+            xdr[t] = xd + (int64_t) mm * NBLK;
+        }
+    }
+    const int xstep = x_tiled ? 1024 : 32, xdstep = x_tiled ? 32 : 1;
+
+    v4i a[2][G][MT], b[2][G];
+    float dx[2][G][MT];
+    uint16_t dw[2][G];
+    auto load = [&](int g, int s) {
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            const int kb = kb0 + g * G + u;
+            b[s][u] = *reinterpret_cast<const v4i *>(wrow + (int64_t) kb * wstep);
+#pragma unroll
+            for (int t = 0; t < MT; t++) a[s][u][t] = *reinterpret_cast<const v4i *>(xrow[t] + (int64_t) kb * xstep);
+            dw[s][u] = wdr[kb * wdstep];
+#pragma unroll
+            for (int t = 0; t < MT; t++) dx[s][u][t] = xdr[t][kb * xdstep];
+        }
+    };
+
+    float acc[MT][16];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
+    load(0, 0);
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const int s = g & 1;
+        if (g + 1 < NG) load(g + 1, s ^ 1);
+#pragma unroll
+        for (int u = 0; u < G; u++) {
+            v8h bdw = v8h{};
+            if (lg == 0) bdw[0] = __builtin_bit_cast(_Float16, dw[s][u]);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                v8h adx = v8h{};
+                if (lg == 0) adx[0] = (_Float16) dx[s][u][t];
+                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[s][u][t], b[s][u], v16i{}, 0, 0, 0);
+                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx, bdw, v16f{}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[t][v] = __builtin_fmaf((float) c[v], sc[v], acc[t][v]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int v = 0; v < 16; v++) red[wave][32 * t + 8 * (v >> 2) + 4 * lg + (v & 3)][li] = acc[t][v];
+    __syncthreads();
+
+    // epilogue: thread -> row (tid / 8) + 32 i, columns 4 * (tid % 8) .. + 4 of the tile
+    int kvcol0 = 0;
+    if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
+    const int cg = tid & 7;
+    const int col = n0 + 4 * cg;
+    float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (out.bias) bias4 = *reinterpret_cast<const float4 *>(out.bias + col);
+#pragma unroll
+    for (int i = 0; i < MT; i++) {
+        const int r = (tid >> 3) + 32 * i;
+        const int row = m0 + r;
+        const bool valid = row < m;
+        float y[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+            y[c] = ((red[0][r][4 * cg + c] + red[1][r][4 * cg + c]) + red[2][r][4 * cg + c]) + red[3][r][4 * cg + c];
+        if (out.bias) {
+            y[0] = y[0] + bias4.x; y[1] = y[1] + bias4.y; y[2] = y[2] + bias4.z; y[3] = y[3] + bias4.w;
+        }
+        if (out.act == 1) {
+#pragma unroll
+            for (int c = 0; c < 4; c++) y[c] = y[c] > 0.0f ? y[c] : 0.0f;
+        }
+        if (out.y && n0 < out.n_store && valid)
+            *reinterpret_cast<float4 *>(out.y + (int64_t) row * out.y_stride + col) = make_float4(y[0], y[1], y[2], y[3]);
+        if (out.yq) {
+            // the 32 columns of the tile are one Q8_0 block of the row, spread over 8 lanes
+            int8_t q[4];
+            const float d = q8_quantize_group<4>(y, q, 8);
+            if (valid) {
+                const int qw = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+                const int nb = n / 32;
+                if (out.yq_layout == Q8_TILED) {
+                    *reinterpret_cast<int *>(out.yq + q8_tiled_offset(row, nb, blockIdx.x, 4 * cg)) = qw;
+                    if (cg == 0) out.yd[q8_tiled_scale(row, nb, blockIdx.x)] = d;
+                } else {
+                    *reinterpret_cast<int *>(out.yq + (int64_t) row * n + col) = qw;
+                    if (cg == 0) out.yd[(int64_t) row * nb + blockIdx.x] = d;
+                }
+            }
+        }
+        if (out.kc && n0 >= out.kv_row0 && valid) {
+            // one 32-column tile = one head of K or V
+            const int rr = n0 - out.kv_row0;
+            const int which = rr / out.d_model;
+            const int h = (rr % out.d_model) >> 5;
+            const int b = row / out.rows_per_seq;
+            const int kcol = kvcol0 + row % out.rows_per_seq;
+            uint16_t * cache = (which == 0 ? out.kc : out.vc) +
+                               (((int64_t) b * out.n_head + h) * out.lstride + kcol) * 32 + 4 * cg;
+            uint2 w;
+            w.x = (uint32_t) f2h(y[0]) | ((uint32_t) f2h(y[1]) << 16);
+            w.y = (uint32_t) f2h(y[2]) | ((uint32_t) f2h(y[3]) << 16);
+            *reinterpret_cast<uint2 *>(cache) = w;
+        }
+    }
+}
+
+// Rows per workgroup of the small-tile kernel (mt = 1, 2 or 4 tiles of 32; 0 picks one).
+int launch_q8_gemm_small(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const int8_t * xs,
+                         const float * xd, bool x_tiled, const LayerOut & out, int mt,
+                         hipStream_t stream) {
+    if (mt == 0) mt = m <= 64 ? 1 : 2;
+    GSVK_REQUIRE(mt == 1 || mt == 2 || mt == 4, "q8_gemm: row tiles per workgroup must be 1, 2 or 4");
+    const dim3 grid((unsigned) (n / 32), (unsigned) ((m + 32 * mt - 1) / (32 * mt)));
+#define GSVK_GS(NB, MT) \
+    hipLaunchKernelGGL((k_q8_gemm_small<NB, MT>), grid, dim3(GS_THREADS), 0, stream, w, (int) n, (int) m, xs, xd, \
+                       x_tiled, out)
+    if (k == 512) {
+        if (mt == 1) GSVK_GS(16, 1);
+        else if (mt == 2) GSVK_GS(16, 2);
+        else GSVK_GS(16, 4);
+    } else {
+        if (mt == 1) GSVK_GS(64, 1);
+        else if (mt == 2) GSVK_GS(64, 2);
+        else GSVK_GS(64, 4);
+    }
+#undef GSVK_GS
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const int8_t * xs,
+                   const float * xd, int x_layout, const LayerOut & out, hipStream_t stream,
+                   int tile_rows) {
+    GSVK_REQUIRE(((w.qn && w.dn) || (w.qt && w.dt)) && xs && xd, "q8_gemm: null pointer");
+    GSVK_REQUIRE(x_layout == Q8_NATURAL || x_layout == Q8_TILED, "q8_gemm: bad activation layout %d", x_layout);
+    GSVK_REQUIRE(!out.yq || out.yq_layout == Q8_NATURAL || out.yq_layout == Q8_TILED,
+                 "q8_gemm: bad output layout %d", out.yq_layout);
+    GSVK_REQUIRE(n > 0 && n % 32 == 0 && n < (1 << 30) && m > 0 && m < (1 << 30),
+                 "q8_gemm: n must be a multiple of 32 (n=%lld m=%lld)", (long long) n, (long long) m);
     GSVK_REQUIRE(k == 512 || k == 2048, "q8_gemm: k must be 512 or 2048 (got %lld)", (long long) k);
     GSVK_REQUIRE(!out.yq || out.yd, "q8_gemm: bad quantised output");
     GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 && out.kv_row0 + 2 * out.d_model <= n),
@@ -274,6 +466,14 @@ int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
     GSVK_REQUIRE(((uintptr_t) out.bias & 15) == 0 && ((uintptr_t) out.y & 15) == 0 && out.y_stride % 4 == 0 &&
                      ((uintptr_t) out.kc & 15) == 0 && ((uintptr_t) out.vc & 15) == 0,
                  "q8_gemm: bias, y (and its row stride) and the K/V caches must be 16-byte aligned");
+    if (m <= GS_MAX_ROWS || n % GM_BN != 0 || !w.qn || x_layout == Q8_TILED)
+        return launch_q8_gemm_small(w, n, k, m, xs, xd, x_layout == Q8_TILED, out, tile_rows, stream);
+    GSVK_REQUIRE(tile_rows == 0, "q8_gemm: row tiles are a choice of the small-batch kernel (m <= %lld)",
+                 (long long) GS_MAX_ROWS);
+    GSVK_REQUIRE(x_layout == Q8_NATURAL && (!out.yq || out.yq_layout == Q8_NATURAL),
+                 "q8_gemm: above %lld rows the operands are in natural order", (long long) GS_MAX_ROWS);
+    const int8_t * ws = w.qn;
+    const uint16_t * wd = w.dn;
     const dim3 grid((unsigned) (n / GM_BN), (unsigned) ((m + GM_BM - 1) / GM_BM));
     if (k == 512)
         hipLaunchKernelGGL(k_q8_gemm<16>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
@@ -288,12 +488,31 @@ int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
 extern "C" int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xq,
                                const float * xd, int64_t m, const float * bias, int act, float * y,
                                void * stream) {
+    return gsvk_op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, act, y, nullptr, nullptr, 0, 0, stream);
+}
+
+extern "C" int gsvk_op_q8_gemm_ex(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k,
+                                  const int8_t * xq, const float * xd, int64_t m, const float * bias,
+                                  int act, float * y, int8_t * yq, float * yd, int tile_rows,
+                                  int tiled, void * stream) {
     gsvk::LayerOut out{};
     out.y = y;
     out.y_stride = n;
     out.n_store = (int) n;
     out.bias = bias;
     out.act = act;
-    GSVK_REQUIRE(y, "q8_gemm: null pointer");
-    return gsvk::launch_q8_gemm(wq, wd, n, k, m, xq, xd, out, (hipStream_t) stream);
+    out.yq = yq;
+    out.yd = yd;
+    out.yq_layout = tiled ? gsvk::Q8_TILED : gsvk::Q8_NATURAL;
+    GSVK_REQUIRE(y || yq, "q8_gemm: null pointer");
+    gsvk::Q8Weights w{};
+    if (tiled) {
+        w.qt = wq;
+        w.dt = wd;
+    } else {
+        w.qn = wq;
+        w.dn = wd;
+    }
+    return gsvk::launch_q8_gemm(w, n, k, m, xq, xd, tiled ? gsvk::Q8_TILED : gsvk::Q8_NATURAL, out,
+                                (hipStream_t) stream, tile_rows);
 }

@@ -39,8 +39,9 @@ struct LayerOut {
     int n_store;
     const float * bias;
     int act;            // 0 none, 1 relu
-    int8_t * yq;        // Q8_0 output (sliced [m][n] + scales [m][n/32]) or null
+    int8_t * yq;        // Q8_0 output (quants + scales [m][n/32]) or null, in yq_layout
     float * yd;
+    int yq_layout;      // Q8Layout: the GEMV writes Q8_SLICED, the GEMMs Q8_NATURAL or Q8_TILED
     // K/V append of rows [kv_row0, kv_row0 + 2*d_model) to fp16 caches [B][n_head][lstride][32]
     // at column *col_ptr + col_add + m % rows_per_seq of sequence m / rows_per_seq
     uint16_t * kc;
@@ -54,15 +55,37 @@ struct LayerOut {
     int col_add;
 };
 
-// Q8_0 x Q8_0 GEMM on the matrix cores (gemm.hip) with the same epilogue options: n % 128 == 0,
-// k in {512, 2048}. Both operands have their quants in natural order (ws [n][k] as in the GGUF
-// blocks, xs [m][k]) with the scales apart (fp16 wd [n][k/32], fp32 xd [m][k/32]); a Q8_0 output
-// (yq) is written in natural order too.
-int launch_q8_gemm(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k, int64_t m,
-                   const int8_t * xs, const float * xd, const LayerOut & out, hipStream_t stream);
+// A Q8_0 weight matrix [n][k] as the GEMMs read it: quants in natural order with the fp16 scales
+// apart (qn [n][k] as in the GGUF blocks, dn [n][k/32]), and/or the same in the Q8_TILED order
+// (qt, dt), which the small-batch kernel loads with whole-line reads.
+struct Q8Weights {
+    const int8_t * qn;
+    const uint16_t * dn;
+    const int8_t * qt;
+    const uint16_t * dt;
+};
 
-// Row count from which the projections run on launch_q8_gemm rather than the GEMV.
+// Q8_0 x Q8_0 GEMM on the matrix cores (gemm.hip) with the same epilogue options: n % 32 == 0,
+// k in {512, 2048}. Activations xs [m][k] with fp32 scales xd [m][k/32] (fp16 values) in
+// x_layout: Q8_NATURAL, or Q8_TILED (rows padded to 32; small-batch kernel only); a Q8_0 output
+// is written in out.yq_layout (Q8_NATURAL or Q8_TILED). Up to 256 rows (or n % 128 != 0) a kernel
+// of 32-column tiles runs (tiled weights if given), tile_rows (1, 2 or 4 row tiles of 32 per
+// workgroup, 0 = its own choice) selecting its row tiling; above, the 128 x 128 kernel (natural
+// operands only).
+int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const int8_t * xs,
+                   const float * xd, int x_layout, const LayerOut & out, hipStream_t stream,
+                   int tile_rows = 0);
+
+// Row count from which the prefill projections run on launch_q8_gemm rather than the GEMV.
 constexpr int64_t GEMM_MIN_ROWS = 64;
+
+// Batch from which the decode step runs its projections on launch_q8_gemm (with the LayerNorms
+// and the embedding as launches of their own) rather than on the fused GEMVs, whose weight
+// re-reads grow with the batch.
+#ifndef GSVK_DECODE_GEMM_MIN_BATCH
+#define GSVK_DECODE_GEMM_MIN_BATCH 64
+#endif
+constexpr int DECODE_GEMM_MIN_BATCH = GSVK_DECODE_GEMM_MIN_BATCH;
 
 // Prefill self-attention on the matrix cores (attn_prefill_mfma.hip): qkv rows [B][S][3*d_model],
 // head_dim 32, 16-byte aligned qkv and out; used from GEMM_MIN_ROWS rows on, like the GEMM.

@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
                                                   const float * __restrict__ wb, int rows, int n,
                                                   float eps, float * __restrict__ y,
                                                   int8_t * __restrict__ yq,
-                                                  float * __restrict__ yd, bool natural) {
+                                                  float * __restrict__ yd, int layout) {
     const int row = blockIdx.x;
     if (row >= rows) return;
     const int lane = threadIdx.x;
@@ -97,13 +97,7 @@ __global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
             }
             int8_t q[8];
             const float d = q8_quantize_group<8>(o, q, 4);
-            if (act) {
-                if (natural)
-                    q8_store_natural(yq + (int64_t) row * n, ch >> 2, ch & 3, q);
-                else
-                    q8_store_sliced(yq + (int64_t) row * n, nblk, ch >> 2, ch & 3, q);
-                if ((ch & 3) == 0) yd[(int64_t) row * nblk + ch / 4] = d;
-            }
+            if (act) q8_store_row8(yq, yd, layout, row, nblk, ch >> 2, ch & 3, q, d, (ch & 3) == 0);
         }
     }
 }
@@ -130,8 +124,10 @@ __global__ void k_add_act(const float * __restrict__ a, const float * __restrict
 }
 
 // ---------------------------------------------------------------------------------------
-// embedding + PE (src/gsv_ar.cpp:798-807): x[b] = emb[tok[b]] + alpha * pe[pos], with Q8_0
-// output. One wave per row; d_model must be 512.
+// embedding + PE (src/gsv_ar.cpp:798-807): x[b] = emb[tok[b]] + alpha * pe[*pos_ptr + pos_add],
+// with its Q8_0 copy (in the given layout), and kv_end[b] = *pos_ptr + kv_end_add
+// when kv_end is given (the step's attention range, as the GEMV's embedding stage sets it). One
+// wave per row; d_model must be 512.
 // ---------------------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
@@ -141,12 +137,16 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
                                                  int pos_add, float alpha, int d,
                                                  float * __restrict__ x,
                                                  int8_t * __restrict__ xq,
-                                                 float * __restrict__ xd) {
+                                                 float * __restrict__ xd,
+                                                 int32_t * __restrict__ kv_end, int kv_end_add,
+                                                 int layout) {
     const int b = blockIdx.x;
     const int lane = threadIdx.x;
     int t = tok[b];
     t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
-    const int pos = *pos_ptr + pos_add;
+    const int step = *pos_ptr;
+    const int pos = step + pos_add;
+    if (kv_end && lane == 0) kv_end[b] = step + kv_end_add;
     const float * er = emb + (int64_t) t * d + lane * 8;
     const float * pr = pe + (int64_t) pos * d + lane * 8;
     float o[8];
@@ -157,41 +157,44 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
     }
     int8_t q[8];
     const float dq = q8_quantize_group<8>(o, q, 4);
-    q8_store_sliced(xq + (int64_t) b * d, d / QK, lane >> 2, lane & 3, q);
-    if ((lane & 3) == 0) xd[(int64_t) b * (d / QK) + lane / 4] = dq;
+    q8_store_row8(xq, xd, layout, b, d / QK, lane >> 2, lane & 3, q, dq, (lane & 3) == 0);
 }
 
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, bool natural) {
+                     hipStream_t stream, int layout) {
     GSVK_REQUIRE(x && wb && y, "layernorm: null pointer");
     GSVK_REQUIRE(rows >= 0 && rows < (1 << 30) && n > 0 && n % 32 == 0 && n <= 4096,
                  "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
                  (long long) rows, (long long) n);
     GSVK_REQUIRE((yq == nullptr) == (yd == nullptr), "layernorm: yq and yd go together");
+    GSVK_REQUIRE(layout >= Q8_SLICED && layout <= Q8_TILED, "layernorm: bad layout %d", layout);
     auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
     GSVK_REQUIRE(al16(x) && al16(r) && al16(bias) && al16(wb), "layernorm: operands must be 16-byte aligned");
     if (rows == 0) return GSVK_OK;
     const dim3 grid((unsigned) rows);
     if (n <= 512)
         hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, natural);
+                           (int) n, eps, y, yq, yd, layout);
     else if (n <= 1024)
         hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, natural);
+                           (int) n, eps, y, yq, yd, layout);
     else
         hipLaunchKernelGGL(k_layernorm<8>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, natural);
+                           (int) n, eps, y, yq, yd, layout);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
 
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
-                    int8_t * xq, float * xd, hipStream_t stream) {
+                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, hipStream_t stream,
+                    int layout) {
     GSVK_REQUIRE(d == 512, "embed_pe: d_model must be 512");
+    GSVK_REQUIRE(layout >= Q8_SLICED && layout <= Q8_TILED, "embed_pe: bad layout %d", layout);
+    GSVK_REQUIRE(emb && pe && tok && pos_ptr && x && xq && xd, "embed_pe: null pointer");
     hipLaunchKernelGGL(k_embed_pe, dim3((unsigned) B), dim3(64), 0, stream, emb, pe, tok, vocab,
-                       pos_ptr, pos_add, alpha, d, x, xq, xd);
+                       pos_ptr, pos_add, alpha, d, x, xq, xd, kv_end, kv_end_add, layout);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -40,8 +40,8 @@ __global__ void __launch_bounds__(64) k_build_xy(const float * __restrict__ text
     }
 }
 
-// feat[r][k] for the R text rows (r enumerates (b, t) in order): bert[b][k][t] for k < bert_dim,
-// 1 at k == bert_dim (the augmented bias column of bert_aug = [W | b]).
+// feat[r][k] for the R text rows listed in row_b/row_t: bert[b][k][t] for k < bert_dim, 1 at
+// k == bert_dim (the augmented bias column of bert_aug = [W | b]); zeros for a request without BERT.
 __global__ void k_bert_feat(const float * __restrict__ bert, const int64_t * __restrict__ boff,
                             const int32_t * __restrict__ row_b, const int32_t * __restrict__ row_t,
                             const int32_t * __restrict__ tlen, int bert_dim, int R,
@@ -55,16 +55,19 @@ __global__ void k_bert_feat(const float * __restrict__ bert, const int64_t * __r
         dst[k] = k == bert_dim ? 1.0f : (src ? src[(int64_t) k * T + t] : 0.0f);
 }
 
-// cur[b][pad_b + t] = xy + proj[r] (ggml_add(x, mul_mat(bert_aug, feat)), src/gsv_ar.cpp:241)
+// cur[b][pad_b + t] = xy + proj[r] (ggml_add(x, mul_mat(bert_aug, feat)), src/gsv_ar.cpp:241).
+// Rows r >= R1 belong to requests without BERT features: their feat row is zeros and a trailing 1,
+// so the projection is the bias column itself (the zero products add only signed zeros to it).
 __global__ void k_add_proj(float * __restrict__ xy, const float * __restrict__ proj,
-                           const int32_t * __restrict__ row_b, const int32_t * __restrict__ row_t,
-                           const int32_t * __restrict__ pad, int S, int d, int R) {
+                           const float * __restrict__ bias, const int32_t * __restrict__ row_b,
+                           const int32_t * __restrict__ row_t, const int32_t * __restrict__ pad,
+                           int S, int d, int R, int R1) {
     const int r = blockIdx.x;
     if (r >= R) return;
     const int b = row_b[r];
     const int s = pad[b] + row_t[r];
     float * dst = xy + ((int64_t) b * S + s) * d;
-    const float * src = proj + (int64_t) r * d;
+    const float * src = r < R1 ? proj + (int64_t) r * d : bias;
     for (int i = threadIdx.x; i < d; i += blockDim.x) dst[i] = dst[i] + src[i];
 }
 
@@ -217,11 +220,12 @@ int launch_bert_feat(const float * bert, const int64_t * boff, const int32_t * r
     return GSVK_OK;
 }
 
-int launch_add_proj(float * xy, const float * proj, const int32_t * row_b, const int32_t * row_t,
-                    const int32_t * pad, int S, int d, int R, hipStream_t stream) {
+int launch_add_proj(float * xy, const float * proj, const float * bias, const int32_t * row_b,
+                    const int32_t * row_t, const int32_t * pad, int S, int d, int R, int R1,
+                    hipStream_t stream) {
     if (R == 0) return GSVK_OK;
-    hipLaunchKernelGGL(k_add_proj, dim3((unsigned) R), dim3(128), 0, stream, xy, proj, row_b, row_t,
-                       pad, S, d, R);
+    hipLaunchKernelGGL(k_add_proj, dim3((unsigned) R), dim3(128), 0, stream, xy, proj, bias, row_b,
+                       row_t, pad, S, d, R, R1);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -33,10 +33,11 @@ __global__ void k_q8_dequant(const uint8_t * __restrict__ blocks, int64_t nblock
     out[i] = h2f(d) * (float) (int8_t) blk[2 + w];
 }
 
-// one thread per (block, group j): copies 4 quants to their slice position (and, when qn is
-// given, to their natural position)
+// one thread per (block, group j): copies 4 quants to their slice position (and, when qn / qt
+// are given, to their natural / tiled positions)
 __global__ void k_q8_repack(const uint8_t * __restrict__ blocks, int64_t rows, int nblk,
-                            int8_t * __restrict__ qs, uint16_t * __restrict__ d, int8_t * __restrict__ qn) {
+                            int8_t * __restrict__ qs, uint16_t * __restrict__ d, int8_t * __restrict__ qn,
+                            int8_t * __restrict__ qt, uint16_t * __restrict__ dt) {
     const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t total = rows * nblk * 8;
     if (i >= total) return;
@@ -52,7 +53,15 @@ __global__ void k_q8_repack(const uint8_t * __restrict__ blocks, int64_t rows, i
 #pragma unroll
         for (int t = 0; t < 4; t++) qn[gb * QK + 4 * j + t] = (int8_t) src[2 + 4 * j + t];
     }
-    if (j == 0) d[gb] = (uint16_t) src[0] | ((uint16_t) src[1] << 8);
+    if (qt) {
+#pragma unroll
+        for (int t = 0; t < 4; t++) qt[q8_tiled_offset(row, nblk, blk, 4 * j + t)] = (int8_t) src[2 + 4 * j + t];
+    }
+    const uint16_t dv = (uint16_t) src[0] | ((uint16_t) src[1] << 8);
+    if (j == 0) {
+        d[gb] = dv;
+        if (dt) dt[q8_tiled_scale(row, nblk, blk)] = dv;
+    }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -61,7 +70,7 @@ __global__ void k_q8_repack(const uint8_t * __restrict__ blocks, int64_t rows, i
 
 __global__ void __launch_bounds__(64) k_q8_quantize(const float * __restrict__ x, int64_t rows,
                                                    int k, int8_t * __restrict__ xs,
-                                                   float * __restrict__ xd, bool natural) {
+                                                   float * __restrict__ xd, int layout) {
     const int nblk = k / QK;
     const int64_t gblk = (int64_t) blockIdx.x * 16 + (threadIdx.x >> 2);   // global block id
     const int sub = threadIdx.x & 3;
@@ -75,11 +84,7 @@ __global__ void __launch_bounds__(64) k_q8_quantize(const float * __restrict__ x
     v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
     int8_t q[8];
     const float d = q8_quantize_group<8>(v, q, 4);
-    if (natural)
-        q8_store_natural(xs + row * k, blk, sub, q);
-    else
-        q8_store_sliced(xs + row * k, nblk, blk, sub, q);
-    if (sub == 0) xd[gblk] = d;
+    q8_store_row8(xs, xd, layout, row, nblk, blk, sub, q, d, sub == 0);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -231,26 +236,29 @@ int launch_q8_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t k,
 }
 
 int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, float * xd,
-                       hipStream_t stream, bool natural) {
+                       hipStream_t stream, int layout) {
     GSVK_REQUIRE(x && xs && xd && rows >= 0 && k > 0 && k % QK == 0 && k <= (1 << 20),
                  "q8_quantize: bad arguments (k must be a multiple of 32)");
+    GSVK_REQUIRE(layout >= Q8_SLICED && layout <= Q8_TILED, "q8_quantize: bad layout %d", layout);
     const int64_t nb = rows * (k / QK);
     if (nb == 0) return GSVK_OK;
     hipLaunchKernelGGL(k_q8_quantize, dim3((unsigned) ((nb + 15) / 16)), dim3(64), 0, stream, x,
-                       rows, (int) k, xs, xd, natural);
+                       rows, (int) k, xs, xd, layout);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
 
 int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
-                     hipStream_t stream, int8_t * qn) {
+                     hipStream_t stream, int8_t * qn, int8_t * qt, uint16_t * dt) {
     GSVK_REQUIRE(blocks && qs && d && rows >= 0 && k > 0 && k % QK == 0 && k <= (1 << 20),
                  "q8_repack: bad arguments (k must be a multiple of 32)");
+    GSVK_REQUIRE((qt == nullptr) == (dt == nullptr) && (!qt || rows % 32 == 0),
+                 "q8_repack: the tiled copy needs quants and scales, and rows % 32 == 0");
     const int nblk = (int) (k / QK);
     const int64_t total = rows * nblk * 8;
     if (total == 0) return GSVK_OK;
     hipLaunchKernelGGL(k_q8_repack, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, stream,
-                       (const uint8_t *) blocks, rows, nblk, qs, d, qn);
+                       (const uint8_t *) blocks, rows, nblk, qs, d, qn, qt, dt);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -27,8 +27,9 @@ int launch_build_xy(const float * text_emb, const float * audio_emb, const float
 int launch_bert_feat(const float * bert, const int64_t * boff, const int32_t * row_b,
                      const int32_t * row_t, const int32_t * tlen, int bert_dim, int R, float * feat,
                      hipStream_t stream);
-int launch_add_proj(float * xy, const float * proj, const int32_t * row_b, const int32_t * row_t,
-                    const int32_t * pad, int S, int d, int R, hipStream_t stream);
+int launch_add_proj(float * xy, const float * proj, const float * bias, const int32_t * row_b,
+                    const int32_t * row_t, const int32_t * pad, int S, int d, int R, int R1,
+                    hipStream_t stream);
 int launch_gather_last(const float * in, int B, int S, int d, float * out, hipStream_t stream);
 int launch_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                         int d_model, float scale, float * out, int8_t * oq, float * od,
@@ -84,8 +85,10 @@ struct PoolArena {
 
 struct Lin {
     int8_t * qs = nullptr;    // sliced quants (GEMV)
-    int8_t * qn = nullptr;    // the same quants in natural order (GEMM)
+    int8_t * qn = nullptr;    // the same quants in natural order (GEMM, large batch)
     uint16_t * d = nullptr;
+    int8_t * qt = nullptr;    // quants and scales in the matrix-core operand order (GEMM, small
+    uint16_t * dt = nullptr;  // batch); rows % 32 == 0 only
     float * b = nullptr;
     int n = 0, k = 0;
 };
@@ -121,6 +124,7 @@ struct gsvk_model {
     void * head = nullptr;        // F16/F32 [V][D]
     Lin head_q8;                  // Q8_0 head
     float * text_emb = nullptr, * audio_emb = nullptr, * bert_aug = nullptr, * pe = nullptr;
+    float * bert_b = nullptr;     // bias column of bert_aug, contiguous [D]
     uint64_t * rng_jump = nullptr, * rng_adv = nullptr;
     int rng_chunk = 17;
     // KV cache
@@ -212,8 +216,12 @@ int load_q8(gsvk_model * m, const GgufFile & g, const GgufTensor * t, Lin & lin,
     GSVK_TRY(m->wmem.alloc(lin.qs, (size_t) lin.n * lin.k));
     GSVK_TRY(m->wmem.alloc(lin.qn, (size_t) lin.n * lin.k));
     GSVK_TRY(m->wmem.alloc(lin.d, (size_t) lin.n * (lin.k / 32)));
+    if (lin.n % 32 == 0) {
+        GSVK_TRY(m->wmem.alloc(lin.qt, (size_t) lin.n * lin.k));
+        GSVK_TRY(m->wmem.alloc(lin.dt, (size_t) lin.n * (lin.k / 32)));
+    }
     GSVK_HIP(hipMemcpyAsync(staging, host.data(), t->nbytes, hipMemcpyHostToDevice, m->stream));
-    GSVK_TRY(launch_q8_repack(staging, lin.n, lin.k, lin.qs, lin.d, m->stream, lin.qn));
+    GSVK_TRY(launch_q8_repack(staging, lin.n, lin.k, lin.qs, lin.d, m->stream, lin.qn, lin.qt, lin.dt));
     GSVK_HIP(hipStreamSynchronize(m->stream));   // host buffer is reused
     return GSVK_OK;
 }
@@ -246,17 +254,26 @@ int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
     m->smem.release();
     const int D = m->D;
     auto & a = m->smem;
+    // Q8_0 activations hold whole 32-row tiles (the matrix-core operand order of the large-batch
+    // path); the padding rows are zero and stay so
+    const size_t Bp = ((size_t) B + 31) / 32 * 32;
     GSVK_TRY(a.alloc(m->x.x, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->x.q, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->x.d, (size_t) B * D / 32));
+    GSVK_TRY(a.alloc(m->x.q, Bp * D));
+    GSVK_TRY(a.alloc(m->x.d, Bp * D / 32));
     GSVK_TRY(a.alloc(m->attn.x, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->attn.q, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->attn.d, (size_t) B * D / 32));
+    GSVK_TRY(a.alloc(m->attn.q, Bp * D));
+    GSVK_TRY(a.alloc(m->attn.d, Bp * D / 32));
     GSVK_TRY(a.alloc(m->n1.x, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->n1.q, (size_t) B * D));
-    GSVK_TRY(a.alloc(m->n1.d, (size_t) B * D / 32));
-    GSVK_TRY(a.alloc(m->hq.q, (size_t) B * m->FFN));
-    GSVK_TRY(a.alloc(m->hq.d, (size_t) B * m->FFN / 32));
+    GSVK_TRY(a.alloc(m->n1.q, Bp * D));
+    GSVK_TRY(a.alloc(m->n1.d, Bp * D / 32));
+    GSVK_TRY(a.alloc(m->hq.q, Bp * m->FFN));
+    GSVK_TRY(a.alloc(m->hq.d, Bp * m->FFN / 32));
+    for (Act * act : {&m->x, &m->attn, &m->n1}) {
+        GSVK_HIP(hipMemset(act->q, 0, Bp * D));
+        GSVK_HIP(hipMemset(act->d, 0, Bp * D / 32 * sizeof(float)));
+    }
+    GSVK_HIP(hipMemset(m->hq.q, 0, Bp * m->FFN));
+    GSVK_HIP(hipMemset(m->hq.d, 0, Bp * m->FFN / 32 * sizeof(float)));
     GSVK_TRY(a.alloc(m->qkv, (size_t) B * 3 * D));
     GSVK_TRY(a.alloc(m->o, (size_t) B * D));
     GSVK_TRY(a.alloc(m->h2, (size_t) B * D));
@@ -323,29 +340,34 @@ int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
 //   hq = Q8_0(relu(W1 . n1 + b1))                (quantised in FFN1's output stage)
 //   h2 = W2 . hq
 // LN2 (cur' = LN2(n1 + h2 + b2)) is the input stage of the next layer's QKV or of final_ln().
+Q8Weights q8w(const Lin & l) { return Q8Weights{l.qn, l.d, l.qt, l.dt}; }
+
 int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
-               float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr) {
+               float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr,
+               int layout = Q8_NATURAL) {
     const int D = m->D, F = m->FFN;
-    if (R >= GEMM_MIN_ROWS && n1) {
-        // many rows: the projections on the matrix cores, LN1 as its own launch (with the Q8_0 copy
-        // the FFN1 GEMM reads)
+    if (n1) {
+        // many rows (the caller's choice): the projections on the matrix cores, LN1 as its own
+        // launch (with the Q8_0 copy the FFN1 GEMM reads); the Q8_0 activations (attention output,
+        // LN1, FFN1 output) in the given layout
         LayerOut oo{};
         oo.y = o;
         oo.y_stride = D;
         oo.n_store = D;
-        GSVK_TRY(launch_q8_gemm(w.out.qn, w.out.d, D, D, R, attn.q, attn.d, oo, m->stream));
-        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream, true));
+        GSVK_TRY(launch_q8_gemm(q8w(w.out), D, D, R, attn.q, attn.d, layout, oo, m->stream));
+        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream, layout));
         LayerOut ho{};
         ho.bias = w.f1.b;
         ho.act = 1;
         ho.yq = hq.q;
         ho.yd = hq.d;
-        GSVK_TRY(launch_q8_gemm(w.f1.qn, w.f1.d, F, D, R, n1->q, n1->d, ho, m->stream));
+        ho.yq_layout = layout;
+        GSVK_TRY(launch_q8_gemm(q8w(w.f1), F, D, R, n1->q, n1->d, layout, ho, m->stream));
         LayerOut h2o{};
         h2o.y = h2;
         h2o.y_stride = D;
         h2o.n_store = D;
-        return launch_q8_gemm(w.f2.qn, w.f2.d, D, F, R, hq.q, hq.d, h2o, m->stream);
+        return launch_q8_gemm(q8w(w.f2), D, F, R, hq.q, hq.d, layout, h2o, m->stream);
     }
     LayerIn qin{};
     qin.mode = IN_Q8;
@@ -415,9 +437,32 @@ int final_ln(gsvk_model * m, int64_t R, const float * n1x, const float * h2, Act
 int enqueue_decode_body(gsvk_model * m) {
     const int B = m->B, D = m->D;
     const float scale = 1.0f / std::sqrt((float) m->HD);
+    const bool mfma = B >= DECODE_GEMM_MIN_BATCH;
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+        if (mfma) {
+            // large batch: embedding / LN2 of the previous layer as their own launches, the QKV
+            // GEMM with the K/V append, attention, then the GEMM tail; every Q8_0 activation in
+            // the matrix-core operand order (rows padded to 32)
+            if (li == 0) {
+                GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
+                                         m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q,
+                                         m->x.d, m->kv_end, m->S, m->stream, Q8_TILED));
+            } else {
+                const LayerW & p = m->L[li - 1];
+                GSVK_TRY(launch_layernorm(m->n1.x, m->h2, p.f2.b, p.ln2, B, D, 1e-5f, m->x.x, m->x.q,
+                                          m->x.d, m->stream, Q8_TILED));
+            }
+            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, B, m->x.q, m->x.d, Q8_TILED,
+                                    qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
+            GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
+                                        m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
+                                        m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream,
+                                        Q8_TILED));
+            GSVK_TRY(layer_tail(m, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2, &m->n1, Q8_TILED));
+            continue;
+        }
         LayerIn in{};
         if (li == 0) {
             in.mode = IN_EMB;
@@ -529,17 +574,24 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         const gsvk_request & r = reqs[b];
         pad[b] = max_len - r.n_phones;
         tlen[b] = r.n_phones;
-        for (int t = 0; t < r.n_phones; t++) {
-            phones[(size_t) b * max_len + pad[b] + t] = r.phones[t];
-            row_b.push_back(b);
-            row_t.push_back(t);
-        }
+        for (int t = 0; t < r.n_phones; t++) phones[(size_t) b * max_len + pad[b] + t] = r.phones[t];
         if (r.bert && r.n_phones > 0) {
             boff[b] = (int64_t) bert_total;
             bert_total += (size_t) BD * r.n_phones;
         }
     }
+    // text rows (b, t): the R1 rows of requests with BERT features first (they need the projection),
+    // then the rows of requests without (their projection is the bias)
+    for (int pass = 0; pass < 2; pass++)
+        for (int b = 0; b < B; b++)
+            if ((boff[b] >= 0) == (pass == 0))
+                for (int t = 0; t < reqs[b].n_phones; t++) {
+                    row_b.push_back(b);
+                    row_t.push_back(t);
+                }
     const int R = (int) row_b.size();
+    int R1 = 0;
+    while (R1 < R && boff[row_b[R1]] >= 0) R1++;
     const int64_t rows = (int64_t) B * S;
 
     PoolArena tmp;
@@ -593,16 +645,15 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     // inputs: xy, then + bert_aug . [feat; 1] on the text rows
     GSVK_TRY(launch_build_xy(m->text_emb, m->audio_emb, m->pe, d_phones, d_pad, d_prompt, B, S,
                              max_len, D, m->text_alpha, m->audio_alpha, cur.x, st));
-    if (R) {
-        GSVK_TRY(tmp.alloc(feat, (size_t) R * (BD + 1)));
-        GSVK_TRY(tmp.alloc(proj, (size_t) R * D));
-        GSVK_TRY(launch_bert_feat(d_bert ? d_bert : cur.x, d_boff, d_rowb, d_rowt, d_tlen, BD, R,
-                                  feat, st));
-        GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R, proj, D, 0, st));
-        GSVK_TRY(launch_add_proj(cur.x, proj, d_rowb, d_rowt, d_pad, S, D, R, st));
+    if (R1) {
+        GSVK_TRY(tmp.alloc(feat, (size_t) R1 * (BD + 1)));
+        GSVK_TRY(tmp.alloc(proj, (size_t) R1 * D));
+        GSVK_TRY(launch_bert_feat(d_bert, d_boff, d_rowb, d_rowt, d_tlen, BD, R1, feat, st));
+        GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R1, proj, D, 0, st));
     }
+    if (R) GSVK_TRY(launch_add_proj(cur.x, proj, m->bert_b, d_rowb, d_rowt, d_pad, S, D, R, R1, st));
     // the layer-0 QKV reads this copy: natural order for the GEMM, sliced for the GEMV
-    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, rows >= GEMM_MIN_ROWS));
+    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, rows >= GEMM_MIN_ROWS ? Q8_NATURAL : Q8_SLICED));
     int32_t * zero = nullptr;
     GSVK_TRY(tmp.alloc(zero, 1));
     GSVK_HIP(hipMemsetAsync(zero, 0, 4, st));
@@ -615,9 +666,10 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
             if (li > 0) {
                 const LayerW & p = m->L[li - 1];
-                GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st, true));
+                GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st,
+                                          Q8_NATURAL));
             }
-            GSVK_TRY(launch_q8_gemm(w.qkv.qn, w.qkv.d, 3 * D, D, rows, cur.q, cur.d,
+            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, rows, cur.q, cur.d, Q8_NATURAL,
                                     qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
         } else {
             LayerIn in{};
@@ -643,7 +695,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
-        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2, &n1));
+        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr));
     }
     GSVK_TRY(final_ln(m, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
@@ -908,6 +960,8 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
         }
         GSVK_TRY(m->wmem.alloc(m->bert_aug, aug.size()));
         GSVK_HIP(hipMemcpy(m->bert_aug, aug.data(), aug.size() * 4, hipMemcpyHostToDevice));
+        GSVK_TRY(m->wmem.alloc(m->bert_b, bv.size()));
+        GSVK_HIP(hipMemcpy(m->bert_b, bv.data(), bv.size() * 4, hipMemcpyHostToDevice));
     }
     {
         std::vector<float> a1, a2;

@@ -26,7 +26,7 @@ EXPORTS = [
     "gsvk_op_q8_repack", "gsvk_op_q8_quantize", "gsvk_op_q8_gemv", "gsvk_op_layernorm", "gsvk_op_add_act",
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
     "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
-    "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_attn_prefill",
+    "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
 ]
 
 
@@ -105,6 +105,7 @@ def lib():
                                        vp, vp, vp]
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
         L.gsvk_op_q8_gemm.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
+        L.gsvk_op_q8_gemm_ex.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp, vp, i32, i32, vp]
         L.gsvk_op_attn_prefill.argtypes = [vp, i32, i32, i32, vp, i32, i32, f32, i32, vp, vp, vp, vp]
         L.gsvk_sample_workspace_bytes.argtypes = [i32]
         L.gsvk_sample_workspace_bytes.restype = C.c_size_t
@@ -168,6 +169,12 @@ def op_q8_gemv(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
 def op_q8_gemm(wq, wd, n, k, xq, xd, m, bias, act, y, stream=None):
     check(lib().gsvk_op_q8_gemm(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y), _stream(stream)),
           "q8_gemm")
+
+
+def op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, act, y=None, yq=None, yd=None, tile_rows=0, tiled=False,
+                  stream=None):
+    check(lib().gsvk_op_q8_gemm_ex(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y), _p(yq),
+                                   _p(yd), tile_rows, 1 if tiled else 0, _stream(stream)), "q8_gemm_ex")
 
 
 def op_ln_gemv(wq, wd, n, res, r, ln_bias, wb, bias, act, y, ln_out=None, stream=None):

@@ -200,10 +200,25 @@ int gsvk_op_q8_gemv(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
  * [n][k] = the GGUF blocks' quants without the scales, xq [m][k]) with the scales apart (wd fp16
  * [n][k/32], xd fp32 [m][k/32] holding fp16 values, as every Q8_0 scale does); the fp32
  * accumulation runs block by block instead of in
- * ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must be a multiple of 128,
- * k 512 or 2048; bias and y 16-byte aligned. */
+ * ggml-cpu's 8-lane x86 order, so results agree to fp32 rounding. n must be a multiple of 32
+ * (of 128 above 256 rows), k 512 or 2048; bias and y 16-byte aligned. Up to 256 rows the
+ * product runs in tiles of 32 columns with the K range split over a workgroup's 4 waves (decode
+ * at large batch), above in tiles of 128 x 128. */
 int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, const int8_t * xq,
                     const float * xd, int64_t m, const float * bias, int act, float * y, void * stream);
+
+/* gsvk_op_q8_gemm with the other outputs of the projections' epilogue: y may be NULL, and yq/yd
+ * (both or neither) receive the Q8_0 quantisation of each 32-column block of the output (quants
+ * [m][n], fp32 scales [m][n/32] holding fp16 values), which the next GEMM reads (the FFN1 output
+ * of src/gsv_ar.cpp:255-260 as the FFN2 input). tile_rows (small-batch kernel only): row tiles of
+ * 32 per workgroup, 1, 2 or 4, 0 = the library's choice. tiled = 1: wq/wd, xq/xd and yq/yd are
+ * in the matrix-core operand order instead of natural order: for each 32-row tile and block, 1 KB
+ * in which bytes [16L, 16L+16), L = 32h + i, hold the quants [16h, 16h+16) of row i of the tile,
+ * and the tile's 32 scales of the block in row order; row counts padded to a multiple of 32 (the
+ * small-batch kernel, any m). */
+int gsvk_op_q8_gemm_ex(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k,
+                       const int8_t * xq, const float * xd, int64_t m, const float * bias, int act,
+                       float * y, int8_t * yq, float * yd, int tile_rows, int tiled, void * stream);
 
 /* y = W . Q8_0(LayerNorm((res + r) + ln_bias) * wb[0:512] + wb[512:1024]) (+ bias) then act:
  * the decoder's fused kernel with its LayerNorm input stage (rows of 512; n % 32 == 0). The

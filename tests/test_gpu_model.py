@@ -59,13 +59,35 @@ def test_kv_write_layer0_bitexact(models):
     assert np.array_equal(vd, v_ref)
 
 
-def test_prefill_on_matrix_cores(models):
+def test_kv_write_layer0_bitexact_without_bert(models):
+    """A request without BERT features gets the projection bias on its text rows instead of the
+    projection of a zero feature row: the layer-0 cache stays bit-exact with the oracle, which
+    projects the zero row, also in a batch that mixes requests with and without features."""
+    g, o = models
+    reqs = _reqs(23, [9, 6, 12], P=8)          # 3 x 20 rows: below the matrix-core path
+    reqs[1]["bert"] = None
+    reqs[2]["bert"] = None
+    for batch in (reqs, reqs[1:]):
+        _, S = g.prefill(batch)
+        k_dev, v_dev = g.kv_read(0)
+        k_ref, v_ref, _ = o.prefill_kv(batch, 0, flags=O.ORC_KV_F16)
+        assert np.array_equal(k_dev[:, :, :S, :].view(np.float16).astype(np.float32), k_ref)
+        assert np.array_equal(v_dev[:, :, :S, :].view(np.float16).astype(np.float32), v_ref)
+
+
+@pytest.mark.parametrize("lens,what", [
+    ([260, 300, 245], "128 x 128 tiles: S = 316, 948 rows; alone: 261 rows and more"),
+    ([70, 100], "32-column tiles, K split over 4 waves: S = 116, 232 rows; alone: 86 and 116 rows"),
+])
+def test_prefill_on_matrix_cores(models, lens, what):
     """Prefills of 64 rows and more run the projections on the MFMA GEMM (fp32 accumulation per
     block, not in ggml-cpu's 8-lane order): logits within 2e-3 of the oracle, the layer-0 K/V
     within one fp16 ulp of the oracle's (the fp32 values differ by rounding, which can move a
-    value across an fp16 rounding boundary), and left padding still changes nothing."""
+    value across an fp16 rounding boundary), and left padding changes nothing as long as the
+    batch and the request alone fall in the same row range of the GEMM (up to 256 rows: the
+    32-column kernel sums 4 K quarters, above: the 128 x 128 kernel accumulates through K)."""
     g, o = models
-    reqs = _reqs(11, [70, 100, 64])            # S = 116, 348 rows; alone: >= 80 rows
+    reqs = _reqs(11, lens)
     got = g.first_logits(reqs)
     ref = o.first_logits(reqs)
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-3
@@ -80,9 +102,9 @@ def test_prefill_on_matrix_cores(models):
         tol = np.maximum(ulp, 1e-6 * np.abs(r).max())
         assert np.all(np.abs(d - r) <= tol), np.abs(d - r).max()
         assert np.mean(d != r) <= 0.01
-    for b in range(3):
+    for b in range(len(lens)):
         alone = g.first_logits([reqs[b]])
-        assert np.array_equal(got[b], alone[0]), b
+        assert np.array_equal(got[b], alone[0]), (what, b)
 
 
 def test_kv_append_matches_prefill(models):
@@ -152,6 +174,35 @@ def test_teacher_forced_greedy_tokens(gpu, model4_path):
         o.close()
 
 
+def test_decode_batch64_on_matrix_cores(gpu, model4_path):
+    """From batch 64 the decode step runs its projections as MFMA GEMMs (LayerNorms and the
+    embedding as launches of their own, natural-order Q8_0 operands): fp32 accumulation per block
+    instead of the x86 8-lane order, so the oracle's tokens are matched except at near-ties of
+    the penalised logits (teacher forcing keeps the histories equal)."""
+    rng = np.random.default_rng(24)
+    lens = rng.integers(3, 21, 64)
+    reqs = _reqs(25, lens, P=8)
+    steps = 8
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    greedy = (1, 1.0, 1.0, 1.35)
+    g = gpu.Model(model4_path)
+    o = O.Model(model4_path)
+    try:
+        res = g.generate(reqs, sampler=greedy, max_steps=steps, oracle=forced, flags=1, want_sampled=True)
+        ref = o.generate(reqs, sampler=greedy, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+    finally:
+        g.close()
+        o.close()
+    assert res["n_steps"] == ref["n_steps"] == steps
+    mism = np.argwhere(res["sampled"] != ref["sampled"])
+    for idx, b in mism:
+        hist = np.concatenate([reqs[b]["prompt"], forced[:idx]])
+        _, margin, scale = _penalised_top2(ref["logits"][idx, b], hist, mask_eos=1024)
+        assert margin <= 2e-3 * scale, (idx, b, margin, scale)
+    assert len(mism) <= max(1, res["sampled"].size // 20), mism
+
+
 def test_generate_rules_match_oracle(models):
     """EOS via teacher forcing at step 14 (after the 11-step EOS mask), early stop, lens order."""
     g, o = models
@@ -191,3 +242,20 @@ def test_top_p_and_temperature(models):
         res = g.generate(reqs, sampler=cfg, max_steps=8, seeds=[5], flags=1)
         ref = o.generate(reqs, sampler=cfg, max_steps=8, seeds=[5], flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL)
         assert np.array_equal(res["tokens"][0][:8 + 4], ref["tokens"][0][:8 + 4]), cfg
+
+
+def test_prefill_workspace_reuse(models):
+    """The prefill workspace is kept by the model and grown to the largest prefill seen: a large
+    prefill, then a smaller one (reusing the start of the pool), then the large one again give the
+    same logits as on first use, bit for bit, on both paths (GEMM from 64 rows, GEMV below)."""
+    g, _ = models
+    big = _reqs(21, [90, 40, 120])        # 3 x (120 + 16) rows: matrix-core path
+    small = _reqs(22, [5, 9])             # 2 x (9 + 16) rows: GEMV path
+    first = g.first_logits(big)
+    s1 = g.first_logits(small)
+    again = g.first_logits(big)
+    s2 = g.first_logits(small)
+    assert np.array_equal(first, again)
+    assert np.array_equal(s1, s2)
+    g.release_cache()                     # frees the pool too; the next prefill allocates anew
+    assert np.array_equal(g.first_logits(big), first)

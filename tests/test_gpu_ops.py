@@ -24,6 +24,21 @@ def unslice(qs: np.ndarray, k: int) -> np.ndarray:
     return qs.reshape(rows, 8, k // 32, 4).transpose(0, 2, 1, 3).reshape(rows, k)
 
 
+def to_tiled(q: np.ndarray, d: np.ndarray):
+    """Quants [R][K] and scales [R][K/32] in the matrix-core operand order: per 32-row tile and
+    block, 1 KB where bytes [16L, 16L+16), L = 32h + i, are quants [16h, 16h+16) of row i; the
+    tile's 32 scales of the block in row order. Rows padded to 32 with zeros."""
+    R, K = q.shape
+    nb, Rp = K // 32, (R + 31) // 32 * 32
+    qp = np.zeros((Rp, K), q.dtype)
+    qp[:R] = q
+    dp = np.zeros((Rp, nb), d.dtype)
+    dp[:R] = d
+    qt = qp.reshape(Rp // 32, 32, nb, 2, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+    dt = dp.reshape(Rp // 32, 32, nb).transpose(0, 2, 1).reshape(-1)
+    return np.ascontiguousarray(qt), np.ascontiguousarray(dt)
+
+
 def blocks_to_split(blocks: np.ndarray, rows: int, k: int):
     b = blocks.reshape(rows, k // 32, 34)
     d = b[:, :, 0:2].copy().view(np.uint16)[:, :, 0]
@@ -290,6 +305,7 @@ def test_attn_decode_parity(gpu):
     (40, 16, 1000, "8 waves per workgroup (640 pairs)"),
     (2, 4, 4096, "8 waves per workgroup, 4 splits merged by the last workgroup"),
     (1, 16, 3000, "8 waves per workgroup, 2 splits"),
+    (64, 16, 3100, "4 waves, rows cut in chunks of 16 blocks (1024 pairs), merged by a second launch"),
 ])
 def test_attn_decode_launch_shapes(gpu, B, nh, lstride, what):
     import torch
@@ -305,6 +321,21 @@ def test_attn_decode_launch_shapes(gpu, B, nh, lstride, what):
     assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-5, what
     if B > 2:
         assert np.all(got[0] == 0.0)
+
+
+def test_attn_decode_rows_longer_than_planned(gpu):
+    """Rows longer than max_keys (the length the launch is planned for: here 3 chunks of 16
+    blocks) get longer runs per split instead of more splits; the output is unchanged."""
+    import torch
+    rng = np.random.default_rng(34)
+    B, nh, lstride = 64, 16, 3700
+    begins = rng.integers(0, 100, B)
+    ends = np.minimum(lstride, begins + rng.integers(2000, lstride, B))
+    ends[3] = lstride
+    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, begins, ends)
+    got, scale, _ = _run_attn(gpu, torch, q, k, v, kb, ke, 3072)
+    ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
+    assert np.abs(got - ref).max() / np.abs(ref).max() <= 1e-5
 
 
 def test_attn_decode_empty_and_constant(gpu):
@@ -418,6 +449,56 @@ def test_q8_gemm_matches_oracle(gpu, n, k, m):
     assert np.abs(got - ref).max() <= 2e-6 * scale, np.abs(got - ref).max() / scale
     ref2 = np.maximum(ref + bias[None, :], 0.0)
     assert np.abs(y2.cpu().numpy() - ref2).max() <= 2e-6 * scale
+
+
+@pytest.mark.parametrize("n,k", [(1536, 512), (512, 2048), (2048, 512)])
+@pytest.mark.parametrize("m", [1, 64, 100, 128, 256])
+def test_q8_gemm_small_tiles(gpu, n, k, m):
+    """The small-batch GEMM (32-column tiles, K split over 4 waves): every row tiling (1, 2, 4
+    tiles of 32 rows per workgroup) gives the same bits, within 2e-6 of the oracle's scale; with
+    bias + ReLU its Q8_0 output is the x86 quantisation of its own fp32 output (natural order)."""
+    import torch
+    rng = np.random.default_rng(7100 + n + k + m)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    wb = sm.q8_quantize_ref(W).ravel()
+    wq_n, wd_n = blocks_to_split(wb, n, k)
+    xq_n, xd_n = blocks_to_split(O.q8_quantize_x86(X), m, k)
+    wq, wd = _dev(wq_n, torch), _dev(wd_n.view(np.int16), torch)
+    xq, xd = _dev(xq_n, torch), _dev(xd_n.view(np.float16).astype(np.float32), torch)
+    bias = _dev(rng.standard_normal(n).astype(np.float32) * 0.02, torch)
+    ref = O.q8_matmul(wb, n, k, X)
+    scale = np.abs(ref).max()
+    outs = []
+    for tr in (1, 2, 4):
+        y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+        yq = torch.zeros((m, n), dtype=torch.int8, device="cuda")
+        yd = torch.zeros((m, n // 32), dtype=torch.float32, device="cuda")
+        gpu.op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, 1, y, yq, yd, tile_rows=tr)
+        torch.cuda.synchronize()
+        outs.append((y.cpu().numpy(), yq.cpu().numpy(), yd.cpu().numpy()))
+    for y, yq, yd in outs[1:]:
+        assert np.array_equal(y, outs[0][0]) and np.array_equal(yq, outs[0][1]) and np.array_equal(yd, outs[0][2])
+    y, yq, yd = outs[0]
+    ref_relu = np.maximum(ref + bias.cpu().numpy()[None, :], 0.0)
+    assert np.abs(y - ref_relu).max() <= 2e-6 * scale
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(y), m, n)
+    assert np.array_equal(yq, q_ref.reshape(m, n))
+    assert np.array_equal(yd, d_ref.view(np.float16).astype(np.float32).reshape(m, n // 32))
+    # the same product on operands in the matrix-core order (whole-line loads): the same bits, and
+    # the Q8_0 output in that order
+    wq_t, wd_t = to_tiled(wq_n, wd_n.view(np.int16))
+    xq_t, xd_t = to_tiled(xq_n, xd_n.view(np.float16).astype(np.float32))
+    mp = (m + 31) // 32 * 32
+    yt = torch.zeros((m, n), dtype=torch.float32, device="cuda")
+    yqt = torch.zeros(mp * n, dtype=torch.int8, device="cuda")
+    ydt = torch.zeros(mp * n // 32, dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemm_ex(_dev(wq_t, torch), _dev(wd_t, torch), n, k, _dev(xq_t, torch), _dev(xd_t, torch), m, bias, 1,
+                      yt, yqt, ydt, tiled=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(yt.cpu().numpy(), y)
+    qt_ref, dt_ref = to_tiled(yq, yd)
+    assert np.array_equal(yqt.cpu().numpy(), qt_ref) and np.array_equal(ydt.cpu().numpy(), dt_ref)
 
 
 @pytest.mark.parametrize("B,S,max_len,pads,what", [
