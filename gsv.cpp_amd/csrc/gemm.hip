@@ -278,7 +278,9 @@ __global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n
                                                                 const float * __restrict__ xd,
                                                                 bool x_tiled, LayerOut out) {
     constexpr int NBW = NBLK / 4;                                  // blocks per wave
-    constexpr int G = NBW <= 4 ? NBW : (MT >= 4 ? 2 : 4);          // blocks per load group
+    // blocks per load group: every load at once for one row tile (16 blocks = 128 VGPRs of
+    // operands), two or eight groups for more rows
+    constexpr int G = (NBW <= 4 || MT == 1) ? NBW : (MT == 2 ? NBW / 2 : 2);
     constexpr int NG = NBW / G;
     static_assert(NBW % G == 0, "load groups must tile the wave's blocks");
     __shared__ float red[4][32 * MT][33];
@@ -290,6 +292,13 @@ __global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n
     const int n0 = blockIdx.x * 32;
     const int m0 = blockIdx.y * 32 * MT;
     const int kb0 = wave * NBW;
+    // the epilogue's own operands first: their round trip overlaps the K loop
+    const int cg = tid & 7;
+    const int col = n0 + 4 * cg;
+    float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (out.bias) bias4 = *reinterpret_cast<const float4 *>(out.bias + col);
+    int kvcol0 = 0;
+    if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
     // operand of block kb: quants at base + kb * step (16 bytes), scale at dbase[kb * dstep]. Tiled:
     // the (tile, block) kilobyte in lane order (one whole-line wave load); natural: 16 bytes of
     // row li.
@@ -368,12 +377,6 @@ __global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n
     __syncthreads();
 
     // epilogue: thread -> row (tid / 8) + 32 i, columns 4 * (tid % 8) .. + 4 of the tile
-    int kvcol0 = 0;
-    if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
-    const int cg = tid & 7;
-    const int col = n0 + 4 * cg;
-    float4 bias4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (out.bias) bias4 = *reinterpret_cast<const float4 *>(out.bias + col);
 #pragma unroll
     for (int i = 0; i < MT; i++) {
         const int r = (tid >> 3) + 32 * i;
