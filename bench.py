@@ -276,6 +276,23 @@ def prefill_line(g, torch):
                         "prefill call incl. head logits"}
 
 
+def b128_line(g, flags):
+    """High-batch long context: batch 128, KV lengths U[1024, 4096] (64 prompt codes), 256 greedy
+    steps (the projections run as matrix-core GEMMs at this batch)."""
+    hb = prefill_requests(B=128, S=4096, P=64, lo=1024, seed=0x6A5E0005, bert=False)
+    seeds = list(range(1, 129))
+    g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=4, seeds=seeds, flags=flags)
+    rb = g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=256, seeds=seeds, flags=flags)
+    ms5 = rb["decode_ms"] / 256
+    b5 = np.mean([decode_bytes_per_step(hb, s) for s in range(0, 256, 16)])
+    return {"tok_s": round(128 * 256 / (rb["decode_ms"] / 1e3), 1), "ms_per_step": round(ms5, 4),
+            "step_bytes_mb": round(b5 / 1e6, 1),
+            "step_hbm_frac": round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+            "prefill_ms": round(rb["prefill_ms"], 1),
+            "workload": "128 sequences, KV lengths U[1024,4096] (phones + 64 prompt codes, "
+                        "no BERT features), 256 greedy steps"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -287,6 +304,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=500)
     ap.add_argument("--no-b128", action="store_true", help="skip the batch-128 long-context decode line")
     ap.add_argument("--prefill-only", action="store_true", help="time only the batch-16 x 1024 prefill")
+    ap.add_argument("--b128-only", action="store_true", help="time only the batch-128 long-context decode")
     ap.add_argument("--kernels-only", action="store_true",
                     help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
@@ -313,6 +331,10 @@ def main():
     g = gsvk.Model(path, device=0)
     if args.prefill_only:
         print(json.dumps({"prefill_b16_s1024": prefill_line(g, torch)}))
+        g.close()
+        return
+    if args.b128_only:
+        print(json.dumps({"b128_long": b128_line(g, gsvk.GSVK_GEN_EOS_MASK_ALL)}))
         g.close()
         return
     cfg = (15, 1.0, 1.0, 1.35)
@@ -353,20 +375,8 @@ def main():
     extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)
     extra["ms_per_step_b64"] = round(rb["decode_ms"] / 200, 4)
     extra["prefill_b16_s1024"] = prefill_line(g, torch)
-    # high-batch long context: batch 128, KV lengths U[1024, 4096] (64 prompt codes), 256 greedy steps
     if not args.no_b128:
-        hb = prefill_requests(B=128, S=4096, P=64, lo=1024, seed=0x6A5E0005, bert=False)
-        seeds = list(range(1, 129))
-        g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=4, seeds=seeds, flags=flags)
-        rb = g.generate(hb, sampler=(1, 1.0, 1.0, 1.0), max_steps=256, seeds=seeds, flags=flags)
-        ms5 = rb["decode_ms"] / 256
-        b5 = np.mean([decode_bytes_per_step(hb, s) for s in range(0, 256, 16)])
-        extra["b128_long"] = {"tok_s": round(128 * 256 / (rb["decode_ms"] / 1e3), 1), "ms_per_step": round(ms5, 4),
-                              "step_bytes_mb": round(b5 / 1e6, 1),
-                              "step_hbm_frac": round(b5 / (ms5 / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
-                              "prefill_ms": round(rb["prefill_ms"], 1),
-                              "workload": "128 sequences, KV lengths U[1024,4096] (phones + 64 prompt codes, "
-                                          "no BERT features), 256 greedy steps"}
+        extra["b128_long"] = b128_line(g, flags)
         g.release_cache()
     g.close()
 
