@@ -277,8 +277,8 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
                      hipStream_t stream, int layout = Q8_SLICED);
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
-                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, hipStream_t stream,
-                    int layout = Q8_SLICED);
+                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, const int32_t * pos_sub,
+                    int pe_rows, hipStream_t stream, int layout = Q8_SLICED);
 size_t attn_workspace_bytes(int B, int nh, int64_t max_keys);
 int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
                        int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,

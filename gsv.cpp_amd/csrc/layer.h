@@ -31,6 +31,10 @@ struct LayerIn {
     // IN_EMB: kv_end[m] = *pos_ptr + kv_end_add, stored by the column-0 workgroups (may be null)
     int32_t * kv_end;
     int kv_end_add;
+    // IN_EMB: the PE row of row m is *pos_ptr + pos_add - pos_sub[m] (pos_sub may be null: 0; a
+    // batch that sequences join while it decodes), clamped into the table's pe_rows rows
+    const int32_t * pos_sub;
+    int pe_rows;
 };
 
 struct LayerOut {

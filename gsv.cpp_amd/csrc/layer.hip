@@ -84,7 +84,7 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
         tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
         pos = *in.pos_ptr;
         const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * 512 + lane * 8);
-        const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) (pos + in.pos_add) * 512 + lane * 8);
+        const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) pe_row(in, pos, mmr) * 512 + lane * 8);
         e0 = er[0]; e1 = er[1]; p0 = pr[0]; p1 = pr[1];
     }
     __builtin_amdgcn_sched_barrier(0);   // keep the input loads ahead of the weight loads

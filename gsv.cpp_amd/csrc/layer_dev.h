@@ -2,8 +2,17 @@
 #pragma once
 
 #include "common.h"
+#include "layer.h"
 
 namespace gsvk {
+
+// PE row of the embedding input stage for activation row `row` at loop position `step`
+// (*in.pos_ptr), clamped into the table.
+__device__ __forceinline__ int pe_row(const LayerIn & in, int step, int row) {
+    int p = step + in.pos_add - (in.pos_sub ? in.pos_sub[row] : 0);
+    p = p < 0 ? 0 : p;
+    return (in.pe_rows > 0 && p >= in.pe_rows) ? in.pe_rows - 1 : p;
+}
 
 // read in place of an absent r or bias operand of the LayerNorm input stage
 static __device__ __align__(16) const float g_zero_row[512] = {};

@@ -139,13 +139,15 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
                                                  int8_t * __restrict__ xq,
                                                  float * __restrict__ xd,
                                                  int32_t * __restrict__ kv_end, int kv_end_add,
+                                                 const int32_t * __restrict__ pos_sub, int pe_rows,
                                                  int layout) {
     const int b = blockIdx.x;
     const int lane = threadIdx.x;
     int t = tok[b];
     t = t < 0 ? 0 : (t >= vocab ? vocab - 1 : t);
     const int step = *pos_ptr;
-    const int pos = step + pos_add;
+    int pos = step + pos_add - (pos_sub ? pos_sub[b] : 0);
+    pos = pos < 0 ? 0 : (pe_rows > 0 && pos >= pe_rows ? pe_rows - 1 : pos);
     if (kv_end && lane == 0) kv_end[b] = step + kv_end_add;
     const float * er = emb + (int64_t) t * d + lane * 8;
     const float * pr = pe + (int64_t) pos * d + lane * 8;
@@ -188,13 +190,13 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
 
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
-                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, hipStream_t stream,
-                    int layout) {
+                    int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, const int32_t * pos_sub,
+                    int pe_rows, hipStream_t stream, int layout) {
     GSVK_REQUIRE(d == 512, "embed_pe: d_model must be 512");
     GSVK_REQUIRE(layout >= Q8_SLICED && layout <= Q8_TILED, "embed_pe: bad layout %d", layout);
     GSVK_REQUIRE(emb && pe && tok && pos_ptr && x && xq && xd, "embed_pe: null pointer");
     hipLaunchKernelGGL(k_embed_pe, dim3((unsigned) B), dim3(64), 0, stream, emb, pe, tok, vocab,
-                       pos_ptr, pos_add, alpha, d, x, xq, xd, kv_end, kv_end_add, layout);
+                       pos_ptr, pos_add, alpha, d, x, xq, xd, kv_end, kv_end_add, pos_sub, pe_rows, layout);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -97,7 +97,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
             int tk = in.tok[b];
             tk = tk < 0 ? 0 : (tk >= in.vocab ? in.vocab - 1 : tk);
             const float4 * er = reinterpret_cast<const float4 *>(in.emb + (int64_t) tk * QA_K + lane * 8);
-            const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) (pos + in.pos_add) * QA_K +
+            const float4 * pr = reinterpret_cast<const float4 *>(in.pe + (int64_t) pe_row(in, pos, b) * QA_K +
                                                                  lane * 8);
             const float4 e0 = er[0], e1 = er[1], p0 = pr[0], p1 = pr[1];
             const float ev[8] = {e0.x, e0.y, e0.z, e0.w, e1.x, e1.y, e1.z, e1.w};

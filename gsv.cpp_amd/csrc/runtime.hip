@@ -156,6 +156,15 @@ struct gsvk_model {
     hipGraphExec_t gexec = nullptr;
     hipGraph_t graph = nullptr;
     bool use_graph = true;
+    // a batch that sequences join and leave while it decodes (gsvk_cb_*): per-row loop index at
+    // which the row joined and its step limit (both non-null only while a session is open), the
+    // session's shape and its host-side slot table
+    DevArena cbmem;
+    int32_t * row_start = nullptr, * row_max = nullptr;
+    bool cb_open = false;
+    int cb_smax = 0, cb_steps = 0, cb_step = 0;
+    std::vector<int> cb_used, cb_start, cb_max;
+    SampleArgs cb_sa{};
 
     ~gsvk_model() {
         if (pf_pool) (void) hipFree(pf_pool);
@@ -184,6 +193,20 @@ void drop_graph(gsvk_model * m) {
     if (m->graph) (void) hipGraphDestroy(m->graph);
     m->gexec = nullptr;
     m->graph = nullptr;
+}
+
+// Close an open batch session (its graph and per-row arrays); the cache and state stay allocated.
+void cb_drop(gsvk_model * m) {
+    if (!m->cb_open) return;
+    (void) hipStreamSynchronize(m->stream);
+    drop_graph(m);
+    m->cbmem.release();
+    m->row_start = m->row_max = nullptr;
+    m->cb_open = false;
+    m->cb_used.clear();
+    m->cb_start.clear();
+    m->cb_max.clear();
+    m->prefilled = false;
 }
 
 int upload(void * dst, const void * src, size_t bytes, hipStream_t st) {
@@ -448,7 +471,7 @@ int enqueue_decode_body(gsvk_model * m) {
             if (li == 0) {
                 GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
                                          m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q,
-                                         m->x.d, m->kv_end, m->S, m->stream, Q8_TILED));
+                                         m->x.d, m->kv_end, m->S, m->row_start, PE_MAX, m->stream, Q8_TILED));
             } else {
                 const LayerW & p = m->L[li - 1];
                 GSVK_TRY(launch_layernorm(m->n1.x, m->h2, p.f2.b, p.ln2, B, D, 1e-5f, m->x.x, m->x.q,
@@ -475,6 +498,8 @@ int enqueue_decode_body(gsvk_model * m) {
             in.vocab = m->V;
             in.kv_end = m->kv_end;
             in.kv_end_add = m->S;
+            in.pos_sub = m->row_start;
+            in.pe_rows = PE_MAX;
         } else {
             const LayerW & p = m->L[li - 1];
             in.mode = IN_LN;
@@ -546,8 +571,13 @@ int check_requests(gsvk_model * m, const gsvk_request * reqs, int B) {
     return GSVK_OK;
 }
 
+// Prefill of B requests. Default: (re)allocates the cache and decode state for this batch and
+// writes the K/V of request b to cache row b, columns [0, S). Slot mode (kv_slot >= 0, one
+// request, a batch that sequences join while it decodes): writes the request's K/V to cache row
+// kv_slot of the existing cache at columns [col0, col0 + S) and its logits to that row of the
+// model's logits, leaving the rest of the model's state as it is.
 int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed, float * logits_host,
-               int hist_len, int max_steps) {
+               int hist_len, int max_steps, int kv_slot = -1, int col0 = 0) {
     GSVK_TRY(check_requests(m, reqs, B));
     const int P = reqs[0].n_prompt;
     int max_len = 0;
@@ -555,14 +585,21 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     const int S = max_len + P;
     GSVK_REQUIRE(S >= 1, "empty input (no phones and no prompt)");
     const int D = m->D, F = m->FFN, BD = m->BERT;
-    GSVK_TRY(alloc_kv(m, B, std::max(lmax_needed, S + 8)));
-    GSVK_TRY(ensure_state(m, B, std::max(hist_len, P + 1), std::max(max_steps, 1)));
-    m->prompt_len = P;
-    m->S = S;
-    m->max_len = max_len;
-    m->B = B;
-    m->host_step = 0;
-    m->prefilled = false;
+    const bool slot_mode = kv_slot >= 0;
+    if (slot_mode) {
+        GSVK_REQUIRE(B == 1 && m->kc && kv_slot < m->kv_B && col0 >= 0 && col0 + S <= m->lstride,
+                     "prefill into slot %d at column %d: outside the cache", kv_slot, col0);
+    } else {
+        GSVK_TRY(alloc_kv(m, B, std::max(lmax_needed, S + 8)));
+        GSVK_TRY(ensure_state(m, B, std::max(hist_len, P + 1), std::max(max_steps, 1)));
+        m->prompt_len = P;
+        m->S = S;
+        m->max_len = max_len;
+        m->B = B;
+        m->host_step = 0;
+        m->prefilled = false;
+    }
+    const size_t slot_off = slot_mode ? (size_t) kv_slot * m->NH * m->lstride * m->HD : 0;
     hipStream_t st = m->stream;
 
     // host-side packing of the requests
@@ -660,7 +697,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     const float scale = 1.0f / std::sqrt((float) m->HD);
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
-        const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+        const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
         const bool gemm = rows >= GEMM_MIN_ROWS;
         if (gemm) {
             // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
@@ -670,7 +707,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                                           Q8_NATURAL));
             }
             GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, rows, cur.q, cur.d, Q8_NATURAL,
-                                    qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
+                                    qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0), st));
         } else {
             LayerIn in{};
             if (li == 0) {
@@ -687,7 +724,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                 in.out_x = cur.x;
             }
             GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
-                                       qkv_out(m, w, loff, qkv, 3 * D, S, zero, 0), st));
+                                       qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0), st));
         }
         if (attn_prefill_uses_mfma(rows))
             GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
@@ -708,8 +745,9 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     }
     // llamafile's tinyBLAS handles the head when the prefill has >= 2 columns
     GSVK_TRY(head_logits(m, lastq, B, S >= 2 ? 1 : 0, lg));
-    GSVK_HIP(hipMemcpyAsync(m->logits, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToDevice, st));
-    GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));
+    GSVK_HIP(hipMemcpyAsync(m->logits + (slot_mode ? (size_t) kv_slot * m->V : 0), lg, (size_t) B * m->V * 4,
+                            hipMemcpyDeviceToDevice, st));
+    if (!slot_mode) GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));
     if (logits_host)
         GSVK_HIP(hipMemcpyAsync(logits_host, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
     GSVK_HIP(hipStreamSynchronize(st));
@@ -723,7 +761,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         else
             (void) hipGetLastError();   // not an error of this call: the next one allocates apart
     }
-    m->prefilled = true;
+    if (!slot_mode) m->prefilled = true;
     return GSVK_OK;
 }
 
@@ -1039,6 +1077,7 @@ extern "C" int gsvk_kv_alloc(gsvk_model * m, int B, int lmax) {
 extern "C" int gsvk_release_cache(gsvk_model * m) {
     GSVK_REQUIRE(m, "null model");
     DeviceGuard guard(m->device);
+    cb_drop(m);
     GSVK_HIP(hipStreamSynchronize(m->stream));
     drop_graph(m);
     m->smem.release();
@@ -1057,6 +1096,7 @@ extern "C" int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int 
     GSVK_REQUIRE(m && logits, "null argument");
     if (B == 0) return GSVK_OK;
     DeviceGuard guard(m->device);
+    cb_drop(m);
     int max_len = 0;
     for (int b = 0; b < B; b++) max_len = std::max(max_len, reqs[b].n_phones);
     return do_prefill(m, reqs, B, max_len + (B > 0 ? reqs[0].n_prompt : 0) + 8, logits, 0, 1);
@@ -1066,6 +1106,7 @@ extern "C" int gsvk_prefill(gsvk_model * m, const gsvk_request * reqs, int B, fl
                             int * S_out) {
     GSVK_REQUIRE(m, "null model");
     DeviceGuard guard(m->device);
+    cb_drop(m);
     int max_len = 0;
     for (int b = 0; b < B && reqs; b++) max_len = std::max(max_len, reqs[b].n_phones);
     const int S = max_len + (B > 0 && reqs ? reqs[0].n_prompt : 0);
@@ -1078,7 +1119,7 @@ extern "C" int gsvk_prefill(gsvk_model * m, const gsvk_request * reqs, int B, fl
 
 extern "C" int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float * logits) {
     GSVK_REQUIRE(m && last_tok, "null argument");
-    if (!m->prefilled) { set_error("decode_step before prefill"); return GSVK_ERR_STATE; }
+    if (!m->prefilled || m->cb_open) { set_error("decode_step before prefill"); return GSVK_ERR_STATE; }
     DeviceGuard guard(m->device);
     const int B = m->B;
     if (m->S + m->host_step >= m->kv_lmax + 1 || m->prompt_len + m->host_step >= PE_MAX) {
@@ -1096,6 +1137,216 @@ extern "C" int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float 
     if (logits) GSVK_HIP(hipMemcpyAsync(logits, m->logits, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
     GSVK_HIP(hipStreamSynchronize(st));
     m->host_step++;
+    return GSVK_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// A batch that sequences join and leave while it decodes (continuous batching)
+// ---------------------------------------------------------------------------------------
+//
+// The batch decodes in lockstep over a shared KV column, as generate does; a request joins at
+// loop index g (the next step) by a prefill of its own, written to a free cache row left-padded
+// so that it ends at the shared column (kv_begin = max_prefill + g - S); its positions, EOS-mask
+// window, step limit and early-stop rule count from g. Rows without a request are finished
+// (fin_step >= 0) and take no part. Per row the arithmetic is that of a batch of its own.
+
+extern "C" int gsvk_cb_open(gsvk_model * m, int capacity, int max_prefill, int max_steps, int prompt_len,
+                            const gsvk_sampler_cfg * cfg, int early_stop_num, unsigned flags) {
+    GSVK_REQUIRE(m && cfg, "null argument");
+    GSVK_REQUIRE(capacity > 0 && capacity <= 65535 && max_prefill >= 1 && max_steps >= 1 &&
+                     prompt_len >= 0 && prompt_len <= max_prefill && max_prefill <= PE_MAX,
+                 "cb_open: bad shape (capacity %d, max_prefill %d, max_steps %d, prompt %d)", capacity,
+                 max_prefill, max_steps, prompt_len);
+    GSVK_REQUIRE(prompt_len + max_steps <= PE_MAX, "cb_open: prompt_len + max_steps = %d exceeds the "
+                 "positional table (%d)", prompt_len + max_steps, PE_MAX);
+    DeviceGuard guard(m->device);
+    cb_drop(m);
+    const int hist_len = prompt_len + max_steps;
+    GSVK_TRY(alloc_kv(m, capacity, max_prefill + max_steps + 8));
+    GSVK_TRY(ensure_state(m, capacity, hist_len, max_steps));
+    m->B = capacity;
+    m->S = max_prefill;
+    m->prompt_len = prompt_len;
+    m->max_len = max_prefill - prompt_len;
+    m->host_step = 0;
+    GSVK_TRY(m->cbmem.alloc(m->row_start, capacity));
+    GSVK_TRY(m->cbmem.alloc(m->row_max, capacity));
+    hipStream_t st = m->stream;
+    // every row starts empty: finished, no steps, an attention range of its own fresh key only
+    const std::vector<int32_t> zero(capacity, 0), none(capacity, -1), begin(capacity, max_prefill),
+        ny(capacity, prompt_len);
+    const std::vector<uint64_t> one(capacity, 1);
+    const int32_t step0 = 0;
+    GSVK_TRY(upload(m->row_start, zero.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->row_max, zero.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->fin_step, zero.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->fin_kind, none.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->kv_begin, begin.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->ny, ny.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->last_tok, zero.data(), (size_t) capacity * 4, st));
+    GSVK_TRY(upload(m->rng, one.data(), (size_t) capacity * 8, st));
+    GSVK_TRY(upload(m->d_step, &step0, 4, st));
+    GSVK_HIP(hipMemsetAsync(m->hist, 0, (size_t) capacity * hist_len * 4, st));
+    GSVK_HIP(hipMemsetAsync(m->logits, 0, (size_t) capacity * m->V * 4, st));
+    GSVK_HIP(hipStreamSynchronize(st));   // the host vectors above live on this stack frame
+
+    SampleArgs & sa = m->cb_sa;
+    sa = SampleArgs{};
+    sa.logits = m->logits;
+    sa.V = m->V;
+    sa.eos = m->EOS;
+    sa.B = capacity;
+    sa.P = prompt_len;
+    sa.hist = m->hist;
+    sa.hist_stride = hist_len;
+    sa.ny = m->ny;
+    sa.fin_step = m->fin_step;
+    sa.fin_kind = m->fin_kind;
+    sa.rng = m->rng;
+    sa.jump = m->rng_jump;
+    sa.adv = m->rng_adv;
+    sa.chunk = m->rng_chunk;
+    sa.top_k = cfg->top_k;
+    sa.top_p = cfg->top_p;
+    sa.temperature = cfg->temperature;
+    sa.rep = cfg->repetition_penalty;
+    sa.step = m->d_step;
+    sa.flags = ((flags & GSVK_GEN_EOS_MASK_ALL) ? 1u : 0u) | 2u;   // early stop per row
+    sa.last_tok = m->last_tok;
+    sa.max_steps = max_steps;
+    sa.done_counter = m->done_counter;
+    sa.n_unfinished = m->n_unfinished;
+    sa.early_stop = early_stop_num;
+    sa.row_start = m->row_start;
+    sa.row_max = m->row_max;
+    m->cb_open = true;
+    m->cb_smax = max_prefill;
+    m->cb_steps = max_steps;
+    m->cb_step = 0;
+    m->cb_used.assign(capacity, 0);
+    m->cb_start.assign(capacity, 0);
+    m->cb_max.assign(capacity, 0);
+    if (m->use_graph) {
+        GSVK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+        int rc = launch_sample(sa, st);
+        if (rc == GSVK_OK) rc = enqueue_decode_body(m);
+        hipGraph_t g = nullptr;
+        const hipError_t e = hipStreamEndCapture(st, &g);
+        if (rc != GSVK_OK) {
+            if (g) (void) hipGraphDestroy(g);
+            cb_drop(m);
+            return rc;
+        }
+        if (e != hipSuccess) {
+            cb_drop(m);
+            GSVK_HIP(e);
+        }
+        m->graph = g;
+        GSVK_HIP(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+    }
+    m->prefilled = true;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_cb_add(gsvk_model * m, const gsvk_request * req, uint64_t seed, int max_steps,
+                           int * slot_out) {
+    GSVK_REQUIRE(m && req && slot_out, "null argument");
+    if (!m->cb_open) { set_error("cb_add: no batch session is open"); return GSVK_ERR_STATE; }
+    GSVK_REQUIRE(req->n_prompt == m->prompt_len, "cb_add: prompt length %d differs from the session's %d",
+                 req->n_prompt, m->prompt_len);
+    const int S = req->n_phones + req->n_prompt;
+    GSVK_REQUIRE(S >= 1 && S <= m->cb_smax, "cb_add: %d prefill rows exceed the session's %d", S, m->cb_smax);
+    GSVK_REQUIRE(max_steps >= 1 && m->cb_step + max_steps <= m->cb_steps,
+                 "cb_add: %d steps from loop index %d exceed the session's %d", max_steps, m->cb_step,
+                 m->cb_steps);
+    int b = 0;
+    while (b < m->B && m->cb_used[b]) b++;
+    if (b == m->B) { set_error("cb_add: no free row (capacity %d)", m->B); return GSVK_ERR_STATE; }
+    DeviceGuard guard(m->device);
+    const int col0 = m->cb_smax + m->cb_step - S;
+    GSVK_TRY(do_prefill(m, req, 1, 0, nullptr, 0, 0, b, col0));
+    hipStream_t st = m->stream;
+    const int P = m->prompt_len;
+    const int32_t fin = -1, ny = P, last = P ? req->prompt[P - 1] : 0, start = m->cb_step, mx = max_steps;
+    const uint64_t rng = seed ? seed : 1;   // gsv_rng: seed 0 -> 1
+    GSVK_TRY(upload(m->kv_begin + b, &col0, 4, st));
+    if (P) GSVK_TRY(upload(m->hist + (size_t) b * m->cb_sa.hist_stride, req->prompt, (size_t) P * 4, st));
+    GSVK_TRY(upload(m->ny + b, &ny, 4, st));
+    GSVK_TRY(upload(m->fin_step + b, &fin, 4, st));
+    GSVK_TRY(upload(m->fin_kind + b, &fin, 4, st));
+    GSVK_TRY(upload(m->last_tok + b, &last, 4, st));
+    GSVK_TRY(upload(m->rng + b, &rng, 8, st));
+    GSVK_TRY(upload(m->row_start + b, &start, 4, st));
+    GSVK_TRY(upload(m->row_max + b, &mx, 4, st));
+    GSVK_HIP(hipStreamSynchronize(st));   // the host values above live on this stack frame
+    m->cb_used[b] = 1;
+    m->cb_start[b] = start;
+    m->cb_max[b] = mx;
+    *slot_out = b;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_cb_step(gsvk_model * m, int n_steps, int * n_running) {
+    GSVK_REQUIRE(m, "null model");
+    if (!m->cb_open) { set_error("cb_step: no batch session is open"); return GSVK_ERR_STATE; }
+    GSVK_REQUIRE(n_steps >= 0 && m->cb_step + n_steps <= m->cb_steps,
+                 "cb_step: %d steps from loop index %d exceed the session's %d", n_steps, m->cb_step,
+                 m->cb_steps);
+    DeviceGuard guard(m->device);
+    hipStream_t st = m->stream;
+    for (int i = 0; i < n_steps; i++) {
+        if (m->gexec) {
+            GSVK_HIP(hipGraphLaunch(m->gexec, st));
+        } else {
+            GSVK_TRY(launch_sample(m->cb_sa, st));
+            GSVK_TRY(enqueue_decode_body(m));
+        }
+    }
+    GSVK_HIP(hipMemcpyAsync(m->h_pinned, m->n_unfinished, 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+    m->cb_step += n_steps;
+    if (n_running) *n_running = n_steps > 0 ? *m->h_pinned : -1;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_cb_take(gsvk_model * m, int slot, int32_t * tokens, int capacity, int * n_tokens,
+                            int * len, int * finished) {
+    GSVK_REQUIRE(m && n_tokens && finished, "null argument");
+    if (!m->cb_open) { set_error("cb_take: no batch session is open"); return GSVK_ERR_STATE; }
+    GSVK_REQUIRE(slot >= 0 && slot < m->B && m->cb_used[slot], "cb_take: row %d holds no request", slot);
+    DeviceGuard guard(m->device);
+    hipStream_t st = m->stream;
+    int32_t fin = -1, ny = 0;
+    GSVK_HIP(hipMemcpyAsync(&fin, m->fin_step + slot, 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipMemcpyAsync(&ny, m->ny + slot, 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+    const int done_steps = m->cb_step - m->cb_start[slot];
+    *finished = (fin >= 0 || done_steps >= m->cb_max[slot]) ? 1 : 0;
+    *n_tokens = 0;
+    if (len) *len = fin >= 0 ? fin : m->cb_max[slot];
+    if (!*finished) return GSVK_OK;
+    // as generate's result: the history minus the stopping token (EOS or early stop), or all of it
+    const int n = fin >= 0 ? ny - 1 : ny;
+    GSVK_REQUIRE(n >= 0 && n <= m->cb_sa.hist_stride, "cb_take: bad history length %d", n);
+    if (tokens) {
+        GSVK_REQUIRE(capacity >= n, "cb_take: %d tokens do not fit in %d", n, capacity);
+        GSVK_HIP(hipMemcpyAsync(tokens, m->hist + (size_t) slot * m->cb_sa.hist_stride, (size_t) n * 4,
+                                hipMemcpyDeviceToHost, st));
+    }
+    // the row leaves the batch: finished, no steps left
+    const int32_t zero = 0;
+    GSVK_TRY(upload(m->fin_step + slot, &zero, 4, st));
+    GSVK_TRY(upload(m->row_max + slot, &zero, 4, st));
+    GSVK_HIP(hipStreamSynchronize(st));
+    *n_tokens = n;
+    m->cb_used[slot] = 0;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_cb_close(gsvk_model * m) {
+    GSVK_REQUIRE(m, "null model");
+    DeviceGuard guard(m->device);
+    cb_drop(m);
     return GSVK_OK;
 }
 
@@ -1119,6 +1370,7 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     GSVK_REQUIRE(reqs && B > 0 && max_steps >= 0, "bad arguments");
     GSVK_REQUIRE(out->tokens && out->tok_len && out->lens, "null output buffers");
     DeviceGuard guard(m->device);
+    cb_drop(m);
     const int P = reqs[0].n_prompt;
     GSVK_REQUIRE(out->tok_stride >= P + max_steps, "tok_stride %d < prompt + max_steps (%d)",
                  out->tok_stride, P + max_steps);

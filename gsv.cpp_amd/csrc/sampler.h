@@ -33,6 +33,13 @@ struct SampleArgs {
     int32_t * done_counter;    // zero between calls
     int32_t * n_unfinished;    // written by the last workgroup
     int early_stop;            // -1 = off
+    // a batch that sequences join while it decodes: row b takes part from loop index
+    // row_start[b] on, for at most row_max[b] steps, its EOS-mask window, oracle, dumps and
+    // finish step counted from there; with bit 1 of flags the early-stop rule is applied per row
+    // (its own token count) instead of on sequence 0 for the whole batch. Null: every row starts
+    // at 0 with max_steps.
+    const int32_t * row_start;
+    const int32_t * row_max;
 };
 
 int launch_sample(const SampleArgs & a, hipStream_t stream);

@@ -115,7 +115,9 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
 
     // every load that does not depend on another is issued here, before the first use: the
     // loop index, this row's state, its logits, the jump matrices and the advance columns
-    const int idx = a.step ? *a.step : 11;   // no loop state: past the EOS-mask window
+    const int gidx = a.step ? *a.step : 11;   // no loop state: past the EOS-mask window
+    const int idx = gidx - (a.row_start ? a.row_start[b] : 0);   // this row's own step
+    const int rmax = a.row_max ? a.row_max[b] : a.max_steps;
     const int fin = a.fin_step ? a.fin_step[b] : -1;
     const int n_hist = a.ny ? a.ny[b] : 0;
     const uint64_t s0 = a.rng[b];
@@ -147,7 +149,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     asm volatile("" ::"v"(st0), "v"(s_next));   // the table loads complete here, not at first use
     __syncthreads();
 
-    const bool running = fin < 0 && idx < a.max_steps;
+    const bool running = fin < 0 && idx >= 0 && idx < rmax;
     if (running) {
         if (tid == 0 && a.step && (idx < 11 || (a.flags & 1u))) lg[a.eos] = -INFINITY;
         // 1) repetition penalty, once per occurrence in the window
@@ -352,7 +354,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
             if (tok < 0 || tok >= V) tok = 0;   // no value > 0: the first index wins
             if (a.tok_out) a.tok_out[b] = tok;
             if (a.step) {
-                if (a.sampled_dump) a.sampled_dump[(int64_t) idx * a.B + b] = tok;
+                if (a.sampled_dump) a.sampled_dump[(int64_t) gidx * a.B + b] = tok;
                 if (a.oracle && idx < a.n_oracle) tok = a.oracle[idx];
                 const int n = n_hist;
                 a.hist[(int64_t) b * a.hist_stride + n] = tok;
@@ -361,6 +363,9 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                 if (tok == a.eos) {
                     a.fin_step[b] = idx;
                     a.fin_kind[b] = 0;
+                } else if ((a.flags & 2u) && a.early_stop != -1 && n + 1 - a.P > a.early_stop) {
+                    a.fin_step[b] = idx;   // the early-stop rule on this row's own tokens
+                    a.fin_kind[b] = 1;
                 }
             }
         }
@@ -374,25 +379,29 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                                                 __HIP_MEMORY_SCOPE_AGENT);
         if (prev == a.B - 1) {
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            if (idx < a.max_steps) {
-                if (a.early_stop != -1) {
+            if (gidx < a.max_steps) {
+                if (a.early_stop != -1 && !(a.flags & 2u)) {
                     const int n0 = __hip_atomic_load(a.ny, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     if (n0 - a.P > a.early_stop) {
                         for (int bb = 0; bb < a.B; bb++) {
                             if (__hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED,
                                                   __HIP_MEMORY_SCOPE_AGENT) < 0) {
-                                a.fin_step[bb] = idx;
+                                a.fin_step[bb] = gidx - (a.row_start ? a.row_start[bb] : 0);
                                 a.fin_kind[bb] = 1;
                             }
                         }
                     }
                 }
+                // unfinished rows; with per-row limits, those that take part in the next step
                 int unfinished = 0;
-                for (int bb = 0; bb < a.B; bb++)
-                    unfinished += __hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT) < 0;
+                for (int bb = 0; bb < a.B; bb++) {
+                    const bool open = __hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT) < 0;
+                    unfinished += a.row_max ? (open && gidx + 1 - (a.row_start ? a.row_start[bb] : 0) < a.row_max[bb])
+                                            : open;
+                }
                 *a.n_unfinished = unfinished;
-                *a.step = idx + 1;
+                *a.step = gidx + 1;
             }
             __hip_atomic_store(a.done_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }

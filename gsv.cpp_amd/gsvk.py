@@ -27,6 +27,7 @@ EXPORTS = [
     "gsvk_op_fdot", "gsvk_attn_workspace_bytes", "gsvk_op_attn_decode", "gsvk_op_ln_gemv",
     "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
     "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
+    "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
 ]
 
 
@@ -89,6 +90,11 @@ def lib():
         L.gsvk_decode_step.argtypes = [vp, vp, vp]
         L.gsvk_kv_read.argtypes = [vp, i32, vp, vp]
         L.gsvk_last_sampled.argtypes = [vp, i32, vp]
+        L.gsvk_cb_open.argtypes = [vp, i32, i32, i32, i32, C.POINTER(SamplerCfg), i32, C.c_uint]
+        L.gsvk_cb_add.argtypes = [vp, C.POINTER(Request), C.c_uint64, i32, C.POINTER(C.c_int)]
+        L.gsvk_cb_step.argtypes = [vp, i32, C.POINTER(C.c_int)]
+        L.gsvk_cb_take.argtypes = [vp, i32, vp, i32, C.POINTER(C.c_int), C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        L.gsvk_cb_close.argtypes = [vp]
         L.gsvk_op_q8_dequant.argtypes = [vp, i64, vp, vp]
         L.gsvk_op_q8_repack.argtypes = [vp, i64, i64, vp, vp, vp]
         L.gsvk_op_q8_quantize.argtypes = [vp, i64, i64, vp, vp, vp]
@@ -323,6 +329,36 @@ class Model:
 
     def release_cache(self):
         check(lib().gsvk_release_cache(self.h), "release_cache")
+
+    # -- a batch that requests join and leave while it decodes (gsvk_cb_*) --
+    def cb_open(self, capacity, max_prefill, max_steps, prompt_len, sampler=(15, 1.0, 1.0, 1.35), early_stop=-1,
+                flags=0):
+        cfg = SamplerCfg(*sampler)
+        check(lib().gsvk_cb_open(self.h, capacity, max_prefill, max_steps, prompt_len, C.byref(cfg), early_stop,
+                                 flags), "cb_open")
+        self._cb_stride = prompt_len + max_steps
+
+    def cb_add(self, req, seed, max_steps):
+        arr, keep = _requests([req])
+        slot = C.c_int(-1)
+        check(lib().gsvk_cb_add(self.h, arr, seed, max_steps, C.byref(slot)), "cb_add")
+        return slot.value
+
+    def cb_step(self, n_steps):
+        running = C.c_int(0)
+        check(lib().gsvk_cb_step(self.h, n_steps, C.byref(running)), "cb_step")
+        return running.value
+
+    def cb_take(self, slot):
+        """(finished, tokens, len) of the request in `slot`; a finished request leaves its row."""
+        buf = np.zeros(self._cb_stride, np.int32)
+        n, ln, fin = C.c_int(0), C.c_int(0), C.c_int(0)
+        check(lib().gsvk_cb_take(self.h, slot, buf.ctypes.data, buf.size, C.byref(n), C.byref(ln), C.byref(fin)),
+              "cb_take")
+        return bool(fin.value), buf[:n.value].copy(), ln.value
+
+    def cb_close(self):
+        check(lib().gsvk_cb_close(self.h), "cb_close")
 
     def generate(self, reqs, sampler=(15, 1.0, 1.0, 1.35), seed_base=0, early_stop=-1, max_steps=1500,
                  oracle=None, seeds=None, flags=0, want_sampled=False, want_probs0=False):

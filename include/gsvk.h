@@ -165,6 +165,41 @@ int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float * logits_ou
  * (for checking the write/gather indexing). */
 int gsvk_kv_read(gsvk_model * m, int layer, uint16_t * k_out, uint16_t * v_out);
 
+/* ---- A batch that sequences join and leave while it decodes (continuous batching) ----------
+ * The reference batches requests per generate call (tools/svc_core.h:1244-1340: a group of
+ * requests with the same prompt, then src/gsv_ar.cpp:719-824 until the last finishes). These
+ * calls keep one batch decoding while requests join and leave it, each with the semantics of a
+ * generate of its own (same tokens for the same seed: per row the arithmetic does not depend on
+ * the other rows). The batch decodes in lockstep over a shared KV column; a request joins with a
+ * prefill of its own into a free cache row, left-padded so that it ends at that column. Any
+ * other prefill / generate / release call closes the session. */
+
+/* Open a session: `capacity` rows, requests of at most max_prefill = phones + prompt_len rows,
+ * the prompt length every request has, at most max_steps decode steps over the whole session
+ * (prompt_len + max_steps <= 4096). cfg, early_stop_num and flags (GSVK_GEN_EOS_MASK_ALL) as
+ * gsvk_generate, the early-stop rule applied to each request's own tokens. */
+int gsvk_cb_open(gsvk_model * m, int capacity, int max_prefill, int max_steps, int prompt_len,
+                 const gsvk_sampler_cfg * cfg, int early_stop_num, unsigned flags);
+
+/* Prefill one request into a free row; its first token is sampled at the next step. It decodes
+ * at most max_steps steps (the session's remaining steps bound it). seed as gsvk_generate's seeds
+ * (0 -> 1). *slot receives the row. */
+int gsvk_cb_add(gsvk_model * m, const gsvk_request * req, uint64_t seed, int max_steps, int * slot);
+
+/* Run n_steps decode steps of every row holding a running request; *n_running (may be NULL)
+ * receives the number still running after them (-1 when n_steps is 0). */
+int gsvk_cb_step(gsvk_model * m, int n_steps, int * n_running);
+
+/* If the request in row `slot` has finished (EOS, early stop or its step limit), copy its tokens
+ * (prompt + generated, without the stopping token, as gsvk_generate) to tokens[capacity], set
+ * *n_tokens, *len (the finishing step, or the step limit) and *finished = 1, and free the row;
+ * else set *finished = 0 and leave it. tokens may be NULL (the request is dropped). */
+int gsvk_cb_take(gsvk_model * m, int slot, int32_t * tokens, int capacity, int * n_tokens, int * len,
+                 int * finished);
+
+/* Close the session (the cache and buffers stay allocated for the next call). */
+int gsvk_cb_close(gsvk_model * m);
+
 /* Sampler choices of the last gsvk_generate before teacher forcing replaced them:
  * [n_steps][B], -1 where a sequence had already finished (greedy-token checks). */
 int gsvk_last_sampled(gsvk_model * m, int n_steps, int32_t * out);

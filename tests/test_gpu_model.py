@@ -259,3 +259,60 @@ def test_prefill_workspace_reuse(models):
     assert np.array_equal(s1, s2)
     g.release_cache()                     # frees the pool too; the next prefill allocates anew
     assert np.array_equal(g.first_logits(big), first)
+
+
+@pytest.mark.parametrize("flags,early_stop", [(1, -1), (0, 6)])
+def test_continuous_batch_matches_generate(gpu, model4_path, flags, early_stop):
+    """Requests that join a decoding batch (a prefill of their own into a free row, left-padded to
+    the batch's KV column) and leave it when done produce the tokens of a generate of their own,
+    bit for bit: per row the arithmetic does not depend on the other rows. Rows are reused after
+    a request leaves; with early stop the rule counts each request's own tokens."""
+    P = 8
+    cfg = (15, 1.0, 1.0, 1.35)
+    reqs = _reqs(41, [20, 9, 30, 14, 25], P=P)
+    seeds = [101, 202, 303, 404, 505]
+    steps = [24, 12, 16, 20, 10]
+    g = gpu.Model(model4_path)
+    try:
+        refs = []
+        for r, sd, st in zip(reqs, seeds, steps):
+            res = g.generate([r], sampler=cfg, max_steps=st, seeds=[sd], flags=flags, early_stop=early_stop)
+            refs.append(res["tokens"][0])
+        g.cb_open(capacity=3, max_prefill=64, max_steps=80, prompt_len=P, sampler=cfg, early_stop=early_stop,
+                  flags=flags)
+        got = {}
+        slots = {}
+
+        def add(i):
+            slots[i] = g.cb_add(reqs[i], seeds[i], steps[i])
+
+        def take_done():
+            for i, sl in list(slots.items()):
+                fin, toks, _ = g.cb_take(sl)
+                if fin:
+                    got[i] = toks
+                    del slots[i]
+
+        add(0)
+        add(1)
+        g.cb_step(5)
+        take_done()
+        add(2)                      # joins 5 steps in
+        g.cb_step(7)
+        take_done()                 # request 1 has run its 12 steps
+        add(3)                      # into the row request 1 left
+        g.cb_step(12)
+        take_done()
+        add(4)
+        g.cb_step(10)
+        take_done()
+        assert sorted(got) == [0, 1, 2, 3, 4] and not slots
+        for i in range(5):
+            assert np.array_equal(got[i], refs[i]), (i, got[i], refs[i])
+        g.cb_close()
+        # the model runs a plain generate again after the session
+        res = g.generate([reqs[0]], sampler=cfg, max_steps=steps[0], seeds=[seeds[0]], flags=flags,
+                         early_stop=early_stop)
+        assert np.array_equal(res["tokens"][0], refs[0])
+    finally:
+        g.close()
