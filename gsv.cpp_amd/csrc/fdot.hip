@@ -71,6 +71,69 @@ __global__ void __launch_bounds__(256) k_fdot_ggml(const WT * __restrict__ W, in
     }
 }
 
+// MODE 0 for many activation rows (the prefill's BERT projection, m in the thousands): each
+// thread keeps the same chains as k_fdot_ggml (slice lane p, fma over the steps of 32 in order,
+// then the butterfly and the leftovers), for RN weight rows x MT activation rows at once, so a
+// step costs RN + MT loads for RN * MT FMAs and the weights are re-read once per MT rows.
+// 256 threads = 8 groups of 32 lanes; workgroup tile 8*RN weight rows x MT activation rows.
+template <typename WT, int RN, int MT>
+__global__ void __launch_bounds__(256) k_fdot_ggml_t(const WT * __restrict__ W, int n, int k,
+                                                     const float * __restrict__ X, int64_t xs, int m,
+                                                     float * __restrict__ Y, int64_t ys) {
+    const bool x16 = sizeof(WT) == 2;
+    const int p = threadIdx.x & 31;
+    const int n0 = blockIdx.x * (8 * RN) + (threadIdx.x >> 5) * RN;
+    const int m0 = blockIdx.y * MT;
+    const WT * wr[RN];
+    const float * xr[MT];
+#pragma unroll
+    for (int j = 0; j < RN; j++) wr[j] = W + (int64_t) min(n0 + j, n - 1) * k;
+#pragma unroll
+    for (int t = 0; t < MT; t++) xr[t] = X + (int64_t) min(m0 + t, m - 1) * xs;
+    const int np = k & ~31;
+    float acc[RN][MT];
+#pragma unroll
+    for (int j = 0; j < RN; j++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) acc[j][t] = 0.0f;
+    for (int i = 0; i < np; i += 32) {
+        float w[RN], x[MT];
+#pragma unroll
+        for (int j = 0; j < RN; j++) w[j] = wload<WT>(wr[j] + i + p);
+#pragma unroll
+        for (int t = 0; t < MT; t++) x[t] = xconv(xr[t][i + p], x16);
+#pragma unroll
+        for (int j = 0; j < RN; j++)
+#pragma unroll
+            for (int t = 0; t < MT; t++) acc[j][t] = __builtin_fmaf(w[j], x[t], acc[j][t]);
+    }
+#pragma unroll
+    for (int j = 0; j < RN; j++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            float v = acc[j][t];
+            v = v + __shfl_xor(v, 16, 64);
+            v = v + __shfl_xor(v, 8, 64);
+            v = v + __shfl_xor(v, 4, 64);
+            v = v + __shfl_xor(v, 1, 64);
+            v = v + __shfl_xor(v, 2, 64);
+            acc[j][t] = v;
+        }
+    if (p != 0) return;
+#pragma unroll
+    for (int j = 0; j < RN; j++)
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int row = n0 + j, mm = m0 + t;
+            if (row < n && mm < m) {
+                float v = acc[j][t];
+                for (int i = np; i < k; i++)
+                    v = __builtin_fmaf(wload<WT>(wr[j] + i), xconv(xr[t][i], x16), v);
+                Y[(int64_t) mm * ys + row] = v;
+            }
+        }
+}
+
 // MODE 0 with K = 32 * NI known at compile time (the decode head, K = 512): the same arithmetic
 // as k_fdot_ggml, with every load issued up front. The MT activation rows (rounded to fp16 for
 // F16 weights) are staged once per workgroup in LDS with 16-byte loads; each lane loads its NI
@@ -196,6 +259,15 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
         else
             hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16>), grid, dim3(256), 0, stream,
                                (const float *) W, (int) n, X, xs, (int) m, Y, ys);
+    } else if (m >= 64) {
+        constexpr int RN = 4, MTT = 16;
+        const dim3 grid((unsigned) ((n + 8 * RN - 1) / (8 * RN)), (unsigned) ((m + MTT - 1) / MTT));
+        if (wtype == 1)
+            hipLaunchKernelGGL((k_fdot_ggml_t<uint16_t, RN, MTT>), grid, dim3(256), 0, stream,
+                               (const uint16_t *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
+        else
+            hipLaunchKernelGGL((k_fdot_ggml_t<float, RN, MTT>), grid, dim3(256), 0, stream,
+                               (const float *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
     } else {
         const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MT - 1) / MT));
         if (wtype == 1)

@@ -16,16 +16,17 @@ namespace gsvk {
 // ---------------------------------------------------------------------------------------
 
 template <int MAXC>
-__global__ void __launch_bounds__(64) k_layernorm(const float * __restrict__ x,
+__global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
                                                   const float * __restrict__ r,
                                                   const float * __restrict__ bias,
                                                   const float * __restrict__ wb, int rows, int n,
                                                   float eps, float * __restrict__ y,
                                                   int8_t * __restrict__ yq,
                                                   float * __restrict__ yd, int layout) {
-    const int row = blockIdx.x;
+    // one wave per row, up to 4 rows per workgroup (the waves are independent: no barrier)
+    const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
-    const int lane = threadIdx.x;
+    const int lane = threadIdx.x & 63;
     const int nchunk = n / 8;
     const float * xr = x + (int64_t) row * n;
     const float * rr = r ? r + (int64_t) row * n : nullptr;
@@ -174,15 +175,18 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
     GSVK_REQUIRE(al16(x) && al16(r) && al16(bias) && al16(wb), "layernorm: operands must be 16-byte aligned");
     if (rows == 0) return GSVK_OK;
-    const dim3 grid((unsigned) rows);
+    // 4 rows (waves) per workgroup from 64 rows on: 16384 one-wave workgroups (a 16 x 1024
+    // prefill) launch slower than the rows take
+    const int rpw = rows >= 64 ? 4 : 1;
+    const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block(64 * rpw);
     if (n <= 512)
-        hipLaunchKernelGGL(k_layernorm<1>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+        hipLaunchKernelGGL(k_layernorm<1>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
                            (int) n, eps, y, yq, yd, layout);
     else if (n <= 1024)
-        hipLaunchKernelGGL(k_layernorm<2>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+        hipLaunchKernelGGL(k_layernorm<2>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
                            (int) n, eps, y, yq, yd, layout);
     else
-        hipLaunchKernelGGL(k_layernorm<8>, grid, dim3(64), 0, stream, x, r, bias, wb, (int) rows,
+        hipLaunchKernelGGL(k_layernorm<8>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
                            (int) n, eps, y, yq, yd, layout);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;

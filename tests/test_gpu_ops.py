@@ -236,14 +236,16 @@ def test_fdot_head_bitexact(gpu, wtype, mode):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max {np.abs(got - ref).max():.3e}"
 
 
-def test_fdot_bert_projection_bitexact(gpu):
-    """K = 1025 (bert_aug = [W | b]): ggml_vec_dot_f32 with a fused leftover."""
+@pytest.mark.parametrize("m", [9, 70, 333])
+def test_fdot_bert_projection_bitexact(gpu, m):
+    """K = 1025 (bert_aug = [W | b]): ggml_vec_dot_f32 with a fused leftover; from 64 rows the
+    kernel that keeps 4 weight rows x 16 activation rows per thread, the same chains."""
     import torch
-    rng = np.random.default_rng(20)
+    rng = np.random.default_rng(20 + m)
     W = rng.standard_normal((512, 1025)).astype(np.float32) * 0.02
-    X = rng.uniform(-1, 1, (9, 1025)).astype(np.float32)
+    X = rng.uniform(-1, 1, (m, 1025)).astype(np.float32)
     X[:, 1024] = 1.0
-    y = torch.zeros((9, 512), dtype=torch.float32, device="cuda")
+    y = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
     gpu.op_fdot(_dev(W, torch), 0, _dev(X, torch), y, 0)
     torch.cuda.synchronize()
     ref = O.f32_matmul(W, X, 0)
