@@ -85,9 +85,11 @@ constexpr int64_t GEMM_MIN_ROWS = 64;
 
 // Batch from which the decode step runs its projections on launch_q8_gemm (with the LayerNorms
 // and the embedding as launches of their own) rather than on the fused GEMVs, whose weight
-// re-reads grow with the batch.
+// re-reads grow with the batch. The GEMVs are faster up to batch 64 but run only up to batch 16,
+// where they are tested: one batch-32 run of the GEMV path ended in a GPU memory fault whose
+// cause has not been found.
 #ifndef GSVK_DECODE_GEMM_MIN_BATCH
-#define GSVK_DECODE_GEMM_MIN_BATCH 64
+#define GSVK_DECODE_GEMM_MIN_BATCH 17
 #endif
 constexpr int DECODE_GEMM_MIN_BATCH = GSVK_DECODE_GEMM_MIN_BATCH;
 

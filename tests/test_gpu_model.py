@@ -174,13 +174,15 @@ def test_teacher_forced_greedy_tokens(gpu, model4_path):
         o.close()
 
 
-def test_decode_batch64_on_matrix_cores(gpu, model4_path):
-    """From batch 64 the decode step runs its projections as MFMA GEMMs (LayerNorms and the
-    embedding as launches of their own, natural-order Q8_0 operands): fp32 accumulation per block
-    instead of the x86 8-lane order, so the oracle's tokens are matched except at near-ties of
-    the penalised logits (teacher forcing keeps the histories equal)."""
+@pytest.mark.parametrize("B", [20, 64])
+def test_decode_batch64_on_matrix_cores(gpu, model4_path, B):
+    """From batch 17 the decode step runs its projections as MFMA GEMMs (LayerNorms and the
+    embedding as launches of their own, Q8_0 operands in the matrix-core order, a partial last
+    tile of 32 rows at batch 20): fp32 accumulation per block instead of the x86 8-lane order, so
+    the oracle's tokens are matched except at near-ties of the penalised logits (teacher forcing
+    keeps the histories equal)."""
     rng = np.random.default_rng(24)
-    lens = rng.integers(3, 21, 64)
+    lens = rng.integers(3, 21, B)
     reqs = _reqs(25, lens, P=8)
     steps = 8
     forced = rng.integers(0, 1024, steps).astype(np.int32)
