@@ -253,7 +253,7 @@ int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, 
     GSVK_REQUIRE(blocks && qs && d && rows >= 0 && k > 0 && k % QK == 0 && k <= (1 << 20),
                  "q8_repack: bad arguments (k must be a multiple of 32)");
     GSVK_REQUIRE((qt == nullptr) == (dt == nullptr) && (!qt || rows % 32 == 0),
-                 "q8_repack: the tiled copy needs quants and scales, and rows % 32 == 0");
+                 "q8_repack: the tiled copy needs quants and scales, and rows %% 32 == 0");
     const int nblk = (int) (k / QK);
     const int64_t total = rows * nblk * 8;
     if (total == 0) return GSVK_OK;

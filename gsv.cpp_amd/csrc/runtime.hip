@@ -346,14 +346,14 @@ int alloc_kv(gsvk_model * m, int B, int lmax) {
     return GSVK_OK;
 }
 
-int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
+int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out, hipStream_t st) {
     if (m->head_type == GGML_Q8_0) {
         GemvEpilogue epi{};
         return launch_q8_gemv(m->head_q8.qs, m->head_q8.d, m->V, m->D, x.q, x.d, B, epi, out,
-                              m->stream);
+                              st);
     }
     return launch_fdot(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, m->D, x.x, m->D, B, out,
-                       m->V, mode, m->stream);
+                       m->V, mode, st);
 }
 
 // The projections of one layer after attention (shared by prefill and decode), with the
@@ -365,7 +365,7 @@ int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out) {
 // LN2 (cur' = LN2(n1 + h2 + b2)) is the input stage of the next layer's QKV or of final_ln().
 Q8Weights q8w(const Lin & l) { return Q8Weights{l.qn, l.d, l.qt, l.dt}; }
 
-int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
+int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
                float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr,
                int layout = Q8_NATURAL) {
     const int D = m->D, F = m->FFN;
@@ -377,20 +377,20 @@ int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x,
         oo.y = o;
         oo.y_stride = D;
         oo.n_store = D;
-        GSVK_TRY(launch_q8_gemm(q8w(w.out), D, D, R, attn.q, attn.d, layout, oo, m->stream));
-        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, m->stream, layout));
+        GSVK_TRY(launch_q8_gemm(q8w(w.out), D, D, R, attn.q, attn.d, layout, oo, st));
+        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout));
         LayerOut ho{};
         ho.bias = w.f1.b;
         ho.act = 1;
         ho.yq = hq.q;
         ho.yd = hq.d;
         ho.yq_layout = layout;
-        GSVK_TRY(launch_q8_gemm(q8w(w.f1), F, D, R, n1->q, n1->d, layout, ho, m->stream));
+        GSVK_TRY(launch_q8_gemm(q8w(w.f1), F, D, R, n1->q, n1->d, layout, ho, st));
         LayerOut h2o{};
         h2o.y = h2;
         h2o.y_stride = D;
         h2o.n_store = D;
-        return launch_q8_gemm(q8w(w.f2), D, F, R, hq.q, hq.d, layout, h2o, m->stream);
+        return launch_q8_gemm(q8w(w.f2), D, F, R, hq.q, hq.d, layout, h2o, st);
     }
     LayerIn qin{};
     qin.mode = IN_Q8;
@@ -400,7 +400,7 @@ int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x,
     oo.y = o;
     oo.y_stride = D;
     oo.n_store = D;
-    GSVK_TRY(launch_layer_gemv(w.out.qs, w.out.d, D, D, R, qin, oo, m->stream));
+    GSVK_TRY(launch_layer_gemv(w.out.qs, w.out.d, D, D, R, qin, oo, st));
     LayerIn lin{};
     lin.mode = IN_LN;
     lin.res = cur_x;
@@ -413,7 +413,7 @@ int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x,
     ho.act = 1;
     ho.yq = hq.q;
     ho.yd = hq.d;
-    GSVK_TRY(launch_layer_gemv(w.f1.qs, w.f1.d, F, D, R, lin, ho, m->stream));
+    GSVK_TRY(launch_layer_gemv(w.f1.qs, w.f1.d, F, D, R, lin, ho, st));
     LayerIn hin{};
     hin.mode = IN_Q8;
     hin.xs = hq.q;
@@ -422,7 +422,7 @@ int layer_tail(gsvk_model * m, const LayerW & w, int64_t R, const float * cur_x,
     h2o.y = h2;
     h2o.y_stride = D;
     h2o.n_store = D;
-    GSVK_TRY(launch_layer_gemv(w.f2.qs, w.f2.d, D, F, R, hin, h2o, m->stream));
+    GSVK_TRY(launch_layer_gemv(w.f2.qs, w.f2.d, D, F, R, hin, h2o, st));
     return GSVK_OK;
 }
 
@@ -447,69 +447,90 @@ LayerOut qkv_out(gsvk_model * m, const LayerW & w, size_t loff, float * y, int n
 }
 
 // LN2 of the last layer: x = LN2(n1 + h2 + b2), quantised too when the head is Q8_0.
-int final_ln(gsvk_model * m, int64_t R, const float * n1x, const float * h2, Act & x) {
+int final_ln(gsvk_model * m, hipStream_t st, int64_t R, const float * n1x, const float * h2, Act & x) {
     const LayerW & w = m->L[m->NL - 1];
     const bool q = m->head_type == GGML_Q8_0;
     return launch_layernorm(n1x, h2, w.f2.b, w.ln2, R, m->D, 1e-5f, x.x, q ? x.q : nullptr,
-                            q ? x.d : nullptr, m->stream);
+                            q ? x.d : nullptr, st);
 }
 
 // Kernels of one decode step at loop index idx = *d_step - 1: the layer-0 QKV embeds last_tok at
 // PE position prompt_len + idx (and sets kv_end = S + idx + 1); every QKV appends K/V at column
 // S + idx; logits of the head.
-int enqueue_decode_body(gsvk_model * m) {
+//
+// Matrix-core path (batch >= DECODE_GEMM_MIN_BATCH): the whole batch on the model's stream.
+int enqueue_decode_mfma(gsvk_model * m) {
     const int B = m->B, D = m->D;
     const float scale = 1.0f / std::sqrt((float) m->HD);
-    const bool mfma = B >= DECODE_GEMM_MIN_BATCH;
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
-        if (mfma) {
-            // large batch: embedding / LN2 of the previous layer as their own launches, the QKV
-            // GEMM with the K/V append, attention, then the GEMM tail; every Q8_0 activation in
-            // the matrix-core operand order (rows padded to 32)
-            if (li == 0) {
-                GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
-                                         m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q,
-                                         m->x.d, m->kv_end, m->S, m->row_start, PE_MAX, m->stream, Q8_TILED));
-            } else {
-                const LayerW & p = m->L[li - 1];
-                GSVK_TRY(launch_layernorm(m->n1.x, m->h2, p.f2.b, p.ln2, B, D, 1e-5f, m->x.x, m->x.q,
-                                          m->x.d, m->stream, Q8_TILED));
-            }
-            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, B, m->x.q, m->x.d, Q8_TILED,
-                                    qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
-            GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
-                                        m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
-                                        m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream,
-                                        Q8_TILED));
-            GSVK_TRY(layer_tail(m, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2, &m->n1, Q8_TILED));
-            continue;
+        // large batch: embedding / LN2 of the previous layer as their own launches, the QKV
+        // GEMM with the K/V append, attention, then the GEMM tail; every Q8_0 activation in
+        // the matrix-core operand order (rows padded to 32)
+        if (li == 0) {
+            GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step,
+                                     m->prompt_len - 1, m->audio_alpha, D, B, m->x.x, m->x.q,
+                                     m->x.d, m->kv_end, m->S, m->row_start, PE_MAX, m->stream, Q8_TILED));
+        } else {
+            const LayerW & p = m->L[li - 1];
+            GSVK_TRY(launch_layernorm(m->n1.x, m->h2, p.f2.b, p.ln2, B, D, 1e-5f, m->x.x, m->x.q,
+                                      m->x.d, m->stream, Q8_TILED));
         }
+        GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, B, m->x.q, m->x.d, Q8_TILED,
+                                qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
+        GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
+                                    m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
+                                    m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream,
+                                    Q8_TILED));
+        GSVK_TRY(layer_tail(m, m->stream, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2, &m->n1, Q8_TILED));
+    }
+    GSVK_TRY(final_ln(m, m->stream, B, m->n1.x, m->h2, m->x));
+    return head_logits(m, m->x, B, 0, m->logits, m->stream);
+}
+
+// GEMV path, batch rows [r0, r0 + n) on stream st. Every kernel of it computes each row on its
+// own: the per-row arithmetic does not depend on which or how many rows a launch holds. (Cutting
+// a batch-16 step in row groups on 2 or 4 streams, forked and joined inside the captured graph,
+// was measured slower, 0.57 -> 0.78 / 1.41 ms per step: the graph ran every branch on one
+// hardware queue, one after the other.)
+int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
+    const int B = m->B, D = m->D, F = m->FFN;
+    const float scale = 1.0f / std::sqrt((float) m->HD);
+    const size_t row_kv = (size_t) m->NH * m->lstride * m->HD;
+    auto rows_of = [r0](const Act & a, int k) {
+        return Act{a.x ? a.x + (size_t) r0 * k : nullptr, a.q ? a.q + (size_t) r0 * k : nullptr,
+                   a.d ? a.d + (size_t) r0 * (k / 32) : nullptr};
+    };
+    Act x = rows_of(m->x, D), attn = rows_of(m->attn, D), n1 = rows_of(m->n1, D), hq = rows_of(m->hq, F);
+    float * o = m->o + (size_t) r0 * D, * h2 = m->h2 + (size_t) r0 * D, * qkv = m->qkv + (size_t) r0 * D;
+    for (int li = 0; li < m->NL; li++) {
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * B * row_kv + (size_t) r0 * row_kv;
         LayerIn in{};
         if (li == 0) {
             in.mode = IN_EMB;
             in.emb = m->audio_emb;
             in.pe = m->pe;
-            in.tok = m->last_tok;
+            in.tok = m->last_tok + r0;
             in.pos_ptr = m->d_step;
             in.pos_add = m->prompt_len - 1;
             in.alpha = m->audio_alpha;
             in.vocab = m->V;
-            in.kv_end = m->kv_end;
+            in.kv_end = m->kv_end + r0;
             in.kv_end_add = m->S;
-            in.pos_sub = m->row_start;
+            in.pos_sub = m->row_start ? m->row_start + r0 : nullptr;
             in.pe_rows = PE_MAX;
         } else {
             const LayerW & p = m->L[li - 1];
             in.mode = IN_LN;
-            in.res = m->n1.x;
-            in.r = m->h2;
+            in.res = n1.x;
+            in.r = h2;
             in.bias = p.f2.b;
             in.wb = p.ln2;
         }
-        in.out_x = m->x.x;
-        if (qkv_attn_preferred(B, m->NH, m->lstride)) {
+        in.out_x = x.x;
+        if (qkv_attn_preferred(n, m->NH, m->lstride)) {
             // QKV + attention in one launch per layer
             QkvAttnArgs qa{};
             qa.ws = w.qkv.qs;
@@ -519,26 +540,31 @@ int enqueue_decode_body(gsvk_model * m) {
             qa.kc = m->kc + loff;
             qa.vc = m->vc + loff;
             qa.lstride = m->lstride;
-            qa.kv_begin = m->kv_begin;
+            qa.kv_begin = m->kv_begin + r0;
             qa.col_ptr = m->d_step;
             qa.col_add = m->S - 1;
             qa.n_head = m->NH;
             qa.scale_log2 = scale * 1.4426950408889634f;
-            qa.out = m->attn.x;
-            qa.oq = m->attn.q;
-            qa.od = m->attn.d;
-            GSVK_TRY(launch_qkv_attn(qa, B, m->lstride, m->stream));
+            qa.out = attn.x;
+            qa.oq = attn.q;
+            qa.od = attn.d;
+            GSVK_TRY(launch_qkv_attn(qa, n, m->lstride, st));
         } else {
-            GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, B, in,
-                                       qkv_out(m, w, loff, m->qkv, D, 1, m->d_step, m->S - 1), m->stream));
-            GSVK_TRY(launch_attn_decode(m->qkv, D, m->kc + loff, m->vc + loff, B, m->NH, m->HD,
-                                        m->lstride, m->kv_begin, m->kv_end, m->lstride, scale,
-                                        m->attn.x, nullptr, m->attn.q, m->attn.d, m->attn_ws, m->stream));
+            GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, n, in,
+                                       qkv_out(m, w, loff, qkv, D, 1, m->d_step, m->S - 1), st));
+            GSVK_TRY(launch_attn_decode(qkv, D, m->kc + loff, m->vc + loff, n, m->NH, m->HD,
+                                        m->lstride, m->kv_begin + r0, m->kv_end + r0, m->lstride, scale,
+                                        attn.x, nullptr, attn.q, attn.d, m->attn_ws, st));
         }
-        GSVK_TRY(layer_tail(m, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2));
+        GSVK_TRY(layer_tail(m, st, w, n, x.x, attn, o, n1.x, hq, h2));
     }
-    GSVK_TRY(final_ln(m, B, m->n1.x, m->h2, m->x));
-    return head_logits(m, m->x, B, 0, m->logits);
+    GSVK_TRY(final_ln(m, st, n, n1.x, h2, x));
+    return head_logits(m, x, n, 0, m->logits + (size_t) r0 * m->V, st);
+}
+
+int enqueue_decode_body(gsvk_model * m) {
+    if (m->B >= DECODE_GEMM_MIN_BATCH) return enqueue_decode_mfma(m);
+    return enqueue_decode_rows(m, 0, m->B, m->stream);
 }
 
 }  // namespace
@@ -732,9 +758,9 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
-        GSVK_TRY(layer_tail(m, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr));
+        GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr));
     }
-    GSVK_TRY(final_ln(m, rows, n1.x, h2, cur));
+    GSVK_TRY(final_ln(m, st, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
     Act lastq;
     lastq.x = last;
@@ -744,7 +770,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         GSVK_TRY(launch_q8_quantize(last, B, D, lastq.q, lastq.d, st));
     }
     // llamafile's tinyBLAS handles the head when the prefill has >= 2 columns
-    GSVK_TRY(head_logits(m, lastq, B, S >= 2 ? 1 : 0, lg));
+    GSVK_TRY(head_logits(m, lastq, B, S >= 2 ? 1 : 0, lg, st));
     GSVK_HIP(hipMemcpyAsync(m->logits + (slot_mode ? (size_t) kv_slot * m->V : 0), lg, (size_t) B * m->V * 4,
                             hipMemcpyDeviceToDevice, st));
     if (!slot_mode) GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));

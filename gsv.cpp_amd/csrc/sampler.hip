@@ -26,7 +26,8 @@ namespace gsvk {
 
 constexpr int SMP_THREADS = 256;
 constexpr int SMP_SORT = 2048;   // >= V
-constexpr int SMP_CH = 32;       // >= ceil(V / 64)
+constexpr int SMP_CH = 32;       // >= ceil(V / 64): the generic instantiation
+constexpr int SMP_CH17 = 17;     // ceil(V / 64) for vocabularies of up to 1088 (1025 here)
 
 // Largest of a uint32 over the 64 lanes (DPP rotations within rows, then the row results).
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
@@ -40,12 +41,16 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
 }
 
 // The k-th largest (1 <= k <= 64, counted with multiplicity) of one uint32 per lane: the largest
-// v with #{lanes u : u >= v} >= k.
+// T with #{lanes : v >= T} >= k, built bit by bit from the top (the count only falls as T grows,
+// and the largest such T is a lane's value). One compare and one ballot per bit.
 __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t v, int k) {
-    int ge = 0;
+    uint32_t prefix = 0u;
 #pragma unroll
-    for (int j = 0; j < 64; j++) ge += (uint32_t) __builtin_amdgcn_readlane((int) v, j) >= v;
-    return wave_max_u32(ge >= k ? v : 0u);
+    for (int bit = 31; bit >= 0; bit--) {
+        const uint32_t trial = prefix | (1u << bit);
+        if ((int) __popcll(__ballot(v >= trial)) >= k) prefix = trial;
+    }
+    return prefix;
 }
 
 // Sum of an int over the 64 lanes, returned to every lane: rotations within each row of 16
@@ -99,6 +104,7 @@ __device__ void bitonic_sort_desc(float * v, int * idx) {
     __syncthreads();
 }
 
+template <int CH>
 __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -106,9 +112,10 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
 
     __shared__ float lg[SMP_SORT];
     __shared__ int cnt[SMP_SORT];
-    __shared__ __align__(16) float sv[SMP_SORT];
-    __shared__ int si[SMP_SORT];
-    __shared__ float su[SMP_SORT];
+    // (64 spare slots past SMP_SORT: a lane's branch-free stores of non-survivors)
+    __shared__ __align__(16) float sv[SMP_SORT + 64];
+    __shared__ int si[SMP_SORT + 64];
+    __shared__ float su[SMP_SORT + 64];
     __shared__ float s_scalar[2];
     __shared__ float s_bestv[1];
     __shared__ int s_besti[1];
@@ -198,10 +205,10 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
             const int chunk = a.chunk;
             const int lane = tid;
             const int base = lane * chunk;
-            float pv[SMP_CH];
-            uint32_t key[SMP_CH];
+            float pv[CH];
+            uint32_t key[CH];
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++) {
+            for (int c = 0; c < CH; c++) {
                 const bool ok = c < chunk && base + c < V;
                 pv[c] = ok ? lg[base + c] : -INFINITY;
                 key[c] = ok ? order_key(pv[c]) : 0u;   // below every value, -inf included
@@ -220,12 +227,12 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                     // fits in one wave, its k-th largest (one sort) is the pivot.
                     uint32_t lmax = 0u;
 #pragma unroll
-                    for (int c = 0; c < SMP_CH; c++) lmax = key[c] > lmax ? key[c] : lmax;
+                    for (int c = 0; c < CH; c++) lmax = key[c] > lmax ? key[c] : lmax;
                     const uint32_t T = wave_kth_largest(lmax, k);
                     int cmine = 0, cbelow = 0, ctotal = 0;
-                    int cpos[SMP_CH];
+                    int cpos[CH];
 #pragma unroll
-                    for (int c = 0; c < SMP_CH; c++) {
+                    for (int c = 0; c < CH; c++) {
                         const bool in = key[c] >= T && key[c] != 0u;
                         const uint64_t m = __ballot(in);
                         cbelow += __popcll(m & ((1ull << lane) - 1ull));
@@ -238,7 +245,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                         cand[lane] = 0u;
                         __builtin_amdgcn_wave_barrier();
 #pragma unroll
-                        for (int c = 0; c < SMP_CH; c++)
+                        for (int c = 0; c < CH; c++)
                             if (cpos[c] >= 0) cand[cbelow + cpos[c]] = key[c];
                         __builtin_amdgcn_wave_barrier();
                         prefix = wave_kth_largest(cand[lane], k);
@@ -251,14 +258,14 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                     const uint32_t want = prefix | (1u << bit);
                     int c1 = 0;
 #pragma unroll
-                    for (int c = 0; c < SMP_CH; c++) c1 += (key[c] & sel) == want;
+                    for (int c = 0; c < CH; c++) c1 += (key[c] & sel) == want;
                     c1 = wave_sum_i32(c1);
                     if (c1 >= rem) prefix = want;
                     else rem -= c1;
                 }
                 const float pivot = key_value(prefix);
 #pragma unroll
-                for (int c = 0; c < SMP_CH; c++)
+                for (int c = 0; c < CH; c++)
                     if (pv[c] < pivot) pv[c] = -INFINITY;
             }
             // 5) softmax over the survivors. They are compacted into LDS in index order (position
@@ -267,13 +274,13 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
             // (adding +0 leaves an fp32 sum unchanged).
             float mx = -INFINITY;
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++) mx = fmaxf(mx, pv[c]);
+            for (int c = 0; c < CH; c++) mx = fmaxf(mx, pv[c]);
             mx = warp_max(mx);
             const uint64_t lt_mask = (1ull << lane) - 1ull;
             int below = 0, total = 0, mine = 0;
-            int pos[SMP_CH];
+            int pos[CH];
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++) {
+            for (int c = 0; c < CH; c++) {
                 const bool sv_c = pv[c] != -INFINITY;
                 const uint64_t m = __ballot(sv_c);
                 below += __popcll(m & lt_mask);
@@ -281,13 +288,16 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                 pos[c] = sv_c ? mine : -1;
                 mine += sv_c;
             }
+            // every slot is stored, a non-survivor to a spare slot of its own lane (past the
+            // SMP_SORT >= V possible survivors), so that the stores need no branch
+            const int spare = SMP_SORT + lane;
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++)
-                if (pos[c] >= 0) {
-                    pos[c] += below;
-                    sv[pos[c]] = pv[c];
-                    si[pos[c]] = base + c;
-                }
+            for (int c = 0; c < CH; c++) {
+                if (pos[c] >= 0) pos[c] += below;
+                const int slot = pos[c] >= 0 ? pos[c] : spare;
+                sv[slot] = pv[c];
+                si[slot] = base + c;
+            }
             __builtin_amdgcn_wave_barrier();
             for (int jx = lane; jx < total; jx += 64) sv[jx] = (float) exp((double) (sv[jx] - mx));
             __builtin_amdgcn_wave_barrier();
@@ -309,14 +319,15 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
             for (int jx = lane; jx < total; jx += 64) sv[jx] = sv[jx] * inv;
             // 6) sample: argmax over p > 0 of p / q, q_i = -log(1 - U_i), U_i the draw of index i.
             // Each lane walks its chunk of the stream and keeps the draws of its survivors.
+            // U = (x >> 40) / 2^24 of x = state * 0x2545F4914F6CDD1D: a 24-bit integer times a
+            // power of two, exact in fp32. Computed for every slot (no branch), stored for the
+            // survivors, the others to the lane's spare slot.
             uint64_t st = st0;
 #pragma unroll
-            for (int c = 0; c < SMP_CH; c++) {
+            for (int c = 0; c < CH; c++) {
                 if (c < chunk && base + c < V) {
-                    if (pos[c] >= 0) {
-                        const uint64_t x = st * 0x2545F4914F6CDD1Dull;
-                        su[pos[c]] = (float) ((double) (x >> 40) * (1.0 / 16777216.0));
-                    }
+                    const uint64_t x = st * 0x2545F4914F6CDD1Dull;
+                    su[pos[c] >= 0 ? pos[c] : spare] = (float) (uint32_t) (x >> 40) * 0x1p-24f;
                     st = xs_step(st);
                 }
             }
@@ -326,7 +337,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
                                                      : (b == 0 ? a.probs_dump + (int64_t) idx * V : nullptr);
             if (dump) {
 #pragma unroll
-                for (int c = 0; c < SMP_CH; c++)
+                for (int c = 0; c < CH; c++)
                     if (c < chunk && base + c < V) dump[base + c] = pos[c] >= 0 ? sv[pos[c]] : 0.0f;
             }
             float best = -INFINITY;
@@ -371,48 +382,55 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
         }
     }
     if (!a.step) return;   // single sampling call: no loop state
-    // the last workgroup applies the early-stop rule and advances the loop index
+    // the last workgroup to finish applies the batch-wide early-stop rule, counts the rows that
+    // take part in the next step and advances the loop index; its threads take the rows in turn
+    __shared__ int s_last, s_unfinished;
     __syncthreads();
     if (tid == 0) {
         __threadfence();
         const int prev = __hip_atomic_fetch_add(a.done_counter, 1, __ATOMIC_ACQ_REL,
                                                 __HIP_MEMORY_SCOPE_AGENT);
-        if (prev == a.B - 1) {
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-            if (gidx < a.max_steps) {
-                if (a.early_stop != -1 && !(a.flags & 2u)) {
-                    const int n0 = __hip_atomic_load(a.ny, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    if (n0 - a.P > a.early_stop) {
-                        for (int bb = 0; bb < a.B; bb++) {
-                            if (__hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT) < 0) {
-                                a.fin_step[bb] = gidx - (a.row_start ? a.row_start[bb] : 0);
-                                a.fin_kind[bb] = 1;
-                            }
-                        }
-                    }
-                }
-                // unfinished rows; with per-row limits, those that take part in the next step
-                int unfinished = 0;
-                for (int bb = 0; bb < a.B; bb++) {
-                    const bool open = __hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED,
-                                                        __HIP_MEMORY_SCOPE_AGENT) < 0;
-                    unfinished += a.row_max ? (open && gidx + 1 - (a.row_start ? a.row_start[bb] : 0) < a.row_max[bb])
-                                            : open;
-                }
-                *a.n_unfinished = unfinished;
-                *a.step = gidx + 1;
+        s_last = prev == a.B - 1;
+        s_unfinished = 0;
+    }
+    __syncthreads();
+    if (!s_last) return;   // uniform over the workgroup
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    if (gidx < a.max_steps) {
+        const bool stop_all = a.early_stop != -1 && !(a.flags & 2u) &&
+                              __hip_atomic_load(a.ny, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) - a.P >
+                                  a.early_stop;
+        int unfinished = 0;
+        for (int bb = tid; bb < a.B; bb += SMP_THREADS) {
+            bool open = __hip_atomic_load(a.fin_step + bb, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < 0;
+            const int rs = a.row_start ? a.row_start[bb] : 0;
+            if (open && stop_all) {   // every row still open stops at this step
+                a.fin_step[bb] = gidx - rs;
+                a.fin_kind[bb] = 1;
+                open = false;
             }
-            __hip_atomic_store(a.done_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            // with per-row limits, only the rows that take part in the next step
+            unfinished += a.row_max ? (open && gidx + 1 - rs < a.row_max[bb]) : open;
+        }
+        if (unfinished) atomicAdd(&s_unfinished, unfinished);
+        __syncthreads();
+        if (tid == 0) {
+            *a.n_unfinished = s_unfinished;
+            *a.step = gidx + 1;
         }
     }
+    if (tid == 0) __hip_atomic_store(a.done_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int launch_sample(const SampleArgs & a, hipStream_t stream) {
     GSVK_REQUIRE(a.V > 0 && a.V <= SMP_SORT && a.B > 0 && a.chunk * 64 >= a.V && a.chunk <= SMP_CH,
                  "sample: vocabulary %d exceeds %d", a.V, SMP_SORT);
     GSVK_REQUIRE(a.top_k < 0 || a.top_k <= SMP_SORT, "sample: bad top_k");
-    hipLaunchKernelGGL(k_sample, dim3((unsigned) a.B), dim3(SMP_THREADS), 0, stream, a);
+    // the per-lane loops run over CH slots: 17 covers the vocabulary of the t2s model exactly
+    if (a.chunk <= SMP_CH17)
+        hipLaunchKernelGGL(k_sample<SMP_CH17>, dim3((unsigned) a.B), dim3(SMP_THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k_sample<SMP_CH>, dim3((unsigned) a.B), dim3(SMP_THREADS), 0, stream, a);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
