@@ -105,6 +105,11 @@ bool GgufFile::open(const std::string & path, std::string & err, bool * io_error
             const uint32_t v = r.u32();
             u32_[key] = v;
             if (key == "general.alignment") alignment = v;
+        } else if (t == T_F32) {
+            const uint32_t v = r.u32();
+            float f;
+            memcpy(&f, &v, 4);
+            f32_[key] = f;
         } else {
             r.skip_value(t);
         }
@@ -150,6 +155,13 @@ bool GgufFile::get_u32(const std::string & key, uint32_t & out) const {
     auto it = u32_.find(key);
     if (it == u32_.end()) return false;
     out = (uint32_t) it->second;
+    return true;
+}
+
+bool GgufFile::get_f32(const std::string & key, float & out) const {
+    auto it = f32_.find(key);
+    if (it == f32_.end()) return false;
+    out = it->second;
     return true;
 }
 

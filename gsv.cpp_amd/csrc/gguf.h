@@ -1,5 +1,5 @@
 // Minimal GGUF (v2/v3) reader: header, key/values and tensor directory, data read on demand.
-// Only what the AR loader needs (u32/i32/f32/string keys; F32, F16 and Q8_0 tensors).
+// Only what the AR and BERT loaders need (u32/i32/f32 keys; F32, F16 and Q8_0 tensors).
 #pragma once
 
 #include <cstdint>
@@ -33,6 +33,7 @@ public:
     bool open(const std::string & path, std::string & err, bool * io_error = nullptr);
     const GgufTensor * tensor(const std::string & name) const;
     bool get_u32(const std::string & key, uint32_t & out) const;
+    bool get_f32(const std::string & key, float & out) const;
     bool read(const GgufTensor & t, void * dst) const;
     const std::vector<GgufTensor> & tensors() const { return tensors_; }
 
@@ -40,6 +41,7 @@ private:
     FILE * f_ = nullptr;
     uint64_t size_ = 0;
     std::map<std::string, uint64_t> u32_;
+    std::map<std::string, float> f32_;
     std::vector<GgufTensor> tensors_;
     std::map<std::string, size_t> index_;
 };

@@ -28,6 +28,7 @@ EXPORTS = [
     "gsvk_sample_workspace_bytes", "gsvk_op_sample", "gsvk_op_qkv_attn",
     "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
+    "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
 ]
 
 
@@ -63,6 +64,11 @@ class ModelInfo(C.Structure):
                 ("kv_lmax", C.c_int)]
 
 
+class BertInfo(C.Structure):
+    _fields_ = [("hidden", C.c_int), ("heads", C.c_int), ("inter", C.c_int), ("layers_used", C.c_int),
+                ("vocab", C.c_int), ("max_pos", C.c_int), ("ln_eps", C.c_float), ("weight_type", C.c_int)]
+
+
 _lib = None
 
 
@@ -78,6 +84,11 @@ def lib():
         L.gsvk_device_count.argtypes = [C.POINTER(C.c_int)]
         L.gsvk_parse_device.argtypes = [C.c_char_p, C.POINTER(C.c_int)]
         L.gsvk_model_load.argtypes = [C.c_char_p, i32, i32, C.POINTER(vp)]
+        L.gsvk_bert_load.argtypes = [C.c_char_p, i32, i32, C.POINTER(vp)]
+        L.gsvk_bert_free.argtypes = [vp]
+        L.gsvk_bert_free.restype = None
+        L.gsvk_bert_get_info.argtypes = [vp, C.POINTER(BertInfo)]
+        L.gsvk_bert_encode.argtypes = [vp, i32, vp, vp, i32, i32, vp]
         L.gsvk_model_free.argtypes = [vp]
         L.gsvk_model_free.restype = None
         L.gsvk_model_get_info.argtypes = [vp, C.POINTER(ModelInfo)]
@@ -391,4 +402,45 @@ class Model:
             res["sampled"] = s[:n]
         if want_probs0:
             res["probs0"] = probs0[:n]
+        return res
+
+
+class Bert:
+    """A loaded BERT text encoder on one HIP device (mirror of the reference's gsv_bert)."""
+
+    def __init__(self, path: str, device: int = 0, verbose: bool = False):
+        h = C.c_void_p()
+        check(lib().gsvk_bert_load(path.encode(), device, int(verbose), C.byref(h)), "bert_load")
+        self.h = h
+        info = BertInfo()
+        check(lib().gsvk_bert_get_info(self.h, C.byref(info)), "bert_get_info")
+        self.info = {k: getattr(info, k) for k, _ in BertInfo._fields_}
+
+    def close(self):
+        if self.h:
+            lib().gsvk_bert_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def encode(self, seqs, n_layers: int = -1, tmax: int = 0):
+        """[hidden][T] float32 per sequence (token ids with [CLS]/[SEP]); all sequences in one
+        call, each attending only to its own tokens."""
+        lens = np.array([len(q) for q in seqs], np.int32)
+        T = int(max(tmax, lens.max()))
+        ids = np.zeros((len(seqs), T), np.int32)
+        for b, q in enumerate(seqs):
+            ids[b, :len(q)] = q
+        D = self.info["hidden"]
+        out = np.zeros(D * int(lens.sum()), np.float32)
+        check(lib().gsvk_bert_encode(self.h, len(seqs), ids.ctypes.data, lens.ctypes.data, T, n_layers,
+                                     out.ctypes.data), "bert_encode")
+        res, off = [], 0
+        for n in lens:
+            res.append(out[off * D:(off + n) * D].reshape(D, n))
+            off += int(n)
         return res

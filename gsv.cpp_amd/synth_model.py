@@ -181,3 +181,67 @@ def synth_requests(seed: int, B: int, prompt_len: int, phone_lens, bert: bool = 
         be = rng.uniform(-1.0, 1.0, size=(bert_dim, T)).astype(np.float32) if bert else None
         reqs.append({"phones": ph, "bert": be, "prompt": prompt.copy()})
     return reqs
+
+
+def write_bert_model(path: str, seed: int = 0x6A5E0010, n_layer: int = 4, layers_used: int = 2,
+                     hidden: int = 1024, heads: int = 16, inter: int = 4096, vocab: int = 1000,
+                     max_pos: int = 512, wtype: str = "f32", ln_eps: float = 1e-12):
+    """A synthetic BERT GGUF with the tensor contract of src/gsv_bert.cpp:398-431 (keys bert.*,
+    tensors bert.word_emb .. bert.l{i}.out_ln_b; projection weights in `wtype`, the rest F32, as
+    tools/export_gguf/convert_bert.py writes them). Returns (path, weights): the fp32 values the
+    loader holds (F16 rounded, Q8_0 dequantised), for the oracle."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    D, F = hidden, inter
+
+    def normal(shape, std):
+        return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
+
+    f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32).tobytes()
+    w = _Writer()
+    w.add_str("general.architecture", "gsv.bert")
+    w.add_str("general.name", "gsv-bert-synthetic")
+    w.add_u32("bert.n_layer", n_layer)
+    w.add_u32("bert.hidden", D)
+    w.add_u32("bert.head", heads)
+    w.add_u32("bert.inter", F)
+    w.add_f32("bert.ln_eps", ln_eps)
+    w.add_u32("bert.vocab", vocab)
+    w.add_u32("bert.max_pos", max_pos)
+    w.add_u32("bert.layers_used", layers_used)
+    w.add_u32("general.alignment", ALIGN)
+    W = {}
+
+    def add(name, a, proj=False):
+        if proj and wtype == "f16":
+            h = a.astype(np.float16)
+            w.add_tensor(name, a.shape, GGML_F16, h.tobytes())
+            W[name] = h.astype(np.float32)
+        elif proj and wtype == "q8_0":
+            blocks = q8_quantize_ref(a)
+            w.add_tensor(name, a.shape, GGML_Q8_0, blocks.tobytes())
+            W[name] = q8_dequant(blocks, a.shape[-1]).reshape(a.shape)
+        else:
+            w.add_tensor(name, a.shape, GGML_F32, f32(a))
+            W[name] = a.astype(np.float32)
+
+    add("bert.word_emb", normal((vocab, D), 0.05))
+    add("bert.pos_emb", normal((max_pos, D), 0.05))
+    add("bert.type_emb", normal((2, D), 0.05))
+    add("bert.emb_ln_w", 1.0 + normal((D,), 0.05))
+    add("bert.emb_ln_b", normal((D,), 0.05))
+    for li in range(n_layer):
+        p = f"bert.l{li}."
+        add(p + "qkv_w", normal((3 * D, D), 0.03), proj=True)
+        add(p + "qkv_b", normal((3 * D,), 0.02))
+        add(p + "attn_out_w", normal((D, D), 0.03), proj=True)
+        add(p + "attn_out_b", normal((D,), 0.02))
+        add(p + "attn_ln_w", 1.0 + normal((D,), 0.05))
+        add(p + "attn_ln_b", normal((D,), 0.05))
+        add(p + "ff1_w", normal((F, D), 0.03), proj=True)
+        add(p + "ff1_b", normal((F,), 0.02))
+        add(p + "ff2_w", normal((D, F), 0.03), proj=True)
+        add(p + "ff2_b", normal((D,), 0.02))
+        add(p + "out_ln_w", 1.0 + normal((D,), 0.05))
+        add(p + "out_ln_b", normal((D,), 0.05))
+    w.write(path)
+    return path, W

@@ -330,6 +330,36 @@ int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len, const int
                          int hd, float scale, int path, float * out, int8_t * oq, float * od,
                          void * stream);
 
+/* ======================================================================================
+ * 3. BERT text encoder (src/gsv_bert.{h,cpp}: chinese-roberta-wwm-ext-large, post-LN, the
+ *    features the AR prefill takes as a request's `bert` input)
+ * ====================================================================================== */
+
+typedef struct gsvk_bert gsvk_bert;
+
+typedef struct {
+    int hidden, heads, inter, layers_used, vocab, max_pos;
+    float ln_eps;
+    int weight_type;   /* GGML type of the projection weights in the file (0 F32, 1 F16, 8 Q8_0) */
+} gsvk_bert_info;
+
+/* Load a gsv BERT GGUF (the tensor contract of src/gsv_bert.cpp:398-431, keys bert.* with the
+ * reference's defaults) onto HIP device `device`. Projection weights may be F32, F16 or Q8_0;
+ * all are held and multiplied in fp32. Only the first layers_used layers are loaded. Replaces
+ * gsv_bert::load (src/gsv_bert.cpp:313-457). */
+int gsvk_bert_load(const char * path, int device, int verbose, gsvk_bert ** out);
+void gsvk_bert_free(gsvk_bert * m);
+int gsvk_bert_get_info(const gsvk_bert * m, gsvk_bert_info * info);
+
+/* Encoder over B sequences: sequence b is ids_flat[b*Tmax .. b*Tmax + lens[b]) (token ids with
+ * [CLS]/[SEP], 1 <= lens[b] <= Tmax <= max_pos), positions 0..lens[b]-1, token type 0, attending
+ * only to its own tokens. Output of layer n_layers (0 = the embedding LayerNorm; < 0 or past
+ * layers_used = all used layers) as [hidden][lens[b]] row-major per sequence, the sequences back
+ * to back in out (host, hidden * sum(lens) floats). Replaces gsv_bert::impl::run / run_g
+ * (src/gsv_bert.cpp:97-233). */
+int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, const int32_t * lens, int Tmax,
+                     int n_layers, float * out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,88 @@
+"""GPU parity of the BERT text encoder (gsvk_bert_*, csrc/bert.hip) against the float64 oracle
+(oracle/bert_oracle.py, a restatement of src/gsv_bert.cpp:128-155) on synthetic BERT-large-shaped
+models (hidden 1024, 16 heads of 64, FFN 4096; fewer layers). The encoder computes in fp32; the
+bar here is max |gpu - oracle| <= 2e-4 * max |oracle| per output (the fp bar of the projections
+and attention is 2e-3 relative)."""
+import numpy as np
+import pytest
+
+import bert_oracle as BO
+import gsvk
+import synth_model as sm
+from conftest import FIXTURE_DIR
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-4
+
+
+def _model(tmp_path_factory, wtype, n_layer, layers_used, vocab=1000):
+    d = tmp_path_factory.mktemp("bert_" + wtype)
+    path, W = sm.write_bert_model(str(d / "bert.gguf"), n_layer=n_layer, layers_used=layers_used, vocab=vocab,
+                                  wtype=wtype)
+    return gsvk.Bert(path), W
+
+
+@pytest.fixture(scope="module")
+def bert_f32(tmp_path_factory):
+    m, W = _model(tmp_path_factory, "f32", 4, 2)
+    yield m, W
+    m.close()
+
+
+def _ids(rng, T, vocab=1000):
+    return rng.integers(0, vocab, size=T).astype(np.int32)
+
+
+def _check(got, ref):
+    err = np.max(np.abs(got.astype(np.float64) - ref)) / np.max(np.abs(ref))
+    assert err <= TOL, err
+    return err
+
+
+@pytest.mark.parametrize("T", [1, 5, 64, 130])
+def test_encode_matches_oracle(bert_f32, T):
+    m, W = bert_f32
+    ids = _ids(np.random.default_rng(T), T)
+    got = m.encode([ids])[0]
+    assert got.shape == (1024, T)
+    _check(got, BO.encode(W, ids, 2, 1024, 16, 1e-12))
+
+
+def test_every_layer_matches_oracle(bert_f32):
+    m, W = bert_f32
+    ids = _ids(np.random.default_rng(11), 40)
+    for k in range(3):
+        _check(m.encode([ids], n_layers=k)[0], BO.encode(W, ids, k, 1024, 16, 1e-12))
+
+
+def test_batch_matches_one_by_one(bert_f32):
+    m, W = bert_f32
+    rng = np.random.default_rng(5)
+    seqs = [_ids(rng, n) for n in (5, 64, 17, 3)]
+    batch = m.encode(seqs, tmax=70)
+    for q, got in zip(seqs, batch):
+        one = m.encode([q])[0]
+        np.testing.assert_allclose(got, one, rtol=0, atol=1e-5 * np.max(np.abs(one)))
+        _check(got, BO.encode(W, q, 2, 1024, 16, 1e-12))
+
+
+def test_longest_sequence_and_limits(bert_f32):
+    m, W = bert_f32
+    ids = _ids(np.random.default_rng(2), 512)
+    _check(m.encode([ids])[0], BO.encode(W, ids, 2, 1024, 16, 1e-12))
+    with pytest.raises(gsvk.GsvkError):
+        m.encode([_ids(np.random.default_rng(2), 513)])
+    with pytest.raises(gsvk.GsvkError):
+        m.encode([np.array([1, 1000, 2], np.int32)])    # id == vocab
+
+
+@pytest.mark.parametrize("wtype", ["f16", "q8_0"])
+def test_quantised_weight_files(tmp_path_factory, wtype):
+    m, W = _model(tmp_path_factory, wtype, 2, 1)
+    try:
+        assert m.info["weight_type"] == (1 if wtype == "f16" else 8)
+        ids = _ids(np.random.default_rng(7), 33)
+        _check(m.encode([ids])[0], BO.encode(W, ids, 1, 1024, 16, 1e-12))
+    finally:
+        m.close()
