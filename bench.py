@@ -35,6 +35,7 @@ import numpy as np  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0
+MFMA_F32_PEAK_TFLOPS = 157.3
 SEED = 0x6A5E0002
 N_LAYER, D, NH, HD, FFN, V = 24, 512, 16, 32, 2048, 1025
 
@@ -293,6 +294,41 @@ def b128_line(g, flags):
                         "no BERT features), 256 greedy steps"}
 
 
+def bert_line(torch):
+    """The BERT text encoder at the shape of chinese-roberta-wwm-ext-large (hidden 1024, 16 heads,
+    FFN 4096, 22 of 24 layers, vocab 21128; synthetic F16 weights, widened to fp32 at load): median
+    wall time of 5 encode calls after one warm-up, for one 64-token sentence and for 8 sentences
+    of 64 tokens in one call, with TFLOP/s over the algorithmic flops (2 per weight per token, 4 x
+    hidden per visible query-key pair) against the fp32 matrix-core peak."""
+    import gsvk
+    import synth_model as sm
+    d = os.path.join(ROOT, "_fixtures")
+    os.makedirs(d, exist_ok=True)
+    path = os.path.join(d, "gsv_bert_large_f16.gguf")
+    if not os.path.exists(path):
+        sm.write_bert_model(path, n_layer=22, layers_used=22, vocab=21128, wtype="f16")
+    m = gsvk.Bert(path)
+    rng = np.random.default_rng(0x6A5E0006)
+    res = {}
+    L, D, F = m.info["layers_used"], m.info["hidden"], m.info["inter"]
+    for name, B, T in (("t64", 1, 64), ("b8_t64", 8, 64)):
+        seqs = [rng.integers(0, 21128, size=T).astype(np.int32) for _ in range(B)]
+        m.encode(seqs)
+        t = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            m.encode(seqs)
+            t.append(time.perf_counter() - t0)
+        s = float(np.median(t))
+        fl = B * T * L * (2.0 * (4 * D * D + 2 * D * F) + 4.0 * T * D)
+        res[name] = {"ms": round(s * 1e3, 3), "tflops": round(fl / s / 1e12, 2),
+                     "frac_fp32_peak": round(fl / s / 1e12 / MFMA_F32_PEAK_TFLOPS, 4)}
+    m.close()
+    res["workload"] = ("BERT encoder, hidden 1024, 16 heads, FFN 4096, 22 layers, fp32 compute; "
+                       "wall time of encode (ids upload to features on the host)")
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -305,6 +341,8 @@ def main():
     ap.add_argument("--no-b128", action="store_true", help="skip the batch-128 long-context decode line")
     ap.add_argument("--prefill-only", action="store_true", help="time only the batch-16 x 1024 prefill")
     ap.add_argument("--b128-only", action="store_true", help="time only the batch-128 long-context decode")
+    ap.add_argument("--bert-only", action="store_true", help="time only the BERT text encoder")
+    ap.add_argument("--no-bert", action="store_true", help="skip the BERT text encoder line")
     ap.add_argument("--kernels-only", action="store_true",
                     help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
@@ -326,6 +364,9 @@ def main():
         res["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         res["copy_probe_bytes"] = copy_probe(torch)
         print(json.dumps({"kernels_only": res}))
+        return
+    if args.bert_only:
+        print(json.dumps({"bert_encode": bert_line(torch)}))
         return
     path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
     g = gsvk.Model(path, device=0)
@@ -379,6 +420,8 @@ def main():
         extra["b128_long"] = b128_line(g, flags)
         g.release_cache()
     g.close()
+    if not args.no_bert:
+        extra["bert_encode"] = bert_line(torch)
 
     roof = None
     if not args.no_kernels:

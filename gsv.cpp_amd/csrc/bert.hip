@@ -13,9 +13,9 @@
 // fp32 GEMMs on rocBLAS (the reference's default export keeps F32 weights, and ggml-cpu computes
 // F32 x F32 products in fp32; F16 and Q8_0 weight files are widened to fp32 at load); bias,
 // GELU and the residual LayerNorms are this library's kernels (norm.hip); attention is
-// k_bert_attn below: one wave per 64 queries of one (sequence, head), the lane's query and
-// output accumulator in registers, keys and values staged through LDS in tiles of 64, an online
-// softmax per chunk of 16 keys, fp32 throughout.
+// k_bert_attn below: one wave per 16 queries of one (sequence, head), four lanes per query
+// (a quarter of the head dims each), keys and values staged through LDS in tiles of 64, an
+// online softmax per chunk of 16 keys, fp32 throughout.
 #include <rocblas/rocblas.h>
 
 #include <cmath>
@@ -35,6 +35,7 @@ namespace {
 constexpr int BA_HD = 64;   // head dim of the kernels below (BERT-large: 1024 / 16)
 constexpr int BA_KT = 64;   // keys per LDS tile
 constexpr int BA_CH = 16;   // keys per softmax chunk
+constexpr int BA_Q = 16;    // queries per workgroup (one wave: 4 lanes per query)
 
 // x[r] = word[id_r] + pos[t_r] + type0 (the sum order of src/gsv_bert.cpp:141-144); one
 // workgroup of 256 threads per row, 4 values per thread and pass.
@@ -55,10 +56,13 @@ __global__ void __launch_bounds__(256) k_bert_embed(const float * __restrict__ w
     }
 }
 
-// Attention of one (sequence b, head h) for queries [64 * blockIdx.x, +64): lane = query. The
-// sequence's rows are [off_b, off_b + len_b) of qkv (row stride 3D: q | k | v, head h at 64h);
-// every query sees every key of its sequence (the block-diagonal mask of
-// src/gsv_bert.cpp:289-296). Output rows of queries past len_b are not written.
+// Attention of one (sequence b, head h) for queries [16 * blockIdx.x, +16): lane = 4 * query +
+// quarter, the quarter c holding dims [16c, 16c + 16) of the query and of its output (a score is
+// the sum of the 4 quarters' partial dots, exchanged within the lane quad). The sequence's rows
+// are [off_b, off_b + len_b) of qkv (row stride 3D: q | k | v, head h at 64h); every query sees
+// every key of its sequence (the block-diagonal mask of src/gsv_bert.cpp:289-296). Keys and
+// values are staged through LDS in tiles of 64; an online softmax runs per chunk of 16 keys.
+// Output rows of queries past len_b are not written.
 __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv,
                                                   const int32_t * __restrict__ seq_off,
                                                   const int32_t * __restrict__ seq_len, int D,
@@ -66,40 +70,40 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
     const int h = blockIdx.y, b = blockIdx.z;
     const int len = seq_len[b];
     const int64_t off = seq_off[b];
-    const int q0 = blockIdx.x * 64;
+    const int q0 = blockIdx.x * BA_Q;
     if (q0 >= len) return;   // uniform over the workgroup
     const int lane = threadIdx.x;
+    const int qq = lane >> 2, c = lane & 3;
     const int64_t rs = 3 * (int64_t) D;
-    const int qi = min(q0 + lane, len - 1);
+    const int qi = min(q0 + qq, len - 1);
 
     __shared__ float4 ks[BA_KT][BA_HD / 4];
     __shared__ float4 vs[BA_KT][BA_HD / 4];
 
-    float q[BA_HD];
+    float q[16];
     {
-        const float4 * qp = reinterpret_cast<const float4 *>(qkv + (off + qi) * rs + h * BA_HD);
+        const float4 * qp = reinterpret_cast<const float4 *>(qkv + (off + qi) * rs + h * BA_HD + 16 * c);
 #pragma unroll
-        for (int i = 0; i < BA_HD / 4; i++) {
+        for (int i = 0; i < 4; i++) {
             const float4 v = qp[i];
             q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
         }
     }
-    float o[BA_HD];
+    float o[16];
 #pragma unroll
-    for (int d = 0; d < BA_HD; d++) o[d] = 0.0f;
+    for (int d = 0; d < 16; d++) o[d] = 0.0f;
     float m = -INFINITY, l = 0.0f;
 
     for (int k0 = 0; k0 < len; k0 += BA_KT) {
         __syncthreads();   // the previous tile has been read
-        {
-            const int kr = min(k0 + lane, len - 1);   // keys past the end repeat the last (unused)
-            const float4 * kp = reinterpret_cast<const float4 *>(qkv + (off + kr) * rs + D + h * BA_HD);
-            const float4 * vp = reinterpret_cast<const float4 *>(qkv + (off + kr) * rs + 2 * D + h * BA_HD);
+        // 64 keys x 16 float4 of K and of V: 16 consecutive lanes read one key's 256 bytes
 #pragma unroll
-            for (int i = 0; i < BA_HD / 4; i++) {
-                ks[lane][i] = kp[i];
-                vs[lane][i] = vp[i];
-            }
+        for (int r = 0; r < BA_KT * (BA_HD / 4) / 64; r++) {
+            const int idx = r * 64 + lane, key = idx >> 4, part = idx & 15;
+            const int kr = min(k0 + key, len - 1);   // keys past the end repeat the last (unused)
+            const float * row = qkv + (off + kr) * rs + h * BA_HD + 4 * part;
+            ks[key][part] = *reinterpret_cast<const float4 *>(row + D);
+            vs[key][part] = *reinterpret_cast<const float4 *>(row + 2 * D);
         }
         __syncthreads();
         const int nk = min(BA_KT, len - k0);
@@ -110,13 +114,15 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
             for (int j = 0; j < BA_CH; j++) {
                 float dot = 0.0f;
 #pragma unroll
-                for (int i = 0; i < BA_HD / 4; i++) {
-                    const float4 kk = ks[c0 + j][i];
+                for (int i = 0; i < 4; i++) {
+                    const float4 kk = ks[c0 + j][4 * c + i];
                     dot = __builtin_fmaf(q[4 * i], kk.x, dot);
                     dot = __builtin_fmaf(q[4 * i + 1], kk.y, dot);
                     dot = __builtin_fmaf(q[4 * i + 2], kk.z, dot);
                     dot = __builtin_fmaf(q[4 * i + 3], kk.w, dot);
                 }
+                dot += __shfl_xor(dot, 1, 64);
+                dot += __shfl_xor(dot, 2, 64);
                 s[j] = c0 + j < nk ? dot * scale : -INFINITY;
                 cmax = fmaxf(cmax, s[j]);
             }
@@ -124,15 +130,15 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
             const float f = expf(m - mn);               // 0 on the first chunk (m = -inf)
             l *= f;
 #pragma unroll
-            for (int d = 0; d < BA_HD; d++) o[d] *= f;
+            for (int d = 0; d < 16; d++) o[d] *= f;
             m = mn;
 #pragma unroll
             for (int j = 0; j < BA_CH; j++) {
                 const float p = expf(s[j] - mn);        // masked keys: exp(-inf) = 0
                 l += p;
 #pragma unroll
-                for (int i = 0; i < BA_HD / 4; i++) {
-                    const float4 vv = vs[c0 + j][i];
+                for (int i = 0; i < 4; i++) {
+                    const float4 vv = vs[c0 + j][4 * c + i];
                     o[4 * i] = __builtin_fmaf(p, vv.x, o[4 * i]);
                     o[4 * i + 1] = __builtin_fmaf(p, vv.y, o[4 * i + 1]);
                     o[4 * i + 2] = __builtin_fmaf(p, vv.z, o[4 * i + 2]);
@@ -141,11 +147,11 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
             }
         }
     }
-    if (q0 + lane >= len) return;
+    if (q0 + qq >= len) return;
     const float inv = 1.0f / l;
-    float4 * op = reinterpret_cast<float4 *>(out + (off + q0 + lane) * (int64_t) D + h * BA_HD);
+    float4 * op = reinterpret_cast<float4 *>(out + (off + q0 + qq) * (int64_t) D + h * BA_HD + 16 * c);
 #pragma unroll
-    for (int i = 0; i < BA_HD / 4; i++)
+    for (int i = 0; i < 4; i++)
         op[i] = make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
 }
 
@@ -450,7 +456,7 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
         const BertLayer & w = m->L[li];
         GSVK_TRY(gemm(m, w.qkv_w, x, qkv, (int) rows, 3 * D, D));
         GSVK_TRY(gsvk_op_add_act(qkv, w.qkv_b, rows * 3 * D, 3 * D, 0, qkv, st));
-        hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + 63) / 64), (unsigned) in.heads, (unsigned) B),
+        hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
                            dim3(64), 0, st, qkv, d_off, d_len, D, scale, att);
         GSVK_LAUNCH_CHECK();
         GSVK_TRY(gemm(m, w.ao_w, att, prj, (int) rows, D, D));
