@@ -24,7 +24,8 @@ def _model(tmp_path_factory, wtype, n_layer, layers_used, vocab=1000):
 
 
 @pytest.fixture(scope="module")
-def bert_f32(tmp_path_factory):
+def bert_f32(gpu, tmp_path_factory):
+    # (gpu: torch initialises the device first, as in every GPU test of the suite)
     m, W = _model(tmp_path_factory, "f32", 4, 2)
     yield m, W
     m.close()
@@ -78,7 +79,7 @@ def test_longest_sequence_and_limits(bert_f32):
 
 
 @pytest.mark.parametrize("wtype", ["f16", "q8_0"])
-def test_quantised_weight_files(tmp_path_factory, wtype):
+def test_quantised_weight_files(gpu, tmp_path_factory, wtype):
     m, W = _model(tmp_path_factory, wtype, 2, 1)
     try:
         assert m.info["weight_type"] == (1 if wtype == "f16" else 8)
