@@ -61,12 +61,13 @@ __global__ void __launch_bounds__(256) k_bert_embed(const float * __restrict__ w
 // the sum of the 4 quarters' partial dots, exchanged within the lane quad). The sequence's rows
 // are [off_b, off_b + len_b) of qkv (row stride 3D: q | k | v, head h at 64h); every query sees
 // every key of its sequence (the block-diagonal mask of src/gsv_bert.cpp:289-296). Keys and
-// values are staged through LDS in tiles of 64; an online softmax runs per chunk of 16 keys.
+// values are staged through LDS in tiles of 64; an online softmax runs per chunk of 16 keys, in
+// log2 units (scores scaled by log2(e) / sqrt(64), the hardware exp2).
 // Output rows of queries past len_b are not written.
 __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv,
                                                   const int32_t * __restrict__ seq_off,
                                                   const int32_t * __restrict__ seq_len, int D,
-                                                  float scale, float * __restrict__ out) {
+                                                  float scale_log2, float * __restrict__ out) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int len = seq_len[b];
     const int64_t off = seq_off[b];
@@ -123,18 +124,18 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
                 }
                 dot += __shfl_xor(dot, 1, 64);
                 dot += __shfl_xor(dot, 2, 64);
-                s[j] = c0 + j < nk ? dot * scale : -INFINITY;
+                s[j] = c0 + j < nk ? dot * scale_log2 : -INFINITY;
                 cmax = fmaxf(cmax, s[j]);
             }
             const float mn = fmaxf(m, cmax);            // finite: each chunk has a key
-            const float f = expf(m - mn);               // 0 on the first chunk (m = -inf)
+            const float f = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first chunk (m = -inf)
             l *= f;
 #pragma unroll
             for (int d = 0; d < 16; d++) o[d] *= f;
             m = mn;
 #pragma unroll
             for (int j = 0; j < BA_CH; j++) {
-                const float p = expf(s[j] - mn);        // masked keys: exp(-inf) = 0
+                const float p = __builtin_amdgcn_exp2f(s[j] - mn);   // masked keys: exp2(-inf) = 0
                 l += p;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -451,13 +452,13 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
                        d_pos, D, prj);
     GSVK_LAUNCH_CHECK();
     GSVK_TRY(launch_layernorm(prj, nullptr, nullptr, m->emb_ln, rows, D, in.ln_eps, x, nullptr, nullptr, st));
-    const float scale = 1.0f / std::sqrt((float) BA_HD);
+    const float scale_log2 = 1.4426950408889634f / std::sqrt((float) BA_HD);
     for (int li = 0; li < n_layers; li++) {
         const BertLayer & w = m->L[li];
         GSVK_TRY(gemm(m, w.qkv_w, x, qkv, (int) rows, 3 * D, D));
         GSVK_TRY(gsvk_op_add_act(qkv, w.qkv_b, rows * 3 * D, 3 * D, 0, qkv, st));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
-                           dim3(64), 0, st, qkv, d_off, d_len, D, scale, att);
+                           dim3(64), 0, st, qkv, d_off, d_len, D, scale_log2, att);
         GSVK_LAUNCH_CHECK();
         GSVK_TRY(gemm(m, w.ao_w, att, prj, (int) rows, D, D));
         GSVK_TRY(launch_layernorm(x, prj, w.ao_b, w.ln1, rows, D, in.ln_eps, x, nullptr, nullptr, st));
