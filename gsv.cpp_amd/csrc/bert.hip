@@ -10,8 +10,9 @@
 // Output [hidden][T] row-major per sequence (src/gsv_bert.cpp:220-228).
 //
 // Design: rows of all sequences packed back to back (no padding rows); the projections are
-// fp32 GEMMs on rocBLAS (the reference's default export keeps F32 weights, and ggml-cpu computes
-// F32 x F32 products in fp32; F16 and Q8_0 weight files are widened to fp32 at load); bias,
+// GEMMs on rocBLAS: F32 weights in fp32 (ggml-cpu's F32 x F32 product), F16 weights kept in fp16
+// with the activations rounded to fp16 and fp32 sums (ggml-cpu converts the activations to the
+// weights' F16 dot type), Q8_0 weight files widened to fp32 at load; bias,
 // GELU and the residual LayerNorms are this library's kernels (norm.hip); attention is
 // k_bert_attn below: one wave per 16 queries of one (sequence, head), four lanes per query
 // (a quarter of the head dims each), keys and values staged through LDS in tiles of 64, an
@@ -177,10 +178,30 @@ float half_to_float(uint16_t h) {
     return x;
 }
 
-struct BertLayer {
-    float * qkv_w = nullptr, * qkv_b = nullptr, * ao_w = nullptr, * ao_b = nullptr, * ln1 = nullptr;
-    float * ff1_w = nullptr, * ff1_b = nullptr, * ff2_w = nullptr, * ff2_b = nullptr, * ln2 = nullptr;
+// A projection weight [N][K]: fp16 bits when the file holds F16 (multiplied as ggml-cpu does,
+// with the activations rounded to fp16 and fp32 accumulation), else fp32.
+struct Proj {
+    void * w = nullptr;
+    bool f16 = false;
 };
+
+struct BertLayer {
+    Proj qkv, ao, ff1, ff2;
+    float * qkv_b = nullptr, * ao_b = nullptr, * ln1 = nullptr;
+    float * ff1_b = nullptr, * ff2_b = nullptr, * ln2 = nullptr;
+};
+
+// fp32 -> fp16, round to nearest even (ggml's FP32_TO_FP16 on F16C hardware)
+__global__ void __launch_bounds__(256) k_to_f16(const float * __restrict__ x, int64_t n,
+                                                _Float16 * __restrict__ y) {
+    const int64_t i = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i + 3 < n) {
+        const float4 v = *reinterpret_cast<const float4 *>(x + i);
+        y[i] = (_Float16) v.x; y[i + 1] = (_Float16) v.y; y[i + 2] = (_Float16) v.z; y[i + 3] = (_Float16) v.w;
+    } else {
+        for (int64_t j = i; j < n; j++) y[j] = (_Float16) x[j];
+    }
+}
 
 }  // namespace
 }  // namespace gsvk
@@ -193,6 +214,7 @@ struct gsvk_bert {
     rocblas_handle blas = nullptr;
     gsvk_bert_info info{};
     std::vector<void *> wmem;   // weight allocations
+    bool any_f16 = false;       // some projection is kept in fp16
     float * word = nullptr, * pos = nullptr, * type0 = nullptr, * emb_ln = nullptr;
     std::vector<BertLayer> L;
     // per-call workspace, grown to the largest call
@@ -206,16 +228,17 @@ struct gsvk_bert {
         if (blas) (void) rocblas_destroy_handle(blas);
         if (stream) (void) hipStreamDestroy(stream);
     }
-    int dev_alloc(float *& out, size_t count) {
+    template <typename T>
+    int dev_alloc(T *& out, size_t count) {
         void * p = nullptr;
-        const hipError_t e = hipMalloc(&p, count * sizeof(float));
+        const hipError_t e = hipMalloc(&p, count * sizeof(T));
         if (e != hipSuccess) {
             (void) hipGetLastError();
-            set_error("hipMalloc of %zu bytes failed: %s", count * sizeof(float), hipGetErrorString(e));
+            set_error("hipMalloc of %zu bytes failed: %s", count * sizeof(T), hipGetErrorString(e));
             return GSVK_ERR_NOMEM;
         }
         wmem.push_back(p);
-        out = (float *) p;
+        out = (T *) p;
         return GSVK_OK;
     }
 };
@@ -245,7 +268,7 @@ struct DevGuard {
 // Read tensor `name` of ggml shape {ne0, ne1} (ne1 = 1 for vectors) as fp32 into a new device
 // buffer. F32, F16 and Q8_0 (rows of ne0 % 32 == 0) are accepted.
 int load_tensor(gsvk_bert * m, const GgufFile & g, const std::string & name, int64_t ne0, int64_t ne1,
-                float *& out) {
+                float *& out, Proj * proj = nullptr) {
     const GgufTensor * t = g.tensor(name);
     if (!t) {
         set_error("BERT GGUF: missing tensor %s", name.c_str());
@@ -267,6 +290,16 @@ int load_tensor(gsvk_bert * m, const GgufFile & g, const std::string & name, int
         set_error("BERT GGUF: reading tensor %s failed", name.c_str());
         return GSVK_ERR_IO;
     }
+    if (proj && t->type == GGML_F16) {   // a projection kept in fp16
+        uint16_t * w16 = nullptr;
+        GSVK_TRY(m->dev_alloc(w16, n));
+        GSVK_HIP(hipMemcpy(w16, raw.data(), n * 2, hipMemcpyHostToDevice));
+        proj->w = w16;
+        proj->f16 = true;
+        m->any_f16 = true;
+        out = nullptr;
+        return GSVK_OK;
+    }
     std::vector<float> f(n);
     if (t->type == GGML_F32) {
         memcpy(f.data(), raw.data(), n * 4);
@@ -284,7 +317,16 @@ int load_tensor(gsvk_bert * m, const GgufFile & g, const std::string & name, int
     }
     GSVK_TRY(m->dev_alloc(out, n));
     GSVK_HIP(hipMemcpy(out, f.data(), n * 4, hipMemcpyHostToDevice));
+    if (proj) {
+        proj->w = out;
+        proj->f16 = false;
+    }
     return GSVK_OK;
+}
+
+int load_proj(gsvk_bert * m, const GgufFile & g, const std::string & name, int64_t ne0, int64_t ne1, Proj & p) {
+    float * f = nullptr;
+    return load_tensor(m, g, name, ne0, ne1, f, &p);
 }
 
 // [w; b] of a LayerNorm, packed as the fused LayerNorm kernel reads it
@@ -299,11 +341,22 @@ int load_ln(gsvk_bert * m, const GgufFile & g, const std::string & wn, const std
     return GSVK_OK;
 }
 
-// Y[M][N] = X[M][K] . W[N][K]^T (row-major), i.e. column-major Y^T = W^T X^T
-int gemm(gsvk_bert * m, const float * W, const float * X, float * Y, int M, int N, int K) {
+// Y[M][N] = X[M][K] . W[N][K]^T (row-major), i.e. column-major Y^T = W^T X^T. An fp16 weight
+// takes X rounded to fp16 (x16: scratch of M*K halves); products are summed in fp32.
+int gemm(gsvk_bert * m, const Proj & W, const float * X, _Float16 * x16, float * Y, int M, int N, int K) {
     const float one = 1.0f, zero = 0.0f;
-    GSVK_BLAS(rocblas_sgemm(m->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W,
-                            K, X, K, &zero, Y, N));
+    if (!W.f16) {
+        GSVK_BLAS(rocblas_sgemm(m->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one,
+                                (const float *) W.w, K, X, K, &zero, Y, N));
+        return GSVK_OK;
+    }
+    const int64_t n = (int64_t) M * K;
+    hipLaunchKernelGGL(k_to_f16, dim3((unsigned) ((n / 4 + 255) / 256 + 1)), dim3(256), 0, m->stream, X, n, x16);
+    GSVK_LAUNCH_CHECK();
+    GSVK_BLAS(rocblas_gemm_ex(m->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W.w,
+                              rocblas_datatype_f16_r, K, x16, rocblas_datatype_f16_r, K, &zero, Y,
+                              rocblas_datatype_f32_r, N, Y, rocblas_datatype_f32_r, N, rocblas_datatype_f32_r,
+                              rocblas_gemm_algo_standard, 0, 0));
     return GSVK_OK;
 }
 
@@ -362,14 +415,14 @@ extern "C" int gsvk_bert_load(const char * path, int device, int verbose, gsvk_b
     for (int li = 0; li < in.layers_used; li++) {
         const std::string p = "bert.l" + std::to_string(li) + ".";
         BertLayer & w = m->L[li];
-        GSVK_TRY(load_tensor(m.get(), g, p + "qkv_w", D, 3 * D, w.qkv_w));
+        GSVK_TRY(load_proj(m.get(), g, p + "qkv_w", D, 3 * D, w.qkv));
         GSVK_TRY(load_tensor(m.get(), g, p + "qkv_b", 3 * D, 1, w.qkv_b));
-        GSVK_TRY(load_tensor(m.get(), g, p + "attn_out_w", D, D, w.ao_w));
+        GSVK_TRY(load_proj(m.get(), g, p + "attn_out_w", D, D, w.ao));
         GSVK_TRY(load_tensor(m.get(), g, p + "attn_out_b", D, 1, w.ao_b));
         GSVK_TRY(load_ln(m.get(), g, p + "attn_ln_w", p + "attn_ln_b", w.ln1));
-        GSVK_TRY(load_tensor(m.get(), g, p + "ff1_w", D, F, w.ff1_w));
+        GSVK_TRY(load_proj(m.get(), g, p + "ff1_w", D, F, w.ff1));
         GSVK_TRY(load_tensor(m.get(), g, p + "ff1_b", F, 1, w.ff1_b));
-        GSVK_TRY(load_tensor(m.get(), g, p + "ff2_w", F, D, w.ff2_w));
+        GSVK_TRY(load_proj(m.get(), g, p + "ff2_w", F, D, w.ff2));
         GSVK_TRY(load_tensor(m.get(), g, p + "ff2_b", D, 1, w.ff2_b));
         GSVK_TRY(load_ln(m.get(), g, p + "out_ln_w", p + "out_ln_b", w.ln2));
     }
@@ -421,7 +474,8 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     hipStream_t st = m->stream;
     // workspace: x, qkv, attention output, projection output, FFN hidden, and the small arrays
     const size_t fl = (size_t) rows * (D + 3 * D + D + D + F);
-    const size_t need = fl * 4 + (size_t) rows * 8 + (size_t) B * 8 + 4096;
+    const size_t h16 = m->any_f16 ? (size_t) rows * (F > D ? F : D) : 0;   // fp16 GEMM input
+    const size_t need = fl * 4 + h16 * 2 + (size_t) rows * 8 + (size_t) B * 8 + 4096;
     if (need > m->ws_bytes) {
         if (m->ws) (void) hipFree(m->ws);
         m->ws = nullptr;
@@ -439,7 +493,8 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     float * att = qkv + rows * 3 * D;
     float * prj = att + rows * D;
     float * h = prj + rows * D;
-    int32_t * d_ids = (int32_t *) (h + rows * F);
+    _Float16 * x16 = (_Float16 *) (h + rows * F);
+    int32_t * d_ids = (int32_t *) (x16 + h16 + (h16 & 1));
     int32_t * d_pos = d_ids + rows;
     int32_t * d_off = d_pos + rows;
     int32_t * d_len = d_off + B;
@@ -455,16 +510,16 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     const float scale_log2 = 1.4426950408889634f / std::sqrt((float) BA_HD);
     for (int li = 0; li < n_layers; li++) {
         const BertLayer & w = m->L[li];
-        GSVK_TRY(gemm(m, w.qkv_w, x, qkv, (int) rows, 3 * D, D));
+        GSVK_TRY(gemm(m, w.qkv, x, x16, qkv, (int) rows, 3 * D, D));
         GSVK_TRY(gsvk_op_add_act(qkv, w.qkv_b, rows * 3 * D, 3 * D, 0, qkv, st));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
                            dim3(64), 0, st, qkv, d_off, d_len, D, scale_log2, att);
         GSVK_LAUNCH_CHECK();
-        GSVK_TRY(gemm(m, w.ao_w, att, prj, (int) rows, D, D));
+        GSVK_TRY(gemm(m, w.ao, att, x16, prj, (int) rows, D, D));
         GSVK_TRY(launch_layernorm(x, prj, w.ao_b, w.ln1, rows, D, in.ln_eps, x, nullptr, nullptr, st));
-        GSVK_TRY(gemm(m, w.ff1_w, x, h, (int) rows, F, D));
+        GSVK_TRY(gemm(m, w.ff1, x, x16, h, (int) rows, F, D));
         GSVK_TRY(gsvk_op_add_act(h, w.ff1_b, rows * F, F, 2, h, st));
-        GSVK_TRY(gemm(m, w.ff2_w, h, prj, (int) rows, D, F));
+        GSVK_TRY(gemm(m, w.ff2, h, x16, prj, (int) rows, D, F));
         GSVK_TRY(launch_layernorm(x, prj, w.ff2_b, w.ln2, rows, D, in.ln_eps, x, nullptr, nullptr, st));
     }
     // [rows][D] -> per sequence [D][len] (src/gsv_bert.cpp:220-228)

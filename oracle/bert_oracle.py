@@ -54,8 +54,10 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.n
     return p @ np.asarray(v, np.float64)
 
 
-def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float) -> np.ndarray:
-    """One sequence of token ids -> [hidden][T] after n_layers layers (0: the embedding LN)."""
+def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float, act_f16: bool = False) -> np.ndarray:
+    """One sequence of token ids -> [hidden][T] after n_layers layers (0: the embedding LN).
+    act_f16: the projections' inputs are rounded to fp16 first, as ggml-cpu does for F16 weights
+    (their vec_dot type is F16: ggml_cpu_fp32_to_fp16 of the activations, then F16 x F16 dots)."""
     ids = np.asarray(ids, np.int64)
     T = len(ids)
     D, hd = hidden, hidden // heads
@@ -63,15 +65,16 @@ def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float) -> 
     x = (g("bert.word_emb")[ids] + g("bert.pos_emb")[:T]) + g("bert.type_emb")[0]
     x = layernorm(x, g("bert.emb_ln_w"), g("bert.emb_ln_b"), eps)
     scale = 1.0 / math.sqrt(hd)
+    r = (lambda a: a.astype(np.float32).astype(np.float16).astype(np.float64)) if act_f16 else (lambda a: a)
     for li in range(n_layers):
         p = f"bert.l{li}."
-        qkv = x @ g(p + "qkv_w").T + g(p + "qkv_b")
+        qkv = r(x) @ g(p + "qkv_w").T + g(p + "qkv_b")
         a = np.empty((T, D))
         for h in range(heads):
             sl = slice(h * hd, (h + 1) * hd)
             a[:, sl] = attention(qkv[:, sl], qkv[:, D:2 * D][:, sl], qkv[:, 2 * D:][:, sl], scale)
-        x = layernorm(x + a @ g(p + "attn_out_w").T + g(p + "attn_out_b"), g(p + "attn_ln_w"),
+        x = layernorm(x + r(a) @ g(p + "attn_out_w").T + g(p + "attn_out_b"), g(p + "attn_ln_w"),
                       g(p + "attn_ln_b"), eps)
-        hh = gelu_erf(x @ g(p + "ff1_w").T + g(p + "ff1_b"))
-        x = layernorm(x + hh @ g(p + "ff2_w").T + g(p + "ff2_b"), g(p + "out_ln_w"), g(p + "out_ln_b"), eps)
+        hh = gelu_erf(r(x) @ g(p + "ff1_w").T + g(p + "ff1_b"))
+        x = layernorm(x + r(hh) @ g(p + "ff2_w").T + g(p + "ff2_b"), g(p + "out_ln_w"), g(p + "out_ln_b"), eps)
     return x.T.copy()

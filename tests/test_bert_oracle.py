@@ -75,3 +75,18 @@ def test_bert_load_rejects_bad_files(tmp_path):
         gsvk.Bert(str(p))
     with pytest.raises(gsvk.GsvkError):
         gsvk.Bert(str(tmp_path / "missing.gguf"))
+
+
+def test_encode_f16_activations_round_each_projection_input(tmp_path):
+    """act_f16 rounds the inputs of the four projections to fp16 and nothing else: with weights
+    and activations exactly representable in fp16 the two modes agree, and in general they differ
+    by about fp16 rounding."""
+    path, W = sm.write_bert_model(str(tmp_path / "b.gguf"), n_layer=1, layers_used=1, vocab=30, max_pos=8,
+                                  wtype="f16")
+    ids = [3, 1, 4, 1, 5]
+    a = BO.encode(W, ids, 1, 1024, 16, 1e-12)
+    b = BO.encode(W, ids, 1, 1024, 16, 1e-12, act_f16=True)
+    d = np.max(np.abs(a - b)) / np.max(np.abs(a))
+    assert 1e-6 < d < 1e-2
+    np.testing.assert_array_equal(BO.encode(W, ids, 0, 1024, 16, 1e-12, act_f16=True),
+                                  BO.encode(W, ids, 0, 1024, 16, 1e-12))
