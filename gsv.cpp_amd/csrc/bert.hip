@@ -123,8 +123,8 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
                     dot = __builtin_fmaf(q[4 * i + 2], kk.z, dot);
                     dot = __builtin_fmaf(q[4 * i + 3], kk.w, dot);
                 }
-                dot += __shfl_xor(dot, 1, 64);
-                dot += __shfl_xor(dot, 2, 64);
+                dot += dpp_f<DPP_XOR1>(dot);   // the quad's 4 quarters (lanes ^1, ^2)
+                dot += dpp_f<DPP_XOR2>(dot);
                 s[j] = c0 + j < nk ? dot * scale_log2 : -INFINITY;
                 cmax = fmaxf(cmax, s[j]);
             }
