@@ -66,9 +66,11 @@ __global__ void __launch_bounds__(256) k_bert_embed(const float * __restrict__ w
 // log2 units (scores scaled by log2(e) / sqrt(64), the hardware exp2).
 // Output rows of queries past len_b are not written.
 __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv,
+                                                  const float * __restrict__ qkv_b,
                                                   const int32_t * __restrict__ seq_off,
                                                   const int32_t * __restrict__ seq_len, int D,
-                                                  float scale_log2, float * __restrict__ out) {
+                                                  float scale_log2, float * __restrict__ out,
+                                                  _Float16 * __restrict__ out16) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int len = seq_len[b];
     const int64_t off = seq_off[b];
@@ -85,12 +87,15 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
     float q[16];
     {
         const float4 * qp = reinterpret_cast<const float4 *>(qkv + (off + qi) * rs + h * BA_HD + 16 * c);
+        const float4 * qb = reinterpret_cast<const float4 *>(qkv_b + h * BA_HD + 16 * c);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const float4 v = qp[i];
-            q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+            const float4 v = qp[i], bb = qb[i];
+            q[4 * i] = v.x + bb.x; q[4 * i + 1] = v.y + bb.y; q[4 * i + 2] = v.z + bb.z; q[4 * i + 3] = v.w + bb.w;
         }
     }
+    const float4 * kbias = reinterpret_cast<const float4 *>(qkv_b + D + h * BA_HD);
+    const float4 * vbias = reinterpret_cast<const float4 *>(qkv_b + 2 * D + h * BA_HD);
     float o[16];
 #pragma unroll
     for (int d = 0; d < 16; d++) o[d] = 0.0f;
@@ -104,8 +109,10 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
             const int idx = r * 64 + lane, key = idx >> 4, part = idx & 15;
             const int kr = min(k0 + key, len - 1);   // keys past the end repeat the last (unused)
             const float * row = qkv + (off + kr) * rs + h * BA_HD + 4 * part;
-            ks[key][part] = *reinterpret_cast<const float4 *>(row + D);
-            vs[key][part] = *reinterpret_cast<const float4 *>(row + 2 * D);
+            const float4 kv = *reinterpret_cast<const float4 *>(row + D), kb = kbias[part];
+            const float4 vv = *reinterpret_cast<const float4 *>(row + 2 * D), vb = vbias[part];
+            ks[key][part] = make_float4(kv.x + kb.x, kv.y + kb.y, kv.z + kb.z, kv.w + kb.w);
+            vs[key][part] = make_float4(vv.x + vb.x, vv.y + vb.y, vv.z + vb.z, vv.w + vb.w);
         }
         __syncthreads();
         const int nk = min(BA_KT, len - k0);
@@ -151,10 +158,36 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
     }
     if (q0 + qq >= len) return;
     const float inv = 1.0f / l;
-    float4 * op = reinterpret_cast<float4 *>(out + (off + q0 + qq) * (int64_t) D + h * BA_HD + 16 * c);
+    const int64_t o0 = (off + q0 + qq) * (int64_t) D + h * BA_HD + 16 * c;
+    if (out16) {   // the fp16 input of an F16 out projection
+#pragma unroll
+        for (int d = 0; d < 16; d++) out16[o0 + d] = (_Float16) (o[d] * inv);
+        return;
+    }
+    float4 * op = reinterpret_cast<float4 *>(out + o0);
 #pragma unroll
     for (int i = 0; i < 4; i++)
         op[i] = make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+}
+
+// h = gelu_erf(h + b[col]) (the add_act of src/gsv_bert.cpp:151-153, as norm.hip's k_add_act),
+// stored in place in fp32, or to h16 in fp16 (the input of an F16 FFN2) when h16 is given
+__global__ void __launch_bounds__(256) k_bias_gelu(float * __restrict__ h, const float * __restrict__ b,
+                                                   int64_t rows, int F, _Float16 * __restrict__ h16) {
+    const int64_t i = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= rows * F) return;   // F % 4 == 0: a thread's 4 values share a row
+    const float4 v = *reinterpret_cast<const float4 *>(h + i);
+    const float4 bb = *reinterpret_cast<const float4 *>(b + i % F);
+    const float x[4] = {v.x + bb.x, v.y + bb.y, v.z + bb.z, v.w + bb.w};
+    float y[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) y[k] = 0.5f * x[k] * (1.0f + erff(x[k] * 0.70710678118654752440f));
+    if (h16) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) h16[i + k] = (_Float16) y[k];
+    } else {
+        *reinterpret_cast<float4 *>(h + i) = make_float4(y[0], y[1], y[2], y[3]);
+    }
 }
 
 float half_to_float(uint16_t h) {
@@ -342,7 +375,8 @@ int load_ln(gsvk_bert * m, const GgufFile & g, const std::string & wn, const std
 }
 
 // Y[M][N] = X[M][K] . W[N][K]^T (row-major), i.e. column-major Y^T = W^T X^T. An fp16 weight
-// takes X rounded to fp16 (x16: scratch of M*K halves); products are summed in fp32.
+// takes X rounded to fp16 (into x16, scratch of M*K halves) or, when X is null, the fp16 rows
+// already in x16; products are summed in fp32.
 int gemm(gsvk_bert * m, const Proj & W, const float * X, _Float16 * x16, float * Y, int M, int N, int K) {
     const float one = 1.0f, zero = 0.0f;
     if (!W.f16) {
@@ -350,9 +384,11 @@ int gemm(gsvk_bert * m, const Proj & W, const float * X, _Float16 * x16, float *
                                 (const float *) W.w, K, X, K, &zero, Y, N));
         return GSVK_OK;
     }
-    const int64_t n = (int64_t) M * K;
-    hipLaunchKernelGGL(k_to_f16, dim3((unsigned) ((n / 4 + 255) / 256 + 1)), dim3(256), 0, m->stream, X, n, x16);
-    GSVK_LAUNCH_CHECK();
+    if (X) {
+        const int64_t n = (int64_t) M * K;
+        hipLaunchKernelGGL(k_to_f16, dim3((unsigned) ((n / 4 + 255) / 256 + 1)), dim3(256), 0, m->stream, X, n, x16);
+        GSVK_LAUNCH_CHECK();
+    }
     GSVK_BLAS(rocblas_gemm_ex(m->blas, rocblas_operation_transpose, rocblas_operation_none, N, M, K, &one, W.w,
                               rocblas_datatype_f16_r, K, x16, rocblas_datatype_f16_r, K, &zero, Y,
                               rocblas_datatype_f32_r, N, Y, rocblas_datatype_f32_r, N, rocblas_datatype_f32_r,
@@ -510,16 +546,20 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     const float scale_log2 = 1.4426950408889634f / std::sqrt((float) BA_HD);
     for (int li = 0; li < n_layers; li++) {
         const BertLayer & w = m->L[li];
+        // the QKV bias is added as attention reads q, k, v; attention and GELU write the fp16
+        // input of an F16 projection directly
         GSVK_TRY(gemm(m, w.qkv, x, x16, qkv, (int) rows, 3 * D, D));
-        GSVK_TRY(gsvk_op_add_act(qkv, w.qkv_b, rows * 3 * D, 3 * D, 0, qkv, st));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
-                           dim3(64), 0, st, qkv, d_off, d_len, D, scale_log2, att);
+                           dim3(64), 0, st, qkv, w.qkv_b, d_off, d_len, D, scale_log2, att,
+                           w.ao.f16 ? x16 : nullptr);
         GSVK_LAUNCH_CHECK();
-        GSVK_TRY(gemm(m, w.ao, att, x16, prj, (int) rows, D, D));
+        GSVK_TRY(gemm(m, w.ao, w.ao.f16 ? nullptr : att, x16, prj, (int) rows, D, D));
         GSVK_TRY(launch_layernorm(x, prj, w.ao_b, w.ln1, rows, D, in.ln_eps, x, nullptr, nullptr, st));
         GSVK_TRY(gemm(m, w.ff1, x, x16, h, (int) rows, F, D));
-        GSVK_TRY(gsvk_op_add_act(h, w.ff1_b, rows * F, F, 2, h, st));
-        GSVK_TRY(gemm(m, w.ff2, h, x16, prj, (int) rows, D, F));
+        hipLaunchKernelGGL(k_bias_gelu, dim3((unsigned) ((rows * F / 4 + 255) / 256)), dim3(256), 0, st, h, w.ff1_b,
+                           rows, F, w.ff2.f16 ? x16 : nullptr);
+        GSVK_LAUNCH_CHECK();
+        GSVK_TRY(gemm(m, w.ff2, w.ff2.f16 ? nullptr : h, x16, prj, (int) rows, D, F));
         GSVK_TRY(launch_layernorm(x, prj, w.ff2_b, w.ln2, rows, D, in.ln_eps, x, nullptr, nullptr, st));
     }
     // [rows][D] -> per sequence [D][len] (src/gsv_bert.cpp:220-228)
