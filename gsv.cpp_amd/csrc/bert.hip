@@ -14,9 +14,9 @@
 // with the activations rounded to fp16 and fp32 sums (ggml-cpu converts the activations to the
 // weights' F16 dot type), Q8_0 weight files widened to fp32 at load; bias,
 // GELU and the residual LayerNorms are this library's kernels (norm.hip); attention is
-// k_bert_attn below: one wave per 16 queries of one (sequence, head), four lanes per query
-// (a quarter of the head dims each), keys and values staged through LDS in tiles of 64, an
-// online softmax per chunk of 16 keys, fp32 throughout.
+// k_bert_attn below: one workgroup per 16 queries of one (sequence, head), four lanes per query
+// (a quarter of the head dims each), keys and values staged through LDS in tiles of 64 whose 4
+// chunks of 16 keys go to its 4 waves (online softmax each, merged at the end), fp32 throughout.
 #include <rocblas/rocblas.h>
 
 #include <cmath>
@@ -36,7 +36,7 @@ namespace {
 constexpr int BA_HD = 64;   // head dim of the kernels below (BERT-large: 1024 / 16)
 constexpr int BA_KT = 64;   // keys per LDS tile
 constexpr int BA_CH = 16;   // keys per softmax chunk
-constexpr int BA_Q = 16;    // queries per workgroup (one wave: 4 lanes per query)
+constexpr int BA_Q = 16;    // queries per workgroup (4 lanes per query in each of its 4 waves)
 
 // x[r] = word[id_r] + pos[t_r] + type0 (the sum order of src/gsv_bert.cpp:141-144); one
 // workgroup of 256 threads per row, 4 values per thread and pass.
@@ -57,32 +57,37 @@ __global__ void __launch_bounds__(256) k_bert_embed(const float * __restrict__ w
     }
 }
 
-// Attention of one (sequence b, head h) for queries [16 * blockIdx.x, +16): lane = 4 * query +
-// quarter, the quarter c holding dims [16c, 16c + 16) of the query and of its output (a score is
-// the sum of the 4 quarters' partial dots, exchanged within the lane quad). The sequence's rows
-// are [off_b, off_b + len_b) of qkv (row stride 3D: q | k | v, head h at 64h); every query sees
-// every key of its sequence (the block-diagonal mask of src/gsv_bert.cpp:289-296). Keys and
-// values are staged through LDS in tiles of 64; an online softmax runs per chunk of 16 keys, in
-// log2 units (scores scaled by log2(e) / sqrt(64), the hardware exp2).
-// Output rows of queries past len_b are not written.
-__global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv,
-                                                  const float * __restrict__ qkv_b,
-                                                  const int32_t * __restrict__ seq_off,
-                                                  const int32_t * __restrict__ seq_len, int D,
-                                                  float scale_log2, float * __restrict__ out,
-                                                  _Float16 * __restrict__ out16) {
+// Attention of one (sequence b, head h) for queries [16 * blockIdx.x, +16). Workgroup = 4 waves
+// over the same 16 queries; in each wave lane = 4 * query + quarter, the quarter c holding dims
+// [16c, 16c + 16) of the query and of its output (a score is the sum of the 4 quarters' partial
+// dots, exchanged within the lane quad on DPP). Keys and values (plus their bias: the QKV bias
+// is added here, as the projection's epilogue would) are staged through LDS in tiles of 64; wave
+// w takes the chunk of 16 keys w of each tile with an online softmax in log2 units (the
+// hardware exp2), and the 4 waves' (m, l, o) are merged through LDS at the end. The sequence's
+// rows are [off_b, off_b + len_b) of qkv (row stride 3D: q | k | v, head h at 64h); every query
+// sees every key of its sequence (the block-diagonal mask of src/gsv_bert.cpp:289-296). Output
+// rows of queries past len_b are not written.
+__global__ void __launch_bounds__(256) k_bert_attn(const float * __restrict__ qkv,
+                                                   const float * __restrict__ qkv_b,
+                                                   const int32_t * __restrict__ seq_off,
+                                                   const int32_t * __restrict__ seq_len, int D,
+                                                   float scale_log2, float * __restrict__ out,
+                                                   _Float16 * __restrict__ out16) {
     const int h = blockIdx.y, b = blockIdx.z;
     const int len = seq_len[b];
     const int64_t off = seq_off[b];
     const int q0 = blockIdx.x * BA_Q;
     if (q0 >= len) return;   // uniform over the workgroup
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const int qq = lane >> 2, c = lane & 3;
     const int64_t rs = 3 * (int64_t) D;
     const int qi = min(q0 + qq, len - 1);
 
     __shared__ float4 ks[BA_KT][BA_HD / 4];
     __shared__ float4 vs[BA_KT][BA_HD / 4];
+    __shared__ float s_ml[4][64][2];
+    __shared__ float4 s_o[4][64][4];
 
     float q[16];
     {
@@ -103,10 +108,10 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
 
     for (int k0 = 0; k0 < len; k0 += BA_KT) {
         __syncthreads();   // the previous tile has been read
-        // 64 keys x 16 float4 of K and of V: 16 consecutive lanes read one key's 256 bytes
+        // 64 keys x 16 float4 of K and of V: 16 consecutive threads read one key's 256 bytes
 #pragma unroll
-        for (int r = 0; r < BA_KT * (BA_HD / 4) / 64; r++) {
-            const int idx = r * 64 + lane, key = idx >> 4, part = idx & 15;
+        for (int r = 0; r < BA_KT * (BA_HD / 4) / 256; r++) {
+            const int idx = r * 256 + tid, key = idx >> 4, part = idx & 15;
             const int kr = min(k0 + key, len - 1);   // keys past the end repeat the last (unused)
             const float * row = qkv + (off + kr) * rs + h * BA_HD + 4 * part;
             const float4 kv = *reinterpret_cast<const float4 *>(row + D), kb = kbias[part];
@@ -116,7 +121,8 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
         }
         __syncthreads();
         const int nk = min(BA_KT, len - k0);
-        for (int c0 = 0; c0 < nk; c0 += BA_CH) {
+        const int c0 = wave * BA_CH;   // this wave's chunk of the tile
+        if (c0 < nk) {                 // uniform per wave
             float s[BA_CH];
             float cmax = -INFINITY;
 #pragma unroll
@@ -135,7 +141,7 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
                 s[j] = c0 + j < nk ? dot * scale_log2 : -INFINITY;
                 cmax = fmaxf(cmax, s[j]);
             }
-            const float mn = fmaxf(m, cmax);            // finite: each chunk has a key
+            const float mn = fmaxf(m, cmax);                  // finite: the chunk has a key
             const float f = __builtin_amdgcn_exp2f(m - mn);   // 0 on the first chunk (m = -inf)
             l *= f;
 #pragma unroll
@@ -156,18 +162,44 @@ __global__ void __launch_bounds__(64) k_bert_attn(const float * __restrict__ qkv
             }
         }
     }
-    if (q0 + qq >= len) return;
-    const float inv = 1.0f / l;
+    // merge the 4 waves (a wave that saw no key has m = -inf and weight 0)
+    s_ml[wave][lane][0] = m;
+    s_ml[wave][lane][1] = l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) s_o[wave][lane][i] = make_float4(o[4 * i], o[4 * i + 1], o[4 * i + 2], o[4 * i + 3]);
+    __syncthreads();
+    if (wave != 0 || q0 + qq >= len) return;
+    float M = s_ml[0][lane][0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) M = fmaxf(M, s_ml[w][lane][0]);
+    float L = 0.0f, O[16];
+#pragma unroll
+    for (int d = 0; d < 16; d++) O[d] = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        const float mw = s_ml[w][lane][0];
+        const float f = mw == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
+        L = __builtin_fmaf(s_ml[w][lane][1], f, L);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float4 ow = s_o[w][lane][i];
+            O[4 * i] = __builtin_fmaf(ow.x, f, O[4 * i]);
+            O[4 * i + 1] = __builtin_fmaf(ow.y, f, O[4 * i + 1]);
+            O[4 * i + 2] = __builtin_fmaf(ow.z, f, O[4 * i + 2]);
+            O[4 * i + 3] = __builtin_fmaf(ow.w, f, O[4 * i + 3]);
+        }
+    }
+    const float inv = 1.0f / L;
     const int64_t o0 = (off + q0 + qq) * (int64_t) D + h * BA_HD + 16 * c;
     if (out16) {   // the fp16 input of an F16 out projection
 #pragma unroll
-        for (int d = 0; d < 16; d++) out16[o0 + d] = (_Float16) (o[d] * inv);
+        for (int d = 0; d < 16; d++) out16[o0 + d] = (_Float16) (O[d] * inv);
         return;
     }
     float4 * op = reinterpret_cast<float4 *>(out + o0);
 #pragma unroll
     for (int i = 0; i < 4; i++)
-        op[i] = make_float4(o[4 * i] * inv, o[4 * i + 1] * inv, o[4 * i + 2] * inv, o[4 * i + 3] * inv);
+        op[i] = make_float4(O[4 * i] * inv, O[4 * i + 1] * inv, O[4 * i + 2] * inv, O[4 * i + 3] * inv);
 }
 
 // h = gelu_erf(h + b[col]) (the add_act of src/gsv_bert.cpp:151-153, as norm.hip's k_add_act),
@@ -550,7 +582,7 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
         // input of an F16 projection directly
         GSVK_TRY(gemm(m, w.qkv, x, x16, qkv, (int) rows, 3 * D, D));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
-                           dim3(64), 0, st, qkv, w.qkv_b, d_off, d_len, D, scale_log2, att,
+                           dim3(256), 0, st, qkv, w.qkv_b, d_off, d_len, D, scale_log2, att,
                            w.ao.f16 ? x16 : nullptr);
         GSVK_LAUNCH_CHECK();
         GSVK_TRY(gemm(m, w.ao, w.ao.f16 ? nullptr : att, x16, prj, (int) rows, D, D));
