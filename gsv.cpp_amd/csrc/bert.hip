@@ -574,25 +574,30 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     hipLaunchKernelGGL(k_bert_embed, dim3((unsigned) rows), dim3(256), 0, st, m->word, m->pos, m->type0, d_ids,
                        d_pos, D, prj);
     GSVK_LAUNCH_CHECK();
-    GSVK_TRY(launch_layernorm(prj, nullptr, nullptr, m->emb_ln, rows, D, in.ln_eps, x, nullptr, nullptr, st));
+    // each LayerNorm also writes the fp16 copy its consumer takes when that is an F16 projection
+    auto h16_for = [&](int li) { return li < n_layers && m->L[li].qkv.f16 ? (uint16_t *) x16 : nullptr; };
+    GSVK_TRY(launch_layernorm(prj, nullptr, nullptr, m->emb_ln, rows, D, in.ln_eps, x, nullptr, nullptr, st,
+                              Q8_SLICED, h16_for(0)));
     const float scale_log2 = 1.4426950408889634f / std::sqrt((float) BA_HD);
     for (int li = 0; li < n_layers; li++) {
         const BertLayer & w = m->L[li];
-        // the QKV bias is added as attention reads q, k, v; attention and GELU write the fp16
-        // input of an F16 projection directly
-        GSVK_TRY(gemm(m, w.qkv, x, x16, qkv, (int) rows, 3 * D, D));
+        // the QKV bias is added as attention reads q, k, v; the LayerNorms, attention and GELU
+        // write the fp16 input of an F16 projection directly
+        GSVK_TRY(gemm(m, w.qkv, w.qkv.f16 ? nullptr : x, x16, qkv, (int) rows, 3 * D, D));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
                            dim3(256), 0, st, qkv, w.qkv_b, d_off, d_len, D, scale_log2, att,
                            w.ao.f16 ? x16 : nullptr);
         GSVK_LAUNCH_CHECK();
         GSVK_TRY(gemm(m, w.ao, w.ao.f16 ? nullptr : att, x16, prj, (int) rows, D, D));
-        GSVK_TRY(launch_layernorm(x, prj, w.ao_b, w.ln1, rows, D, in.ln_eps, x, nullptr, nullptr, st));
-        GSVK_TRY(gemm(m, w.ff1, x, x16, h, (int) rows, F, D));
+        GSVK_TRY(launch_layernorm(x, prj, w.ao_b, w.ln1, rows, D, in.ln_eps, x, nullptr, nullptr, st, Q8_SLICED,
+                                  w.ff1.f16 ? (uint16_t *) x16 : nullptr));
+        GSVK_TRY(gemm(m, w.ff1, w.ff1.f16 ? nullptr : x, x16, h, (int) rows, F, D));
         hipLaunchKernelGGL(k_bias_gelu, dim3((unsigned) ((rows * F / 4 + 255) / 256)), dim3(256), 0, st, h, w.ff1_b,
                            rows, F, w.ff2.f16 ? x16 : nullptr);
         GSVK_LAUNCH_CHECK();
         GSVK_TRY(gemm(m, w.ff2, w.ff2.f16 ? nullptr : h, x16, prj, (int) rows, D, F));
-        GSVK_TRY(launch_layernorm(x, prj, w.ff2_b, w.ln2, rows, D, in.ln_eps, x, nullptr, nullptr, st));
+        GSVK_TRY(launch_layernorm(x, prj, w.ff2_b, w.ln2, rows, D, in.ln_eps, x, nullptr, nullptr, st, Q8_SLICED,
+                                  h16_for(li + 1)));
     }
     // [rows][D] -> per sequence [D][len] (src/gsv_bert.cpp:220-228)
     std::vector<float> host((size_t) rows * D);

@@ -272,9 +272,10 @@ int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, fl
 int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
                      hipStream_t stream, int8_t * qn = nullptr, int8_t * qt = nullptr,
                      uint16_t * dt = nullptr);
+// (y16: optional fp16 copy of y, rounded to nearest even)
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, int layout = Q8_SLICED);
+                     hipStream_t stream, int layout = Q8_SLICED, uint16_t * y16 = nullptr);
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
                     int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, const int32_t * pos_sub,

@@ -22,7 +22,8 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
                                                   const float * __restrict__ wb, int rows, int n,
                                                   float eps, float * __restrict__ y,
                                                   int8_t * __restrict__ yq,
-                                                  float * __restrict__ yd, int layout) {
+                                                  float * __restrict__ yd, int layout,
+                                                  uint16_t * __restrict__ y16) {
     // one wave per row, up to 4 rows per workgroup (the waves are independent: no barrier)
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -89,6 +90,7 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
             for (int i = 0; i < 8; i++) {
                 o[i] = __builtin_fmaf((v[c][i] - mean) * inv, w[base + i], b[base + i]);
                 yr[base + i] = o[i];
+                if (y16) y16[(int64_t) row * n + base + i] = f2h(o[i]);   // fp16 copy, nearest even
             }
         }
         if (yq && (64 * c) < nchunk) {   // uniform across the wave
@@ -165,7 +167,7 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
 
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, int layout) {
+                     hipStream_t stream, int layout, uint16_t * y16) {
     GSVK_REQUIRE(x && wb && y, "layernorm: null pointer");
     GSVK_REQUIRE(rows >= 0 && rows < (1 << 30) && n > 0 && n % 32 == 0 && n <= 4096,
                  "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
@@ -181,13 +183,13 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block(64 * rpw);
     if (n <= 512)
         hipLaunchKernelGGL(k_layernorm<1>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout);
+                           (int) n, eps, y, yq, yd, layout, y16);
     else if (n <= 1024)
         hipLaunchKernelGGL(k_layernorm<2>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout);
+                           (int) n, eps, y, yq, yd, layout, y16);
     else
         hipLaunchKernelGGL(k_layernorm<8>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout);
+                           (int) n, eps, y, yq, yd, layout, y16);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
