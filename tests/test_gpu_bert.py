@@ -89,3 +89,34 @@ def test_quantised_weight_files(gpu, tmp_path_factory, wtype):
         _check(m.encode([ids])[0], BO.encode(W, ids, 1, 1024, 16, 1e-12, act_f16=wtype == "f16"))
     finally:
         m.close()
+
+
+def test_gsv_bert_class_drop_in(bert_f32, tmp_path_factory):
+    """The C++ gsv_bert class (include/gsv_bert.h) through every member, driven by
+    tests/dropin/gsv_bert_check.cpp (built by oracle/Makefile, target bertcheck)."""
+    import os
+    import subprocess
+    binp = os.path.join(os.path.dirname(os.path.abspath(__file__)), "dropin", "gsv_bert_check")
+    if not os.path.exists(binp):
+        pytest.skip("tests/dropin/gsv_bert_check was not built")
+    m, W = bert_f32
+    d = tmp_path_factory.mktemp("bert_class")
+    path, _ = sm.write_bert_model(str(d / "b.gguf"), n_layer=4, layers_used=2, vocab=1000)   # same seed
+    p = subprocess.run([binp, path], capture_output=True, text=True, timeout=180)
+    print(p.stdout, p.stderr)
+    assert p.returncode == 0, p.stderr
+    out = {l.split()[0]: l.split()[1:] for l in p.stdout.splitlines() if l.strip()}
+    assert out["load_cpu_null"] == ["1"] and out["load_missing_null"] == ["1"]
+    assert out["info"] == ["1024", "2", "512"]
+    s1 = np.array([1, 17, 29, 4, 811, 2], np.int32)
+    e = m.encode([s1])[0].astype(np.float64).ravel()
+    ref = float(np.sum(e * (np.arange(e.size) % 7 + 1)))
+    assert abs(float(out["encode_checksum"][0]) - ref) <= 1e-6 * np.sum(np.abs(e) * 7)
+    assert out["feat_ok"] == ["1"]
+    assert out["cache"] == ["1", "4", "1"]                         # hits, misses, cached == uncached
+    ok, n1, n2, rel = out["batch"]
+    assert ok == "1" and int(n1) == 1024 * 4 and int(n2) == 1024 * 7 and float(rel) <= 1e-5
+    assert out["batch_bad_args"] == ["1"]
+    assert out["layers"] == ["3", "1"]                             # depths 0..2; the last equals encode
+    assert out["too_long_empty"] == ["1"]
+    assert "done" in out
