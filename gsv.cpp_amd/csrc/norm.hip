@@ -15,7 +15,7 @@ namespace gsvk {
 // writes exactly those two FMAs, so every other operation rounds where the C expression does.
 // ---------------------------------------------------------------------------------------
 
-template <int MAXC>
+template <int MAXC, bool F16OUT>
 __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
                                                   const float * __restrict__ r,
                                                   const float * __restrict__ bias,
@@ -90,7 +90,7 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
             for (int i = 0; i < 8; i++) {
                 o[i] = __builtin_fmaf((v[c][i] - mean) * inv, w[base + i], b[base + i]);
                 yr[base + i] = o[i];
-                if (y16) y16[(int64_t) row * n + base + i] = f2h(o[i]);   // fp16 copy, nearest even
+                if constexpr (F16OUT) y16[(int64_t) row * n + base + i] = f2h(o[i]);   // fp16 copy, nearest even
             }
         }
         if (yq && (64 * c) < nchunk) {   // uniform across the wave
@@ -181,15 +181,18 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     // prefill) launch slower than the rows take
     const int rpw = rows >= 64 ? 4 : 1;
     const dim3 grid((unsigned) ((rows + rpw - 1) / rpw)), block(64 * rpw);
-    if (n <= 512)
-        hipLaunchKernelGGL(k_layernorm<1>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout, y16);
-    else if (n <= 1024)
-        hipLaunchKernelGGL(k_layernorm<2>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout, y16);
-    else
-        hipLaunchKernelGGL(k_layernorm<8>, grid, block, 0, stream, x, r, bias, wb, (int) rows,
-                           (int) n, eps, y, yq, yd, layout, y16);
+    // (the fp16 copy is a separate instantiation: the kernel without it stays as it was)
+#define GSVK_LN(C, H)                                                                              \
+    hipLaunchKernelGGL((k_layernorm<C, H>), grid, block, 0, stream, x, r, bias, wb, (int) rows, (int) n, eps, \
+                       y, yq, yd, layout, y16)
+    if (n <= 512) {
+        if (y16) GSVK_LN(1, true); else GSVK_LN(1, false);
+    } else if (n <= 1024) {
+        if (y16) GSVK_LN(2, true); else GSVK_LN(2, false);
+    } else {
+        if (y16) GSVK_LN(8, true); else GSVK_LN(8, false);
+    }
+#undef GSVK_LN
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
