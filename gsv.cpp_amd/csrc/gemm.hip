@@ -269,21 +269,20 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
 // (lane (li, lg): 16 values of row/column li, half lg of the block), a group of blocks ahead of
 // its use. The four partial tiles are summed through LDS in wave order, so the result does not
 // depend on timing. Same arithmetic per block as k_q8_gemm.
-constexpr int GS_THREADS = 256;
 constexpr int64_t GS_MAX_ROWS = 256;      // launch_q8_gemm takes this kernel up to this many rows
 
-template <int NBLK, int MT>
-__global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n, int m,
+template <int NBLK, int MT, int W = 4>   // W waves, each a W-th of K
+__global__ void __launch_bounds__(W * 64) k_q8_gemm_small(Q8Weights w, int n, int m,
                                                                 const int8_t * __restrict__ xs,
                                                                 const float * __restrict__ xd,
                                                                 bool x_tiled, LayerOut out) {
-    constexpr int NBW = NBLK / 4;                                  // blocks per wave
+    constexpr int NBW = NBLK / W;                                  // blocks per wave
     // blocks per load group: every load at once for one row tile (16 blocks = 128 VGPRs of
     // operands), two or eight groups for more rows
     constexpr int G = (NBW <= 4 || MT == 1) ? NBW : (MT == 2 ? NBW / 2 : 2);
     constexpr int NG = NBW / G;
     static_assert(NBW % G == 0, "load groups must tile the wave's blocks");
-    __shared__ float red[4][32 * MT][33];
+    __shared__ float red[W][32 * MT][33];
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -376,16 +375,22 @@ __global__ void __launch_bounds__(GS_THREADS) k_q8_gemm_small(Q8Weights w, int n
         for (int v = 0; v < 16; v++) red[wave][32 * t + 8 * (v >> 2) + 4 * lg + (v & 3)][li] = acc[t][v];
     __syncthreads();
 
-    // epilogue: thread -> row (tid / 8) + 32 i, columns 4 * (tid % 8) .. + 4 of the tile
+    // epilogue: thread -> row (tid / 8) + 8 W i, columns 4 * (tid % 8) .. + 4 of the tile
+    constexpr int RPP = 8 * W;   // rows per pass
 #pragma unroll
-    for (int i = 0; i < MT; i++) {
-        const int r = (tid >> 3) + 32 * i;
+    for (int i = 0; i < (32 * MT + RPP - 1) / RPP; i++) {
+        const int r = (tid >> 3) + RPP * i;
+        if (RPP > 32 * MT && r >= 32 * MT) break;
         const int row = m0 + r;
         const bool valid = row < m;
         float y[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++)
-            y[c] = ((red[0][r][4 * cg + c] + red[1][r][4 * cg + c]) + red[2][r][4 * cg + c]) + red[3][r][4 * cg + c];
+        for (int c = 0; c < 4; c++) {
+            float t = red[0][r][4 * cg + c];   // the waves' partials in wave order
+#pragma unroll
+            for (int q = 1; q < W; q++) t = t + red[q][r][4 * cg + c];
+            y[c] = t;
+        }
         if (out.bias) {
             y[0] = y[0] + bias4.x; y[1] = y[1] + bias4.y; y[2] = y[2] + bias4.z; y[3] = y[3] + bias4.w;
         }
@@ -435,17 +440,21 @@ int launch_q8_gemm_small(const Q8Weights & w, int64_t n, int64_t k, int64_t m, c
     if (mt == 0) mt = m <= 64 ? 1 : 2;
     GSVK_REQUIRE(mt == 1 || mt == 2 || mt == 4, "q8_gemm: row tiles per workgroup must be 1, 2 or 4");
     const dim3 grid((unsigned) (n / 32), (unsigned) ((m + 32 * mt - 1) / (32 * mt)));
-#define GSVK_GS(NB, MT) \
-    hipLaunchKernelGGL((k_q8_gemm_small<NB, MT>), grid, dim3(GS_THREADS), 0, stream, w, (int) n, (int) m, xs, xd, \
+#define GSVK_GS(NB, MT, W) \
+    hipLaunchKernelGGL((k_q8_gemm_small<NB, MT, W>), grid, dim3(W * 64), 0, stream, w, (int) n, (int) m, xs, xd, \
                        x_tiled, out)
+    // a 512-column projection has only 16 column tiles: 8 waves per workgroup (each an eighth
+    // of K) put twice the waves on the chip and halve each wave's chain
+    // (for every row tiling alike, so that the tiling does not change a bit of the result)
+    const bool wide = n == 512;
     if (k == 512) {
-        if (mt == 1) GSVK_GS(16, 1);
-        else if (mt == 2) GSVK_GS(16, 2);
-        else GSVK_GS(16, 4);
+        if (mt == 1) { if (wide) GSVK_GS(16, 1, 8); else GSVK_GS(16, 1, 4); }
+        else if (mt == 2) { if (wide) GSVK_GS(16, 2, 8); else GSVK_GS(16, 2, 4); }
+        else { if (wide) GSVK_GS(16, 4, 8); else GSVK_GS(16, 4, 4); }
     } else {
-        if (mt == 1) GSVK_GS(64, 1);
-        else if (mt == 2) GSVK_GS(64, 2);
-        else GSVK_GS(64, 4);
+        if (mt == 1) { if (wide) GSVK_GS(64, 1, 8); else GSVK_GS(64, 1, 4); }
+        else if (mt == 2) { if (wide) GSVK_GS(64, 2, 8); else GSVK_GS(64, 2, 4); }
+        else { if (wide) GSVK_GS(64, 4, 8); else GSVK_GS(64, 4, 4); }
     }
 #undef GSVK_GS
     GSVK_LAUNCH_CHECK();
