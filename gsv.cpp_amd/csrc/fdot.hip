@@ -13,6 +13,7 @@
 //
 // For F16 weights the activations are first rounded to fp16 (ggml's vec_dot_type for F16).
 #include "common.h"
+#include "layer_dev.h"
 
 namespace gsvk {
 
@@ -138,11 +139,18 @@ __global__ void __launch_bounds__(256) k_fdot_ggml_t(const WT * __restrict__ W, 
 // as k_fdot_ggml, with every load issued up front. The MT activation rows (rounded to fp16 for
 // F16 weights) are staged once per workgroup in LDS with 16-byte loads; each lane loads its NI
 // weights before the first use. 256 threads = 8 rows x 32 lanes; grid (ceil(n/8), ceil(m/MT)).
-template <typename WT, int MT, int NI>
+// LNIN: the MT rows are LayerNorm((res + r) + bias) * w + b of the decoder's last layer,
+// computed here (one wave per row, the arithmetic of the LayerNorm kernel) instead of read from X.
+struct LnSrc {
+    const float * res, * r, * bias, * wb;
+};
+
+template <typename WT, int MT, int NI, bool LNIN = false>
 __global__ void __launch_bounds__(256) k_fdot_ggml_k(const WT * __restrict__ W, int n,
                                                      const float * __restrict__ X, int64_t xs, int m,
-                                                     float * __restrict__ Y, int64_t ys) {
+                                                     float * __restrict__ Y, int64_t ys, LnSrc ln) {
     constexpr int K = 32 * NI;
+    static_assert(!LNIN || (K == 512 && MT % 4 == 0), "LayerNorm input: rows of 512, MT / 4 rows per wave");
     const bool x16 = sizeof(WT) == 2;
     const int tid = threadIdx.x;
     const int p = tid & 31;
@@ -151,26 +159,49 @@ __global__ void __launch_bounds__(256) k_fdot_ggml_k(const WT * __restrict__ W, 
     const int rowc = row < n ? row : n - 1;
     __shared__ __align__(16) float s_x[MT][K];
     constexpr int X4 = MT * K / 4;                       // float4 chunks of the MT rows
-    constexpr int XN = (X4 + 255) / 256;
+    constexpr int XN = LNIN ? 1 : (X4 + 255) / 256;
+    constexpr int LR = LNIN ? MT / 4 : 1;                // LayerNorm rows per wave
     float4 xv[XN];
+    LnRow lr[LR];
+    const int wave = tid >> 6, lane = tid & 63;
+    if constexpr (LNIN) {
 #pragma unroll
-    for (int u = 0; u < XN; u++) {
-        int c = tid + u * 256;
-        c = c < X4 ? c : X4 - 1;
-        const int mm = min(m0 + c / (K / 4), m - 1);
-        xv[u] = *reinterpret_cast<const float4 *>(X + (int64_t) mm * xs + (c % (K / 4)) * 4);
+        for (int u = 0; u < LR; u++) {
+            const int mm = min(m0 + wave + 4 * u, m - 1);
+            ln_row_load(ln.res + (int64_t) mm * K, ln.r ? ln.r + (int64_t) mm * K : g_zero_row,
+                        ln.bias ? ln.bias : g_zero_row, ln.wb, lane, lr[u]);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < XN; u++) {
+            int c = tid + u * 256;
+            c = c < X4 ? c : X4 - 1;
+            const int mm = min(m0 + c / (K / 4), m - 1);
+            xv[u] = *reinterpret_cast<const float4 *>(X + (int64_t) mm * xs + (c % (K / 4)) * 4);
+        }
     }
     const WT * wr = W + (int64_t) rowc * K;
     float w[NI];
 #pragma unroll
     for (int i = 0; i < NI; i++) w[i] = wload<WT>(wr + 32 * i + p);
+    if constexpr (LNIN) {
 #pragma unroll
-    for (int u = 0; u < XN; u++) {
-        const int c = tid + u * 256;
-        if (c < X4) {
-            float4 v = xv[u];
-            v.x = xconv(v.x, x16); v.y = xconv(v.y, x16); v.z = xconv(v.z, x16); v.w = xconv(v.w, x16);
-            *reinterpret_cast<float4 *>(&s_x[c / (K / 4)][(c % (K / 4)) * 4]) = v;
+        for (int u = 0; u < LR; u++) {
+            float o[8];
+            ln_row_compute(lr[u], o);
+            float * dst = &s_x[wave + 4 * u][lane * 8];
+#pragma unroll
+            for (int i = 0; i < 8; i++) dst[i] = xconv(o[i], x16);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < XN; u++) {
+            const int c = tid + u * 256;
+            if (c < X4) {
+                float4 v = xv[u];
+                v.x = xconv(v.x, x16); v.y = xconv(v.y, x16); v.z = xconv(v.z, x16); v.w = xconv(v.w, x16);
+                *reinterpret_cast<float4 *>(&s_x[c / (K / 4)][(c % (K / 4)) * 4]) = v;
+            }
         }
     }
     __syncthreads();
@@ -255,10 +286,10 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
         const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MTK - 1) / MTK));
         if (wtype == 1)
             hipLaunchKernelGGL((k_fdot_ggml_k<uint16_t, MTK, 16>), grid, dim3(256), 0, stream,
-                               (const uint16_t *) W, (int) n, X, xs, (int) m, Y, ys);
+                               (const uint16_t *) W, (int) n, X, xs, (int) m, Y, ys, LnSrc{});
         else
             hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16>), grid, dim3(256), 0, stream,
-                               (const float *) W, (int) n, X, xs, (int) m, Y, ys);
+                               (const float *) W, (int) n, X, xs, (int) m, Y, ys, LnSrc{});
     } else if (m >= 64) {
         constexpr int RN = 4, MTT = 16;
         const dim3 grid((unsigned) ((n + 8 * RN - 1) / (8 * RN)), (unsigned) ((m + MTT - 1) / MTT));
@@ -277,6 +308,32 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
             hipLaunchKernelGGL((k_fdot_ggml<float, MT>), grid, dim3(256), 0, stream,
                                (const float *) W, (int) n, (int) k, X, xs, (int) m, Y, ys);
     }
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk
+
+namespace gsvk {
+
+// The decode head (K = 512, mode 0) with the last layer's LayerNorm as its input stage: logits
+// of m rows of LayerNorm((res + r) + bias) * w + b, in the order of launch_fdot's K = 512 kernel.
+int launch_head_ln(const void * W, int wtype, int64_t n, const float * res, const float * r, const float * bias,
+                   const float * wb, int64_t m, float * Y, int64_t ys, hipStream_t stream) {
+    GSVK_REQUIRE(W && res && wb && Y && (wtype == 0 || wtype == 1) && n > 0 && n < (1 << 30) && m > 0 &&
+                     m < (1 << 30) && ys >= n,
+                 "head_ln: bad arguments");
+    auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
+    GSVK_REQUIRE(al16(res) && al16(r) && al16(bias) && al16(wb), "head_ln: operands must be 16-byte aligned");
+    constexpr int MTK = 8;
+    const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MTK - 1) / MTK));
+    const LnSrc ln{res, r, bias, wb};
+    if (wtype == 1)
+        hipLaunchKernelGGL((k_fdot_ggml_k<uint16_t, MTK, 16, true>), grid, dim3(256), 0, stream,
+                           (const uint16_t *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
+    else
+        hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16, true>), grid, dim3(256), 0, stream,
+                           (const float *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

@@ -19,6 +19,8 @@
 namespace gsvk {
 
 // kernels defined in the other translation units
+int launch_head_ln(const void * W, int wtype, int64_t n, const float * res, const float * r, const float * bias,
+                   const float * wb, int64_t m, float * Y, int64_t ys, hipStream_t stream);
 int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
                 int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream);
 int launch_build_xy(const float * text_emb, const float * audio_emb, const float * pe,
@@ -454,6 +456,19 @@ int final_ln(gsvk_model * m, hipStream_t st, int64_t R, const float * n1x, const
                             q ? x.d : nullptr, st);
 }
 
+// Logits of a decode step: the last layer's LN2 then the head. An F16 / F32 head takes the
+// LayerNorm as its input stage (the same arithmetic as the LayerNorm launch, one launch fewer).
+int decode_head(gsvk_model * m, int n, const float * n1x, const float * h2, Act & x, float * logits,
+                hipStream_t st) {
+    if (m->head_type != GGML_Q8_0 && m->D == 512) {
+        const LayerW & w = m->L[m->NL - 1];
+        return launch_head_ln(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, n1x, h2, w.f2.b, w.ln2, n,
+                              logits, m->V, st);
+    }
+    GSVK_TRY(final_ln(m, st, n, n1x, h2, x));
+    return head_logits(m, x, n, 0, logits, st);
+}
+
 // Kernels of one decode step at loop index idx = *d_step - 1: the layer-0 QKV embeds last_tok at
 // PE position prompt_len + idx (and sets kv_end = S + idx + 1); every QKV appends K/V at column
 // S + idx; logits of the head.
@@ -485,8 +500,7 @@ int enqueue_decode_mfma(gsvk_model * m) {
                                     Q8_TILED));
         GSVK_TRY(layer_tail(m, m->stream, w, B, m->x.x, m->attn, m->o, m->n1.x, m->hq, m->h2, &m->n1, Q8_TILED));
     }
-    GSVK_TRY(final_ln(m, m->stream, B, m->n1.x, m->h2, m->x));
-    return head_logits(m, m->x, B, 0, m->logits, m->stream);
+    return decode_head(m, B, m->n1.x, m->h2, m->x, m->logits, m->stream);
 }
 
 // GEMV path, batch rows [r0, r0 + n) on stream st. Every kernel of it computes each row on its
@@ -558,8 +572,7 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
         }
         GSVK_TRY(layer_tail(m, st, w, n, x.x, attn, o, n1.x, hq, h2));
     }
-    GSVK_TRY(final_ln(m, st, n, n1.x, h2, x));
-    return head_logits(m, x, n, 0, m->logits + (size_t) r0 * m->V, st);
+    return decode_head(m, n, n1.x, h2, x, m->logits + (size_t) r0 * m->V, st);
 }
 
 int enqueue_decode_body(gsvk_model * m) {
