@@ -23,11 +23,13 @@ namespace gsvk {
 constexpr int LG_THREADS = 256;
 constexpr int LG_ROWS = 32;   // output rows per workgroup
 
-template <int NB4, int MT, int MODE>
-__global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __restrict__ ws,
+template <int NB4, int MT, int MODE, int WAVES = 4>
+__global__ void __launch_bounds__(WAVES * 64) k_layer_gemv(const int8_t * __restrict__ ws,
                                                            const uint16_t * __restrict__ wd, int n,
                                                            int m, LayerIn in, LayerOut out) {
-    static_assert(MODE == IN_Q8 || MT <= LG_THREADS / 64, "one wave per LayerNorm / embedding row");
+    constexpr int NT = WAVES * 64;     // threads
+    constexpr int ROWS = WAVES * 8;    // output rows of the workgroup
+    static_assert(MODE == IN_Q8 || MT <= WAVES, "one wave per LayerNorm / embedding row");
     constexpr int K = NB4 * 128;
     constexpr int NBLK = K / 32;
     const int tid = threadIdx.x;
@@ -35,7 +37,7 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     const int wave = tid >> 6;
     const int r = lane >> 3;
     const int j = lane & 7;
-    const int row = blockIdx.x * LG_ROWS + wave * 8 + r;
+    const int row = blockIdx.x * ROWS + wave * 8 + r;
     const int m0 = blockIdx.y * MT;
     const bool valid = row < n;
     const int rowc = valid ? row : n - 1;
@@ -44,15 +46,15 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     constexpr int SLICE_B = NBLK * 4 + 16;
     __shared__ __align__(16) int8_t s_x[MT][8 * SLICE_B];
     __shared__ __align__(16) float s_d[MT][NBLK];
-    __shared__ float s_out[MT][LG_ROWS];
+    __shared__ float s_out[MT][ROWS];
 
     // Loads go out in the order their data is needed, each thread issuing a fixed number of them
     // (indices clamped rather than skipped, so that no wave-dependent branch separates a load
     // from its use and every wait is exact): the input rows first, then the weights. Waiting for
     // the input then does not wait for the weights, whose HBM latency overlaps the input stage.
     constexpr int CH = K / 16;                                      // 16-byte chunks per row
-    constexpr int QN = (MT * CH + LG_THREADS - 1) / LG_THREADS;     // chunks per thread
-    constexpr int DN = (MT * NBLK + LG_THREADS - 1) / LG_THREADS;   // scales per thread
+    constexpr int QN = (MT * CH + NT - 1) / NT;     // chunks per thread
+    constexpr int DN = (MT * NBLK + NT - 1) / NT;   // scales per thread
     constexpr int CPS = NBLK / 4;                                   // 16-byte chunks per slice
     int4 xq[MODE == IN_Q8 ? QN : 1];
     float xdv[MODE == IN_Q8 ? DN : 1];
@@ -64,14 +66,14 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     if constexpr (MODE == IN_Q8) {
 #pragma unroll
         for (int u = 0; u < QN; u++) {
-            int c = tid + u * LG_THREADS;
+            int c = tid + u * NT;
             c = c < MT * CH ? c : MT * CH - 1;
             const int mm = min(m0 + c / CH, m - 1);
             xq[u] = *reinterpret_cast<const int4 *>(in.xs + (int64_t) mm * K + (c % CH) * 16);
         }
 #pragma unroll
         for (int u = 0; u < DN; u++) {
-            int c = tid + u * LG_THREADS;
+            int c = tid + u * NT;
             c = c < MT * NBLK ? c : MT * NBLK - 1;
             const int mm = min(m0 + c / NBLK, m - 1);
             xdv[u] = in.xd[(int64_t) mm * NBLK + c % NBLK];
@@ -104,7 +106,7 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     if constexpr (MODE == IN_Q8) {
 #pragma unroll
         for (int u = 0; u < QN; u++) {
-            const int c = tid + u * LG_THREADS;
+            const int c = tid + u * NT;
             if (c < MT * CH) {
                 const int t = c / CH, cc = c % CH;
                 *reinterpret_cast<int4 *>(&s_x[t][(cc / CPS) * SLICE_B + (cc % CPS) * 16]) = xq[u];
@@ -112,7 +114,7 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
         }
 #pragma unroll
         for (int u = 0; u < DN; u++) {
-            const int c = tid + u * LG_THREADS;
+            const int c = tid + u * NT;
             if (c < MT * NBLK) s_d[c / NBLK][c % NBLK] = xdv[u];
         }
     } else {
@@ -200,12 +202,12 @@ __global__ void __launch_bounds__(LG_THREADS) k_layer_gemv(const int8_t * __rest
     if (out.yq) {
         __syncthreads();
         // one 32-value block per activation row: block index blockIdx.x of a row of n values
-        for (int t = wave; t < MT; t += LG_THREADS / 64) {
+        for (int t = wave; t < MT; t += NT / 64) {
             const int mm = m0 + t;
-            float v1[1] = {lane < LG_ROWS ? s_out[t][lane] : 0.0f};
+            float v1[1] = {lane < ROWS ? s_out[t][lane] : 0.0f};
             int8_t q1[1];
             const float d = q8_quantize_group<1>(v1, q1, 32);
-            if (mm < m && lane < LG_ROWS) {
+            if (mm < m && lane < ROWS) {
                 const int nblk_out = n / 32;
                 out.yq[(int64_t) mm * n + q8_sliced_offset(nblk_out, blockIdx.x, lane)] = q1[0];
                 if (lane == 0) out.yd[(int64_t) mm * nblk_out + blockIdx.x] = d;
@@ -238,7 +240,12 @@ int launch_layer_gemv(const int8_t * ws, const uint16_t * wd, int64_t n, int64_t
                        dim3(LG_THREADS), 0, stream, ws, wd, (int) n, (int) m, in, out)
     if (k == 512) {
         if (in.mode == IN_Q8) {
-            if (m <= 16) GSVK_LG(4, 1, IN_Q8);
+            if (m <= 16 && !out.yq) {
+                // one wave (8 output rows) per workgroup: the out projection's 512 rows over 64
+                // workgroups per activation row instead of 16 (2.24 -> 2.10 us at batch 16)
+                hipLaunchKernelGGL((k_layer_gemv<4, 1, IN_Q8, 1>), dim3((unsigned) (n / 8), (unsigned) m), dim3(64),
+                                   0, stream, ws, wd, (int) n, (int) m, in, out);
+            } else if (m <= 16) GSVK_LG(4, 1, IN_Q8);
             else if (m <= 64) GSVK_LG(4, 2, IN_Q8);
             else GSVK_LG(4, 4, IN_Q8);
         } else if (in.mode == IN_LN) {
