@@ -118,6 +118,30 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
     const int wave = tid >> 6;
     const int n0 = blockIdx.x * GM_BN;
     const int m0 = blockIdx.y * GM_BM;
+    if (out.row_pad) {   // a tile of padding rows only: zeros out, no products (uniform branch)
+        bool all_pad = true;
+        const int S = out.rows_per_seq;
+        const int mend = min(m0 + GM_BM, m);
+        for (int r0 = m0; r0 < mend && all_pad;) {
+            const int b = r0 / S;
+            const int e = min((b + 1) * S, mend);
+            if (e - b * S > out.row_pad[b]) all_pad = false;
+            r0 = e;
+        }
+        if (all_pad) {
+            const int nblk_out = n / 32;
+            for (int i = tid; i < (mend - m0) * (GM_BN / 4); i += GM_THREADS) {
+                const int row = m0 + i / (GM_BN / 4), c4 = n0 + 4 * (i % (GM_BN / 4));
+                if (out.y && c4 < out.n_store)
+                    *reinterpret_cast<float4 *>(out.y + (int64_t) row * out.y_stride + c4) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (out.yq) {
+                    *reinterpret_cast<int *>(out.yq + (int64_t) row * n + c4) = 0;   // natural order
+                    if ((c4 & 31) == 0) out.yd[(int64_t) row * nblk_out + (c4 >> 5)] = 0.0f;
+                }
+            }
+            return;
+        }
+    }
     const int wm = (wave >> 1) * 64;   // this wave's rows within the tile
     const int wn = (wave & 1) * 64;    // and columns
     const int li = lane & 31;          // MFMA: row of A / column of B held by this lane
@@ -482,6 +506,7 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
         return launch_q8_gemm_small(w, n, k, m, xs, xd, x_layout == Q8_TILED, out, tile_rows, stream);
     GSVK_REQUIRE(tile_rows == 0, "q8_gemm: row tiles are a choice of the small-batch kernel (m <= %lld)",
                  (long long) GS_MAX_ROWS);
+    GSVK_REQUIRE(!out.row_pad || out.rows_per_seq > 0, "q8_gemm: padding rows need rows_per_seq");
     GSVK_REQUIRE(x_layout == Q8_NATURAL && (!out.yq || out.yq_layout == Q8_NATURAL),
                  "q8_gemm: above %lld rows the operands are in natural order", (long long) GS_MAX_ROWS);
     const int8_t * ws = w.qn;

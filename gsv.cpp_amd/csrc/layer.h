@@ -57,6 +57,10 @@ struct LayerOut {
     int rows_per_seq;
     const int32_t * col_ptr;
     int col_add;
+    // (128 x 128 GEMM only) left-padding rows per sequence of rows_per_seq rows: a row tile that
+    // holds only padding rows writes zeros to y / yq / yd and skips its products and K/V (no
+    // query attends a padding key), or null
+    const int32_t * row_pad;
 };
 
 // A Q8_0 weight matrix [n][k] as the GEMMs read it: quants in natural order with the fp16 scales

@@ -369,7 +369,7 @@ Q8Weights q8w(const Lin & l) { return Q8Weights{l.qn, l.d, l.qt, l.dt}; }
 
 int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
                float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr,
-               int layout = Q8_NATURAL) {
+               int layout = Q8_NATURAL, const int32_t * row_pad = nullptr, int rows_per_seq = 0) {
     const int D = m->D, F = m->FFN;
     if (n1) {
         // many rows (the caller's choice): the projections on the matrix cores, LN1 as its own
@@ -379,6 +379,8 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
         oo.y = o;
         oo.y_stride = D;
         oo.n_store = D;
+        oo.row_pad = row_pad;           // (prefill: tiles of left-padding rows are skipped)
+        oo.rows_per_seq = rows_per_seq;
         GSVK_TRY(launch_q8_gemm(q8w(w.out), D, D, R, attn.q, attn.d, layout, oo, st));
         GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout));
         LayerOut ho{};
@@ -387,11 +389,15 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
         ho.yq = hq.q;
         ho.yd = hq.d;
         ho.yq_layout = layout;
+        ho.row_pad = row_pad;
+        ho.rows_per_seq = rows_per_seq;
         GSVK_TRY(launch_q8_gemm(q8w(w.f1), F, D, R, n1->q, n1->d, layout, ho, st));
         LayerOut h2o{};
         h2o.y = h2;
         h2o.y_stride = D;
         h2o.n_store = D;
+        h2o.row_pad = row_pad;
+        h2o.rows_per_seq = rows_per_seq;
         return launch_q8_gemm(q8w(w.f2), D, F, R, hq.q, hq.d, layout, h2o, st);
     }
     LayerIn qin{};
@@ -745,8 +751,9 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                 GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st,
                                           Q8_NATURAL));
             }
-            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, rows, cur.q, cur.d, Q8_NATURAL,
-                                    qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0), st));
+            LayerOut qo = qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0);
+            qo.row_pad = d_pad;   // row tiles of left padding only: zeros, no K/V (never attended)
+            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, rows, cur.q, cur.d, Q8_NATURAL, qo, st));
         } else {
             LayerIn in{};
             if (li == 0) {
@@ -771,7 +778,8 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
-        GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr));
+        GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr,
+                            Q8_NATURAL, d_pad, S));
     }
     GSVK_TRY(final_ln(m, st, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
