@@ -17,6 +17,8 @@
 //
 // Numerics: softmax(q.k * scale) . V over the valid keys with fp32 accumulation; the output is
 // divided by the sum (multiplied by its reciprocal), as ggml_flash_attn_ext does.
+#include <mutex>
+
 #include "attn_dev.h"
 
 namespace gsvk {
@@ -310,7 +312,82 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
     return GSVK_OK;
 }
 
+// ---- the same attention with its workspace in a library-owned device array ------------------
+// For callers that cannot allocate (code under graph capture, serving loops that forbid
+// hipMalloc): the split partials and merge counters live in `scratch`, one copy per GPU, held
+// until the process ends. Every call on a GPU uses that GPU's copy, so calls that overlap on one
+// GPU (two streams, two threads) race on it and must be serialised by the caller.
+constexpr size_t ATT_SCRATCH_BYTES = (size_t) 8 << 20;
+static __device__ __align__(256) unsigned char scratch[ATT_SCRATCH_BYTES];
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+
+// Device address of `scratch` on the current device, looked up once per device (the name of the
+// array is a host-side stand-in and must never reach a kernel).
+int scratch_address(void ** out) {
+    static std::mutex mu;
+    static void * addr[SCRATCH_MAX_DEVICES] = {};
+    int dev = -1;
+    GSVK_HIP(hipGetDevice(&dev));
+    GSVK_REQUIRE(dev >= 0 && dev < SCRATCH_MAX_DEVICES, "attn_decode_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        void * p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            (void) hipGetLastError();
+            set_error("attn_decode_noalloc: hipGetSymbolAddress(scratch) failed: %s", hipGetErrorString(e));
+            return GSVK_ERR_HIP;
+        }
+        addr[dev] = p;
+    }
+    *out = addr[dev];
+    return GSVK_OK;
+}
+
+__global__ void k_zero_words(int32_t * __restrict__ p, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+int launch_attn_decode_noalloc(const float * q, const uint16_t * k, const uint16_t * v, int B, int nh,
+                               int hd, int64_t lstride, const int32_t * kv_begin,
+                               const int32_t * kv_end, int64_t max_keys, float scale, float * out,
+                               uint16_t * out16, int8_t * oq, float * od, hipStream_t stream) {
+    GSVK_REQUIRE(B > 0 && B <= 65535 && nh > 0 && nh <= 65535 && max_keys >= 0,
+                 "attn_decode_noalloc: bad shape B=%d nh=%d max_keys=%lld", B, nh, (long long) max_keys);
+    const size_t need = attn_workspace_bytes(B, nh, max_keys);
+    GSVK_REQUIRE(need <= ATT_SCRATCH_BYTES,
+                 "attn_decode_noalloc: the shape needs %zu bytes of workspace, more than the %zu of "
+                 "the library's scratch array", need, ATT_SCRATCH_BYTES);
+    void * ws = nullptr;
+    GSVK_TRY(scratch_address(&ws));
+    const AttnPlan plan = attn_plan(B, nh, max_keys);
+    if (plan.nsplit > 1 && plan.chunk == 0) {
+        // the merge counters (the tail of the workspace) must start at zero: a fill kernel, not a
+        // memset, so that the call can also be captured into a graph
+        const size_t part_bytes = (size_t) B * nh * plan.nsplit * ATT_PART * sizeof(float);
+        int32_t * counters = (int32_t *) ((char *) ws + ((part_bytes + 255) / 256) * 256);
+        const int n = B * nh;
+        hipLaunchKernelGGL(k_zero_words, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream,
+                           counters, n);
+        GSVK_LAUNCH_CHECK();
+    }
+    return launch_attn_decode(q, (int64_t) nh * hd, k, v, B, nh, hd, lstride, kv_begin, kv_end,
+                              max_keys, scale, out, out16, oq, od, ws, stream);
+}
+
 }  // namespace gsvk
+
+extern "C" int gsvk_op_attn_decode_noalloc(const float * q, const uint16_t * k, const uint16_t * v,
+                                           int B, int nh, int hd, int64_t lstride,
+                                           const int32_t * kv_begin, const int32_t * kv_end,
+                                           int64_t max_keys, float scale, float * out,
+                                           uint16_t * out_f16, int8_t * oq, float * od,
+                                           void * stream) {
+    return gsvk::launch_attn_decode_noalloc(q, k, v, B, nh, hd, lstride, kv_begin, kv_end, max_keys,
+                                            scale, out, out_f16, oq, od, (hipStream_t) stream);
+}
 
 extern "C" size_t gsvk_attn_workspace_bytes(int B, int nh, int64_t max_keys) {
     return gsvk::attn_workspace_bytes(B, nh, max_keys);

@@ -29,6 +29,7 @@ EXPORTS = [
     "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
+    "gsvk_op_attn_decode_noalloc",
 ]
 
 
@@ -118,6 +119,8 @@ def lib():
         L.gsvk_attn_workspace_bytes.restype = C.c_size_t
         L.gsvk_op_attn_decode.argtypes = [vp, vp, vp, i32, i32, i32, i64, vp, vp, i64, f32, vp, vp, vp,
                                           vp, vp, vp]
+        L.gsvk_op_attn_decode_noalloc.argtypes = [vp, vp, vp, i32, i32, i32, i64, vp, vp, i64, f32, vp, vp,
+                                                  vp, vp, vp]
         L.gsvk_op_qkv_attn.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp, i64, vp, vp, f32, vp, vp,
                                        vp, vp, vp]
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
@@ -226,6 +229,16 @@ def op_attn_decode(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, 
     check(lib().gsvk_op_attn_decode(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin), _p(kv_end),
                                     max_keys, scale, _p(out), _p(out16), _p(oq), _p(od), _p(ws),
                                     _stream(stream)), "attn_decode")
+
+
+def op_attn_decode_noalloc(q, k, v, kv_begin, kv_end, max_keys, scale, out, out16=None, oq=None, od=None,
+                           stream=None):
+    """op_attn_decode with its workspace in the library's own device array (no allocation)."""
+    B, nh, hd = q.shape
+    lstride = k.shape[2]
+    check(lib().gsvk_op_attn_decode_noalloc(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin),
+                                            _p(kv_end), max_keys, scale, _p(out), _p(out16), _p(oq), _p(od),
+                                            _stream(stream)), "attn_decode_noalloc")
 
 
 def op_attn_prefill(qkv, max_len, pad, nh, scale, out, oq=None, od=None, path=0, stream=None):

@@ -318,6 +318,18 @@ int gsvk_op_attn_decode(const float * q, const uint16_t * k, const uint16_t * v,
                         int64_t max_keys, float scale, float * out, uint16_t * out_f16,
                         int8_t * oq, float * od, void * ws, void * stream);
 
+/* gsvk_op_attn_decode without the ws argument, for callers that cannot allocate device memory
+ * (code under graph capture, serving loops that forbid hipMalloc). No counterpart in the
+ * reference. It allocates nothing: the split partials and merge counters live in a device array
+ * the library holds on each GPU until the process ends (8 MiB, one per GPU). Shapes whose
+ * gsvk_attn_workspace_bytes() exceed 8 MiB are rejected with GSVK_ERR_ARG. stream must belong to
+ * the current device. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams or threads) race and must be serialised by the caller. */
+int gsvk_op_attn_decode_noalloc(const float * q, const uint16_t * k, const uint16_t * v, int B,
+                                int nh, int hd, int64_t lstride, const int32_t * kv_begin,
+                                const int32_t * kv_end, int64_t max_keys, float scale, float * out,
+                                uint16_t * out_f16, int8_t * oq, float * od, void * stream);
+
 /* Prefill self-attention (the flash_attn_ext of src/gsv_ar.cpp:257 over all B*S rows, masks of
  * src/gsv_ar.cpp:215-223): qkv fp32 [B][S][3*nh*hd] (Q, K, V of head h at h*hd, D + h*hd,
  * 2*D + h*hd); pad device int32 [B]; query s of sequence b sees keys [pad[b], max_len) when

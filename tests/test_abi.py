@@ -122,3 +122,13 @@ def test_op_argument_errors_need_no_device():
                                None, None)
     assert rc == 1
     assert gsvk.attn_workspace_bytes(16, 16, 1000) > 0
+
+
+def test_attn_noalloc_rejects_shapes_beyond_its_scratch():
+    # 4096 x 16 rows of 4096 keys need 35 MB of split partials, more than the 8 MiB array; the
+    # size check runs on the host before any device call
+    L = gsvk.lib()
+    assert gsvk.attn_workspace_bytes(4096, 16, 4096) > (8 << 20)
+    rc = L.gsvk_op_attn_decode_noalloc(None, None, None, 4096, 16, 32, 4096, None, None, 4096, 1.0, None,
+                                       None, None, None, None)
+    assert rc == 1 and "scratch" in gsvk.last_error()
