@@ -103,10 +103,17 @@ class _Writer:
 
 def write_model(path: str, seed: int = 0x6A5E0000, n_layer: int = 24, d_model: int = 512,
                 n_head: int = 16, ffn: int = 2048, vocab: int = 1025, phone_vocab: int = 732,
-                eos: int = 1024, head_type: str = "f16", bert_dim: int = 1024) -> str:
-    """Write the synthetic model to ``path`` (returns path)."""
+                eos: int = 1024, head_type: str = "f16", bert_dim: int = 1024,
+                override: dict | None = None, text_alpha: float = 1.0, audio_alpha: float = 1.0) -> str:
+    """Write the synthetic model to ``path`` (returns path).
+
+    override maps tensor names to the values to store instead of the random ones (the random
+    stream is drawn as usual, so the other tensors do not change): fp32 arrays of the tensor's
+    shape, stored in the tensor's type (Q8_0 through q8_quantize_ref, F16 rounded), or, for a
+    Q8_0 tensor, a uint8 array of ready GGUF blocks (exact scales, see q8_blocks)."""
     rng = np.random.Generator(np.random.PCG64(seed))
     D = d_model
+    override = override or {}
 
     def normal(shape, std):
         return (rng.standard_normal(size=shape, dtype=np.float32) * np.float32(std)).astype(np.float32)
@@ -125,37 +132,70 @@ def write_model(path: str, seed: int = 0x6A5E0000, n_layer: int = 24, d_model: i
 
     f32 = lambda a: np.ascontiguousarray(a, dtype=np.float32).tobytes()
     emb16 = lambda a: a.astype(np.float16).astype(np.float32)
-    w.add_tensor("ar.text_emb", (phone_vocab, D), GGML_F32, f32(emb16(normal((phone_vocab, D), 0.02))))
-    w.add_tensor("ar.audio_emb", (vocab, D), GGML_F32, f32(emb16(normal((vocab, D), 0.02))))
-    w.add_tensor("ar.bert_proj", (D, bert_dim), GGML_F32, f32(normal((D, bert_dim), 0.02)))
-    w.add_tensor("ar.bert_proj_b", (D,), GGML_F32, f32(normal((D,), 0.02)))
-    w.add_tensor("ar.text_pe_alpha", (1,), GGML_F32, f32(np.ones(1)))
-    w.add_tensor("ar.audio_pe_alpha", (1,), GGML_F32, f32(np.ones(1)))
+
+    def put(name, shape, ggml_type, values):
+        v = override.get(name, values)
+        if ggml_type == GGML_Q8_0:
+            if v.dtype == np.uint8:
+                assert v.size == int(np.prod(shape)) // 32 * 34, name
+                data = np.ascontiguousarray(v).tobytes()
+            else:
+                data = q8_quantize_ref(np.asarray(v, np.float32).reshape(shape)).tobytes()
+        elif ggml_type == GGML_F16:
+            data = np.asarray(v, np.float32).reshape(shape).astype(np.float16).tobytes()
+        else:
+            data = f32(np.asarray(v, np.float32).reshape(shape))
+        w.add_tensor(name, shape, ggml_type, data)
+
+    put("ar.text_emb", (phone_vocab, D), GGML_F32, emb16(normal((phone_vocab, D), 0.02)))
+    put("ar.audio_emb", (vocab, D), GGML_F32, emb16(normal((vocab, D), 0.02)))
+    put("ar.bert_proj", (D, bert_dim), GGML_F32, normal((D, bert_dim), 0.02))
+    put("ar.bert_proj_b", (D,), GGML_F32, normal((D,), 0.02))
+    put("ar.text_pe_alpha", (1,), GGML_F32, np.full(1, text_alpha, np.float32))
+    put("ar.audio_pe_alpha", (1,), GGML_F32, np.full(1, audio_alpha, np.float32))
     pred = normal((vocab, D), 0.02)
     if head_type == "f16":
-        w.add_tensor("ar.predict", (vocab, D), GGML_F16, pred.astype(np.float16).tobytes())
+        put("ar.predict", (vocab, D), GGML_F16, pred)
     elif head_type == "f32":
-        w.add_tensor("ar.predict", (vocab, D), GGML_F32, f32(pred))
+        put("ar.predict", (vocab, D), GGML_F32, pred)
     elif head_type == "q8_0":
-        w.add_tensor("ar.predict", (vocab, D), GGML_Q8_0, q8_quantize_ref(pred).tobytes())
+        put("ar.predict", (vocab, D), GGML_Q8_0, pred)
     else:
         raise ValueError("head_type must be f16, f32 or q8_0")
     for li in range(n_layer):
         p = f"transformer.block{li}"
-        w.add_tensor(f"{p}.qkv_w", (3 * D, D), GGML_Q8_0, q8_quantize_ref(normal((3 * D, D), 0.02)).tobytes())
-        w.add_tensor(f"{p}.qkv_b", (3 * D,), GGML_F32, f32(normal((3 * D,), 0.02)))
-        w.add_tensor(f"{p}.out_w", (D, D), GGML_Q8_0, q8_quantize_ref(normal((D, D), 0.02)).tobytes())
-        w.add_tensor(f"{p}.out_b", (D,), GGML_F32, f32(normal((D,), 0.02)))
-        w.add_tensor(f"{p}.norm1_w", (D,), GGML_F32, f32(1.0 + normal((D,), 0.05)))
-        w.add_tensor(f"{p}.norm1_b", (D,), GGML_F32, f32(normal((D,), 0.05)))
-        w.add_tensor(f"{p}.ffn1_w", (ffn, D), GGML_Q8_0, q8_quantize_ref(normal((ffn, D), 0.02)).tobytes())
-        w.add_tensor(f"{p}.ffn1_b", (ffn,), GGML_F32, f32(normal((ffn,), 0.02)))
-        w.add_tensor(f"{p}.ffn2_w", (D, ffn), GGML_Q8_0, q8_quantize_ref(normal((D, ffn), 0.02)).tobytes())
-        w.add_tensor(f"{p}.ffn2_b", (D,), GGML_F32, f32(normal((D,), 0.02)))
-        w.add_tensor(f"{p}.norm2_w", (D,), GGML_F32, f32(1.0 + normal((D,), 0.05)))
-        w.add_tensor(f"{p}.norm2_b", (D,), GGML_F32, f32(normal((D,), 0.05)))
+        put(f"{p}.qkv_w", (3 * D, D), GGML_Q8_0, normal((3 * D, D), 0.02))
+        put(f"{p}.qkv_b", (3 * D,), GGML_F32, normal((3 * D,), 0.02))
+        put(f"{p}.out_w", (D, D), GGML_Q8_0, normal((D, D), 0.02))
+        put(f"{p}.out_b", (D,), GGML_F32, normal((D,), 0.02))
+        put(f"{p}.norm1_w", (D,), GGML_F32, 1.0 + normal((D,), 0.05))
+        put(f"{p}.norm1_b", (D,), GGML_F32, normal((D,), 0.05))
+        put(f"{p}.ffn1_w", (ffn, D), GGML_Q8_0, normal((ffn, D), 0.02))
+        put(f"{p}.ffn1_b", (ffn,), GGML_F32, normal((ffn,), 0.02))
+        put(f"{p}.ffn2_w", (D, ffn), GGML_Q8_0, normal((D, ffn), 0.02))
+        put(f"{p}.ffn2_b", (D,), GGML_F32, normal((D,), 0.02))
+        put(f"{p}.norm2_w", (D,), GGML_F32, 1.0 + normal((D,), 0.05))
+        put(f"{p}.norm2_b", (D,), GGML_F32, normal((D,), 0.05))
     w.write(path)
     return path
+
+
+def q8_blocks(n: int, k: int, cols=None, scale_log2: int = -6) -> np.ndarray:
+    """GGUF Q8_0 blocks of an n x k matrix whose row r holds one non-zero, exactly 1.0, at column
+    cols[r] (default r % k), stored as d = 2**scale_log2 (exact in fp16) and q = 2**-scale_log2;
+    cols[r] < 0 leaves row r zero. All other blocks have d = 0, q = 0."""
+    cols = np.arange(n) % k if cols is None else np.asarray(cols)
+    q = 2 ** (-scale_log2)
+    assert 1 <= q <= 127
+    blk = np.zeros((n, k // 32, 34), np.uint8)
+    d16 = np.array([2.0 ** scale_log2], np.float16).view(np.uint8)
+    for r in range(n):
+        c = int(cols[r])
+        if c < 0:
+            continue
+        blk[r, c // 32, 0:2] = d16
+        blk[r, c // 32, 2 + c % 32] = np.uint8(q)
+    return blk.reshape(-1)
 
 
 def cached_model(cache_dir: str, **kw) -> str:

@@ -929,6 +929,16 @@ int orc_generate(orc_model * m, const orc_request * reqs, int B, int top_k, floa
         }
     out->n_steps = steps;
     out->decode_ms = (omp_get_wtime() - t1) * 1e3;
+    if ((out->kv_k || out->kv_v) && out->kv_layer >= 0 && out->kv_layer < m->NL && out->kv_cols > 0 &&
+        out->kv_cols <= c.Lmax + 1)
+        for (int b = 0; b < B; b++)
+            for (int h = 0; h < m->NH; h++)
+                for (int s = 0; s < out->kv_cols; s++) {
+                    const size_t o = (((size_t) b * m->NH + h) * out->kv_cols + s) * m->HD;
+                    const size_t src = cidx(m, &c, out->kv_layer, b, h, s);
+                    if (out->kv_k) memcpy(out->kv_k + o, c.k + src, sizeof(float) * (size_t) m->HD);
+                    if (out->kv_v) memcpy(out->kv_v + o, c.v + src, sizeof(float) * (size_t) m->HD);
+                }
     free(row); free(probs); free(x_in); free(lg); free(ny); free(idx_list); free(rng); free(pad);
     free(c.k); free(c.v);
     return 0;

@@ -31,8 +31,13 @@
  *   orc_logits_to_probs, orc_rng_*,       golden vectors written by the reference's own
  *   orc_sample, orc_argmax_probs_over_q   src/gsv_sampler.cpp compiled from source
  *   orc_pe_table                          fp64 closed form
- *   orc_generate, orc_prefill_kv,         left-padding invariance, text/semantic mask
- *   orc_first_logits                      properties, EOS / early-stop / oracle-token traces
+ *   orc_generate, orc_prefill_kv,         known-answer models (tests/test_oracle_composition.py):
+ *   orc_first_logits                      zero / exact-identity projections give float64 closed
+ *                                         forms of the input rows (BERT projection, PE positions,
+ *                                         alphas, padding), the LayerNorm chain with b_o and b_2,
+ *                                         the head over the last row, the attention masks, the
+ *                                         decode embedding position and K/V cache column; plus
+ *                                         left-padding invariance and EOS / early-stop traces
  * Parity unpinned: the ORDER of ggml-cpu's floating-point arithmetic (the x86 activation
  * rounding mode, the 8-lane Q8_0 and F16 dot orders, flash_attn_ext's online-softmax order and
  * expf) lives in llama.cpp f0c41e01, which is not under the reference tree, and no reference
@@ -135,6 +140,12 @@ typedef struct orc_gen_out {
     int32_t   n_steps;
     double    prefill_ms;  /* wall clock of the prefill */
     double    decode_ms;   /* wall clock of the decode loop */
+    /* optional: layer kv_layer's K/V cache after the loop, [B][NH][kv_cols][HD], columns
+     * [0, kv_cols) (the prefill's S columns, then one column per decode step); NULL = not wanted */
+    int32_t   kv_layer;
+    int32_t   kv_cols;
+    float   * kv_k;
+    float   * kv_v;
 } orc_gen_out;
 
 orc_model * orc_model_load(const char * gguf_path, char * err, int errlen);

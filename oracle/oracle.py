@@ -38,7 +38,8 @@ class _GenOut(C.Structure):
     _fields_ = [("tokens", C.c_void_p), ("tok_stride", C.c_int32), ("tok_len", C.c_void_p),
                 ("lens", C.c_void_p), ("finish_seq", C.c_void_p), ("sampled", C.c_void_p),
                 ("logits", C.c_void_p), ("probs0", C.c_void_p), ("n_steps", C.c_int32),
-                ("prefill_ms", C.c_double), ("decode_ms", C.c_double)]
+                ("prefill_ms", C.c_double), ("decode_ms", C.c_double), ("kv_layer", C.c_int32),
+                ("kv_cols", C.c_int32), ("kv_k", C.c_void_p), ("kv_v", C.c_void_p)]
 
 
 _lib = None
@@ -297,7 +298,10 @@ class Model:
         return k, v, lg
 
     def generate(self, reqs, sampler=(15, 1.0, 1.0, 1.35), seed_base=0, early_stop=-1, max_steps=50,
-                 oracle=None, seeds=None, flags=0, nthreads=None, want_logits=False, want_probs0=False):
+                 oracle=None, seeds=None, flags=0, nthreads=None, want_logits=False, want_probs0=False,
+                 kv_layer=None):
+        """kv_layer: also return that layer's K/V cache after the loop as "kv" = (K, V), each
+        [B][NH][S + n_steps][HD] (the prefill's S columns, then one per decode step that ran)."""
         B = len(reqs)
         P = len(reqs[0]["prompt"])
         arr, keep = _reqs_struct(reqs)
@@ -312,6 +316,15 @@ class Model:
         o = _GenOut(tokens.ctypes.data, stride, tok_len.ctypes.data, lens.ctypes.data, fin.ctypes.data,
                     sampled.ctypes.data, None if logits is None else logits.ctypes.data,
                     None if probs0 is None else probs0.ctypes.data, 0, 0.0, 0.0)
+        S = max(len(r["phones"]) for r in reqs) + P
+        kk = vv = None
+        if kv_layer is not None:
+            kk = np.zeros((B, self.NH, S + max_steps, self.HD), np.float32)
+            vv = np.zeros_like(kk)
+            o.kv_layer, o.kv_cols = int(kv_layer), S + max_steps
+            o.kv_k, o.kv_v = kk.ctypes.data, vv.ctypes.data
+        else:
+            o.kv_layer, o.kv_cols = -1, 0
         orc = None if oracle is None else np.ascontiguousarray(oracle, np.int32)
         sd = None if seeds is None else np.ascontiguousarray(seeds, np.uint64)
         rc = lib().orc_generate(self.h, arr, B, sampler[0], sampler[1], sampler[2], sampler[3], seed_base,
@@ -323,7 +336,8 @@ class Model:
         return {"tokens": [tokens[b, :tok_len[b]].copy() for b in range(B)], "lens": lens.copy(),
                 "finish_seq": fin.copy(), "sampled": sampled[:n].copy(), "n_steps": n,
                 "logits": None if logits is None else logits[:n], "probs0": None if probs0 is None else probs0[:n],
-                "prefill_ms": o.prefill_ms, "decode_ms": o.decode_ms}
+                "prefill_ms": o.prefill_ms, "decode_ms": o.decode_ms,
+                "kv": None if kk is None else (kk[:, :, :S + n], vv[:, :, :S + n])}
 
 
 # ---- reference sampler (compiled from the reference sources in this container) -------------

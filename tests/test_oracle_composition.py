@@ -1,0 +1,346 @@
+"""CPU known-answer tests of the oracle's layer composition (src/gsv_ar.cpp:186-293, :296-358,
+:719-824; src/gsv_bert.cpp:141-155).
+
+The component pins (tests/test_oracle_pins.py) fix each op; these fix how the ops are chained:
+which terms enter each LayerNorm, where the BERT projection and its bias apply, the PE position
+and alpha of every row (prefill and decode), the attention masks, the cache column of each decode
+step and the head over the last row. Each test runs the oracle on a model whose projections are
+zero or exact identities (tests/known_models.py) and compares with a float64 closed form under a
+bound derived from the Q8_0 activation quantisation; each also checks that the plausible wrong
+compositions (a dropped bias, a PE position off by one, a swapped alpha, a wrong mask) miss that
+bound by a wide margin, so the test has the power to catch them.
+"""
+import numpy as np
+import pytest
+
+import bert_oracle as BO
+import known_models as KM
+import oracle as O
+import synth_model as sm
+
+N_THREADS = 4
+
+
+@pytest.fixture(scope="module")
+def zero2(tmp_path_factory):
+    """2 layers, every projection zero."""
+    d = tmp_path_factory.mktemp("km")
+    return KM.write(str(d / "zero2.gguf"), 11, [{}, {}])
+
+
+@pytest.fixture(scope="module")
+def idqkv(tmp_path_factory):
+    """1 layer: Wqkv = [I; I; I] (q = k = v = the quantised input + bias), the rest zero."""
+    d = tmp_path_factory.mktemp("km")
+    return KM.write(str(d / "idqkv.gguf"), 12, [{"qkv": "id"}])
+
+
+@pytest.fixture(scope="module")
+def attnout(tmp_path_factory):
+    """2 layers: layer 0 Wq = Wk = 0, Wv = I, Wo = I (attention = mean of the visible V rows);
+    layer 1 Wqkv = [I; I; I] (its K cache shows layer 0's output of every row)."""
+    d = tmp_path_factory.mktemp("km")
+    vcols = np.concatenate([np.full(2 * KM.D, -1), np.arange(KM.D)])
+    return KM.write(str(d / "attnout.gguf"), 13, [{"qkv": vcols, "out": "id"}, {"qkv": "id"}])
+
+
+def _reqs(seed, lens, P, bert=(True,)):
+    reqs = sm.synth_requests(seed, len(lens), P, lens)
+    for i, r in enumerate(reqs):
+        if not bert[i % len(bert)]:
+            r["bert"] = None
+    return reqs
+
+
+def _excess(got, ref, bound):
+    """max of |got - ref| / bound (<= 1 means within the bound)."""
+    return float(np.max(np.abs(np.asarray(got, np.float64) - ref) / bound))
+
+
+# ---------------------------------------------------------------------------- prefill logits
+
+def test_first_logits_zero_projections(zero2):
+    """n1 = LN1(x + b_o), x' = LN2(n1 + b_2) per layer, then the head over the LAST row, whose
+    input is the last prompt code at PE position P-1 with audio_alpha."""
+    path, p, perm, scale = zero2
+    m = O.Model(path)
+    pe = KM.pe(64)
+    reqs = _reqs(21, [5, 9, 1], 7)
+    got = m.first_logits(reqs, nthreads=N_THREADS)
+    P = 7
+    x = KM.decode_input64(p, reqs[0]["prompt"][P - 1], P - 1, pe)
+    ref = KM.head64(KM.zero_layers64(p, x, 2), perm, scale)
+    bound = 2.0 ** -10 * np.abs(ref) + 1e-6
+    for b in range(3):
+        assert _excess(got[b], ref, bound) <= 1.0
+    # the wrong compositions miss the bound by far
+    wrong = {
+        "b_o not in LN1": lambda p2: p2.__setitem__("transformer.block0.out_b", 0 * p["transformer.block0.out_b"]),
+        "b_2 not in LN2": lambda p2: p2.__setitem__("transformer.block1.ffn2_b", 0 * p["transformer.block1.ffn2_b"]),
+        "LN1 and LN2 swapped": lambda p2: (p2.__setitem__("transformer.block0.norm1_w", p["transformer.block0.norm2_w"]),
+                                           p2.__setitem__("transformer.block0.norm2_w", p["transformer.block0.norm1_w"])),
+    }
+    for what, edit in wrong.items():
+        p2 = dict(p)
+        edit(p2)
+        alt = KM.head64(KM.zero_layers64(p2, x, 2), perm, scale)
+        assert _excess(got[0], alt, bound) > 100, what
+    for what, alt_x in {"PE position P": KM.decode_input64(p, reqs[0]["prompt"][P - 1], P, pe),
+                        "text alpha": p["ar.audio_emb"][reqs[0]["prompt"][P - 1]] + KM.TEXT_ALPHA * pe[P - 1],
+                        "first prompt row": KM.decode_input64(p, reqs[0]["prompt"][0], 0, pe)}.items():
+        alt = KM.head64(KM.zero_layers64(p, alt_x, 2), perm, scale)
+        assert _excess(got[0], alt, bound) > 100, what
+    # one layer only (the second layer's LN pair dropped)
+    alt = KM.head64(KM.zero_layers64(p, x, 1), perm, scale)
+    assert _excess(got[0], alt, bound) > 100
+
+
+# ---------------------------------------------------------------------------- decode logits
+
+def test_decode_logits_zero_projections(zero2):
+    """The logits entering loop step idx + 1 come from the token of step idx embedded at PE
+    position prompt_len + idx with audio_alpha (src/gsv_ar.cpp:798-807)."""
+    path, p, perm, scale = zero2
+    m = O.Model(path)
+    pe = KM.pe(64)
+    P = 6
+    reqs = _reqs(22, [4, 7], P)
+    forced = np.array([17, 900, 3, 1000, 250, 64], np.int32)
+    r = m.generate(reqs, sampler=(1, 1.0, 1.0, 1.0), max_steps=len(forced), oracle=forced, seeds=[1, 2],
+                   flags=O.ORC_EOS_MASK_ALL, nthreads=N_THREADS, want_logits=True)
+    lg = r["logits"]
+    assert lg.shape[0] == len(forced)
+    for idx in range(len(forced) - 1):
+        x = KM.decode_input64(p, forced[idx], P + idx, pe)
+        ref = KM.head64(KM.zero_layers64(p, x, 2), perm, scale)
+        bound = 2.0 ** -10 * np.abs(ref) + 1e-6
+        for b in range(2):
+            assert _excess(lg[idx + 1, b], ref, bound) <= 1.0, idx
+        for what, alt_x in {"PE position + 1": KM.decode_input64(p, forced[idx], P + idx + 1, pe),
+                            "PE position - 1": KM.decode_input64(p, forced[idx], P + idx - 1, pe),
+                            "PE position idx": KM.decode_input64(p, forced[idx], idx, pe),
+                            "text alpha": p["ar.audio_emb"][forced[idx]] + KM.TEXT_ALPHA * pe[P + idx]}.items():
+            alt = KM.head64(KM.zero_layers64(p, alt_x, 2), perm, scale)
+            assert _excess(lg[idx + 1, 0], alt, bound) > 100, (what, idx)
+
+
+# ---------------------------------------------------------------------------- the layer input
+
+def _kv_bound(x, bias):
+    """|K - (x + bias)| for K = dequant(quant_x86(x)) + bias in fp32."""
+    return KM.block_amax(x) * KM.Q8_ERR * 1.001 + 2e-7 * (np.abs(x) + np.abs(bias)) + 1e-7
+
+
+def _heads(a):
+    """[B][NH][S][HD] -> [B][S][D] (head h holds dims 32h .. 32h + 31)."""
+    B, nh, S, hd = a.shape
+    return a.transpose(0, 2, 1, 3).reshape(B, S, nh * hd)
+
+
+def test_prefill_inputs_and_kv_cache(idqkv):
+    """The layer-0 K and V of every prefill row equal the row's input x plus the bias: text rows
+    with the BERT projection and its bias (or the bias alone without features), prompt rows
+    without either, left-pad rows zero; text PE positions start at 0 after the pad, prompt PE
+    positions at 0 after max_len."""
+    path, p, perm, scale = idqkv
+    m = O.Model(path)
+    pe = KM.pe(64)
+    reqs = _reqs(23, [6, 13, 1, 9], 5, bert=(True, True, False, True))
+    k, v, _ = m.prefill_kv(reqs, 0, nthreads=N_THREADS)
+    x, S, max_len = KM.inputs64(p, reqs, pe)
+    bk = p["transformer.block0.qkv_b"][KM.D:2 * KM.D].astype(np.float64)
+    bv = p["transformer.block0.qkv_b"][2 * KM.D:].astype(np.float64)
+    K, Vv = _heads(k), _heads(v)
+    assert _excess(K, x + bk, _kv_bound(x, bk)) <= 1.0
+    assert _excess(Vv, x + bv, _kv_bound(x, bv)) <= 1.0
+    # the wrong inputs miss the bound
+    Wb, bb = p["ar.bert_proj"].astype(np.float64), p["ar.bert_proj_b"].astype(np.float64)
+    b = 0                                      # 6 phones after 7 pad rows
+    T = len(reqs[b]["phones"])
+    pad = max_len - T
+    assert pad > 0
+    t = 3
+    row = K[b, pad + t]
+    good = x[b, pad + t] + bk
+    bnd = _kv_bound(x[b, pad + t], bk)
+    te = p["ar.text_emb"][reqs[b]["phones"][t]]
+    alts = {
+        "no BERT projection": good - Wb @ reqs[b]["bert"][:, t],
+        "no BERT bias": good - bb,
+        "PE position pad + t": te + KM.TEXT_ALPHA * pe[pad + t] + Wb @ reqs[b]["bert"][:, t] + bb + bk,
+        "audio alpha on text": te + KM.AUDIO_ALPHA * pe[t] + Wb @ reqs[b]["bert"][:, t] + bb + bk,
+    }
+    for what, alt in alts.items():
+        assert _excess(row, alt, bnd) > 50, what
+    prow = K[b, max_len + 2]
+    pgood = x[b, max_len + 2] + bk
+    pb = _kv_bound(x[b, max_len + 2], bk)
+    for what, alt in {"BERT bias on a prompt row": pgood + bb,
+                      "prompt PE after the text": pgood + KM.AUDIO_ALPHA * (pe[max_len + 2] - pe[2]),
+                      "text alpha on prompt": pgood + (KM.TEXT_ALPHA - KM.AUDIO_ALPHA) * pe[2]}.items():
+        assert _excess(prow, alt, pb) > 50, what
+    # pad rows: the bias alone (x = 0)
+    assert np.all(K[2, :max_len - 1] == bk.astype(np.float32))
+
+
+def test_decode_kv_append_column_and_position(idqkv):
+    """Decode step idx writes K/V of its token, embedded at PE position P + idx, at cache column
+    S + idx of every sequence; the prefill columns are left as they were."""
+    path, p, perm, scale = idqkv
+    m = O.Model(path)
+    pe = KM.pe(64)
+    P = 5
+    reqs = _reqs(24, [3, 8], P)
+    forced = np.array([40, 41, 1020, 7, 300, 12, 999], np.int32)
+    n = len(forced)
+    r = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=n, oracle=forced, seeds=[3, 4],
+                   flags=O.ORC_EOS_MASK_ALL, nthreads=N_THREADS, kv_layer=0)
+    k, v = r["kv"]
+    kp, vp, _ = m.prefill_kv(reqs, 0, nthreads=N_THREADS)
+    S = kp.shape[2]
+    assert k.shape[2] == S + n
+    assert np.array_equal(k[:, :, :S], kp) and np.array_equal(v[:, :, :S], vp)
+    bk = p["transformer.block0.qkv_b"][KM.D:2 * KM.D].astype(np.float64)
+    K = _heads(k)
+    for idx in range(n):
+        x = KM.decode_input64(p, forced[idx], P + idx, pe)
+        for b in range(2):
+            assert _excess(K[b, S + idx], x + bk, _kv_bound(x, bk)) <= 1.0, idx
+        alt = KM.decode_input64(p, forced[idx], P + idx + 1, pe) + bk
+        assert _excess(K[0, S + idx], alt, _kv_bound(x, bk)) > 50
+    # the ORC_KV_F16 cache is the same values rounded to fp16 (the device's storage)
+    r16 = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=n, oracle=forced, seeds=[3, 4],
+                     flags=O.ORC_EOS_MASK_ALL | O.ORC_KV_F16, nthreads=N_THREADS, kv_layer=0)
+    assert np.array_equal(r16["kv"][0], k.astype(np.float16).astype(np.float32))
+
+
+# ---------------------------------------------------------------------------- attention + out
+
+def _q8(x):
+    """x after the x86 activation quantisation and dequantisation (the pinned oracle functions),
+    row by row: what an identity Q8_0 projection passes on."""
+    x32 = np.asarray(x, np.float32)
+    return O.q8_dequant(O.q8_quantize_x86(x32)).reshape(x32.shape).astype(np.float64)
+
+
+def _attn_layer64(p, x, S, max_len, pads, mask_kind="reference"):
+    """Layer 0 of the attnout model: q and k are the constant biases, so attention is the plain
+    mean of the visible V rows (v = quant(x) + b_v); o = quant(attention); then the two
+    LayerNorms. float64, with the three activation quantisations of the path modelled by the
+    pinned quantiser (x -> v, attention -> o, and the caller's layer-1 input)."""
+    B = x.shape[0]
+    b0 = "transformer.block0"
+    bv = p[f"{b0}.qkv_b"][2 * KM.D:].astype(np.float64)
+    v = _q8(x) + bv
+    out = np.zeros_like(x)
+    for b in range(B):
+        for s in range(S):
+            if mask_kind == "reference":
+                keys = range(pads[b], max_len) if s < max_len else range(pads[b], s + 1)
+            elif mask_kind == "text causal":
+                keys = range(pads[b], s + 1) if s >= pads[b] else range(pads[b], max_len)
+            elif mask_kind == "semantic sees all":
+                keys = range(pads[b], max_len) if s < max_len else range(pads[b], S)
+            elif mask_kind == "pads visible":
+                keys = range(0, max_len) if s < max_len else range(0, s + 1)
+            keys = list(keys)
+            out[b, s] = v[b, keys].mean(axis=0) if keys else 0.0
+    n1 = KM.ln64(x + _q8(out) + p[f"{b0}.out_b"], p[f"{b0}.norm1_w"], p[f"{b0}.norm1_b"])
+    return KM.ln64(n1 + p[f"{b0}.ffn2_b"], p[f"{b0}.norm2_w"], p[f"{b0}.norm2_b"])
+
+
+def test_prefill_attention_masks_and_out_projection(attnout):
+    """Layer 0 output of every row (seen through layer 1's K cache): LN2(LN1(x + mean of the
+    visible V rows + b_o) + b_2), text queries seeing [pad, max_len), semantic queries [pad, q].
+    The closed form models the quantisations exactly, so it agrees with the oracle to fp32
+    rounding except where that rounding moves a value across a quantisation boundary (one step,
+    amax/127, of that element; a few elements in a thousand)."""
+    path, p, perm, scale = attnout
+    m = O.Model(path)
+    pe = KM.pe(64)
+    reqs = _reqs(25, [7, 12, 3], 6)
+    k1, _, _ = m.prefill_kv(reqs, 1, nthreads=N_THREADS)
+    x, S, max_len = KM.inputs64(p, reqs, pe)
+    pads = [max_len - len(r["phones"]) for r in reqs]
+    bk1 = p["transformer.block1.qkv_b"][KM.D:2 * KM.D].astype(np.float64)
+    K1 = _heads(k1).astype(np.float64)
+
+    def check(cur):
+        ref = _q8(cur) + bk1
+        d = np.abs(K1 - ref)
+        close = d <= 1e-4 * (1.0 + np.abs(ref))
+        step = KM.block_amax(cur) / 127.0 * 1.01 + 1e-4
+        return float(close.mean()), bool(np.all(d <= step + 0.05 * np.abs(ref)))
+
+    frac, bounded = check(_attn_layer64(p, x, S, max_len, pads))
+    assert frac >= 0.99 and bounded, frac
+    for kind in ("text causal", "semantic sees all", "pads visible"):
+        frac_alt, _ = check(_attn_layer64(p, x, S, max_len, pads, kind))
+        assert frac_alt < 0.9, (kind, frac_alt)
+    p2 = dict(p)
+    p2["transformer.block0.out_b"] = 0 * p["transformer.block0.out_b"]
+    frac_alt, _ = check(_attn_layer64(p2, x, S, max_len, pads))
+    assert frac_alt < 0.1, frac_alt
+
+
+# ---------------------------------------------------------------------------- BERT encoder
+
+def _bert_params(seed, n_layer, D=64, F=256, vocab=40, max_pos=16, ident=False):
+    rng = np.random.default_rng(seed)
+    W = {"bert.word_emb": rng.standard_normal((vocab, D)), "bert.pos_emb": rng.standard_normal((max_pos, D)),
+         "bert.type_emb": rng.standard_normal((2, D)), "bert.emb_ln_w": rng.uniform(0.5, 1.5, D),
+         "bert.emb_ln_b": rng.standard_normal(D) * 0.3}
+    for li in range(n_layer):
+        q = f"bert.l{li}."
+        W[q + "qkv_w"] = np.zeros((3 * D, D))
+        W[q + "attn_out_w"] = np.zeros((D, D))
+        W[q + "ff1_w"] = np.zeros((F, D))
+        W[q + "ff2_w"] = np.zeros((D, F))
+        if ident:
+            W[q + "qkv_w"][2 * D:, :] = np.eye(D)                 # v = x; q = k = 0
+            W[q + "attn_out_w"] = np.eye(D)
+            W[q + "ff1_w"][:D, :] = np.eye(D)
+            W[q + "ff2_w"][:, :D] = np.eye(D)
+        W[q + "qkv_b"] = rng.standard_normal(3 * D) * 0.5
+        W[q + "attn_out_b"] = rng.standard_normal(D) * 0.5
+        W[q + "ff1_b"] = rng.standard_normal(F) * 0.5
+        W[q + "ff2_b"] = rng.standard_normal(D) * 0.5
+        for n in ("attn_ln", "out_ln"):
+            W[q + n + "_w"] = rng.uniform(0.5, 1.5, D)
+            W[q + n + "_b"] = rng.standard_normal(D) * 0.3
+    return W
+
+
+def _bert_closed(W, ids, n_layers, ident, drop=None):
+    import math
+    ids = np.asarray(ids)
+    T = len(ids)
+    x = (W["bert.word_emb"][ids] + W["bert.pos_emb"][:T]) + W["bert.type_emb"][0]
+    x = KM.ln64(x, W["bert.emb_ln_w"], W["bert.emb_ln_b"], 1e-12)
+    gelu = np.vectorize(lambda t: 0.5 * t * (1.0 + math.erf(t / math.sqrt(2.0))))
+    for li in range(n_layers):
+        q = f"bert.l{li}."
+        D = x.shape[1]
+        bv = W[q + "qkv_b"][2 * D:]
+        a = (x + bv).mean(axis=0, keepdims=True) if ident else bv[None, :]   # uniform attention
+        o = a if ident else 0.0
+        x = KM.ln64(x + o + (0 if drop == "b_o" else W[q + "attn_out_b"]), W[q + "attn_ln_w"], W[q + "attn_ln_b"], 1e-12)
+        h = gelu((np.pad(x, ((0, 0), (0, W[q + "ff1_b"].size - D))) if ident else 0.0) + W[q + "ff1_b"])
+        f = h[:, :D] if ident else 0.0
+        x = KM.ln64(x + f + (0 if drop == "b_2" else W[q + "ff2_b"]), W[q + "out_ln_w"], W[q + "out_ln_b"], 1e-12)
+    return x.T
+
+
+@pytest.mark.parametrize("ident", [False, True])
+@pytest.mark.parametrize("n_layers", [1, 2])
+def test_bert_encoder_composition(ident, n_layers):
+    """src/gsv_bert.cpp:147-155 with zero / identity projections: x = LN1(x + Wo.a + b_o),
+    x = LN2(x + W2.gelu(W1.x + b1) + b2), a = softmax attention over the sequence's own tokens
+    (uniform here: q = k = 0)."""
+    W = _bert_params(31 + n_layers, n_layers, ident=ident)
+    ids = [3, 17, 5, 39, 0, 11]
+    got = BO.encode(W, ids, n_layers, 64, 4, 1e-12)
+    ref = _bert_closed(W, ids, n_layers, ident)
+    np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-9)
+    for drop in ("b_o", "b_2"):
+        assert np.max(np.abs(got - _bert_closed(W, ids, n_layers, ident, drop))) > 1e-2
