@@ -1,0 +1,78 @@
+// Decode step at small batch in two launches per decoder layer (decode_layer.hip).
+#pragma once
+
+#include "common.h"
+#include "layer.h"
+
+namespace gsvk {
+
+// Hidden-unit groups of the FFN launch: each workgroup computes FFN1 for 2048 / DEC_FFN_GROUPS
+// hidden units of one sequence and their share of FFN2, written as one partial row of 512.
+constexpr int DEC_FFN_GROUPS = 16;
+
+// Launch 1 of a layer, workgroup (head h, sequence b):
+//   input row  x = LN2((res + parts[0] + ... + parts[NP-1]) + bias) (the previous layer's LN1
+//              output, FFN2 partials and b_2), or emb[tok] + alpha * PE[pos] for layer 0;
+//   QKV of head h (the x86 Q8_0 dot of the GEMV), K/V append, attention over [kv_begin, col];
+//   the head's attention output quantised to one Q8_0 block and multiplied by the 512 x 32
+//   slice of the out projection: partial row p1[h][b][0:512].
+struct DecAttnArgs {
+    int mode;                 // IN_LN or IN_EMB
+    const float * res;        // IN_LN: [B][512]
+    const float * parts;      // IN_LN: [DEC_FFN_GROUPS][B][512]
+    const float * bias;       // IN_LN: [512]
+    const float * wb;         // IN_LN: [w; b], 1024
+    const float * emb;        // IN_EMB: embedding table [vocab][512]
+    const float * pe;         // IN_EMB: positional table [pe_rows][512]
+    const int32_t * tok;      // IN_EMB: [B]
+    const int32_t * pos_ptr;  // IN_EMB: the PE row of sequence b is *pos_ptr + pos_add - pos_sub[b]
+    int pos_add;
+    const int32_t * pos_sub;  // (may be null)
+    int pe_rows;
+    float alpha;
+    int vocab;
+    int32_t * kv_end;         // IN_EMB: kv_end[b] = *pos_ptr + kv_end_add (may be null)
+    int kv_end_add;
+    float * x_out;            // the input row x [B][512], stored by the head-0 workgroups
+    const int8_t * wq;        // QKV weights, sliced Q8_0 [1536][512], fp16 scales, bias
+    const uint16_t * wd;
+    const float * bqkv;
+    uint16_t * kc;            // this layer's fp16 caches [B][16][lstride][32]
+    uint16_t * vc;
+    int64_t lstride;
+    const int32_t * kv_begin; // [B]
+    const int32_t * col_ptr;  // the new key's column: *col_ptr + col_add
+    int col_add;
+    float scale_log2;
+    const int8_t * woq;       // out projection [512][512] in the Q8_TILED order
+    const uint16_t * wod;
+    float * p1;               // [16][B][512]
+    int B;
+};
+
+// Launch 2 of a layer, workgroup (hidden group g, sequence b):
+//   n1 = LN1((res + p1[0] + ... + p1[15]) + bo), stored by the group-0 workgroups;
+//   the group's 2048 / DEC_FFN_GROUPS hidden units h = relu(W1 . n1 + b1) (x86 Q8_0 dot),
+//   quantised to Q8_0 blocks, times the matching columns of W2: partial row p2[g][b][0:512].
+struct DecFfnArgs {
+    const float * res;        // [B][512] (x_out of launch 1)
+    const float * p1;         // [16][B][512]
+    const float * bo;         // [512]
+    const float * wb1;        // LN1 [w; b]
+    float * n1_out;           // [B][512]
+    const int8_t * w1q;       // FFN1 sliced Q8_0 [2048][512], fp16 scales, bias
+    const uint16_t * w1d;
+    const float * b1;
+    const int8_t * w2q;       // FFN2 [512][2048] in the Q8_TILED order
+    const uint16_t * w2d;
+    float * p2;               // [DEC_FFN_GROUPS][B][512]
+    int B;
+};
+
+// 1 when the two-launch layer covers this shape: d_model 512, 16 heads of 32, FFN 2048, at most
+// 16 sequences, and rows the attention takes in one workgroup per (sequence, head).
+bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys);
+int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream);
+int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream);
+
+}  // namespace gsvk

@@ -1,0 +1,456 @@
+// Decode step at small batch (up to 16 sequences) in two launches per decoder layer, for gfx950.
+//
+// The decoder layer of src/gsv_ar.cpp:392-413 (QKV, K/V append, flash_attn_ext, out projection,
+// LN1, FFN1 + ReLU, FFN2, LN2) has three all-to-all dependencies inside a sequence's row: the out
+// projection needs every head, LN1 and FFN1 need every output of the out projection, FFN2 needs
+// every hidden unit. The layer runs as two launches by splitting the two K-reductions that cross
+// workgroups into partial rows that the next launch sums in a fixed order:
+//
+//   k_dec_attn, workgroup (head h, sequence b), 8 waves:
+//     every thread loads element `tid` of the input row's operands (the previous layer's LN1
+//     output, its DEC_FFN_GROUPS FFN2 partial rows, b_2, LN2's w and b), every wave its share of
+//     head h's 96 QKV weight rows and of the 512 x 32 out-projection slice of head h, and its
+//     first block of cached keys, all before any of them is used;
+//     LN2 over the workgroup (double sums, one value per thread), the x86 Q8_0 quantisation of
+//     the row into LDS (layer 0: the embedding + alpha * PE);
+//     head h's q, k, v (the x86 8-lane Q8_0 dot of q8.hip), the fp16 K/V append and the attention
+//     of attention.hip over [kv_begin, col];
+//     the head's 32 outputs quantised to one Q8_0 block (the block the out projection's activation
+//     quantisation gives them: head h is block h of the row) and multiplied by the slice: for
+//     output n, (d_w d_a) * (exact int32 block dot), the partial row p1[h][b].
+//   k_dec_ffn, workgroup (hidden group g of 128 units, sequence b), 8 waves:
+//     LN1((x + sum_h p1[h]) + b_o), quantised; FFN1 + b_1 + ReLU for the group's 128 units (the
+//     8-lane dot), quantised to 4 Q8_0 blocks (those of FFN2's activation row), and the 512 x 128
+//     slice of FFN2: p2[g][b][n] = sum over the 4 blocks of (d_w d_h) * (int32 block dot).
+//
+// The sums over heads and groups change only fp32 summation orders against ggml's single 8-lane
+// chain over all blocks (each block's int32 dot is exact either way). The out-projection and
+// FFN2 weights are read in the matrix-core operand order (Q8_TILED): one 16-byte load per lane
+// covers a whole 32-row x 32-column tile in 8 full 128-byte lines.
+#include "attn_dev.h"
+#include "decode_layer.h"
+#include "layer_dev.h"
+
+namespace gsvk {
+
+namespace {
+constexpr int DL_K = 512;                // d_model
+constexpr int DL_NBLK = DL_K / 32;       // Q8_0 blocks of a row
+constexpr int DL_NH = 16;                // heads
+constexpr int DL_FFN = 2048;
+constexpr int DL_THREADS = 512;          // one row element per thread
+constexpr int DL_WAVES = DL_THREADS / 64;
+constexpr int DL_SLICE_B = DL_NBLK * 4 + 16;   // LDS row slices padded by 16 bytes
+constexpr int DL_QKV_ROWS = 3 * ATT_HD;
+
+// Row LayerNorm over the workgroup, one value per thread: the LayerNorm of norm.hip and
+// layer_dev.h (sums of the values and their squares in double, var = E[v^2] - mean^2 in float).
+__device__ __forceinline__ float wg_layernorm(float v, float w, float c, int lane, int wave,
+                                              double (*s_red)[DL_WAVES]) {
+    double s = wave_sum_d_uniform((double) v);
+    double s2 = wave_sum_d_uniform((double) v * (double) v);
+    if (lane == 0) {
+        s_red[0][wave] = s;
+        s_red[1][wave] = s2;
+    }
+    __syncthreads();
+    double S = 0.0, S2 = 0.0;
+#pragma unroll
+    for (int w2 = 0; w2 < DL_WAVES; w2++) {
+        S += s_red[0][w2];
+        S2 += s_red[1][w2];
+    }
+    const float mean = (float) (S / (double) DL_K);
+    const float var = __builtin_fmaf(-mean, mean, (float) (S2 / (double) DL_K));
+    const float inv = 1.0f / __builtin_sqrtf(var + 1e-5f);
+    return __builtin_fmaf((v - mean) * inv, w, c);
+}
+
+// The x86 Q8_0 quantisation of element tid of a row of 512 held one per thread (a block is the
+// 32 threads of a half wave), stored into the sliced LDS row (s_x, s_d) that the 8-lane dot reads.
+__device__ __forceinline__ void wg_quantize_row(float y, int tid, int8_t * s_x, float * s_d) {
+    float amax = fabsf(y);
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float d = amax / 127.0f;
+    const float id = (amax != 0.0f) ? 127.0f / amax : 0.0f;
+    const int8_t q = (int8_t) (int) __builtin_rintf(y * id);
+    const int blk = tid >> 5, c = tid & 31;
+    s_x[(c >> 2) * DL_SLICE_B + blk * 4 + (c & 3)] = q;
+    if (c == 0) s_d[blk] = h2f(f2h(d));
+}
+
+// One 8-lane x86 Q8_0 dot of a weight row (sliced, 4 int4 of quants + their 16 fp16 scales
+// held by this lane) with the LDS row: lane j's chain over the 16 blocks, then the 3-step
+// butterfly over the 8 lanes (the order of q8.hip).
+__device__ __forceinline__ float row_dot8(const int4 (&w)[4], const uint2 (&dh)[4], const int8_t * s_x,
+                                          const float * s_d, int j) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float dw0 = h2f((uint16_t) (dh[i].x & 0xffff)), dw1 = h2f((uint16_t) (dh[i].x >> 16));
+        const float dw2 = h2f((uint16_t) (dh[i].y & 0xffff)), dw3 = h2f((uint16_t) (dh[i].y >> 16));
+        const int4 xv = *reinterpret_cast<const int4 *>(&s_x[j * DL_SLICE_B + 16 * i]);
+        const float4 dx = *reinterpret_cast<const float4 *>(&s_d[4 * i]);
+        acc = __builtin_fmaf(dw0 * dx.x, (float) __builtin_amdgcn_sdot4(w[i].x, xv.x, 0, false), acc);
+        acc = __builtin_fmaf(dw1 * dx.y, (float) __builtin_amdgcn_sdot4(w[i].y, xv.y, 0, false), acc);
+        acc = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w[i].z, xv.z, 0, false), acc);
+        acc = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w[i].w, xv.w, 0, false), acc);
+    }
+    acc = acc + __shfl_xor(acc, 4, 64);
+    acc = acc + __shfl_xor(acc, 2, 64);
+    acc = acc + __shfl_xor(acc, 1, 64);
+    return acc;
+}
+
+// The exact int32 dot of one tiled 32 x 32 weight tile-block row with a Q8_0 activation block in
+// LDS: lane 32 hh + i holds quants [16 hh, 16 hh + 16) of row i; both halves end with the sum.
+__device__ __forceinline__ int tile_dot(const int4 & w, const int8_t * a_blk, int lane) {
+    const int4 av = *reinterpret_cast<const int4 *>(a_blk + 16 * (lane >> 5));
+    int s = __builtin_amdgcn_sdot4(w.x, av.x, 0, false);
+    s = __builtin_amdgcn_sdot4(w.y, av.y, s, false);
+    s = __builtin_amdgcn_sdot4(w.z, av.z, s, false);
+    s = __builtin_amdgcn_sdot4(w.w, av.w, s, false);
+    return s + __shfl_xor(s, 32, 64);
+}
+
+}  // namespace
+
+template <int MODE>
+__global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
+    constexpr int NW = DL_WAVES;
+    constexpr int NP = DEC_FFN_GROUPS;
+    constexpr int PASSES = (DL_QKV_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
+    constexpr int WO_T = DL_NBLK / NW;                        // out-projection tiles per wave
+    const int h = blockIdx.x;
+    const int b = blockIdx.y;
+    const int B = a.B;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int ks = lane >> 2;
+    const int qd = lane & 3;
+    const int rsub = lane >> 3;
+    const int j = lane & 7;
+
+    __shared__ __align__(16) int8_t s_x[8 * DL_SLICE_B];
+    __shared__ __align__(16) float s_d[DL_NBLK];
+    __shared__ double s_red[2][DL_WAVES];
+    __shared__ __align__(16) float s_q[ATT_HD];
+    __shared__ __align__(16) uint16_t s_kv[2][ATT_HD];
+    __shared__ float s_m[NW];
+    __shared__ float s_l[NW];
+    __shared__ float s_o[NW][ATT_HD];
+    __shared__ __align__(16) int8_t s_a[ATT_HD];
+    __shared__ float s_ad;
+
+    // ---- loads, in the order their data is needed, with no branch between them ----
+    const int col = *a.col_ptr + a.col_add;   // column of this step's key
+    int beg = a.kv_begin[b];
+    float xr = 0.0f, xb = 0.0f, xw = 0.0f, xc = 0.0f, xe = 0.0f, xpe = 0.0f;
+    float xp[NP];
+    int pos = 0;
+    if constexpr (MODE == IN_LN) {
+        xr = a.res[(int64_t) b * DL_K + tid];
+#pragma unroll
+        for (int g = 0; g < NP; g++) xp[g] = a.parts[((int64_t) g * B + b) * DL_K + tid];
+        xb = a.bias[tid];
+        xw = a.wb[tid];
+        xc = a.wb[DL_K + tid];
+    } else {
+        pos = *a.pos_ptr;
+        int tk = a.tok[b];
+        tk = tk < 0 ? 0 : (tk >= a.vocab ? a.vocab - 1 : tk);
+        int pr = pos + a.pos_add - (a.pos_sub ? a.pos_sub[b] : 0);
+        pr = pr < 0 ? 0 : pr;
+        pr = (a.pe_rows > 0 && pr >= a.pe_rows) ? a.pe_rows - 1 : pr;
+        xe = a.emb[(int64_t) tk * DL_K + tid];
+        xpe = a.pe[(int64_t) pr * DL_K + tid];
+    }
+    int4 w[PASSES][4];
+    uint2 dh[PASSES][4];
+    float rbias[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int rl = (p * NW + wave) * 8 + rsub;
+        const int rlc = rl < DL_QKV_ROWS ? rl : DL_QKV_ROWS - 1;
+        const int row = (rlc >> 5) * DL_K + h * ATT_HD + (rlc & 31);
+        const int4 * wsl = reinterpret_cast<const int4 *>(a.wq + ((int64_t) row * 8 + j) * DL_NBLK * 4);
+        const uint2 * wdr = reinterpret_cast<const uint2 *>(a.wd + (int64_t) row * DL_NBLK);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w[p][i] = wsl[i];
+            dh[p][i] = wdr[i];
+        }
+        rbias[p] = a.bqkv[row];
+    }
+    int4 wo[WO_T];
+    uint16_t wos[WO_T];
+#pragma unroll
+    for (int u = 0; u < WO_T; u++) {
+        const int t = wave + NW * u;    // 32-row tile of the out projection's 512 outputs
+        wo[u] = *reinterpret_cast<const int4 *>(a.woq + (((int64_t) t * DL_NBLK + h) << 10) + lane * 16);
+        wos[u] = a.wod[(((int64_t) t * DL_NBLK + h) << 5) + (lane & 31)];
+    }
+    // the first block of cached keys [beg, col) (the new key is substituted later); a wave past
+    // the last block loads that block again and does not use it
+    const bool col_ok = col >= 0 && col < a.lstride;
+    beg = beg < 0 ? 0 : (beg < a.lstride ? beg : (int) a.lstride - 1);
+    const int end = col + 1;
+    const int nkeys = (col_ok && end > beg) ? end - beg : 0;
+    const int nblk = (nkeys + ATT_BLK - 1) / ATT_BLK;
+    const int64_t pair = (int64_t) b * DL_NH + h;
+    const uint16_t * kb = a.kc + pair * a.lstride * ATT_HD + qd * 8;
+    const uint16_t * vb = a.vc + pair * a.lstride * ATT_HD + qd * 8;
+    int last_old = col > beg ? col - 1 : beg;
+    last_old = last_old < a.lstride ? last_old : (int) a.lstride - 1;
+    int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
+    KV8 cur;
+    load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+
+    // ---- the input row: LN2 of the previous layer (or the embedding), quantised into LDS ----
+    float x;
+    if constexpr (MODE == IN_LN) {
+        float r = xp[0];
+#pragma unroll
+        for (int g = 1; g < NP; g++) r = r + xp[g];
+        x = wg_layernorm((xr + r) + xb, xw, xc, lane, wave, s_red);
+    } else {
+        x = __builtin_fmaf(a.alpha, xpe, xe);
+        if (h == 0 && tid == 0 && a.kv_end) a.kv_end[b] = pos + a.kv_end_add;
+    }
+    if (h == 0 && a.x_out) a.x_out[(int64_t) b * DL_K + tid] = x;
+    wg_quantize_row(x, tid, s_x, s_d);
+    __syncthreads();
+
+    // ---- q, k, v of head h; the new K/V appended at column col ----
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int rl = (p * NW + wave) * 8 + rsub;
+        if ((p * NW + wave) * 8 >= DL_QKV_ROWS) break;   // uniform per wave
+        const float acc = row_dot8(w[p], dh[p], s_x, s_d, j);
+        if (j == 0 && rl < DL_QKV_ROWS) {
+            const int which = rl >> 5, dd = rl & 31;
+            const float v = acc + rbias[p];
+            if (which == 0) {
+                s_q[dd] = v;
+            } else {
+                const uint16_t hv = f2h(v);
+                s_kv[which - 1][dd] = hv;
+                if (col_ok) (which == 1 ? a.kc : a.vc)[(pair * a.lstride + col) * ATT_HD + dd] = hv;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- attention over [beg, col] (the block loop of attention.hip) ----
+    float m = -INFINITY, l = 0.0f;
+    float o[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = 0.0f;
+    if (nkeys > 0) {   // uniform over the workgroup
+        float qv[8];
+        const float4 q0 = *reinterpret_cast<const float4 *>(&s_q[qd * 8]);
+        const float4 q1 = *reinterpret_cast<const float4 *>(&s_q[qd * 8 + 4]);
+        qv[0] = q0.x; qv[1] = q0.y; qv[2] = q0.z; qv[3] = q0.w;
+        qv[4] = q1.x; qv[5] = q1.y; qv[6] = q1.z; qv[7] = q1.w;
+        const uint4 knew = *reinterpret_cast<const uint4 *>(&s_kv[0][qd * 8]);
+        const uint4 vnew = *reinterpret_cast<const uint4 *>(&s_kv[1][qd * 8]);
+        if (wave < nblk) {
+            while (blk + NW < nblk) {
+                KV8 pre;
+                load_block(kb, vb, beg + (blk + NW) * ATT_BLK, last_old, ks, pre);
+                attn_block_step<true>(cur, beg + blk * ATT_BLK, end, ks, qv, a.scale_log2, col, knew, vnew, m, l, o);
+                cur = pre;
+                blk += NW;
+            }
+            attn_block_step<true>(cur, beg + blk * ATT_BLK, end, ks, qv, a.scale_log2, col, knew, vnew, m, l, o);
+        }
+        l = slot_sum(l);
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = slot_sum(o[i]);
+        if (lane < 4) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) s_o[wave][lane * 8 + i] = o[i];
+            if (lane == 0) {
+                s_l[wave] = l;
+                s_m[wave] = m;
+            }
+        }
+    }
+    __syncthreads();
+    // wave 0: merge the waves, the head's output as one Q8_0 block (no valid key: 0, as ggml)
+    if (wave == 0) {
+        float val = 0.0f;
+        if (nkeys > 0) {
+            float M = s_m[0];
+#pragma unroll
+            for (int w2 = 1; w2 < NW; w2++) M = fmaxf(M, s_m[w2]);
+            float L = 0.0f, O = 0.0f;
+#pragma unroll
+            for (int w2 = 0; w2 < NW; w2++) {
+                const float f = s_m[w2] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w2] - M);
+                L = __builtin_fmaf(s_l[w2], f, L);
+                if (lane < ATT_HD) O = __builtin_fmaf(s_o[w2][lane], f, O);
+            }
+            val = O * (1.0f / L);
+        }
+        float v1[1] = {lane < ATT_HD ? val : 0.0f};
+        int8_t q1[1];
+        const float d = q8_quantize_group<1>(v1, q1, 32);
+        if (lane < ATT_HD) s_a[lane] = q1[0];
+        if (lane == 0) s_ad = d;
+    }
+    __syncthreads();
+
+    // ---- out projection of head h: partial row p1[h][b] ----
+    const float da = s_ad;
+    float * prow = a.p1 + ((int64_t) h * B + b) * DL_K;
+#pragma unroll
+    for (int u = 0; u < WO_T; u++) {
+        const int t = wave + NW * u;
+        const int isum = tile_dot(wo[u], s_a, lane);
+        const float y = (h2f(wos[u]) * da) * (float) isum;
+        if (lane < 32) prow[t * 32 + lane] = y;
+    }
+}
+
+template <int G>
+__global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
+    constexpr int NW = DL_WAVES;
+    constexpr int U = DL_FFN / G;              // hidden units of the group
+    constexpr int UB = U / 32;                 // their Q8_0 blocks
+    constexpr int PASSES = U / (8 * NW);       // FFN1 rows: 8 per wave and pass
+    constexpr int W2_T = (DL_K / 32) / NW;     // FFN2 output tiles per wave
+    constexpr int K2_NBLK = DL_FFN / 32;       // blocks of an FFN2 weight row
+    static_assert(U % (8 * NW) == 0 && UB * 32 == U && W2_T * NW * 32 == DL_K, "group shape");
+    const int g = blockIdx.x;
+    const int b = blockIdx.y;
+    const int B = a.B;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int rsub = lane >> 3;
+    const int j = lane & 7;
+
+    __shared__ __align__(16) int8_t s_x[8 * DL_SLICE_B];
+    __shared__ __align__(16) float s_d[DL_NBLK];
+    __shared__ double s_red[2][DL_WAVES];
+    __shared__ float s_h[U];
+    __shared__ __align__(16) int8_t s_hq[U];
+    __shared__ float s_hd[UB];
+
+    // ---- loads: the LN1 operands of element tid, then the group's weights ----
+    const float xr = a.res[(int64_t) b * DL_K + tid];
+    float xp[DL_NH];
+#pragma unroll
+    for (int hh = 0; hh < DL_NH; hh++) xp[hh] = a.p1[((int64_t) hh * B + b) * DL_K + tid];
+    const float xb = a.bo[tid];
+    const float xw = a.wb1[tid];
+    const float xc = a.wb1[DL_K + tid];
+    int4 w1[PASSES][4];
+    uint2 d1[PASSES][4];
+    float rb1[PASSES];
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int row = g * U + (p * NW + wave) * 8 + rsub;
+        const int4 * wsl = reinterpret_cast<const int4 *>(a.w1q + ((int64_t) row * 8 + j) * DL_NBLK * 4);
+        const uint2 * wdr = reinterpret_cast<const uint2 *>(a.w1d + (int64_t) row * DL_NBLK);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            w1[p][i] = wsl[i];
+            d1[p][i] = wdr[i];
+        }
+        rb1[p] = a.b1[row];
+    }
+    int4 w2[W2_T][UB];
+    uint16_t d2[W2_T][UB];
+#pragma unroll
+    for (int u = 0; u < W2_T; u++) {
+        const int t = wave + NW * u;
+#pragma unroll
+        for (int k = 0; k < UB; k++) {
+            const int64_t tb = (int64_t) t * K2_NBLK + g * UB + k;
+            w2[u][k] = *reinterpret_cast<const int4 *>(a.w2q + (tb << 10) + lane * 16);
+            d2[u][k] = a.w2d[(tb << 5) + (lane & 31)];
+        }
+    }
+
+    // ---- n1 = LN1((x + o) + b_o), quantised into LDS ----
+    float r = xp[0];
+#pragma unroll
+    for (int hh = 1; hh < DL_NH; hh++) r = r + xp[hh];
+    const float y = wg_layernorm((xr + r) + xb, xw, xc, lane, wave, s_red);
+    if (g == 0) a.n1_out[(int64_t) b * DL_K + tid] = y;
+    wg_quantize_row(y, tid, s_x, s_d);
+    __syncthreads();
+
+    // ---- FFN1 + b_1 + ReLU of the group's units ----
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const float acc = row_dot8(w1[p], d1[p], s_x, s_d, j);
+        if (j == 0) {
+            float v = acc + rb1[p];
+            v = v > 0.0f ? v : 0.0f;
+            s_h[(p * NW + wave) * 8 + rsub] = v;
+        }
+    }
+    __syncthreads();
+    // their Q8_0 blocks: wave k quantises block k
+    if (wave < UB) {
+        float v1[1] = {lane < 32 ? s_h[wave * 32 + lane] : 0.0f};
+        int8_t q1[1];
+        const float d = q8_quantize_group<1>(v1, q1, 32);
+        if (lane < 32) s_hq[wave * 32 + lane] = q1[0];
+        if (lane == 0) s_hd[wave] = d;
+    }
+    __syncthreads();
+
+    // ---- FFN2 over the group's blocks: partial row p2[g][b] ----
+    float * prow = a.p2 + ((int64_t) g * B + b) * DL_K;
+#pragma unroll
+    for (int u = 0; u < W2_T; u++) {
+        const int t = wave + NW * u;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < UB; k++) {
+            const int isum = tile_dot(w2[u][k], s_hq + k * 32, lane);
+            acc = __builtin_fmaf(h2f(d2[u][k]) * s_hd[k], (float) isum, acc);
+        }
+        if (lane < 32) prow[t * 32 + lane] = acc;
+    }
+}
+
+bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys) {
+    return B >= 1 && B <= 16 && nh == DL_NH && d_model == DL_K && ffn == DL_FFN &&
+           attn_nsplit(B, nh, max_keys) == 1;
+}
+
+int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream) {
+    GSVK_REQUIRE(a.B >= 1 && a.B <= 16, "dec_attn: batch %d out of range (1..16)", a.B);
+    GSVK_REQUIRE(a.wq && a.wd && a.bqkv && a.kc && a.vc && a.kv_begin && a.col_ptr && a.woq && a.wod && a.p1,
+                 "dec_attn: null pointer");
+    GSVK_REQUIRE(a.lstride > 0, "dec_attn: bad cache stride");
+    GSVK_REQUIRE(a.mode == IN_LN ? (a.res && a.parts && a.bias && a.wb)
+                                 : (a.mode == IN_EMB && a.emb && a.pe && a.tok && a.pos_ptr),
+                 "dec_attn: bad input stage");
+    const dim3 grid(DL_NH, (unsigned) a.B);
+    if (a.mode == IN_LN)
+        hipLaunchKernelGGL(k_dec_attn<IN_LN>, grid, dim3(DL_THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k_dec_attn<IN_EMB>, grid, dim3(DL_THREADS), 0, stream, a);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream) {
+    GSVK_REQUIRE(a.B >= 1 && a.B <= 16, "dec_ffn: batch %d out of range (1..16)", a.B);
+    GSVK_REQUIRE(a.res && a.p1 && a.bo && a.wb1 && a.n1_out && a.w1q && a.w1d && a.b1 && a.w2q && a.w2d && a.p2,
+                 "dec_ffn: null pointer");
+    hipLaunchKernelGGL(k_dec_ffn<DEC_FFN_GROUPS>, dim3(DEC_FFN_GROUPS, (unsigned) a.B), dim3(DL_THREADS), 0,
+                       stream, a);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+}  // namespace gsvk

@@ -143,9 +143,13 @@ __global__ void __launch_bounds__(256) k_fdot_ggml_t(const WT * __restrict__ W, 
 // computed here (one wave per row, the arithmetic of the LayerNorm kernel) instead of read from X.
 struct LnSrc {
     const float * res, * r, * bias, * wb;
+    // (NPARTS > 0) r = parts[0] + parts[1] + ... in that order, part g of row m at
+    // parts + g * pstride + m * 512 (the FFN2 partial rows of the two-launch decode layer)
+    const float * parts;
+    int64_t pstride;
 };
 
-template <typename WT, int MT, int NI, bool LNIN = false>
+template <typename WT, int MT, int NI, bool LNIN = false, int NPARTS = 0>
 __global__ void __launch_bounds__(256) k_fdot_ggml_k(const WT * __restrict__ W, int n,
                                                      const float * __restrict__ X, int64_t xs, int m,
                                                      float * __restrict__ Y, int64_t ys, LnSrc ln) {
@@ -168,8 +172,25 @@ __global__ void __launch_bounds__(256) k_fdot_ggml_k(const WT * __restrict__ W, 
 #pragma unroll
         for (int u = 0; u < LR; u++) {
             const int mm = min(m0 + wave + 4 * u, m - 1);
-            ln_row_load(ln.res + (int64_t) mm * K, ln.r ? ln.r + (int64_t) mm * K : g_zero_row,
+            ln_row_load(ln.res + (int64_t) mm * K, (ln.r && NPARTS == 0) ? ln.r + (int64_t) mm * K : g_zero_row,
                         ln.bias ? ln.bias : g_zero_row, ln.wb, lane, lr[u]);
+            if constexpr (NPARTS > 0) {
+                float4 pa[NPARTS], pb[NPARTS];
+#pragma unroll
+                for (int g = 0; g < NPARTS; g++) {
+                    const gf4ptr pp = as_global_f4(ln.parts + g * ln.pstride + (int64_t) mm * K + lane * 8);
+                    pa[g] = ld4(pp, 0);
+                    pb[g] = ld4(pp, 1);
+                }
+                float4 ra = pa[0], rb = pb[0];
+#pragma unroll
+                for (int g = 1; g < NPARTS; g++) {
+                    ra.x = ra.x + pa[g].x; ra.y = ra.y + pa[g].y; ra.z = ra.z + pa[g].z; ra.w = ra.w + pa[g].w;
+                    rb.x = rb.x + pb[g].x; rb.y = rb.y + pb[g].y; rb.z = rb.z + pb[g].z; rb.w = rb.w + pb[g].w;
+                }
+                lr[u].ra = ra;
+                lr[u].rb = rb;
+            }
         }
     } else {
 #pragma unroll
@@ -333,6 +354,30 @@ int launch_head_ln(const void * W, int wtype, int64_t n, const float * res, cons
                            (const uint16_t *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
     else
         hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16, true>), grid, dim3(256), 0, stream,
+                           (const float *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+// The decode head after the two-launch layer: LayerNorm((res + parts[0] + ... + parts[15]) +
+// bias) of each row, then the F16 / F32 head (4 rows per workgroup: one per wave).
+int launch_head_ln_parts(const void * W, int wtype, int64_t n, const float * res, const float * parts,
+                         int nparts, int64_t pstride, const float * bias, const float * wb, int64_t m,
+                         float * Y, int64_t ys, hipStream_t stream) {
+    GSVK_REQUIRE(W && res && parts && wb && Y && (wtype == 0 || wtype == 1) && n > 0 && n < (1 << 30) &&
+                     m > 0 && m < (1 << 30) && ys >= n && nparts == 16 && pstride >= m * 512,
+                 "head_ln_parts: bad arguments");
+    auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
+    GSVK_REQUIRE(al16(res) && al16(parts) && al16(bias) && al16(wb) && pstride % 4 == 0,
+                 "head_ln_parts: operands must be 16-byte aligned");
+    constexpr int MTK = 4;
+    const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MTK - 1) / MTK));
+    const LnSrc ln{res, nullptr, bias, wb, parts, pstride};
+    if (wtype == 1)
+        hipLaunchKernelGGL((k_fdot_ggml_k<uint16_t, MTK, 16, true, 16>), grid, dim3(256), 0, stream,
+                           (const uint16_t *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
+    else
+        hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16, true, 16>), grid, dim3(256), 0, stream,
                            (const float *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;

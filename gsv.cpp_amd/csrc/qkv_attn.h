@@ -27,7 +27,7 @@ struct QkvAttnArgs {
 // One workgroup per (sequence, head) covers rows up to the longest: false when the standalone
 // attention would split the rows (few sequences, long rows), which the fused kernel does not.
 bool qkv_attn_supported(int B, int nh, int64_t max_keys);
-// what the decode path uses: supported, and at most 32 sequences
+// what the decode's GEMV chain uses: supported, and fewer than DECODE_GEMM_MIN_BATCH sequences
 bool qkv_attn_preferred(int B, int nh, int64_t max_keys);
 int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream);
 

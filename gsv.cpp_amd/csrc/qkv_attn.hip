@@ -232,10 +232,10 @@ bool qkv_attn_supported(int B, int nh, int64_t max_keys) {
     return attn_nsplit(B, nh, max_keys) == 1;
 }
 
-// Each workgroup reads its head's 52 KB of weights, so the batch multiplies the weight reads
-// (from L2): at 32 sequences and more the tiled QKV GEMV + attention pair is faster.
+// The decode's GEMV chain runs below DECODE_GEMM_MIN_BATCH sequences only (from there the
+// matrix-core path takes over), so the fused kernel is used below it as well.
 bool qkv_attn_preferred(int B, int nh, int64_t max_keys) {
-    return B <= 32 && qkv_attn_supported(B, nh, max_keys);
+    return B < DECODE_GEMM_MIN_BATCH && qkv_attn_supported(B, nh, max_keys);
 }
 
 int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream) {

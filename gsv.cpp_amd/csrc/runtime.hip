@@ -11,6 +11,7 @@
 #include <vector>
 
 #include "common.h"
+#include "decode_layer.h"
 #include "gguf.h"
 #include "layer.h"
 #include "qkv_attn.h"
@@ -21,6 +22,9 @@ namespace gsvk {
 // kernels defined in the other translation units
 int launch_head_ln(const void * W, int wtype, int64_t n, const float * res, const float * r, const float * bias,
                    const float * wb, int64_t m, float * Y, int64_t ys, hipStream_t stream);
+int launch_head_ln_parts(const void * W, int wtype, int64_t n, const float * res, const float * parts,
+                         int nparts, int64_t pstride, const float * bias, const float * wb, int64_t m,
+                         float * Y, int64_t ys, hipStream_t stream);
 int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
                 int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream);
 int launch_build_xy(const float * text_emb, const float * audio_emb, const float * pe,
@@ -143,6 +147,8 @@ struct gsvk_model {
     int64_t s_lstride = 0;
     Act x, attn, n1, hq;
     float * qkv = nullptr, * o = nullptr, * h2 = nullptr, * logits = nullptr;
+    float * p1 = nullptr, * p2 = nullptr;   // partial rows of the two-launch decode layer
+    int decode_path = GSVK_DECODE_AUTO;
     void * attn_ws = nullptr;
     int32_t * kv_begin = nullptr, * kv_end = nullptr;
     int32_t * d_step = nullptr, * hist = nullptr, * ny = nullptr, * fin_step = nullptr,
@@ -303,6 +309,8 @@ int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
     GSVK_TRY(a.alloc(m->o, (size_t) B * D));
     GSVK_TRY(a.alloc(m->h2, (size_t) B * D));
     GSVK_TRY(a.alloc(m->logits, (size_t) B * m->V));
+    GSVK_TRY(a.alloc(m->p1, (size_t) m->NH * B * D));
+    GSVK_TRY(a.alloc(m->p2, (size_t) DEC_FFN_GROUPS * B * D));
     char * ws = nullptr;
     GSVK_TRY(a.alloc(ws, attn_workspace_bytes(B, m->NH, m->lstride)));
     GSVK_HIP(hipMemset(ws, 0, attn_workspace_bytes(B, m->NH, m->lstride)));
@@ -515,6 +523,8 @@ int enqueue_decode_mfma(gsvk_model * m) {
 // was measured slower, 0.57 -> 0.78 / 1.41 ms per step: the graph ran every branch on one
 // hardware queue, one after the other.)
 int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
+    // the GEMV chain runs (and is tested) up to DECODE_GEMM_MIN_BATCH - 1 rows only
+    GSVK_REQUIRE(n >= 1 && n < DECODE_GEMM_MIN_BATCH, "decode: %d rows on the GEMV path", n);
     const int B = m->B, D = m->D, F = m->FFN;
     const float scale = 1.0f / std::sqrt((float) m->HD);
     const size_t row_kv = (size_t) m->NH * m->lstride * m->HD;
@@ -581,7 +591,100 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
     return decode_head(m, n, n1.x, h2, x, m->logits + (size_t) r0 * m->V, st);
 }
 
+// Two launches per layer (decode_layer.hip) for the whole batch on the model's stream: the
+// attention launch (input LayerNorm over the previous layer's partial rows, QKV, K/V append,
+// attention, out-projection partial rows per head) and the FFN launch (LN1 over those partials,
+// FFN1 + ReLU of a group of hidden units, FFN2 partial rows per group); the head sums the last
+// layer's partials in its LayerNorm input stage.
+int enqueue_decode_fused(gsvk_model * m) {
+    const int B = m->B, D = m->D;
+    const float scale = 1.0f / std::sqrt((float) m->HD);
+    hipStream_t st = m->stream;
+    for (int li = 0; li < m->NL; li++) {
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+        DecAttnArgs aa{};
+        if (li == 0) {
+            aa.mode = IN_EMB;
+            aa.emb = m->audio_emb;
+            aa.pe = m->pe;
+            aa.tok = m->last_tok;
+            aa.pos_ptr = m->d_step;
+            aa.pos_add = m->prompt_len - 1;
+            aa.pos_sub = m->row_start;
+            aa.pe_rows = PE_MAX;
+            aa.alpha = m->audio_alpha;
+            aa.vocab = m->V;
+            aa.kv_end = m->kv_end;
+            aa.kv_end_add = m->S;
+        } else {
+            const LayerW & p = m->L[li - 1];
+            aa.mode = IN_LN;
+            aa.res = m->n1.x;
+            aa.parts = m->p2;
+            aa.bias = p.f2.b;
+            aa.wb = p.ln2;
+        }
+        aa.x_out = m->x.x;
+        aa.wq = w.qkv.qs;
+        aa.wd = w.qkv.d;
+        aa.bqkv = w.qkv.b;
+        aa.kc = m->kc + loff;
+        aa.vc = m->vc + loff;
+        aa.lstride = m->lstride;
+        aa.kv_begin = m->kv_begin;
+        aa.col_ptr = m->d_step;
+        aa.col_add = m->S - 1;
+        aa.scale_log2 = scale * 1.4426950408889634f;
+        aa.woq = w.out.qt;
+        aa.wod = w.out.dt;
+        aa.p1 = m->p1;
+        aa.B = B;
+        GSVK_TRY(launch_dec_attn(aa, st));
+        DecFfnArgs fa{};
+        fa.res = m->x.x;
+        fa.p1 = m->p1;
+        fa.bo = w.out.b;
+        fa.wb1 = w.ln1;
+        fa.n1_out = m->n1.x;
+        fa.w1q = w.f1.qs;
+        fa.w1d = w.f1.d;
+        fa.b1 = w.f1.b;
+        fa.w2q = w.f2.qt;
+        fa.w2d = w.f2.dt;
+        fa.p2 = m->p2;
+        fa.B = B;
+        GSVK_TRY(launch_dec_ffn(fa, st));
+    }
+    const LayerW & last = m->L[m->NL - 1];
+    return launch_head_ln_parts(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, m->n1.x, m->p2,
+                                DEC_FFN_GROUPS, (int64_t) B * D, last.f2.b, last.ln2, B, m->logits, m->V,
+                                st);
+}
+
+// The two-launch layer covers the shape and the weights it reads (tiled out / FFN2 copies, an
+// F16 / F32 head).
+bool fused_decode_ok(const gsvk_model * m) {
+    if (m->head_type == GGML_Q8_0 || !dec_layer_supported(m->B, m->NH, m->D, m->FFN, m->lstride)) return false;
+    for (const LayerW & w : m->L)
+        if (!w.out.qt || !w.f2.qt) return false;
+    return true;
+}
+
 int enqueue_decode_body(gsvk_model * m) {
+    switch (m->decode_path) {
+    case GSVK_DECODE_GEMV:
+        if (m->B < DECODE_GEMM_MIN_BATCH) return enqueue_decode_rows(m, 0, m->B, m->stream);
+        break;
+    case GSVK_DECODE_FUSED:
+        if (fused_decode_ok(m)) return enqueue_decode_fused(m);
+        break;
+    case GSVK_DECODE_MFMA:
+        return enqueue_decode_mfma(m);
+    default:
+        if (m->B < DECODE_GEMM_MIN_BATCH && fused_decode_ok(m)) return enqueue_decode_fused(m);
+        break;
+    }
     if (m->B >= DECODE_GEMM_MIN_BATCH) return enqueue_decode_mfma(m);
     return enqueue_decode_rows(m, 0, m->B, m->stream);
 }
@@ -1119,6 +1222,16 @@ extern "C" int gsvk_kv_alloc(gsvk_model * m, int B, int lmax) {
     GSVK_REQUIRE(m && B > 0 && lmax > 0, "bad arguments");
     DeviceGuard guard(m->device);
     return alloc_kv(m, B, lmax);
+}
+
+extern "C" int gsvk_model_set_decode_path(gsvk_model * m, int path) {
+    GSVK_REQUIRE(m, "null model");
+    GSVK_REQUIRE(path >= GSVK_DECODE_AUTO && path <= GSVK_DECODE_MFMA, "bad decode path %d", path);
+    DeviceGuard guard(m->device);
+    cb_drop(m);
+    drop_graph(m);
+    m->decode_path = path;
+    return GSVK_OK;
 }
 
 extern "C" int gsvk_release_cache(gsvk_model * m) {

@@ -29,8 +29,10 @@ EXPORTS = [
     "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
-    "gsvk_op_attn_decode_noalloc",
+    "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path",
 ]
+
+GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
 
 
 class GsvkError(RuntimeError):
@@ -97,6 +99,7 @@ def lib():
                                     i32, vp, i32, vp, C.c_uint, C.POINTER(GenOut)]
         L.gsvk_first_logits.argtypes = [vp, C.POINTER(Request), i32, vp]
         L.gsvk_release_cache.argtypes = [vp]
+        L.gsvk_model_set_decode_path.argtypes = [vp, i32]
         L.gsvk_kv_alloc.argtypes = [vp, i32, i32]
         L.gsvk_prefill.argtypes = [vp, C.POINTER(Request), i32, vp, C.POINTER(C.c_int)]
         L.gsvk_decode_step.argtypes = [vp, vp, vp]
@@ -353,6 +356,10 @@ class Model:
 
     def release_cache(self):
         check(lib().gsvk_release_cache(self.h), "release_cache")
+
+    def set_decode_path(self, path: int):
+        """GSVK_DECODE_AUTO / _GEMV / _FUSED / _MFMA (include/gsvk.h)."""
+        check(lib().gsvk_model_set_decode_path(self.h, path), "set_decode_path")
 
     # -- a batch that requests join and leave while it decodes (gsvk_cb_*) --
     def cb_open(self, capacity, max_prefill, max_steps, prompt_len, sampler=(15, 1.0, 1.0, 1.35), early_stop=-1,

@@ -141,6 +141,24 @@ int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_s
 /* Prefill only, last-position logits [B][vocab]: replaces gsv_ar::first_logits (:707-717). */
 int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out);
 
+/* Which kernels run a decode step (the arithmetic of src/gsv_ar.cpp:380-467 in every case):
+ *  GSVK_DECODE_AUTO  the library's choice (default): up to 16 sequences the two-launch layer,
+ *                    from 17 the matrix-core GEMMs;
+ *  GSVK_DECODE_GEMV  up to 16 sequences the GEMV chain whose projections and LayerNorms are
+ *                    bit-exact with ggml-cpu's x86 order (4 launches per layer);
+ *  GSVK_DECODE_FUSED up to 16 sequences two launches per layer (attention + out-projection
+ *                    partial rows per head; LN1 + FFN1 + FFN2 partial rows per group of hidden
+ *                    units): the same int32 block dots, fp32 sums over heads and groups in a fixed
+ *                    order (agrees with the GEMV chain to fp32 rounding);
+ *  GSVK_DECODE_MFMA  the matrix-core GEMMs at any batch.
+ * A choice that does not cover the batch (or model) falls back to AUTO's. No counterpart in the
+ * reference (it has one CPU path); for tests and benchmarks. */
+#define GSVK_DECODE_AUTO   0
+#define GSVK_DECODE_GEMV   1
+#define GSVK_DECODE_FUSED  2
+#define GSVK_DECODE_MFMA   3
+int gsvk_model_set_decode_path(gsvk_model * m, int path);
+
 /* Free the resident KV cache: replaces gsv_ar::release_cache (:826). */
 int gsvk_release_cache(gsvk_model * m);
 

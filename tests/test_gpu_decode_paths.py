@@ -1,0 +1,177 @@
+"""The decode step's kernel paths against each other, the oracle and the known-answer closed forms.
+
+* GSVK_DECODE_GEMV: four launches per layer, projections and LayerNorms bit-exact with the
+  oracle (ggml-cpu's x86 order).
+* GSVK_DECODE_FUSED (the default up to 16 sequences): two launches per layer; the out projection
+  and FFN2 are summed over heads / hidden groups as partial rows, so they agree with the GEMV
+  chain to fp32 rounding; everything before the first of those sums (the layer-0 input, QKV, the
+  K/V append of layer 0) is unchanged and stays bit-exact.
+"""
+import numpy as np
+import pytest
+
+import known_models as KM
+import oracle as O
+import synth_model as sm
+
+pytestmark = pytest.mark.gpu
+
+GREEDY = (1, 1.0, 1.0, 1.35)
+
+
+def _reqs(seed, lens, P):
+    return sm.synth_requests(seed, len(lens), P, lens)
+
+
+def _step_logits(g, reqs, forced, steps, path):
+    """Prefill then `steps` decode steps fed the forced tokens; logits entering each step."""
+    g.set_decode_path(path)
+    B = len(reqs)
+    S = max(len(r["phones"]) for r in reqs) + len(reqs[0]["prompt"])
+    import gsvk
+    gsvk.check(gsvk.lib().gsvk_kv_alloc(g.h, B, S + steps + 8), "kv_alloc")
+    lg, _ = g.prefill(reqs)
+    out = [lg]
+    for i in range(steps - 1):
+        out.append(g.decode_step(np.full(B, forced[i], np.int32)))
+    return np.array(out)
+
+
+@pytest.mark.parametrize("B", [1, 3, 16])
+def test_fused_layer_matches_gemv_chain(gpu, model4_path, B):
+    """Logits of every decode step of the two paths, same forced tokens: equal to fp32 rounding
+    at the median step; a step where some layer's Q8_0 re-quantisation of an activation lands on
+    the other side of a rounding boundary moves by that one int8 step (amax / 127 of a block),
+    which the later layers spread: within 1e-2 of the row's scale (the same bound as the drift
+    of the oracle's own re-quantisation, test_gpu_configs.py). Layer-0 K/V equal to the bit."""
+    rng = np.random.default_rng(60 + B)
+    reqs = _reqs(61 + B, rng.integers(3, 40, B), 16)
+    steps = 12
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    g = gpu.Model(model4_path)
+    try:
+        print(f"fused vs GEMV chain, batch {B}", flush=True)
+        a = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_GEMV)
+        ka, va = g.kv_read(0)
+        b = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_FUSED)
+        kb, vb = g.kv_read(0)
+    finally:
+        g.close()
+    assert np.array_equal(a[0], b[0])                       # the prefill is the same kernels
+    rel = np.abs(a - b).max(axis=2) / np.abs(a).max(axis=2)
+    assert np.median(rel[1:]) <= 1e-5, np.median(rel[1:])
+    assert rel.max() <= 1e-2, rel.max()
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+@pytest.mark.parametrize("path", ["GEMV", "FUSED"])
+def test_decode_kv_cache_matches_oracle(gpu, model4_path, path):
+    """The K/V rows every decode step appends (layer 0: the embedding at PE position P + idx, its
+    QKV at column S + idx) are the oracle's cache after the same teacher-forced steps, bit for
+    bit, on both paths; the later layers' rows within fp16 rounding of the attention's last-bit
+    differences."""
+    rng = np.random.default_rng(70)
+    reqs = _reqs(71, [12, 30, 5, 21], 16)
+    steps = 10
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    g = gpu.Model(model4_path)
+    o = O.Model(model4_path)
+    try:
+        g.set_decode_path(getattr(gpu, f"GSVK_DECODE_{path}"))
+        g.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced, flags=1)
+        k0, v0 = g.kv_read(0)
+        k3, _ = g.kv_read(3)
+        ref = o.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, kv_layer=0)
+        ref3 = o.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced,
+                          flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, kv_layer=3)
+    finally:
+        g.close()
+        o.close()
+    rk, rv = ref["kv"]
+    S = max(len(r["phones"]) for r in reqs) + 16
+    assert rk.shape[2] == S + steps
+    for b, r in enumerate(reqs):
+        pad = S - 16 - len(r["phones"])
+        # decode columns: bit for bit
+        sl = slice(S, S + steps)
+        assert np.array_equal(k0[b, :, sl].view(np.float16).astype(np.float32), rk[b, :, sl]), b
+        assert np.array_equal(v0[b, :, sl].view(np.float16).astype(np.float32), rv[b, :, sl]), b
+        # prefill columns (4 x 46 rows: the matrix-core GEMM, fp32 sums per block): within one
+        # fp16 ulp
+        for dev, ref_ in ((k0, rk), (v0, rv)):
+            d = dev[b, :, pad:S].view(np.float16).astype(np.float32)
+            rr = ref_[b, :, pad:S]
+            assert np.all(np.abs(d - rr) <= np.spacing(np.abs(rr).astype(np.float16)).astype(np.float32)), b
+        d3 = k3[b, :, S:S + steps].view(np.float16).astype(np.float32)
+        r3 = ref3["kv"][0][b, :, S:S + steps]
+        assert np.abs(d3 - r3).max() <= 2e-2 * np.abs(r3).max()
+
+
+@pytest.fixture(scope="module")
+def zero2_gpu(tmp_path_factory):
+    d = tmp_path_factory.mktemp("kmg")
+    return KM.write(str(d / "zero2.gguf"), 11, [{}, {}])
+
+
+@pytest.fixture(scope="module")
+def idqkv_gpu(tmp_path_factory):
+    d = tmp_path_factory.mktemp("kmg")
+    return KM.write(str(d / "idqkv.gguf"), 12, [{"qkv": "id"}])
+
+
+@pytest.mark.parametrize("path", ["GEMV", "FUSED"])
+def test_decode_logits_known_answer(gpu, zero2_gpu, path):
+    """Zero projections: the logits entering step idx + 1 are the closed form of the token of step
+    idx embedded at PE position P + idx (tests/known_models.py), on the device as in the oracle."""
+    mpath, p, perm, scale = zero2_gpu
+    pe = KM.pe(64)
+    P = 6
+    reqs = _reqs(22, [4, 7, 11], P)
+    forced = np.array([17, 900, 3, 1000, 250, 64], np.int32)
+    g = gpu.Model(mpath)
+    try:
+        lg = _step_logits(g, reqs, forced, len(forced), getattr(gpu, f"GSVK_DECODE_{path}"))
+    finally:
+        g.close()
+    x = KM.decode_input64(p, reqs[0]["prompt"][P - 1], P - 1, pe)
+    for idx in range(len(forced)):
+        if idx > 0:
+            x = KM.decode_input64(p, forced[idx - 1], P + idx - 1, pe)
+        ref = KM.head64(KM.zero_layers64(p, x, 2), perm, scale)
+        bound = 2.0 ** -10 * np.abs(ref) + 1e-6
+        for b in range(3):
+            assert np.all(np.abs(lg[idx, b] - ref) <= bound), (idx, b)
+
+
+@pytest.mark.parametrize("path", ["GEMV", "FUSED"])
+def test_decode_kv_known_answer(gpu, idqkv_gpu, path):
+    """Identity QKV: the K row appended at column S + idx is the quantised input row + b_k, the
+    input being the token of step idx at PE position P + idx (bound from the activation
+    quantisation), and equals the oracle's to the bit."""
+    mpath, p, perm, scale = idqkv_gpu
+    pe = KM.pe(64)
+    P = 5
+    reqs = _reqs(24, [3, 8], P)
+    forced = np.array([40, 41, 1020, 7, 300, 12, 999], np.int32)
+    n = len(forced)
+    g = gpu.Model(mpath)
+    o = O.Model(mpath)
+    try:
+        g.set_decode_path(getattr(gpu, f"GSVK_DECODE_{path}"))
+        g.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=n, oracle=forced, seeds=[3, 4], flags=1)
+        k0, _ = g.kv_read(0)
+        ref = o.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=n, oracle=forced, seeds=[3, 4],
+                         flags=O.ORC_EOS_MASK_ALL | O.ORC_KV_F16, kv_layer=0)
+    finally:
+        g.close()
+        o.close()
+    S = 8 + P
+    bk = p["transformer.block0.qkv_b"][KM.D:2 * KM.D].astype(np.float64)
+    for idx in range(n):
+        x = KM.decode_input64(p, forced[idx], P + idx, pe)
+        bound = KM.block_amax(x) * KM.Q8_ERR * 1.001 + 2.0 ** -10 * np.abs(x + bk) + 1e-6
+        for b in range(2):
+            dev = k0[b, :, S + idx].view(np.float16).astype(np.float64).reshape(-1)
+            assert np.all(np.abs(dev - (x + bk)) <= bound), (idx, b)
+            assert np.array_equal(k0[b, :, S + idx].view(np.float16).astype(np.float32), ref["kv"][0][b, :, S + idx])
