@@ -79,6 +79,7 @@ constexpr int DPP_ROR1 = 0x121;   // row_ror within 16-lane rows
 constexpr int DPP_ROR2 = 0x122;
 constexpr int DPP_ROR4 = 0x124;
 constexpr int DPP_ROR8 = 0x128;   // rotation by 8 of 16 = lane i <- lane i ^ 8
+constexpr int DPP_ROR12 = 0x12C;  // lane i <- lane (i + 4) mod 16 within 16-lane rows
 
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {

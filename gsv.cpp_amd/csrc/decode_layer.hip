@@ -66,12 +66,31 @@ __device__ __forceinline__ float wg_layernorm(float v, float w, float c, int lan
     return __builtin_fmaf((v - mean) * inv, w, c);
 }
 
+// Maximum of |v| over the 32 lanes of each half wave, in every lane (DPP within rows of 16,
+// then a swizzle across the two rows of the half; max is exact in any order).
+__device__ __forceinline__ float half_wave_amax(float v) {
+    float a = fabsf(v);
+    a = fmaxf(a, dpp_f<DPP_XOR1>(a));
+    a = fmaxf(a, dpp_f<DPP_XOR2>(a));
+    a = fmaxf(a, dpp_f<DPP_ROR4>(a));
+    a = fmaxf(a, dpp_f<DPP_ROR8>(a));
+    return fmaxf(a, swz_xor16(a));
+}
+
+// The x86 Q8_0 quantisation of one value per lane, a block being the 32 lanes of a half wave
+// (q8_quantize_group's arithmetic). Returns fp32(fp16(d)).
+__device__ __forceinline__ float half_wave_quantize(float v, int8_t & q) {
+    const float amax = half_wave_amax(v);
+    const float d = amax / 127.0f;
+    const float id = (amax != 0.0f) ? 127.0f / amax : 0.0f;
+    q = (int8_t) (int) __builtin_rintf(v * id);
+    return h2f(f2h(d));
+}
+
 // The x86 Q8_0 quantisation of element tid of a row of 512 held one per thread (a block is the
 // 32 threads of a half wave), stored into the sliced LDS row (s_x, s_d) that the 8-lane dot reads.
 __device__ __forceinline__ void wg_quantize_row(float y, int tid, int8_t * s_x, float * s_d) {
-    float amax = fabsf(y);
-#pragma unroll
-    for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+    const float amax = half_wave_amax(y);
     const float d = amax / 127.0f;
     const float id = (amax != 0.0f) ? 127.0f / amax : 0.0f;
     const int8_t q = (int8_t) (int) __builtin_rintf(y * id);
@@ -97,21 +116,26 @@ __device__ __forceinline__ float row_dot8(const int4 (&w)[4], const uint2 (&dh)[
         acc = __builtin_fmaf(dw2 * dx.z, (float) __builtin_amdgcn_sdot4(w[i].z, xv.z, 0, false), acc);
         acc = __builtin_fmaf(dw3 * dx.w, (float) __builtin_amdgcn_sdot4(w[i].w, xv.w, 0, false), acc);
     }
-    acc = acc + __shfl_xor(acc, 4, 64);
-    acc = acc + __shfl_xor(acc, 2, 64);
-    acc = acc + __shfl_xor(acc, 1, 64);
+    // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)) in lane j = 0 of each 8-lane row (the other lanes
+    // hold partial values): rotating a 16-lane DPP row by 12 brings lane j + 4 to lanes j < 4 of
+    // either 8-lane half
+    acc = acc + dpp_f<DPP_ROR12>(acc);
+    acc = acc + dpp_f<DPP_XOR2>(acc);
+    acc = acc + dpp_f<DPP_XOR1>(acc);
     return acc;
 }
 
 // The exact int32 dot of one tiled 32 x 32 weight tile-block row with a Q8_0 activation block in
-// LDS: lane 32 hh + i holds quants [16 hh, 16 hh + 16) of row i; both halves end with the sum.
+// LDS: lane 32 hh + i holds quants [16 hh, 16 hh + 16) of row i; lane i < 32 ends with the sum.
 __device__ __forceinline__ int tile_dot(const int4 & w, const int8_t * a_blk, int lane) {
     const int4 av = *reinterpret_cast<const int4 *>(a_blk + 16 * (lane >> 5));
     int s = __builtin_amdgcn_sdot4(w.x, av.x, 0, false);
     s = __builtin_amdgcn_sdot4(w.y, av.y, s, false);
     s = __builtin_amdgcn_sdot4(w.z, av.z, s, false);
     s = __builtin_amdgcn_sdot4(w.w, av.w, s, false);
-    return s + __shfl_xor(s, 32, 64);
+    // lanes i < 32 add lane i + 32 (the other lanes' results are not used)
+    const auto sw = __builtin_amdgcn_permlane32_swap(s, s, false, false);
+    return s + (int) sw[1];
 }
 
 }  // namespace
@@ -141,8 +165,7 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     __shared__ float s_m[NW];
     __shared__ float s_l[NW];
     __shared__ float s_o[NW][ATT_HD];
-    __shared__ __align__(16) int8_t s_a[ATT_HD];
-    __shared__ float s_ad;
+    __shared__ __align__(16) int8_t s_a[DL_WAVES][ATT_HD];
 
     // ---- loads, in the order their data is needed, with no branch between them ----
     const int col = *a.col_ptr + a.col_add;   // column of this step's key
@@ -279,37 +302,35 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
         }
     }
     __syncthreads();
-    // wave 0: merge the waves, the head's output as one Q8_0 block (no valid key: 0, as ggml)
-    if (wave == 0) {
-        float val = 0.0f;
-        if (nkeys > 0) {
-            float M = s_m[0];
+    // every wave merges the waves' partials (the same arithmetic in each) into the head's output,
+    // lane d < 32 holding dimension d, quantised to one Q8_0 block (no valid key: 0, as ggml) and
+    // kept in the wave's own LDS slot: no further barrier
+    float val = 0.0f;
+    if (nkeys > 0) {
+        float M = s_m[0];
 #pragma unroll
-            for (int w2 = 1; w2 < NW; w2++) M = fmaxf(M, s_m[w2]);
-            float L = 0.0f, O = 0.0f;
+        for (int w2 = 1; w2 < NW; w2++) M = fmaxf(M, s_m[w2]);
+        float L = 0.0f, O = 0.0f;
+        const int dl = lane & (ATT_HD - 1);
 #pragma unroll
-            for (int w2 = 0; w2 < NW; w2++) {
-                const float f = s_m[w2] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w2] - M);
-                L = __builtin_fmaf(s_l[w2], f, L);
-                if (lane < ATT_HD) O = __builtin_fmaf(s_o[w2][lane], f, O);
-            }
-            val = O * (1.0f / L);
+        for (int w2 = 0; w2 < NW; w2++) {
+            const float f = s_m[w2] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(s_m[w2] - M);
+            L = __builtin_fmaf(s_l[w2], f, L);
+            O = __builtin_fmaf(s_o[w2][dl], f, O);
         }
-        float v1[1] = {lane < ATT_HD ? val : 0.0f};
-        int8_t q1[1];
-        const float d = q8_quantize_group<1>(v1, q1, 32);
-        if (lane < ATT_HD) s_a[lane] = q1[0];
-        if (lane == 0) s_ad = d;
+        val = O * (1.0f / L);
     }
-    __syncthreads();
+    int8_t qa;
+    const float da = half_wave_quantize(lane < ATT_HD ? val : 0.0f, qa);
+    if (lane < ATT_HD) s_a[wave][lane] = qa;
+    __builtin_amdgcn_wave_barrier();
 
     // ---- out projection of head h: partial row p1[h][b] ----
-    const float da = s_ad;
     float * prow = a.p1 + ((int64_t) h * B + b) * DL_K;
 #pragma unroll
     for (int u = 0; u < WO_T; u++) {
         const int t = wave + NW * u;
-        const int isum = tile_dot(wo[u], s_a, lane);
+        const int isum = tile_dot(wo[u], s_a[wave], lane);
         const float y = (h2f(wos[u]) * da) * (float) isum;
         if (lane < 32) prow[t * 32 + lane] = y;
     }
@@ -398,10 +419,9 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
     __syncthreads();
     // their Q8_0 blocks: wave k quantises block k
     if (wave < UB) {
-        float v1[1] = {lane < 32 ? s_h[wave * 32 + lane] : 0.0f};
-        int8_t q1[1];
-        const float d = q8_quantize_group<1>(v1, q1, 32);
-        if (lane < 32) s_hq[wave * 32 + lane] = q1[0];
+        int8_t q1;
+        const float d = half_wave_quantize(lane < 32 ? s_h[wave * 32 + lane] : 0.0f, q1);
+        if (lane < 32) s_hq[wave * 32 + lane] = q1;
         if (lane == 0) s_hd[wave] = d;
     }
     __syncthreads();
