@@ -13,10 +13,12 @@ resident on the device (the prefill runs before it and is reported separately).
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 16] [--no-cpu]
 
-Prints one JSON line. The roofline object times the dominant decode kernel alone with HIP events
-on the stream it runs on, rotating through buffers larger than the 256 MB MALL; cpu_baseline
-times the oracle (the CPU restatement of the reference path) on this host's cores on a bounded
-sample of the same workload.
+Prints one JSON line. The roofline object times the dominant decode kernel (the attention launch
+of the two-launch layer at batch <= 16) alone with HIP events on the stream it runs on, at the
+mid-run shape of the line's own steps, rotating through buffers larger than the 256 MB MALL; its
+traffic is the HBM-counter ratio of profiles/decode_layer_b16_hbm.md times those algorithmic
+bytes. cpu_baseline times the oracle (the CPU restatement of the reference path) on this host's
+cores on the same requests and the same steps, repeated to at least 10 s of decode.
 """
 from __future__ import annotations
 
@@ -106,82 +108,90 @@ def time_events(fn, iters, torch):
     return e0.elapsed_time(e1) / iters
 
 
-def kernel_roofline(gsvk, torch, reqs, steps):
-    """Time the decode-step kernels alone at the mid-run shape of the workload."""
-    B = len(reqs)
+def kernel_shape(reqs, steps):
+    """The mid-run shape of a decode run of `steps` steps: loop index steps // 2, every sequence's
+    valid keys [pad_b, S + idx]."""
     T = np.array([len(r["phones"]) for r in reqs])
     P = len(reqs[0]["prompt"])
     max_len = int(T.max())
     S = max_len + P
-    lstride = S + steps + 8 + 1
     mid = steps // 2
-    kv_begin = torch.tensor(max_len - T, dtype=torch.int32, device="cuda")
+    return {"S": S, "mid": mid, "pad": (max_len - T).astype(np.int32), "nkeys": int((S + mid + 1 - (max_len - T)).sum()),
+            "lstride": S + steps + 8 + 1}
+
+
+def kernel_roofline(gsvk, torch, reqs, steps):
+    """Time the decode-step kernels alone at the mid-run shape of the line's own run (`steps`
+    steps), each in a captured graph of many launches timed with HIP events on its stream,
+    rotating through weight copies and K/V caches larger than the 256 MB MALL."""
+    B = len(reqs)
+    sh = kernel_shape(reqs, steps)
+    S, mid, lstride = sh["S"], sh["mid"], sh["lstride"]
+    kv_begin = torch.tensor(sh["pad"], dtype=torch.int32, device="cuda")
     kv_end = torch.full((B,), S + mid + 1, dtype=torch.int32, device="cuda")
-    nkeys = int((S + mid + 1 - (max_len - T)).sum())
+    col = torch.tensor([S + mid], dtype=torch.int32, device="cuda")
+    nkeys = sh["nkeys"]
+    kv_bytes = nkeys * NH * 2 * HD * 2
     res = {}
-    # attention: rotate over the 24 per-layer caches (24 x 29.8 MB > MALL)
     rot = N_LAYER
-    kc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda")
-    vc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda")
+    scale = 1.0 / np.sqrt(32.0)
+    small = B <= 16
+    kc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
+    vc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
+    qkv_w = 3 * D * D // 32 * 34
+    out_w = D * D // 32 * 34
+    ffn_w = FFN * D // 32 * 34
+    rnd_q = lambda n: torch.randint(-127, 128, (rot, n), dtype=torch.int8, device="cuda")
+    rnd_d = lambda n: (torch.rand((rot, n), device="cuda") * 0.001).half().view(torch.int16)
+    if small:
+        # the two-launch layer of the decode (batch <= 16)
+        wq, wd = rnd_q(3 * D * D), rnd_d(3 * D * D // 32)
+        woq, wod = rnd_q(D * D), rnd_d(D * D // 32)
+        w1q, w1d = rnd_q(FFN * D), rnd_d(FFN * D // 32)
+        w2q, w2d = rnd_q(FFN * D), rnd_d(FFN * D // 32)
+        bq = torch.randn(3 * D, device="cuda") * 0.02
+        b1 = torch.randn(FFN, device="cuda") * 0.02
+        bo = torch.randn(D, device="cuda") * 0.02
+        xres = torch.randn((B, D), device="cuda")
+        parts = torch.randn((16, B, D), device="cuda") * 0.1
+        wb = torch.cat([torch.ones(D), torch.zeros(D)]).cuda()
+        x_out = torch.zeros((B, D), device="cuda")
+        n1 = torch.zeros((B, D), device="cuda")
+        p1 = torch.zeros((16, B, D), device="cuda")
+        p2 = torch.zeros((16, B, D), device="cuda")
+
+        def dec_attn(i):
+            r = i % rot
+            gsvk.op_dec_attn(B, wq[r], wd[r], bq, kc[r], vc[r], kv_begin, col, scale, woq[r], wod[r], p1,
+                             x_out=x_out, res=xres, parts=parts, ln_bias=bo, ln_wb=wb)
+
+        def dec_ffn(i):
+            r = i % rot
+            gsvk.op_dec_ffn(B, xres, parts, bo, wb, n1, w1q[r], w1d[r], b1, w2q[r], w2d[r], p2)
+        ms = time_events(dec_attn, 240, torch)
+        ab = kv_bytes + qkv_w + out_w
+        res["dec_attn"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER,
+                           "in_decode": True}
+        ms = time_events(dec_ffn, 240, torch)
+        fb = 2 * ffn_w
+        res["dec_ffn"] = {"ms": ms, "bytes": fb, "gbs": fb / ms / 1e6, "launches_per_step": N_LAYER,
+                          "in_decode": True}
+        del wq, wd, woq, wod, w1q, w1d, w2q, w2d
+    # the standalone decode attention (the matrix-core path's, from batch 17)
     q = torch.randn((B, NH, HD), dtype=torch.float32, device="cuda")
     out = torch.zeros((B, NH * HD), dtype=torch.float32, device="cuda")
     oq = torch.zeros(B * D, dtype=torch.int8, device="cuda")
     od = torch.zeros(B * NH, dtype=torch.float32, device="cuda")
     ws = torch.zeros(gsvk.attn_workspace_bytes(B, NH, lstride), dtype=torch.uint8, device="cuda")
-    scale = 1.0 / np.sqrt(32.0)
 
     def attn(i):
         gsvk.op_attn_decode(q, kc[i % rot], vc[i % rot], kv_begin, kv_end, lstride, scale, out, oq=oq,
                             od=od, ws=ws)
     ms = time_events(attn, 240, torch)
-    ab = nkeys * NH * 2 * HD * 2
-    fused = B <= 32   # the decode path runs QKV + attention as one kernel up to 32 sequences
-    res["attn_decode"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER,
-                          "in_decode": not fused}
-    # the fused QKV projection + attention: head h's QKV weight rows + the same K/V rows; rotates
-    # over 24 weight copies as well
-    wqkv = torch.randint(-127, 128, (rot, 3 * D * D), dtype=torch.int8, device="cuda")
-    wdqkv = (torch.rand((rot, 3 * D * D // 32), device="cuda") * 0.001).half().view(torch.int16)
-    bqkv = torch.randn(3 * D, dtype=torch.float32, device="cuda") * 0.02
-    lres = torch.randn((B, D), dtype=torch.float32, device="cuda")
-    lr = torch.randn((B, D), dtype=torch.float32, device="cuda")
-    lwb = torch.cat([torch.ones(D), torch.zeros(D)]).cuda()
-    col = torch.tensor([S + mid], dtype=torch.int32, device="cuda")
-
-    def qkv_attn(i):
-        gsvk.op_qkv_attn(wqkv[i % rot], wdqkv[i % rot], bqkv, lres, lr, None, lwb, kc[i % rot], vc[i % rot],
-                         kv_begin, col, scale, out, oq=oq, od=od)
-    if gsvk.qkv_attn_supported(B, NH, lstride):
-        ms = time_events(qkv_attn, 240, torch)
-        fb = ab + 3 * D * D // 32 * 34
-        res["qkv_attn"] = {"ms": ms, "bytes": fb, "gbs": fb / ms / 1e6, "launches_per_step": N_LAYER,
-                           "in_decode": fused}
-    del kc, vc, wqkv, wdqkv
-    # Q8_0 GEMVs at batch B (the decoder's fused kernel): rotate over 96 weight copies (> MALL).
-    # QKV and FFN1 run with their LayerNorm input stage, out and FFN2 read Q8_0 rows.
-    xq = torch.randint(-127, 128, (B * FFN,), dtype=torch.int8, device="cuda")
-    xd = torch.rand((B * FFN // 32,), dtype=torch.float32, device="cuda") * 0.01
-    xres = torch.randn((B, D), dtype=torch.float32, device="cuda")
-    xr = torch.randn((B, D), dtype=torch.float32, device="cuda")
-    wb = torch.cat([torch.ones(D), torch.zeros(D)]).cuda()
-    for name, n, k, ln in (("gemv_qkv", 3 * D, D, True), ("gemv_out", D, D, False), ("gemv_ffn1", FFN, D, True),
-                           ("gemv_ffn2", D, FFN, False)):
-        copies = 96
-        wq = torch.randint(-127, 128, (copies, n * k), dtype=torch.int8, device="cuda")
-        wd = (torch.rand((copies, n * k // 32), device="cuda") * 0.001).half().view(torch.int16)
-        y = torch.zeros((B, n), dtype=torch.float32, device="cuda")
-
-        def gemv(i, wq=wq, wd=wd, n=n, k=k, y=y, ln=ln):
-            if ln:
-                gsvk.op_ln_gemv(wq[i % copies], wd[i % copies], n, xres, xr, None, wb, None, 0, y)
-            else:
-                gsvk.op_q8_gemv(wq[i % copies], wd[i % copies], n, k, xq, xd, B, None, 0, y)
-        ms = time_events(gemv, 480, torch)
-        b = n * k // 32 * 34
-        res[name] = {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": N_LAYER,
-                     "in_decode": name != "gemv_qkv" or not fused}
-        del wq, wd
-    return res
+    res["attn_decode"] = {"ms": ms, "bytes": kv_bytes, "gbs": kv_bytes / ms / 1e6, "launches_per_step": N_LAYER,
+                          "in_decode": not small}
+    del kc, vc
+    return res, sh
 
 
 def attn_microkernel(gsvk, torch, seed=0x6A5E0003, B=64, sets=8):
@@ -224,36 +234,61 @@ def copy_probe(torch, nbytes=256 << 20):
     return nbytes
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` at the workload shape, from the committed counter summary
-    (rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE passes over `bench.py --kernels-only`, each scaled
-    by what the counter reads for a 256 MiB copy), or None when no summary holds it."""
-    path = os.path.join(ROOT, "profiles", "attn_decode_gemv_b16_kernels_hbm.md")
-    key = {"attn_decode": "attn_decode_b16", "qkv_attn": "qkv_attn_b16"}.get(kernel)
-    if key is None or not os.path.exists(path):
+PROFILE_HBM = os.path.join("profiles", "decode_layer_b16_hbm.md")
+
+
+def traffic_ratio(kernel):
+    """(HBM traffic / algorithmic bytes per launch, the shape it was measured at) of `kernel`
+    from the committed counter summary: two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
+    over `bench.py --kernels-only` at that shape, each scaled by what the counter reads for a
+    256 MiB copy. None when the summary does not hold the kernel."""
+    path = os.path.join(ROOT, PROFILE_HBM)
+    if not os.path.exists(path):
         return None
     for line in open(path):
         f = line.split()
-        if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == key:
-            return int(f[2])
+        if len(f) >= 5 and f[0] == "traffic_ratio" and f[1] == kernel:
+            return float(f[2]), " ".join(f[4:])
     return None
 
 
-def cpu_baseline(reqs, steps):
+def physical_cores():
+    """Physical cores of this host (unique (core, socket) pairs of lscpu -p), or None."""
+    import subprocess
+    try:
+        out = subprocess.run(["lscpu", "-p=CORE,SOCKET"], capture_output=True, text=True, check=True).stdout
+    except Exception:
+        return None
+    pairs = {tuple(l.split(",")) for l in out.splitlines() if l and not l.startswith("#")}
+    return len(pairs) or None
+
+
+def cpu_baseline(reqs, steps, min_s=10.0):
+    """The oracle (the CPU restatement of the reference's ggml path) on this host: the same
+    requests and the same `steps` decode steps as the GPU line (each run preceded by its own,
+    untimed prefill), repeated until at least min_s seconds of CPU work have run; the rate is the
+    tokens of the timed decode loops over their total time."""
     import oracle
     import synth_model as sm
     nthreads = oracle.nthreads_default()
     path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
     m = oracle.Model(path)
+    runs, dec_ms, pf_ms = 0, 0.0, 0.0
     try:
-        r = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=steps, seeds=list(range(1, len(reqs) + 1)),
-                       flags=oracle.ORC_EOS_MASK_ALL, nthreads=nthreads)
+        while runs == 0 or dec_ms + pf_ms < min_s * 1e3:
+            r = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=steps, seeds=list(range(1, len(reqs) + 1)),
+                           flags=oracle.ORC_EOS_MASK_ALL, nthreads=nthreads)
+            runs += 1
+            dec_ms += r["decode_ms"]
+            pf_ms += r["prefill_ms"]
     finally:
         m.close()
-    tok_s = len(reqs) * steps / (r["decode_ms"] / 1e3)
-    return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": nthreads, "kind": "port",
-            "sample": f"batch {len(reqs)}, same requests, prefill ({r['prefill_ms'] / 1e3:.1f} s, untimed) then "
-                      f"{steps} decode steps timed; F32 KV cache, OpenMP over {nthreads} threads"}
+    tok_s = len(reqs) * steps * runs / (dec_ms / 1e3)
+    return {"value": round(tok_s, 2), "unit": "tokens/s", "cores": nthreads, "physical_cores": physical_cores(),
+            "kind": "port",
+            "sample": f"batch {len(reqs)}, the same requests and the same {steps} decode steps as the GPU line, "
+                      f"{runs} run(s): {dec_ms / 1e3:.2f} s of decode timed (their prefills, {pf_ms / 1e3:.1f} s, "
+                      f"untimed); F32 KV cache, OpenMP over {nthreads} threads"}
 
 
 def prefill_line(g, torch):
@@ -338,7 +373,6 @@ def main():
     ap.add_argument("--batch", type=int, default=16)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-kernels", action="store_true")
-    ap.add_argument("--cpu-steps", type=int, default=500)
     ap.add_argument("--no-b128", action="store_true", help="skip the batch-128 long-context decode line")
     ap.add_argument("--prefill-only", action="store_true", help="time only the batch-16 x 1024 prefill")
     ap.add_argument("--b128-only", action="store_true", help="time only the batch-128 long-context decode")
@@ -359,9 +393,10 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.kernels_only:
-        kr = kernel_roofline(gsvk, torch, workload_requests(args.batch), args.steps)
+        kr, sh = kernel_roofline(gsvk, torch, workload_requests(args.batch), args.steps)
         res = {k: {"us": round(v["ms"] * 1e3, 3), "bytes": v["bytes"], "GBs": round(v["gbs"], 1),
                    "in_decode": v["in_decode"]} for k, v in kr.items()}
+        res["shape"] = {"batch": args.batch, "steps": args.steps, "mid_step": sh["mid"], "valid_keys": sh["nkeys"]}
         res["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         res["copy_probe_bytes"] = copy_probe(torch)
         print(json.dumps({"kernels_only": res}))
@@ -401,6 +436,9 @@ def main():
     tok_s = B * args.steps / dec_s
     ms_step = r["decode_ms"] / args.steps
     step_bytes = np.mean([decode_bytes_per_step(reqs, s) for s in range(0, args.steps, max(1, args.steps // 16))])
+    Tn = np.array([len(r["phones"]) for r in reqs])
+    step_kv_lo = Tn.min() + len(reqs[0]["prompt"]) + 1
+    step_kv_hi = Tn.max() + len(reqs[0]["prompt"]) + args.steps
     extra = {"prefill_ms": round(r["prefill_ms"], 2), "wall_s_incl_prefill": round(wall, 3),
              "step_bytes_mb": round(step_bytes / 1e6, 1),
              "step_hbm_frac": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
@@ -426,18 +464,25 @@ def main():
 
     roof = None
     if not args.no_kernels:
-        kr = kernel_roofline(gsvk, torch, reqs, args.steps)
+        kr, sh = kernel_roofline(gsvk, torch, reqs, args.steps)
         extra["kernels"] = {k: {"us": round(v["ms"] * 1e3, 2), "GBs": round(v["gbs"], 1),
-                                "frac": round(v["gbs"] / HBM_PEAK_GBS, 4)} for k, v in kr.items()}
+                                "frac": round(v["gbs"] / HBM_PEAK_GBS, 4), "in_decode": v["in_decode"]}
+                            for k, v in kr.items()}
         extra["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         dom = max((k for k in kr if kr[k]["in_decode"]), key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
         d = kr[dom]
+        tr = traffic_ratio(dom)
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(dom),
-                "bytes_per_launch": int(d["bytes"]), "us_per_launch": round(d["ms"] * 1e3, 3)}
+                "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
+                "traffic": None if tr is None else int(round(tr[0] * d["bytes"])),
+                "bytes_per_launch": int(d["bytes"]), "us_per_launch": round(d["ms"] * 1e3, 3),
+                "shape": f"batch {B}, mid-run of {args.steps} steps (loop index {sh['mid']}), "
+                         f"{sh['nkeys']} valid keys per head",
+                "traffic_basis": None if tr is None else
+                {"ratio": tr[0], "measured_at": tr[1], "profile": PROFILE_HBM}}
     cpu = None
     if not args.no_cpu:
-        cpu = cpu_baseline(reqs, args.cpu_steps)
+        cpu = cpu_baseline(reqs, args.steps)
 
     line = {
         "metric": "AR decode tokens/sec at batch 1/16/64; attn+Q8_0 GEMV % of HBM roofline",
@@ -445,8 +490,10 @@ def main():
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "q8_0 int8 dot, fp32 accumulate, fp16 KV",
         "data": "synthetic (random-init weights from a fixed seed, seeded requests)",
-        "config": {"workload": "batched AR decode, 24-layer t2s decoder (d512, 16x32 heads, FFN 2048, "
-                               "Q8_0), batch 16, prompt lengths U[100,400], 500 steps, top-k 15 sampling",
+        "config": {"workload": f"batched AR decode, 24-layer t2s decoder (d512, 16x32 heads, FFN 2048, Q8_0, "
+                               f"F16 head), batch {B}, prompt lengths U[100,400] (64 prompt codes), fp16 KV, "
+                               f"top-k 15 sampling, the first {args.steps} decode steps of the configuration's 500 "
+                               f"(KV {int(step_kv_lo)}-{int(step_kv_hi)} keys per sequence over the timed steps)",
                    "batch": B, "decode_steps": args.steps, "prompt_codes": 64,
                    "kv": "fp16", "parallelism": "single GPU"},
         "roofline": roof,

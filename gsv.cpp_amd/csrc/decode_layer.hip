@@ -474,3 +474,63 @@ int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream) {
 }
 
 }  // namespace gsvk
+
+extern "C" int gsvk_op_dec_attn(int B, const float * res, const float * parts, const float * ln_bias,
+                                const float * ln_wb, const float * emb, const float * pe, const int32_t * tok,
+                                const int32_t * pos, int pos_add, float alpha, int vocab, int pe_rows,
+                                float * x_out, const int8_t * wq, const uint16_t * wd, const float * bqkv,
+                                uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                                const int32_t * col, float scale, const int8_t * woq, const uint16_t * wod,
+                                float * p1, void * stream) {
+    using namespace gsvk;
+    DecAttnArgs a{};
+    a.mode = res ? IN_LN : IN_EMB;
+    a.res = res;
+    a.parts = parts;
+    a.bias = ln_bias;
+    a.wb = ln_wb;
+    a.emb = emb;
+    a.pe = pe;
+    a.tok = tok;
+    a.pos_ptr = pos;
+    a.pos_add = pos_add;
+    a.pe_rows = pe_rows;
+    a.alpha = alpha;
+    a.vocab = vocab;
+    a.x_out = x_out;
+    a.wq = wq;
+    a.wd = wd;
+    a.bqkv = bqkv;
+    a.kc = k;
+    a.vc = v;
+    a.lstride = lstride;
+    a.kv_begin = kv_begin;
+    a.col_ptr = col;
+    a.col_add = 0;
+    a.scale_log2 = scale * LOG2E;
+    a.woq = woq;
+    a.wod = wod;
+    a.p1 = p1;
+    a.B = B;
+    return launch_dec_attn(a, (hipStream_t) stream);
+}
+
+extern "C" int gsvk_op_dec_ffn(int B, const float * res, const float * p1, const float * bo, const float * ln1_wb,
+                               float * n1_out, const int8_t * w1q, const uint16_t * w1d, const float * b1,
+                               const int8_t * w2q, const uint16_t * w2d, float * p2, void * stream) {
+    using namespace gsvk;
+    DecFfnArgs a{};
+    a.res = res;
+    a.p1 = p1;
+    a.bo = bo;
+    a.wb1 = ln1_wb;
+    a.n1_out = n1_out;
+    a.w1q = w1q;
+    a.w1d = w1d;
+    a.b1 = b1;
+    a.w2q = w2q;
+    a.w2d = w2d;
+    a.p2 = p2;
+    a.B = B;
+    return launch_dec_ffn(a, (hipStream_t) stream);
+}

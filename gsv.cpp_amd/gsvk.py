@@ -29,7 +29,7 @@ EXPORTS = [
     "gsvk_qkv_attn_supported", "gsvk_op_q8_gemm", "gsvk_op_q8_gemm_ex", "gsvk_op_attn_prefill",
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
-    "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path",
+    "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
@@ -100,6 +100,9 @@ def lib():
         L.gsvk_first_logits.argtypes = [vp, C.POINTER(Request), i32, vp]
         L.gsvk_release_cache.argtypes = [vp]
         L.gsvk_model_set_decode_path.argtypes = [vp, i32]
+        L.gsvk_op_dec_attn.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp,
+                                       vp, i64, vp, vp, f32, vp, vp, vp, vp]
+        L.gsvk_op_dec_ffn.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.gsvk_kv_alloc.argtypes = [vp, i32, i32]
         L.gsvk_prefill.argtypes = [vp, C.POINTER(Request), i32, vp, C.POINTER(C.c_int)]
         L.gsvk_decode_step.argtypes = [vp, vp, vp]
@@ -242,6 +245,24 @@ def op_attn_decode_noalloc(q, k, v, kv_begin, kv_end, max_keys, scale, out, out1
     check(lib().gsvk_op_attn_decode_noalloc(_p(q), _p(k), _p(v), B, nh, hd, lstride, _p(kv_begin),
                                             _p(kv_end), max_keys, scale, _p(out), _p(out16), _p(oq), _p(od),
                                             _stream(stream)), "attn_decode_noalloc")
+
+
+def op_dec_attn(B, wq, wd, bqkv, k, v, kv_begin, col, scale, woq, wod, p1, x_out=None, res=None, parts=None,
+                ln_bias=None, ln_wb=None, emb=None, pe=None, tok=None, pos=None, pos_add=0, alpha=1.0, vocab=0,
+                pe_rows=0, stream=None):
+    """Launch 1 of the two-launch decode layer (include/gsvk.h gsvk_op_dec_attn); k, v
+    [B][16][lstride][32] fp16 (as int16 tensors)."""
+    lstride = k.shape[2]
+    check(lib().gsvk_op_dec_attn(B, _p(res), _p(parts), _p(ln_bias), _p(ln_wb), _p(emb), _p(pe), _p(tok), _p(pos),
+                                 pos_add, alpha, vocab, pe_rows, _p(x_out), _p(wq), _p(wd), _p(bqkv), _p(k), _p(v),
+                                 lstride, _p(kv_begin), _p(col), scale, _p(woq), _p(wod), _p(p1), _stream(stream)),
+          "dec_attn")
+
+
+def op_dec_ffn(B, res, p1, bo, ln1_wb, n1_out, w1q, w1d, b1, w2q, w2d, p2, stream=None):
+    """Launch 2 of the two-launch decode layer (include/gsvk.h gsvk_op_dec_ffn)."""
+    check(lib().gsvk_op_dec_ffn(B, _p(res), _p(p1), _p(bo), _p(ln1_wb), _p(n1_out), _p(w1q), _p(w1d), _p(b1), _p(w2q),
+                                _p(w2d), _p(p2), _stream(stream)), "dec_ffn")
 
 
 def op_attn_prefill(qkv, max_len, pad, nh, scale, out, oq=None, od=None, path=0, stream=None):

@@ -348,6 +348,33 @@ int gsvk_op_attn_decode_noalloc(const float * q, const uint16_t * k, const uint1
                                 const int32_t * kv_end, int64_t max_keys, float scale, float * out,
                                 uint16_t * out_f16, int8_t * oq, float * od, void * stream);
 
+/* The decode layer of up to 16 sequences in two launches (GSVK_DECODE_FUSED; d_model 512, 16
+ * heads of 32, FFN 2048). Launch 1, per (head, sequence): the input row x = LayerNorm((res +
+ * parts[0] + ... + parts[15]) + ln_bias) with ln_wb = [w; b] (parts [16][B][512]: the previous
+ * layer's FFN2 partial rows), or, when res is NULL, emb[tok[b]] + alpha * pe[*pos + pos_add]
+ * (row clamped into pe_rows); x stored to x_out [B][512]; q, k, v of the head with the QKV
+ * weights wq/wd (sliced Q8_0 [1536][512]) + bqkv; k, v appended to the fp16 caches k, v
+ * [B][16][lstride][32] at column *col; attention over [kv_begin[b], *col]; the head's output
+ * quantised to one Q8_0 block times the out projection (woq/wod: Q8_0 [512][512] in the
+ * matrix-core operand order of gsvk_op_q8_gemm_ex) gives the partial row p1[head][b][0:512].
+ * Replaces the QKV projection, K/V append, flash_attn_ext and out projection of
+ * src/gsv_ar.cpp:392-407; sum_h p1[h] is the out projection. */
+int gsvk_op_dec_attn(int B, const float * res, const float * parts, const float * ln_bias,
+                     const float * ln_wb, const float * emb, const float * pe, const int32_t * tok,
+                     const int32_t * pos, int pos_add, float alpha, int vocab, int pe_rows,
+                     float * x_out, const int8_t * wq, const uint16_t * wd, const float * bqkv,
+                     uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                     const int32_t * col, float scale, const int8_t * woq, const uint16_t * wod,
+                     float * p1, void * stream);
+/* Launch 2, per (group of 128 hidden units, sequence): n1 = LayerNorm((res + p1[0] + ... +
+ * p1[15]) + bo) with ln1_wb, stored to n1_out [B][512]; h = relu(W1 . n1 + b1) for the group's
+ * units (w1q/w1d sliced Q8_0 [2048][512]), quantised to Q8_0; p2[group][b][0:512] = the FFN2
+ * columns of the group (w2q/w2d: Q8_0 [512][2048] in the matrix-core operand order) times those
+ * blocks. Replaces LN1, FFN1 + ReLU and FFN2 of src/gsv_ar.cpp:408-411; sum_g p2[g] is FFN2. */
+int gsvk_op_dec_ffn(int B, const float * res, const float * p1, const float * bo, const float * ln1_wb,
+                    float * n1_out, const int8_t * w1q, const uint16_t * w1d, const float * b1,
+                    const int8_t * w2q, const uint16_t * w2d, float * p2, void * stream);
+
 /* Prefill self-attention (the flash_attn_ext of src/gsv_ar.cpp:257 over all B*S rows, masks of
  * src/gsv_ar.cpp:215-223): qkv fp32 [B][S][3*nh*hd] (Q, K, V of head h at h*hd, D + h*hd,
  * 2*D + h*hd); pad device int32 [B]; query s of sequence b sees keys [pad[b], max_len) when

@@ -175,3 +175,117 @@ def test_decode_kv_known_answer(gpu, idqkv_gpu, path):
             dev = k0[b, :, S + idx].view(np.float16).astype(np.float64).reshape(-1)
             assert np.all(np.abs(dev - (x + bk)) <= bound), (idx, b)
             assert np.array_equal(k0[b, :, S + idx].view(np.float16).astype(np.float32), ref["kv"][0][b, :, S + idx])
+
+
+# ---------------------------------------------------------------------------- the two kernels alone
+
+def _q8_weights(gpu, torch, rng, n, k, tiled=False):
+    """Random Q8_0 weights [n][k]: (sliced quants, fp16 scales) as the GEMV reads them, and with
+    tiled=True also the matrix-core operand order the two-launch layer reads."""
+    from test_gpu_ops import _dev, blocks_to_split, to_tiled
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    blk = sm.q8_quantize_ref(W).ravel()
+    qs = torch.zeros(n * k, dtype=torch.int8, device="cuda")
+    d = torch.zeros(n * k // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(_dev(blk, torch), n, k, qs, d)
+    if not tiled:
+        return qs, d
+    qn, dn = blocks_to_split(blk, n, k)
+    qt, dt = to_tiled(qn, dn.view(np.int16))
+    return qs, d, _dev(qt, torch), _dev(dt, torch)
+
+
+def _seq_sum(parts):
+    """parts[0] + parts[1] + ... in that order, in fp32 (the kernels' order)."""
+    r = parts[0].copy()
+    for p in parts[1:]:
+        r = (r + p).astype(np.float32)
+    return r
+
+
+@pytest.mark.parametrize("B", [1, 5, 16])
+def test_dec_attn_op_matches_separate_kernels(gpu, B):
+    """Launch 1 against the GEMV chain's kernels on the same inputs: the LayerNorm row and the
+    K/V append bit for bit; the sum of the 16 per-head partial rows is the out projection of the
+    same Q8_0 attention output, to fp32 summation order (2e-6 of its scale)."""
+    import torch
+    from test_gpu_ops import _dev
+    rng = np.random.default_rng(8000 + B)
+    D, nh, lstride = 512, 16, 700
+    wq, wd = _q8_weights(gpu, torch, rng, 3 * D, D)
+    wos, wod_s, woq, wod = _q8_weights(gpu, torch, rng, D, D, tiled=True)
+    bqkv = rng.standard_normal(3 * D).astype(np.float32) * 0.02
+    res = rng.standard_normal((B, D)).astype(np.float32)
+    parts = (rng.standard_normal((16, B, D)) * 0.1).astype(np.float32)
+    lb = (rng.standard_normal(D) * 0.02).astype(np.float32)
+    wb = np.concatenate([1 + 0.05 * rng.standard_normal(D), 0.05 * rng.standard_normal(D)]).astype(np.float32)
+    kc = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16)
+    vc = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16)
+    col = lstride - 5
+    begins = rng.integers(0, 200, B).astype(np.int32)
+    begins[0] = 0
+    scale = float(1.0 / np.sqrt(32.0))
+    d = lambda a: _dev(a, torch)
+    kb, colt = d(begins), torch.tensor([col], dtype=torch.int32, device="cuda")
+    # the two-launch layer's first kernel
+    k1, v1 = d(kc).view(torch.int16), d(vc).view(torch.int16)
+    x1 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    p1 = torch.zeros((16, B, D), dtype=torch.float32, device="cuda")
+    gpu.op_dec_attn(B, wq, wd, d(bqkv), k1, v1, kb, colt, scale, woq, wod, p1, x_out=x1, res=d(res),
+                    parts=d(parts), ln_bias=d(lb), ln_wb=d(wb))
+    # the GEMV chain's kernels
+    k2, v2 = d(kc), d(vc)
+    qkv = torch.zeros((B, 3 * D), dtype=torch.float32, device="cuda")
+    x2 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_ln_gemv(wq, wd, 3 * D, d(res), d(_seq_sum(parts)), d(lb), d(wb), d(bqkv), 0, qkv, ln_out=x2)
+    k2[:, :, col, :] = qkv[:, D:2 * D].reshape(B, nh, 32).half()
+    v2[:, :, col, :] = qkv[:, 2 * D:].reshape(B, nh, 32).half()
+    att = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    oq = torch.zeros(B * D, dtype=torch.int8, device="cuda")
+    od = torch.zeros(B * nh, dtype=torch.float32, device="cuda")
+    ws = torch.zeros(gpu.attn_workspace_bytes(B, nh, lstride), dtype=torch.uint8, device="cuda")
+    ke = torch.full((B,), col + 1, dtype=torch.int32, device="cuda")
+    gpu.op_attn_decode(qkv[:, :D].reshape(B, nh, 32).contiguous(), k2.view(torch.int16), v2.view(torch.int16), kb,
+                       ke, lstride, scale, att, oq=oq, od=od, ws=ws)
+    y = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemv(wos, wod_s, D, D, oq, od, B, None, 0, y)
+    torch.cuda.synchronize()
+    assert torch.equal(x1, x2)
+    assert torch.equal(k1, k2.view(torch.int16)) and torch.equal(v1, v2.view(torch.int16))
+    yref = y.cpu().numpy().astype(np.float64)
+    ysum = p1.cpu().numpy().astype(np.float64).sum(axis=0)
+    assert np.abs(ysum - yref).max() <= 2e-6 * np.abs(yref).max()
+
+
+@pytest.mark.parametrize("B", [1, 5, 16])
+def test_dec_ffn_op_matches_separate_kernels(gpu, B):
+    """Launch 2 against the GEMV chain's kernels on the same inputs: LN1 bit for bit; the sum of
+    the 16 per-group partial rows is FFN2 of the same Q8_0 hidden row, to fp32 summation order."""
+    import torch
+    from test_gpu_ops import _dev
+    rng = np.random.default_rng(8100 + B)
+    D, F = 512, 2048
+    w1q, w1d = _q8_weights(gpu, torch, rng, F, D)
+    w2s, w2d_s, w2q, w2d = _q8_weights(gpu, torch, rng, D, F, tiled=True)
+    b1 = (rng.standard_normal(F) * 0.02).astype(np.float32)
+    res = rng.standard_normal((B, D)).astype(np.float32)
+    p1 = (rng.standard_normal((16, B, D)) * 0.1).astype(np.float32)
+    bo = (rng.standard_normal(D) * 0.02).astype(np.float32)
+    wb = np.concatenate([1 + 0.05 * rng.standard_normal(D), 0.05 * rng.standard_normal(D)]).astype(np.float32)
+    d = lambda a: _dev(a, torch)
+    n1 = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    p2 = torch.zeros((16, B, D), dtype=torch.float32, device="cuda")
+    gpu.op_dec_ffn(B, d(res), d(p1), d(bo), d(wb), n1, w1q, w1d, d(b1), w2q, w2d, p2)
+    h = torch.zeros((B, F), dtype=torch.float32, device="cuda")
+    n1r = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_ln_gemv(w1q, w1d, F, d(res), d(_seq_sum(p1)), d(bo), d(wb), d(b1), 1, h, ln_out=n1r)
+    hq = torch.zeros(B * F, dtype=torch.int8, device="cuda")
+    hd = torch.zeros(B * F // 32, dtype=torch.float32, device="cuda")
+    gpu.op_q8_quantize(h, hq, hd)
+    y = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    gpu.op_q8_gemv(w2s, w2d_s, D, F, hq, hd, B, None, 0, y)
+    torch.cuda.synchronize()
+    assert torch.equal(n1, n1r)
+    yref = y.cpu().numpy().astype(np.float64)
+    ysum = p2.cpu().numpy().astype(np.float64).sum(axis=0)
+    assert np.abs(ysum - yref).max() <= 2e-6 * np.abs(yref).max()
