@@ -369,6 +369,11 @@ float orc_rng_exponential(uint64_t * state) {
     return -logf(1.0f - u);
 }
 
+/* n draws of orc_rng_exponential in order (test helper: the q values of a run of sampling steps) */
+void orc_rng_exponential_n(uint64_t * state, int64_t n, float * out) {
+    for (int64_t i = 0; i < n; i++) out[i] = orc_rng_exponential(state);
+}
+
 int orc_argmax_probs_over_q(const float * probs, const float * q, int V) {
     int best = 0;
     float bv = -INFINITY;

@@ -108,6 +108,7 @@ void     orc_logits_to_probs(int top_k, float top_p, float temperature, float re
                              int V, const int32_t * prev, int n_prev, float * probs);
 uint64_t orc_rng_next(uint64_t * state);
 float    orc_rng_exponential(uint64_t * state);
+void     orc_rng_exponential_n(uint64_t * state, int64_t n, float * out);
 int      orc_argmax_probs_over_q(const float * probs, const float * q, int V);
 int      orc_sample(const float * probs, int V, uint64_t * state);
 

@@ -78,6 +78,7 @@ def lib():
         L.orc_rng_next.argtypes = [C.POINTER(C.c_uint64)]
         L.orc_rng_exponential.restype = C.c_float
         L.orc_rng_exponential.argtypes = [C.POINTER(C.c_uint64)]
+        L.orc_rng_exponential_n.argtypes = [C.POINTER(C.c_uint64), C.c_int64, _f32p]
         L.orc_argmax_probs_over_q.restype = C.c_int
         L.orc_argmax_probs_over_q.argtypes = [_f32p, _f32p, C.c_int]
         L.orc_sample.restype = C.c_int
@@ -224,6 +225,14 @@ def rng_exponential(seed, n):
     s = C.c_uint64(seed if seed else 1)
     out = np.array([lib().orc_rng_exponential(C.byref(s)) for _ in range(n)], np.float32)
     return out, s.value
+
+
+def rng_exponential_n(seed, n):
+    """n draws of rng_exponential from `seed` (0 -> 1), as float32."""
+    s = C.c_uint64(seed if seed else 1)
+    out = np.zeros(n, np.float32)
+    lib().orc_rng_exponential_n(C.byref(s), n, out)
+    return out
 
 
 def sample(probs, seed):

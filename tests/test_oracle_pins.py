@@ -350,3 +350,10 @@ def test_generate_loop_rules(tiny_path):
     # sampled EOS is impossible before step 11 without the oracle
     r = m.generate(reqs, max_steps=11, sampler=(0, 1.0, 1.0, 1.0), seeds=[5, 6, 7], nthreads=2)
     assert all(128 not in list(t[P:]) for t in r["tokens"])
+
+
+def test_rng_exponential_n_is_the_same_stream():
+    """The bulk draw helper the workload tests use equals the golden-pinned one-draw function."""
+    for seed in (0, 1, 7, 2 ** 63 + 5):
+        a, _ = O.rng_exponential(seed, 2100)
+        assert np.array_equal(O.rng_exponential_n(seed, 2100).view(np.uint32), a.view(np.uint32))
