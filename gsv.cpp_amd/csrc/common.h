@@ -66,8 +66,12 @@ __device__ __forceinline__ float h2f(uint16_t h) {
     return (float) v;
 }
 
-// fp32 -> fp16, round to nearest even (the F16C conversion ggml-cpu uses).
+// fp32 -> fp16, round to nearest even (the F16C conversion ggml-cpu uses), of the fp32 value f.
+// The empty asm makes f opaque: without it the compiler may fuse the FMA or multiply that
+// produced f with the conversion (v_fma_mixlo_f16), rounding the exact result once to fp16
+// instead of first to fp32, which differs where the fp32 value is an fp16 tie.
 __device__ __forceinline__ uint16_t f2h(float f) {
+    __asm__("" : "+v"(f));
     _Float16 v = (_Float16) f;
     return __builtin_bit_cast(uint16_t, v);
 }

@@ -40,6 +40,12 @@ int launch_gather_last(const float * in, int B, int S, int d, float * out, hipSt
 int launch_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                         int d_model, float scale, float * out, int8_t * oq, float * od,
                         hipStream_t stream);
+int launch_attn_exact_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v, int B,
+                             int nh, int64_t lstride, const int32_t * kv_begin, const int32_t * kv_end,
+                             float scale, float * out, int8_t * oq, float * od, hipStream_t stream,
+                             int oq_layout);
+int launch_attn_exact_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
+                              int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream);
 
 constexpr int PE_MAX = 4096;   // Y_PE_MAX, src/gsv_ar.cpp:44
 
@@ -149,6 +155,7 @@ struct gsvk_model {
     float * qkv = nullptr, * o = nullptr, * h2 = nullptr, * logits = nullptr;
     float * p1 = nullptr, * p2 = nullptr;   // partial rows of the two-launch decode layer
     int decode_path = GSVK_DECODE_AUTO;
+    bool exact = false;   // gsvk_model_set_exact: ggml-cpu's arithmetic order throughout
     void * attn_ws = nullptr;
     int32_t * kv_begin = nullptr, * kv_end = nullptr;
     int32_t * d_step = nullptr, * hist = nullptr, * ny = nullptr, * fin_step = nullptr,
@@ -560,7 +567,14 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
             in.wb = p.ln2;
         }
         in.out_x = x.x;
-        if (qkv_attn_preferred(n, m->NH, m->lstride)) {
+        if (m->exact) {
+            // the GEMV QKV, then attention in ggml-cpu's sequential order with glibc's expf
+            GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, n, in,
+                                       qkv_out(m, w, loff, qkv, D, 1, m->d_step, m->S - 1), st));
+            GSVK_TRY(launch_attn_exact_decode(qkv, D, m->kc + loff, m->vc + loff, n, m->NH, m->lstride,
+                                              m->kv_begin + r0, m->kv_end + r0, scale, attn.x, attn.q, attn.d, st,
+                                              Q8_SLICED));
+        } else if (qkv_attn_preferred(n, m->NH, m->lstride)) {
             // QKV + attention in one launch per layer
             QkvAttnArgs qa{};
             qa.ws = w.qkv.qs;
@@ -672,6 +686,11 @@ bool fused_decode_ok(const gsvk_model * m) {
 }
 
 int enqueue_decode_body(gsvk_model * m) {
+    if (m->exact) {
+        GSVK_REQUIRE(m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences (got %d)",
+                     DECODE_GEMM_MIN_BATCH - 1, m->B);
+        return enqueue_decode_rows(m, 0, m->B, m->stream);
+    }
     switch (m->decode_path) {
     case GSVK_DECODE_GEMV:
         if (m->B < DECODE_GEMM_MIN_BATCH) return enqueue_decode_rows(m, 0, m->B, m->stream);
@@ -837,8 +856,11 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R1, proj, D, 0, st));
     }
     if (R) GSVK_TRY(launch_add_proj(cur.x, proj, m->bert_b, d_rowb, d_rowt, d_pad, S, D, R, R1, st));
+    // projections on the matrix-core GEMMs from GEMM_MIN_ROWS rows on, except in exact mode (the
+    // GEMV chain in ggml-cpu's order and the sequential attention at any row count)
+    const bool gemm = !m->exact && rows >= GEMM_MIN_ROWS;
     // the layer-0 QKV reads this copy: natural order for the GEMM, sliced for the GEMV
-    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, rows >= GEMM_MIN_ROWS ? Q8_NATURAL : Q8_SLICED));
+    GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, gemm ? Q8_NATURAL : Q8_SLICED));
     int32_t * zero = nullptr;
     GSVK_TRY(tmp.alloc(zero, 1));
     GSVK_HIP(hipMemsetAsync(zero, 0, 4, st));
@@ -846,7 +868,6 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     for (int li = 0; li < m->NL; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
-        const bool gemm = rows >= GEMM_MIN_ROWS;
         if (gemm) {
             // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
             if (li > 0) {
@@ -875,13 +896,16 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, rows, in,
                                        qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0), st));
         }
-        if (attn_prefill_uses_mfma(rows))
+        if (m->exact)
+            GSVK_TRY(launch_attn_exact_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
+                                               attn.d, st));
+        else if (attn_prefill_uses_mfma(rows))
             GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                               attn.d, st));
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
-        GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, rows >= GEMM_MIN_ROWS ? &n1 : nullptr,
+        GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, gemm ? &n1 : nullptr,
                             Q8_NATURAL, d_pad, S));
     }
     GSVK_TRY(final_ln(m, st, rows, n1.x, h2, cur));
@@ -1231,6 +1255,15 @@ extern "C" int gsvk_model_set_decode_path(gsvk_model * m, int path) {
     cb_drop(m);
     drop_graph(m);
     m->decode_path = path;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_model_set_exact(gsvk_model * m, int on) {
+    GSVK_REQUIRE(m, "null model");
+    DeviceGuard guard(m->device);
+    cb_drop(m);
+    drop_graph(m);
+    m->exact = on != 0;
     return GSVK_OK;
 }
 

@@ -30,6 +30,7 @@ EXPORTS = [
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
+    "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
@@ -100,6 +101,9 @@ def lib():
         L.gsvk_first_logits.argtypes = [vp, C.POINTER(Request), i32, vp]
         L.gsvk_release_cache.argtypes = [vp]
         L.gsvk_model_set_decode_path.argtypes = [vp, i32]
+        L.gsvk_model_set_exact.argtypes = [vp, i32]
+        L.gsvk_op_attn_exact.argtypes = [vp, vp, vp, i32, i32, i64, vp, vp, f32, vp, vp, vp, vp]
+        L.gsvk_op_expf_exact.argtypes = [vp, i64, vp, vp]
         L.gsvk_op_dec_attn.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp,
                                        vp, i64, vp, vp, f32, vp, vp, vp, vp]
         L.gsvk_op_dec_ffn.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -247,6 +251,22 @@ def op_attn_decode_noalloc(q, k, v, kv_begin, kv_end, max_keys, scale, out, out1
                                             _stream(stream)), "attn_decode_noalloc")
 
 
+def op_attn_exact(q, k, v, kv_begin, kv_end, scale, out, oq=None, od=None, stream=None):
+    """Decode attention in ggml-cpu's sequential order (include/gsvk.h gsvk_op_attn_exact): q [B][nh][32]
+    fp32, k, v [B][nh][lstride][32] fp16 (as int16 tensors)."""
+    B, nh, hd = q.shape
+    if hd != 32:
+        raise ValueError("attn_exact: head_dim must be 32")
+    lstride = k.shape[2]
+    check(lib().gsvk_op_attn_exact(_p(q), _p(k), _p(v), B, nh, lstride, _p(kv_begin), _p(kv_end), scale, _p(out),
+                                   _p(oq), _p(od), _stream(stream)), "attn_exact")
+
+
+def op_expf_exact(x, y, stream=None):
+    """y = expf(x) elementwise on the device with glibc's results (float32 tensors)."""
+    check(lib().gsvk_op_expf_exact(_p(x), x.numel(), _p(y), _stream(stream)), "expf_exact")
+
+
 def op_dec_attn(B, wq, wd, bqkv, k, v, kv_begin, col, scale, woq, wod, p1, x_out=None, res=None, parts=None,
                 ln_bias=None, ln_wb=None, emb=None, pe=None, tok=None, pos=None, pos_add=0, alpha=1.0, vocab=0,
                 pe_rows=0, stream=None):
@@ -381,6 +401,10 @@ class Model:
     def set_decode_path(self, path: int):
         """GSVK_DECODE_AUTO / _GEMV / _FUSED / _MFMA (include/gsvk.h)."""
         check(lib().gsvk_model_set_decode_path(self.h, path), "set_decode_path")
+
+    def set_exact(self, on: bool = True):
+        """Exact mode (include/gsvk.h gsvk_model_set_exact): ggml-cpu's arithmetic order throughout."""
+        check(lib().gsvk_model_set_exact(self.h, 1 if on else 0), "set_exact")
 
     # -- a batch that requests join and leave while it decodes (gsvk_cb_*) --
     def cb_open(self, capacity, max_prefill, max_steps, prompt_len, sampler=(15, 1.0, 1.0, 1.35), early_stop=-1,

@@ -159,6 +159,15 @@ int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * 
 #define GSVK_DECODE_MFMA   3
 int gsvk_model_set_decode_path(gsvk_model * m, int path);
 
+/* Exact mode (on != 0): every projection, LayerNorm, quantisation and attention row of the
+ * prefill and the decode in ggml-cpu's x86 arithmetic order, so that logits and tokens are those
+ * of the CPU reference bit for bit: the GEMV chain at every row count (no matrix-core GEMM) and
+ * the attention of each (row, head) as flash_attn_ext's sequential online softmax with glibc's
+ * expf (gsvk_op_attn_exact). Slower than the default kernels; decodes up to 16 sequences. No
+ * counterpart in the reference (whose one CPU path is this arithmetic); for callers that need
+ * its exact tokens and for tests. */
+int gsvk_model_set_exact(gsvk_model * m, int on);
+
 /* Free the resident KV cache: replaces gsv_ar::release_cache (:826). */
 int gsvk_release_cache(gsvk_model * m);
 
@@ -347,6 +356,20 @@ int gsvk_op_attn_decode_noalloc(const float * q, const uint16_t * k, const uint1
                                 int nh, int hd, int64_t lstride, const int32_t * kv_begin,
                                 const int32_t * kv_end, int64_t max_keys, float scale, float * out,
                                 uint16_t * out_f16, int8_t * oq, float * od, void * stream);
+
+/* Decode attention in ggml-cpu's order (ggml_compute_forward_flash_attn_ext_f16_one_chunk,
+ * ggml/src/ggml-cpu/ops.cpp, as src/gsv_ar.cpp:412 calls it): for each (sequence b, head h) the
+ * keys [kv_begin[b], kv_end[b]) of the fp16 caches k, v [B][nh][lstride][32] in order, score
+ * dot(k, q) * scale in ggml_vec_dot_f32's lane order, the online softmax with glibc's expf,
+ * out [B][nh*32] = acc / S; oq/od (both or neither) get the sliced Q8_0 copy. Same arguments as
+ * gsvk_op_attn_decode without its split. */
+int gsvk_op_attn_exact(const float * q, const uint16_t * k, const uint16_t * v, int B, int nh,
+                       int64_t lstride, const int32_t * kv_begin, const int32_t * kv_end, float scale,
+                       float * out, int8_t * oq, float * od, void * stream);
+
+/* y[i] = expf(x[i]) with the results of glibc's x86-64 expf, computed on the device (the
+ * exponential of gsvk_op_attn_exact; replaces the libm call inside ggml's softmax). */
+int gsvk_op_expf_exact(const float * x, int64_t n, float * y, void * stream);
 
 /* The decode layer of up to 16 sequences in two launches (GSVK_DECODE_FUSED; d_model 512, 16
  * heads of 32, FFN 2048). Launch 1, per (head, sequence): the input row x = LayerNorm((res +

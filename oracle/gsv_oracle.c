@@ -263,6 +263,10 @@ void orc_attn_row(const float * q, const float * k, const float * v, int64_t kst
     for (int d = 0; d < hd; d++) out[d] = acc[d] * Sinv;
 }
 
+void orc_expf_n(const float * x, int64_t n, float * y) {
+    for (int64_t i = 0; i < n; i++) y[i] = expf(x[i]);
+}
+
 void orc_attn_decode_f16(const float * q, const uint16_t * k, const uint16_t * v, int B, int nh,
                          int hd, int64_t lstride, const int32_t * kv_begin,
                          const int32_t * kv_end, float scale, float * out, int nthreads) {

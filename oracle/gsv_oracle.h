@@ -91,6 +91,9 @@ void orc_add_act(const float * a, const float * b, int64_t n, int64_t ne0, int a
  * out[hd]. */
 void orc_attn_row(const float * q, const float * k, const float * v, int64_t kstride, int hd,
                   int64_t L, const uint8_t * mask_skip, float scale, float * out);
+/* y[i] = expf(x[i]) with this host's libm (glibc: the exponential of flash_attn_ext's online
+ * softmax above and in ggml-cpu) */
+void orc_expf_n(const float * x, int64_t n, float * y);
 /* decode attention over an fp16 cache laid out [B][nh][lstride][hd] (the device layout), keys
  * [kv_begin[b], kv_end[b]) valid: out [B][nh*hd]. */
 void orc_attn_decode_f16(const float * q, const uint16_t * k, const uint16_t * v, int B, int nh,

@@ -79,6 +79,7 @@ def lib():
         L.orc_rng_exponential.restype = C.c_float
         L.orc_rng_exponential.argtypes = [C.POINTER(C.c_uint64)]
         L.orc_rng_exponential_n.argtypes = [C.POINTER(C.c_uint64), C.c_int64, _f32p]
+        L.orc_expf_n.argtypes = [_f32p, C.c_int64, _f32p]
         L.orc_argmax_probs_over_q.restype = C.c_int
         L.orc_argmax_probs_over_q.argtypes = [_f32p, _f32p, C.c_int]
         L.orc_sample.restype = C.c_int
@@ -204,6 +205,14 @@ def attn_prefill(qkv, max_len, pad, nh, scale, nthreads=None):
     lib().orc_attn_prefill(qkv, B, S, max_len, np.ascontiguousarray(pad, np.int32), nh, D // nh, scale, out,
                            nthreads or nthreads_default())
     return out
+
+
+def expf(x):
+    """expf of this host's libm, elementwise (float32 in, float32 out)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_expf_n(x.reshape(-1), x.size, y.reshape(-1))
+    return y
 
 
 def logits_to_probs(cfg, logits, prev):

@@ -21,6 +21,11 @@ scores within 2e of tok (greedy: the top two penalised logits within 2e). Every 
 give the oracle's token. The device's own choices are also checked against its own logits:
 the sampler run on the host over the device's step logits and the same draws gives the device's
 token at every step (the graph of generate and the per-step path compute the same logits).
+
+The same workloads in exact mode (gsvk_model_set_exact: ggml-cpu's arithmetic order throughout)
+have no fragile steps to allow for: the logits entering every teacher-forced step equal the
+oracle's to the bit, and a free run (no forcing, every sequence sampling its own tokens) gives the
+oracle's free run's tokens, every one of every sequence.
 """
 import numpy as np
 import pytest
@@ -134,6 +139,23 @@ def _check_workload(gpu, model24_path, reqs, cfg, steps, seeds):
     print(f"batch {B}: {B * steps} choices, {n_mis} differ from the oracle's, all at fragile steps "
           f"({n_fragile} fragile); worst logit drift {worst:.2e} of the scale", flush=True)
     assert worst <= 3e-2, worst
+
+    g = gpu.Model(model24_path)
+    try:
+        g.set_exact(True)
+        print("device, exact mode: free run and step logits", flush=True)
+        res_x = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=1, want_sampled=True)
+        dev_x = _device_step_logits(g, reqs, forced, steps)
+    finally:
+        g.close()
+    assert np.array_equal(dev_x.view(np.uint32), ref["logits"][:steps].view(np.uint32)), \
+        np.abs(dev_x - ref["logits"][:steps]).max()
+    assert res_x["n_steps"] == free["n_steps"]
+    assert np.array_equal(res_x["sampled"], free["sampled"])
+    for b in range(B):
+        assert np.array_equal(res_x["tokens"][b], free["tokens"][b]), b
+    print(f"batch {B}, exact mode: {B * steps} choices, every one the oracle's; logits equal to the bit",
+          flush=True)
     return n_mis, n_fragile
 
 
