@@ -9,11 +9,8 @@
 #include <cstdlib>
 #include <vector>
 
+#include "gsv_progress.h"   // the engine's /progress counters (src/gsv_progress.h)
 #include "gsvk.h"
-
-#ifdef GSV_WITH_PROGRESS
-#include "gsv_progress.h"   // the engine's /progress atomics (src/gsv_progress.h)
-#endif
 
 struct gsv_ar::impl {
     gsvk_model * m = nullptr;
@@ -44,11 +41,7 @@ std::vector<gsvk_request> to_c(const std::vector<gsv_ar_request> & reqs) {
     return out;
 }
 
-void progress_tick(void *, int) {
-#ifdef GSV_WITH_PROGRESS
-    gsvprog::tick();
-#endif
-}
+void progress_tick(void *, int) { gsvprog::tick(); }
 
 }  // namespace
 
@@ -133,9 +126,7 @@ gsv_ar_result gsv_ar::generate(const std::vector<gsv_ar_request> & reqs,
     out.lens = lens.data();
     out.probs0 = dump_path ? probs.data() : nullptr;
     out.progress = progress_tick;
-#ifdef GSV_WITH_PROGRESS
     gsvprog::begin(2, max_steps);
-#endif
     const double t0 = now_ms();
     const int rc = gsvk_generate(p->m, c.data(), B, &sc, seed_base, early_stop_num, max_steps,
                                  oracle_tokens ? oracle_tokens->data() : nullptr,

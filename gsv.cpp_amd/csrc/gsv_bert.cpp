@@ -6,6 +6,9 @@
 
 #include <cstdio>
 #include <cstring>
+#include <list>
+#include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "gsvk.h"
@@ -13,16 +16,18 @@
 struct gsv_bert::impl {
     gsvk_bert * m = nullptr;
     gsvk_bert_info info{};
-    // encode_feat_cached's LRU, keyed by the full id sequence (src/gsv_bert.cpp:246-283)
-    int feat_cache_n = 0;
-    uint64_t feat_use = 0;
+    // encode_feat_cached's cache of at most `capacity` id sequences (the reference's observable
+    // behaviour, src/gsv_bert.cpp:242-264: a hit refreshes the entry, a miss inserts it and, when
+    // full, first drops the entry unused for longest). A recency list, most recent first, and an
+    // index from the sequence's bytes to its list node.
+    int capacity = 0;
     int hits = 0, misses = 0;
-    struct entry {
-        uint64_t h, use;
-        std::vector<int32_t> ids;
+    struct Cached {
+        std::string key;   // the ids as raw bytes
         std::vector<float> feat;
     };
-    std::vector<entry> cache;
+    std::list<Cached> recency;
+    std::unordered_map<std::string, std::list<Cached>::iterator> index;
 
     // [hidden][T] of one sequence after n_layers layers; false (and out empty) on error
     bool run(const int32_t * ids, int T, int n_layers, std::vector<float> & out) {
@@ -40,17 +45,6 @@ struct gsv_bert::impl {
 };
 
 namespace {
-
-uint64_t hash_ids(const int32_t * ids, int T) {   // FNV-1a over the ids, then T
-    uint64_t h = 1469598103934665603ull;
-    for (int i = 0; i < T; i++) {
-        h ^= (uint32_t) ids[i];
-        h *= 1099511628211ull;
-    }
-    h ^= (uint64_t) (uint32_t) T;
-    h *= 1099511628211ull;
-    return h;
-}
 
 // [hidden][T] -> [hidden][T-2] without [CLS] and [SEP]
 void drop_cls_sep(const std::vector<float> & full, int D, int T, std::vector<float> & feat) {
@@ -87,7 +81,7 @@ gsv_bert * gsv_bert::load(const std::string & gguf_path, const gsv_bert_cfg & cf
     gsv_bert * b = new gsv_bert();
     b->p->m = m;
     gsvk_bert_get_info(m, &b->p->info);
-    b->p->feat_cache_n = cfg.feat_cache > 0 ? cfg.feat_cache : 0;
+    b->p->capacity = cfg.feat_cache > 0 ? cfg.feat_cache : 0;
     return b;
 }
 
@@ -107,29 +101,27 @@ void gsv_bert::encode_feat(const int32_t * ids, int T, std::vector<float> & feat
 }
 
 void gsv_bert::encode_feat_cached(const int32_t * ids, int T, std::vector<float> & feat) {
-    impl & s = *p;
-    if (s.feat_cache_n <= 0) {
+    impl & c = *p;
+    if (c.capacity <= 0) {
         encode_feat(ids, T, feat);
         return;
     }
-    const uint64_t h = hash_ids(ids, T);
-    for (impl::entry & e : s.cache) {
-        if (e.h == h && (int) e.ids.size() == T && memcmp(e.ids.data(), ids, (size_t) T * 4) == 0) {
-            feat = e.feat;
-            e.use = ++s.feat_use;
-            s.hits++;
-            return;
-        }
+    std::string key(reinterpret_cast<const char *>(ids), (ids && T > 0) ? (size_t) T * sizeof(int32_t) : 0);
+    const auto found = c.index.find(key);
+    if (found != c.index.end()) {
+        c.recency.splice(c.recency.begin(), c.recency, found->second);   // now the most recent
+        feat = found->second->feat;
+        c.hits++;
+        return;
     }
-    s.misses++;
-    encode_feat(ids, T, feat);
-    if ((int) s.cache.size() >= s.feat_cache_n) {   // evict the least recently used
-        size_t victim = 0;
-        for (size_t i = 1; i < s.cache.size(); i++)
-            if (s.cache[i].use < s.cache[victim].use) victim = i;
-        s.cache.erase(s.cache.begin() + (long) victim);
+    c.misses++;
+    encode_feat(ids, T, feat);   // a failed encode is remembered too (empty), as the reference does
+    if ((int) c.recency.size() >= c.capacity) {
+        c.index.erase(c.recency.back().key);
+        c.recency.pop_back();
     }
-    s.cache.push_back(impl::entry{h, ++s.feat_use, std::vector<int32_t>(ids, ids + T), feat});
+    c.recency.push_front(impl::Cached{std::move(key), feat});
+    c.index.emplace(c.recency.front().key, c.recency.begin());
 }
 
 void gsv_bert::feat_cache_stats(int & hits, int & misses) const {
@@ -140,9 +132,10 @@ void gsv_bert::feat_cache_stats(int & hits, int & misses) const {
 bool gsv_bert::encode_feat_batch(int B, const int32_t * ids_flat, const int * lens, int Tmax,
                                  std::vector<std::vector<float>> & feats) {
     feats.assign((size_t) (B > 0 ? B : 0), {});
-    if (B <= 0 || !ids_flat || !lens || Tmax < 3 || Tmax > p->info.max_pos) {
-        fprintf(stderr, "[gsv_bert] encode_feat_batch: bad args (B=%d Tmax=%d max_pos=%d)\n", B, Tmax,
-                p->info.max_pos);
+    const bool ok = B > 0 && ids_flat && lens && Tmax >= 3 && Tmax <= p->info.max_pos;
+    if (!ok) {
+        fprintf(stderr, "[gsv_bert] encode_feat_batch refused: %d sequences of up to %d tokens (positions: %d)\n",
+                B, Tmax, p->info.max_pos);
         return false;
     }
     const int D = p->info.hidden;
@@ -168,12 +161,10 @@ bool gsv_bert::encode_feat_batch(int B, const int32_t * ids_flat, const int * le
 
 void gsv_bert::encode_layers(const int32_t * ids, int T, std::vector<float> & features,
                              std::vector<std::vector<float>> & per_layer) {
-    features.clear();
-    per_layer.assign((size_t) p->info.layers_used + 1, {});
-    for (int k = 0; k <= p->info.layers_used; k++) {
-        std::vector<float> out;
-        p->run(ids, T, k, out);
-        if (k == p->info.layers_used) features = out;
-        per_layer[k] = std::move(out);
-    }
+    // hidden state k (the embedding for k = 0) is the encoder stopped after k layers
+    const int depth = p->info.layers_used;
+    per_layer.resize((size_t) depth + 1);
+    int k = 0;
+    for (std::vector<float> & h : per_layer) p->run(ids, T, k++, h);
+    features = per_layer[(size_t) depth];
 }

@@ -164,6 +164,10 @@ struct gsvk_model {
     uint64_t * rng = nullptr;
     float * probs_dump = nullptr;
     int32_t * h_pinned = nullptr;   // pinned host word for the unfinished count
+    // generate's completion check: the sampler also stores the unfinished count into this
+    // mapped pinned word (d_unfinished_host: its device address); one event per step in flight
+    int32_t * h_unfinished = nullptr, * d_unfinished_host = nullptr;
+    hipEvent_t step_ev[2] = {nullptr, nullptr};
     // sequence state
     int prompt_len = 0, S = 0, max_len = 0, B = 0, host_step = 0;
     bool prefilled = false;
@@ -186,6 +190,9 @@ struct gsvk_model {
         if (gexec) (void) hipGraphExecDestroy(gexec);
         if (graph) (void) hipGraphDestroy(graph);
         if (h_pinned) (void) hipHostFree(h_pinned);
+        if (h_unfinished) (void) hipHostFree(h_unfinished);
+        for (hipEvent_t & e : step_ev)
+            if (e) (void) hipEventDestroy(e);
         if (stream) (void) hipStreamDestroy(stream);
     }
 };
@@ -1206,6 +1213,9 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
         GSVK_HIP(hipMemcpy(m->rng_adv, adv.data(), adv.size() * 8, hipMemcpyHostToDevice));
     }
     GSVK_HIP(hipHostMalloc((void **) &m->h_pinned, 64, hipHostMallocDefault));
+    GSVK_HIP(hipHostMalloc((void **) &m->h_unfinished, 64, hipHostMallocMapped | hipHostMallocCoherent));
+    GSVK_HIP(hipHostGetDevicePointer((void **) &m->d_unfinished_host, m->h_unfinished, 0));
+    for (hipEvent_t & e : m->step_ev) GSVK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     GSVK_HIP(hipStreamSynchronize(m->stream));
     if (verbose)
         fprintf(stderr, "[gsvk] loaded %s on HIP device %d: D=%d heads=%d layers=%d vocab=%d EOS=%d "
@@ -1635,6 +1645,7 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     sa.max_steps = max_steps;
     sa.done_counter = m->done_counter;
     sa.n_unfinished = m->n_unfinished;
+    sa.n_unfinished_host = m->d_unfinished_host;
     sa.early_stop = early_stop_num;
     auto enqueue_step = [&]() -> int {
         GSVK_TRY(launch_sample(sa, st));
@@ -1652,20 +1663,30 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
         m->graph = g;
         GSVK_HIP(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
     }
-    const int check_every = 8;
-    int steps_run = 0;
+    // Completion: STEPS_IN_FLIGHT steps are queued ahead of the one whose count the host reads.
+    // Before launching step idx the host waits for step idx - STEPS_IN_FLIGHT to end (the GPU
+    // still has the steps after it queued) and reads the unfinished count its sampler stored in
+    // pinned memory; 0 ends the loop. At most STEPS_IN_FLIGHT - 1 steps run after the one where
+    // the last sequence finished (they sample nothing: every row is closed).
+    constexpr int STEPS_IN_FLIGHT = 2;
+    *(volatile int32_t *) m->h_unfinished = B;
+    int ticked = 0;   // progress callbacks so far: one per step known to have run for a sequence
+    auto tick = [&]() {
+        if (out->progress) out->progress(out->progress_user, ticked);
+        ticked++;
+    };
     GSVK_HIP(hipStreamSynchronize(st));
     const auto t_dec = std::chrono::steady_clock::now();
     for (int idx = 0; idx < max_steps; idx++) {
+        hipEvent_t & ev = m->step_ev[idx % STEPS_IN_FLIGHT];
+        if (idx >= STEPS_IN_FLIGHT) {
+            GSVK_HIP(hipEventSynchronize(ev));
+            tick();   // step idx - STEPS_IN_FLIGHT ran with sequences still open
+            if (*(volatile int32_t *) m->h_unfinished == 0) break;
+        }
         if (m->gexec) GSVK_HIP(hipGraphLaunch(m->gexec, st));
         else GSVK_TRY(enqueue_step());
-        steps_run++;
-        if (out->progress) out->progress(out->progress_user, idx);
-        if ((idx + 1) % check_every == 0 || idx + 1 == max_steps) {
-            GSVK_HIP(hipMemcpyAsync(m->h_pinned, m->n_unfinished, 4, hipMemcpyDeviceToHost, st));
-            GSVK_HIP(hipStreamSynchronize(st));
-            if (*m->h_pinned == 0) break;
-        }
+        GSVK_HIP(hipEventRecord(ev, st));
     }
     GSVK_HIP(hipStreamSynchronize(st));
     out->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_dec).count();
@@ -1700,10 +1721,10 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
         if (out->finish_seq) out->finish_seq[i] = order[i].b;
     }
     out->n_steps = all ? last_fin + 1 : max_steps;
+    while (ticked < out->n_steps) tick();
     if ((flags & GSVK_GEN_PROB_DUMP) && out->probs0 && out->n_steps > 0)
         GSVK_HIP(hipMemcpy(out->probs0, m->probs_dump, (size_t) out->n_steps * m->V * 4,
                            hipMemcpyDeviceToHost));
-    (void) steps_run;
     return GSVK_OK;
 }
 

@@ -32,6 +32,8 @@ struct SampleArgs {
     int max_steps;
     int32_t * done_counter;    // zero between calls
     int32_t * n_unfinished;    // written by the last workgroup
+    int32_t * n_unfinished_host;   // the same count in mapped pinned host memory (or null): the
+                                   // host reads it once the step's event has completed
     int early_stop;            // -1 = off
     // a batch that sequences join while it decodes: row b takes part from loop index
     // row_start[b] on, for at most row_max[b] steps, its EOS-mask window, oracle, dumps and

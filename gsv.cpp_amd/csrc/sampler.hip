@@ -416,6 +416,8 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
         __syncthreads();
         if (tid == 0) {
             *a.n_unfinished = s_unfinished;
+            if (a.n_unfinished_host)
+                __hip_atomic_store(a.n_unfinished_host, s_unfinished, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             *a.step = gidx + 1;
         }
     }

@@ -122,8 +122,9 @@ typedef struct gsvk_gen_out {
     int32_t * finish_seq;
     float   * probs0;
     int32_t   n_steps;
-    /* optional progress callback, called once per decode-loop iteration launched
-     * (gsvprog::tick in the reference, src/gsv_ar.cpp:761-763) */
+    /* optional progress callback, called once per decode step that ran (n_steps calls in all,
+     * step = 0, 1, ...), a step or two behind the GPU while it decodes (gsvprog::tick in the
+     * reference, src/gsv_ar.cpp:761-763) */
     void   (*progress)(void * user, int step);
     void    * progress_user;
     /* wall-clock split measured by the runtime, stream-synchronised on both sides */

@@ -56,6 +56,12 @@ int main(int argc, char ** argv) {
     int hits = -1, misses = -1;
     b->feat_cache_stats(hits, misses);
     printf("cache %d %d %d\n", hits, misses, cache_same ? 1 : 0);
+    // the cache now holds s3 (older) and s1. s3 hits and becomes the newest, s2 misses and must
+    // evict s1 (least recently used; first-in-first-out would evict s3), so s3 hits again
+    for (const std::vector<int32_t> * s : {&s3, &s2, &s3}) b->encode_feat_cached(s->data(), (int) s->size(), c);
+    int hits2 = -1, misses2 = -1;
+    b->feat_cache_stats(hits2, misses2);
+    printf("lru %d %d\n", hits2 - hits, misses2 - misses);
 
     // batch of s1, s2 (Tmax 9) against one-by-one
     std::vector<int32_t> flat(2 * 9, 0);

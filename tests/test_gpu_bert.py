@@ -114,6 +114,7 @@ def test_gsv_bert_class_drop_in(bert_f32, tmp_path_factory):
     assert abs(float(out["encode_checksum"][0]) - ref) <= 1e-6 * np.sum(np.abs(e) * 7)
     assert out["feat_ok"] == ["1"]
     assert out["cache"] == ["1", "4", "1"]                         # hits, misses, cached == uncached
+    assert out["lru"] == ["2", "1"]                                # recency, not insertion order, evicts
     ok, n1, n2, rel = out["batch"]
     assert ok == "1" and int(n1) == 1024 * 4 and int(n2) == 1024 * 7 and float(rel) <= 1e-5
     assert out["batch_bad_args"] == ["1"]

@@ -27,3 +27,21 @@ def test_reference_caller_runs_unchanged(gpu, small_model_path):
     assert [int(r[0]) for r in rows] == [1, 2, 4, 8]
     for r in rows:
         assert float(r[-1]) > 0.0   # tok/s
+
+
+def test_generate_ticks_the_engine_progress_counters(gpu, small_model_path):
+    """gsv_ar::generate sets the engine's /progress counters (src/gsv_ar.cpp:761-763): stage 2 with
+    the step budget as total, one tick per decode step, seen from the calling program (the
+    counters are one object per process). tests/dropin/gsv_ar_progress_check.cpp, built by
+    oracle/Makefile (target progresscheck)."""
+    binp = os.path.join(ROOT, "tests", "dropin", "gsv_ar_progress_check")
+    if not os.path.exists(binp):
+        pytest.skip("tests/dropin/gsv_ar_progress_check was not built")
+    p = subprocess.run([binp, small_model_path], capture_output=True, text=True, timeout=180)
+    print(p.stdout, p.stderr)
+    assert p.returncode == 0, p.stderr
+    line = [l for l in p.stdout.splitlines() if l.startswith("progress ")]
+    stage, cur, total, generated = (int(x) for x in line[0].split()[1:])
+    assert stage == 2 and total == 17
+    # every step that ran ticked once: the generated tokens, plus the step that chose EOS if any
+    assert generated <= cur <= min(17, generated + 1)
