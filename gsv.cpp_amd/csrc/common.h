@@ -277,6 +277,10 @@ int launch_q8_quantize(const float * x, int64_t rows, int64_t k, int8_t * xs, fl
 int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
                      hipStream_t stream, int8_t * qn = nullptr, int8_t * qt = nullptr,
                      uint16_t * dt = nullptr);
+// The sliced (qs, d) and natural (qn) copies of a weight given in the Q8_TILED order (qt, dt;
+// rows % 32 == 0): the load of a pre-swizzled GGUF
+int launch_q8_untile(const int8_t * qt, const uint16_t * dt, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
+                     int8_t * qn, hipStream_t stream);
 // (y16: optional fp16 copy of y, rounded to nearest even)
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,

@@ -67,6 +67,7 @@ uint64_t tensor_bytes(uint32_t type, int64_t nelem) {
         case GGML_F32: return (uint64_t) nelem * 4;
         case GGML_F16: return (uint64_t) nelem * 2;
         case GGML_Q8_0: return nelem % 32 ? 0 : (uint64_t) (nelem / 32) * 34;
+        case GGML_I8: return (uint64_t) nelem;
         default: return 0;
     }
 }

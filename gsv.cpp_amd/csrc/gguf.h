@@ -1,5 +1,5 @@
 // Minimal GGUF (v2/v3) reader: header, key/values and tensor directory, data read on demand.
-// Only what the AR and BERT loaders need (u32/i32/f32 keys; F32, F16 and Q8_0 tensors).
+// Only what the AR and BERT loaders need (u32/i32/f32 keys; F32, F16, Q8_0 and I8 tensors).
 #pragma once
 
 #include <cstdint>
@@ -10,7 +10,7 @@
 
 namespace gsvk {
 
-enum GgmlType : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8 };
+enum GgmlType : uint32_t { GGML_F32 = 0, GGML_F16 = 1, GGML_Q8_0 = 8, GGML_I8 = 24 };
 
 struct GgufTensor {
     std::string name;

@@ -64,6 +64,28 @@ __global__ void k_q8_repack(const uint8_t * __restrict__ blocks, int64_t rows, i
     }
 }
 
+// The sliced (qs, d) and natural (qn) copies of a weight stored in the matrix-core operand
+// order (qt, dt: the on-disk tiled layout of a pre-swizzled GGUF); one thread per 4-quant
+// group, the inverse of k_q8_repack's tiled store.
+__global__ void k_q8_untile(const int8_t * __restrict__ qt, const uint16_t * __restrict__ dt, int64_t rows,
+                            int nblk, int8_t * __restrict__ qs, uint16_t * __restrict__ d,
+                            int8_t * __restrict__ qn) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * nblk * 8) return;
+    const int j = (int) (i & 7);
+    const int64_t gb = i >> 3;
+    const int64_t row = gb / nblk;
+    const int blk = (int) (gb % nblk);
+    int8_t * dst = qs + ((row * 8 + j) * nblk + blk) * 4;
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        const int8_t v = qt[q8_tiled_offset(row, nblk, blk, 4 * j + t)];
+        dst[t] = v;
+        qn[gb * QK + 4 * j + t] = v;
+    }
+    if (j == 0) d[gb] = dt[q8_tiled_scale(row, nblk, blk)];
+}
+
 // ---------------------------------------------------------------------------------------
 // activation quantisation: 4 lanes per 32-block, 8 consecutive values each
 // ---------------------------------------------------------------------------------------
@@ -259,6 +281,20 @@ int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, 
     if (total == 0) return GSVK_OK;
     hipLaunchKernelGGL(k_q8_repack, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, stream,
                        (const uint8_t *) blocks, rows, nblk, qs, d, qn, qt, dt);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+int launch_q8_untile(const int8_t * qt, const uint16_t * dt, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
+                     int8_t * qn, hipStream_t stream) {
+    GSVK_REQUIRE(qt && dt && qs && d && qn && rows >= 0 && rows % 32 == 0 && k > 0 && k % QK == 0 &&
+                     k <= (1 << 20),
+                 "q8_untile: bad arguments (rows %% 32 == 0, k %% 32 == 0)");
+    const int nblk = (int) (k / QK);
+    const int64_t total = rows * nblk * 8;
+    if (total == 0) return GSVK_OK;
+    hipLaunchKernelGGL(k_q8_untile, dim3((unsigned) ((total + 255) / 256)), dim3(256), 0, stream, qt, dt, rows,
+                       nblk, qs, d, qn);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

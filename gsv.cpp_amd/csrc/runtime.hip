@@ -271,6 +271,37 @@ int load_q8(gsvk_model * m, const GgufFile & g, const GgufTensor * t, Lin & lin,
     return GSVK_OK;
 }
 
+// Read a projection of a pre-swizzled file: quants (I8) and scales (F16) already in the Q8_TILED
+// order go to the device as they are; the sliced and natural copies are derived there.
+int load_q8_tiled(gsvk_model * m, const GgufFile & g, const GgufTensor * tq, const GgufTensor * td, Lin & lin,
+                  std::vector<uint8_t> & host) {
+    if (tq->type != GGML_I8 || tq->ne.size() != 2 || td->type != GGML_F16 || td->ne.size() != 2 ||
+        td->ne[0] * 32 != tq->ne[0] || td->ne[1] != tq->ne[1]) {
+        set_error("%s / %s: expected I8 [k, n] quants and F16 [k/32, n] scales", tq->name.c_str(), td->name.c_str());
+        return GSVK_ERR_FORMAT;
+    }
+    lin.k = (int) tq->ne[0];
+    lin.n = (int) tq->ne[1];
+    if (lin.k % 128 != 0 || lin.n % 32 != 0) {
+        set_error("%s: row length %d must be a multiple of 128 and rows %d of 32", tq->name.c_str(), lin.k, lin.n);
+        return GSVK_ERR_FORMAT;
+    }
+    const size_t nq = (size_t) lin.n * lin.k, nd = (size_t) lin.n * (lin.k / 32);
+    GSVK_TRY(m->wmem.alloc(lin.qs, nq));
+    GSVK_TRY(m->wmem.alloc(lin.qn, nq));
+    GSVK_TRY(m->wmem.alloc(lin.d, nd));
+    GSVK_TRY(m->wmem.alloc(lin.qt, nq));
+    GSVK_TRY(m->wmem.alloc(lin.dt, nd));
+    host.resize(tq->nbytes);
+    if (!g.read(*tq, host.data())) { set_error("read of %s failed", tq->name.c_str()); return GSVK_ERR_IO; }
+    GSVK_HIP(hipMemcpy(lin.qt, host.data(), nq, hipMemcpyHostToDevice));
+    host.resize(td->nbytes);
+    if (!g.read(*td, host.data())) { set_error("read of %s failed", td->name.c_str()); return GSVK_ERR_IO; }
+    GSVK_HIP(hipMemcpy(lin.dt, host.data(), nd * 2, hipMemcpyHostToDevice));
+    GSVK_TRY(launch_q8_untile(lin.qt, lin.dt, lin.n, lin.k, lin.qs, lin.d, lin.qn, m->stream));
+    return GSVK_OK;
+}
+
 int load_f32(gsvk_model * m, const GgufFile & g, const char * name, int64_t expect, float *& dst,
              std::vector<float> * keep = nullptr) {
     const GgufTensor * t = g.tensor(name);
@@ -993,7 +1024,14 @@ namespace {
 
 struct Hparams {
     int D = 512, NH = 16, NL = 24, V = 1025, PH = 732, EOS = 1024, FFN = 2048;
+    bool tiled = false;   // a pre-swizzled file: layer projections in the matrix-core order
 };
+
+// Key of a pre-swizzled GGUF (gsv.cpp_amd/gguf_tiled.py): 1 = every layer's Q8_0 projection
+// `X` is stored as `X.qt` (I8, its quants in the Q8_TILED order) and `X.dt` (F16, its scales in
+// the Q8_TILED order), all other tensors unchanged.
+constexpr const char * KEY_Q8_LAYOUT = "gsvk.q8_layout";
+constexpr uint32_t Q8_LAYOUT_TILED32 = 1;
 
 // Check the whole tensor contract of tools/export_gguf/convert_ar.py (names, types, shapes) before
 // anything touches the device, so a bad file fails the same way with or without a GPU.
@@ -1014,6 +1052,13 @@ int validate_gguf(const GgufFile & g, Hparams & hp) {
         set_error("bad hparams vocab=%d eos=%d layers=%d phones=%d", hp.V, hp.EOS, hp.NL, hp.PH);
         return GSVK_ERR_FORMAT;
     }
+    if (g.get_u32(KEY_Q8_LAYOUT, v)) {
+        if (v != Q8_LAYOUT_TILED32) {
+            set_error("%s = %u: unknown weight layout (1 = tiled)", KEY_Q8_LAYOUT, v);
+            return GSVK_ERR_FORMAT;
+        }
+        hp.tiled = true;
+    }
     auto need = [&](const std::string & name, std::initializer_list<uint32_t> types,
                     std::initializer_list<int64_t> ne) -> int {
         const GgufTensor * t = g.tensor(name);
@@ -1030,16 +1075,22 @@ int validate_gguf(const GgufFile & g, Hparams & hp) {
         }
         return GSVK_OK;
     };
-    const GgufTensor * f1 = g.tensor("transformer.block0.ffn1_w");
+    const GgufTensor * f1 = g.tensor(hp.tiled ? "transformer.block0.ffn1_w.qt" : "transformer.block0.ffn1_w");
     if (f1 && f1->ne.size() == 2) hp.FFN = (int) f1->ne[1];
     const int D = hp.D, F = hp.FFN;
     if (F <= 0 || F % 128 != 0) { set_error("ffn size %d must be a multiple of 128", F); return GSVK_ERR_FORMAT; }
+    // a Q8_0 projection [n][k]: the GGUF tensor, or its tiled pair in a pre-swizzled file
+    auto need_q8 = [&](const std::string & name, int64_t k, int64_t n) -> int {
+        if (!hp.tiled) return need(name, {GGML_Q8_0}, {k, n});
+        GSVK_TRY(need(name + ".qt", {GGML_I8}, {k, n}));
+        return need(name + ".dt", {GGML_F16}, {k / 32, n});
+    };
     for (int li = 0; li < hp.NL; li++) {
         const std::string p = "transformer.block" + std::to_string(li) + ".";
-        GSVK_TRY(need(p + "qkv_w", {GGML_Q8_0}, {D, 3 * D}));
-        GSVK_TRY(need(p + "out_w", {GGML_Q8_0}, {D, D}));
-        GSVK_TRY(need(p + "ffn1_w", {GGML_Q8_0}, {D, F}));
-        GSVK_TRY(need(p + "ffn2_w", {GGML_Q8_0}, {F, D}));
+        GSVK_TRY(need_q8(p + "qkv_w", D, 3 * D));
+        GSVK_TRY(need_q8(p + "out_w", D, D));
+        GSVK_TRY(need_q8(p + "ffn1_w", D, F));
+        GSVK_TRY(need_q8(p + "ffn2_w", F, D));
         GSVK_TRY(need(p + "qkv_b", {GGML_F32}, {3 * D}));
         GSVK_TRY(need(p + "out_b", {GGML_F32}, {D}));
         GSVK_TRY(need(p + "ffn1_b", {GGML_F32}, {F}));
@@ -1107,9 +1158,16 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
             {"ffn1_w", &w.f1, -1, m->D}, {"ffn2_w", &w.f2, m->D, -1}};
         for (auto & q : q8s) {
             snprintf(nm, sizeof nm, "transformer.block%d.%s", li, q.suffix);
-            const GgufTensor * t = g.tensor(nm);
-            if (!t) { set_error("missing tensor %s", nm); return GSVK_ERR_FORMAT; }
-            GSVK_TRY(load_q8(m.get(), g, t, *q.lin, staging, staging_bytes, host));
+            if (hp.tiled) {
+                const GgufTensor * tq = g.tensor(std::string(nm) + ".qt");
+                const GgufTensor * td = g.tensor(std::string(nm) + ".dt");
+                if (!tq || !td) { set_error("missing tensor %s.qt / .dt", nm); return GSVK_ERR_FORMAT; }
+                GSVK_TRY(load_q8_tiled(m.get(), g, tq, td, *q.lin, host));
+            } else {
+                const GgufTensor * t = g.tensor(nm);
+                if (!t) { set_error("missing tensor %s", nm); return GSVK_ERR_FORMAT; }
+                GSVK_TRY(load_q8(m.get(), g, t, *q.lin, staging, staging_bytes, host));
+            }
             if ((q.expect_n >= 0 && q.lin->n != q.expect_n) || (q.expect_k >= 0 && q.lin->k != q.expect_k)) {
                 set_error("%s: shape [%d, %d] does not match the model", nm, q.lin->n, q.lin->k);
                 return GSVK_ERR_FORMAT;
