@@ -59,9 +59,7 @@ def build(verbose: bool = False) -> str:
             if msg.strip() and verbose:
                 print(msg, file=sys.stderr)
     tmp = LIB + ".tmp"
-    # rocBLAS: the fp32 projections of the BERT encoder (bert.hip)
-    cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs + \
-        ["-L" + os.path.join(ROCM, "lib"), "-lrocblas", "-Wl,-rpath," + os.path.join(ROCM, "lib")]
+    cmd = [HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
