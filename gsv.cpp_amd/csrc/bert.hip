@@ -32,6 +32,7 @@
 
 #include "common.h"
 #include "gguf.h"
+#include "layer.h"
 #include "gsvk.h"
 
 namespace gsvk {
@@ -250,6 +251,10 @@ float half_to_float(uint16_t h) {
 struct Proj {
     void * w = nullptr;
     bool f16 = false;
+    // Q8_0 weights: natural-order quants [N][K] and fp16 scales [N][K/32], multiplied on the int8
+    // GEMM with the activations quantised as ggml-cpu quantises them (its vec_dot type for Q8_0)
+    int8_t * q8 = nullptr;
+    uint16_t * q8d = nullptr;
 };
 
 struct BertLayer {
@@ -425,7 +430,8 @@ constexpr int BL_MAXP = 8;
 __global__ void __launch_bounds__(BL_THREADS) k_bert_ln(const float * __restrict__ x, const float * __restrict__ r,
                                                         int np, int64_t pstride, const float * __restrict__ bias,
                                                         const float * __restrict__ wb, int n, float eps,
-                                                        float * __restrict__ y, _Float16 * __restrict__ y16) {
+                                                        float * __restrict__ y, _Float16 * __restrict__ y16,
+                                                        int8_t * __restrict__ yq, float * __restrict__ yd) {
     __shared__ double s_red[2][BL_THREADS / 64];
     const int64_t row = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -485,6 +491,28 @@ __global__ void __launch_bounds__(BL_THREADS) k_bert_ln(const float * __restrict
         const uint32_t h1 = (uint32_t) f2h(out[2]) | ((uint32_t) f2h(out[3]) << 16);
         *reinterpret_cast<uint2 *>(y16 + bt_off(row, c, n)) = make_uint2(h0, h1);
     }
+    if (yq) {   // the x86 Q8_0 quantisation of the row (natural order): a block is 8 threads
+        int8_t q[4];
+        const float d = q8_quantize_group<4>(out, q, 8);
+        *reinterpret_cast<int *>(yq + o) = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+        if ((c & 31) == 0) yd[row * (n / 32) + c / 32] = d;
+    }
+}
+
+// h = gelu_erf(h) (bias already added by the FFN1 GEMM), then its x86 Q8_0 quantisation in natural
+// order for a Q8_0 FFN2: 4 values per thread, a block is 8 threads
+__global__ void __launch_bounds__(256) k_bert_gelu_q8(const float * __restrict__ h, int64_t n, int8_t * __restrict__ hq,
+                                                      float * __restrict__ hd) {
+    const int64_t i = ((int64_t) blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= n) return;   // n % 32 == 0: whole blocks leave together
+    const float4 v = *reinterpret_cast<const float4 *>(h + i);
+    float y[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int k = 0; k < 4; k++) y[k] = 0.5f * y[k] * (1.0f + erff(y[k] * 0.70710678118654752440f));
+    int8_t q[4];
+    const float d = q8_quantize_group<4>(y, q, 8);
+    *reinterpret_cast<int *>(hq + i) = (q[0] & 0xff) | ((q[1] & 0xff) << 8) | ((q[2] & 0xff) << 16) | ((q[3] & 0xff) << 24);
+    if ((i & 31) == 0) hd[i / 32] = d;
 }
 
 }  // namespace
@@ -498,6 +526,7 @@ struct gsvk_bert {
     gsvk_bert_info info{};
     std::vector<void *> wmem;   // weight allocations
     bool any_f16 = false;       // some projection is kept in fp16
+    bool any_q8 = false;        // some projection is Q8_0 (int8 GEMM)
     float * word = nullptr, * pos = nullptr, * type0 = nullptr, * emb_ln = nullptr;
     std::vector<BertLayer> L;
     // per-call workspace, grown to the largest call
@@ -584,6 +613,23 @@ int load_tensor(gsvk_bert * m, const GgufFile & g, const std::string & name, int
         proj->w = w16;
         proj->f16 = true;
         m->any_f16 = true;
+        out = nullptr;
+        return GSVK_OK;
+    }
+    if (proj && t->type == GGML_Q8_0) {   // a Q8_0 projection: quants and scales apart
+        const size_t nb = n / 32;
+        std::vector<int8_t> q(n);
+        std::vector<uint16_t> d(nb);
+        for (size_t blk = 0; blk < nb; blk++) {
+            const uint8_t * p = raw.data() + blk * 34;
+            memcpy(&d[blk], p, 2);
+            memcpy(&q[blk * 32], p + 2, 32);
+        }
+        GSVK_TRY(m->dev_alloc(proj->q8, n));
+        GSVK_TRY(m->dev_alloc(proj->q8d, nb));
+        GSVK_HIP(hipMemcpy(proj->q8, q.data(), n, hipMemcpyHostToDevice));
+        GSVK_HIP(hipMemcpy(proj->q8d, d.data(), nb * 2, hipMemcpyHostToDevice));
+        m->any_q8 = true;
         out = nullptr;
         return GSVK_OK;
     }
@@ -687,13 +733,29 @@ int gemm(gsvk_bert * m, const Proj & W, const float * X, const _Float16 * X16, i
     return GSVK_OK;
 }
 
+// A Q8_0 projection on the int8 GEMM of the AR path: Y = X . W^T (+ bias) with X the Q8_0 rows
+// (natural order) that the producer quantised as ggml-cpu's x86 quantiser does.
+int gemm_q8(gsvk_bert * m, const Proj & W, const int8_t * xq, const float * xd, int64_t M, int N, int K, float * y,
+            const float * bias) {
+    LayerOut lo{};
+    lo.y = y;
+    lo.y_stride = N;
+    lo.n_store = N;
+    lo.bias = bias;
+    Q8Weights qw{};
+    qw.qn = W.q8;
+    qw.dn = W.q8d;
+    return launch_q8_gemm(qw, N, K, M, xq, xd, Q8_NATURAL, lo, m->stream);
+}
+
 int bert_ln(gsvk_bert * m, const float * x, const float * r, int np, int64_t pstride, const float * bias,
-            const float * wb, int64_t rows, float * y, _Float16 * y16) {
+            const float * wb, int64_t rows, float * y, _Float16 * y16, int8_t * yq = nullptr,
+            float * yd = nullptr) {
     const int D = m->info.hidden;
     GSVK_REQUIRE(D % 4 == 0 && D <= 4 * BL_THREADS && np >= 1 && np <= BL_MAXP,
                  "bert layernorm: hidden %d (<= %d), %d partial rows", D, 4 * BL_THREADS, np);
     hipLaunchKernelGGL(k_bert_ln, dim3((unsigned) rows), dim3(BL_THREADS), 0, m->stream, x, r, np, pstride, bias,
-                       wb, D, m->info.ln_eps, y, y16);
+                       wb, D, m->info.ln_eps, y, y16, yq, yd);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -761,6 +823,10 @@ extern "C" int gsvk_bert_load(const char * path, int device, int verbose, gsvk_b
         GSVK_TRY(load_proj(m.get(), g, p + "ff2_w", F, D, w.ff2));
         GSVK_TRY(load_tensor(m.get(), g, p + "ff2_b", D, 1, w.ff2_b));
         GSVK_TRY(load_ln(m.get(), g, p + "out_ln_w", p + "out_ln_b", w.ln2));
+        const int nq8 = (w.qkv.q8 != nullptr) + (w.ao.q8 != nullptr) + (w.ff1.q8 != nullptr) + (w.ff2.q8 != nullptr);
+        GSVK_REQUIRE(nq8 == 0 || nq8 == 4, "BERT GGUF: layer %d mixes Q8_0 and other projection types", li);
+        GSVK_REQUIRE(nq8 == 0 || (D == 1024 && F == 4096),
+                     "BERT GGUF: Q8_0 projections need hidden 1024 and FFN 4096 (the int8 GEMM's K)");
     }
     GSVK_HIP(hipDeviceSynchronize());
     if (verbose)
@@ -814,7 +880,8 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     const size_t fl = (size_t) rows * (D + 3 * D + D + (size_t) BERT_MAX_SLICES * D + F);
     const int64_t rows64 = (rows + BG_BM - 1) / BG_BM * BG_BM;   // fp16 operands: rows padded to 64
     const size_t n16 = m->any_f16 ? (size_t) rows64 * (D + F) : 0;
-    const size_t need = fl * 4 + n16 * 2 + (size_t) rows * 8 + (size_t) B * 8 + 4096;
+    const size_t nq = m->any_q8 ? (size_t) rows * (D + F) : 0;   // Q8_0 activations: quants
+    const size_t need = fl * 4 + n16 * 2 + nq + (nq / 32) * 4 + (size_t) rows * 8 + (size_t) B * 8 + 8192;
     if (need > m->ws_bytes) {
         if (m->ws) (void) hipFree(m->ws);
         m->ws = nullptr;
@@ -834,7 +901,11 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     float * h = prj + (size_t) BERT_MAX_SLICES * rows * D;
     _Float16 * x16 = (_Float16 *) (h + rows * F);            // fp16 input of the D-wide projections
     _Float16 * h16 = m->any_f16 ? x16 + rows64 * D : nullptr;   // fp16 FFN hidden (FFN2's input)
-    int32_t * d_ids = (int32_t *) (x16 + n16 + (n16 & 1));
+    int8_t * xq = (int8_t *) (x16 + n16);                          // D-wide Q8_0 rows (+ scales)
+    int8_t * hq = xq + (m->any_q8 ? rows * D : 0);                  // the FFN hidden's
+    float * xqd = (float *) (((uintptr_t) (xq + nq) + 15) & ~(uintptr_t) 15);
+    float * hqd = xqd + (m->any_q8 ? rows * D / 32 : 0);
+    int32_t * d_ids = (int32_t *) (((uintptr_t) (xqd + nq / 32) + 15) & ~(uintptr_t) 15);
     int32_t * d_pos = d_ids + rows;
     int32_t * d_off = d_pos + rows;
     int32_t * d_len = d_off + B;
@@ -860,30 +931,52 @@ extern "C" int gsvk_bert_encode(gsvk_bert * m, int B, const int32_t * ids_flat, 
     hipLaunchKernelGGL(k_bert_embed, dim3((unsigned) rows), dim3(256), 0, st, m->word, m->pos, m->type0, d_ids,
                        d_pos, D, prj);
     GSVK_LAUNCH_CHECK();
-    // each LayerNorm also writes the fp16 copy its consumer takes when that is an F16 projection
+    // each LayerNorm also writes the fp16 copy (F16 consumer) or the Q8_0 rows (Q8_0 consumer) its
+    // consumer takes
     auto x16_for = [&](int li) { return li < n_layers && m->L[li].qkv.f16 ? x16 : nullptr; };
-    GSVK_TRY(bert_ln(m, prj, nullptr, 1, 0, nullptr, m->emb_ln, rows, x, x16_for(0)));
+    auto xq_for = [&](int li) { return li < n_layers && m->L[li].qkv.q8 ? xq : nullptr; };
+    GSVK_TRY(bert_ln(m, prj, nullptr, 1, 0, nullptr, m->emb_ln, rows, x, x16_for(0), xq_for(0), xqd));
     const float scale_log2 = 1.4426950408889634f / std::sqrt((float) BA_HD);
     auto kmult = [](const Proj & w) { return BG_WAVES * BG_U * (w.f16 ? BgStep<_Float16>::K : BgStep<float>::K); };
     const int64_t pst = rows * D;   // floats between partial rows of the D-wide projections
     for (int li = 0; li < n_layers; li++) {
         const BertLayer & w = m->L[li];
         // QKV (its bias is added as attention reads q, k, v)
-        GSVK_TRY(gemm(m, w.qkv, x, x16, rows, 3 * D, D, 1, BgOut{qkv, 0, nullptr, 0, nullptr}));
+        if (w.qkv.q8)
+            GSVK_TRY(gemm_q8(m, w.qkv, xq, xqd, rows, 3 * D, D, qkv, nullptr));
+        else
+            GSVK_TRY(gemm(m, w.qkv, x, x16, rows, 3 * D, D, 1, BgOut{qkv, 0, nullptr, 0, nullptr}));
         hipLaunchKernelGGL(k_bert_attn, dim3((unsigned) ((Tmax + BA_Q - 1) / BA_Q), (unsigned) in.heads, (unsigned) B),
                            dim3(256), 0, st, qkv, w.qkv_b, d_off, d_len, D, scale_log2, att,
                            w.ao.f16 ? x16 : nullptr);
         GSVK_LAUNCH_CHECK();
-        // out projection in K slices when the rows are few; LN1 sums the slices
-        const int s1 = bert_kslices(rows, D, D, kmult(w.ao), BERT_MAX_SLICES);
-        GSVK_TRY(gemm(m, w.ao, att, x16, rows, D, D, s1, BgOut{prj, pst, nullptr, 0, nullptr}));
-        GSVK_TRY(bert_ln(m, x, prj, s1, pst, w.ao_b, w.ln1, rows, x, w.ff1.f16 ? x16 : nullptr));
-        // FFN1 with bias + GELU in its epilogue, to fp32 (an F32 FFN2) or fp16 (an F16 FFN2)
-        GSVK_TRY(gemm(m, w.ff1, x, x16, rows, F, D, 1,
-                      BgOut{w.ff2.f16 ? nullptr : h, 0, w.ff1_b, 1, w.ff2.f16 ? h16 : nullptr}));
-        const int s2 = bert_kslices(rows, D, F, kmult(w.ff2), BERT_MAX_SLICES);
-        GSVK_TRY(gemm(m, w.ff2, h, h16, rows, D, F, s2, BgOut{prj, pst, nullptr, 0, nullptr}));
-        GSVK_TRY(bert_ln(m, x, prj, s2, pst, w.ff2_b, w.ln2, rows, x, x16_for(li + 1)));
+        // out projection (F16 / F32: in K slices when the rows are few; LN1 sums the slices)
+        int s1 = 1;
+        if (w.ao.q8) {
+            GSVK_TRY(launch_q8_quantize(att, rows, D, xq, xqd, st, Q8_NATURAL));
+            GSVK_TRY(gemm_q8(m, w.ao, xq, xqd, rows, D, D, prj, nullptr));
+        } else {
+            s1 = bert_kslices(rows, D, D, kmult(w.ao), BERT_MAX_SLICES);
+            GSVK_TRY(gemm(m, w.ao, att, x16, rows, D, D, s1, BgOut{prj, pst, nullptr, 0, nullptr}));
+        }
+        GSVK_TRY(bert_ln(m, x, prj, s1, pst, w.ao_b, w.ln1, rows, x, w.ff1.f16 ? x16 : nullptr,
+                         w.ff1.q8 ? xq : nullptr, xqd));
+        // FFN1 + bias + GELU, FFN2
+        int s2 = 1;
+        if (w.ff1.q8) {
+            GSVK_TRY(gemm_q8(m, w.ff1, xq, xqd, rows, F, D, h, w.ff1_b));
+            const int64_t nh = rows * F;
+            hipLaunchKernelGGL(k_bert_gelu_q8, dim3((unsigned) ((nh / 4 + 255) / 256)), dim3(256), 0, st, h, nh, hq, hqd);
+            GSVK_LAUNCH_CHECK();
+            GSVK_TRY(gemm_q8(m, w.ff2, hq, hqd, rows, D, F, prj, nullptr));
+        } else {
+            // bias + GELU in the FFN1 epilogue, to fp32 (an F32 FFN2) or fp16 (an F16 FFN2)
+            GSVK_TRY(gemm(m, w.ff1, x, x16, rows, F, D, 1,
+                          BgOut{w.ff2.f16 ? nullptr : h, 0, w.ff1_b, 1, w.ff2.f16 ? h16 : nullptr}));
+            s2 = bert_kslices(rows, D, F, kmult(w.ff2), BERT_MAX_SLICES);
+            GSVK_TRY(gemm(m, w.ff2, h, h16, rows, D, F, s2, BgOut{prj, pst, nullptr, 0, nullptr}));
+        }
+        GSVK_TRY(bert_ln(m, x, prj, s2, pst, w.ff2_b, w.ln2, rows, x, x16_for(li + 1), xq_for(li + 1), xqd));
     }
     // [rows][D] -> per sequence [D][len] (src/gsv_bert.cpp:220-228)
     GSVK_HIP(hipMemcpyAsync(m->pin, x, (size_t) rows * D * 4, hipMemcpyDeviceToHost, st));

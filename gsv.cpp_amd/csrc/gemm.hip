@@ -475,10 +475,18 @@ int launch_q8_gemm_small(const Q8Weights & w, int64_t n, int64_t k, int64_t m, c
         if (mt == 1) { if (wide) GSVK_GS(16, 1, 8); else GSVK_GS(16, 1, 4); }
         else if (mt == 2) { if (wide) GSVK_GS(16, 2, 8); else GSVK_GS(16, 2, 4); }
         else { if (wide) GSVK_GS(16, 4, 8); else GSVK_GS(16, 4, 4); }
-    } else {
+    } else if (k == 1024) {   // (the BERT encoder's Q8_0 files)
+        if (mt == 1) GSVK_GS(32, 1, 4);
+        else if (mt == 2) GSVK_GS(32, 2, 4);
+        else GSVK_GS(32, 4, 4);
+    } else if (k == 2048) {
         if (mt == 1) { if (wide) GSVK_GS(64, 1, 8); else GSVK_GS(64, 1, 4); }
         else if (mt == 2) { if (wide) GSVK_GS(64, 2, 8); else GSVK_GS(64, 2, 4); }
         else { if (wide) GSVK_GS(64, 4, 8); else GSVK_GS(64, 4, 4); }
+    } else {   // k == 4096: 8 waves, so that a wave's blocks (16) fit its registers
+        if (mt == 1) GSVK_GS(128, 1, 8);
+        else if (mt == 2) GSVK_GS(128, 2, 8);
+        else GSVK_GS(128, 4, 8);
     }
 #undef GSVK_GS
     GSVK_LAUNCH_CHECK();
@@ -494,7 +502,8 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
                  "q8_gemm: bad output layout %d", out.yq_layout);
     GSVK_REQUIRE(n > 0 && n % 32 == 0 && n < (1 << 30) && m > 0 && m < (1 << 30),
                  "q8_gemm: n must be a multiple of 32 (n=%lld m=%lld)", (long long) n, (long long) m);
-    GSVK_REQUIRE(k == 512 || k == 2048, "q8_gemm: k must be 512 or 2048 (got %lld)", (long long) k);
+    GSVK_REQUIRE(k == 512 || k == 1024 || k == 2048 || k == 4096,
+                 "q8_gemm: k must be 512, 1024, 2048 or 4096 (got %lld)", (long long) k);
     GSVK_REQUIRE(!out.yq || out.yd, "q8_gemm: bad quantised output");
     GSVK_REQUIRE(!out.kc || (out.vc && out.col_ptr && out.rows_per_seq > 0 && out.kv_row0 + 2 * out.d_model <= n),
                  "q8_gemm: bad KV epilogue");
@@ -514,8 +523,12 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
     const dim3 grid((unsigned) (n / GM_BN), (unsigned) ((m + GM_BM - 1) / GM_BM));
     if (k == 512)
         hipLaunchKernelGGL(k_q8_gemm<16>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
-    else
+    else if (k == 1024)
+        hipLaunchKernelGGL(k_q8_gemm<32>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
+    else if (k == 2048)
         hipLaunchKernelGGL(k_q8_gemm<64>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
+    else
+        hipLaunchKernelGGL(k_q8_gemm<128>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

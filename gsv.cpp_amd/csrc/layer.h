@@ -74,8 +74,8 @@ struct Q8Weights {
 };
 
 // Q8_0 x Q8_0 GEMM on the matrix cores (gemm.hip) with the same epilogue options: n % 32 == 0,
-// k in {512, 2048}. Activations xs [m][k] with fp32 scales xd [m][k/32] (fp16 values) in
-// x_layout: Q8_NATURAL, or Q8_TILED (rows padded to 32; small-batch kernel only); a Q8_0 output
+// k in {512, 1024, 2048, 4096} (1024 and 4096: the BERT encoder's Q8_0 projections). Activations
+// xs [m][k] with fp32 scales xd [m][k/32] (fp16 values) in x_layout: Q8_NATURAL, or Q8_TILED (rows padded to 32; small-batch kernel only); a Q8_0 output
 // is written in out.yq_layout (Q8_NATURAL or Q8_TILED). Up to 256 rows (or n % 128 != 0) a kernel
 // of 32-column tiles runs (tiled weights if given), tile_rows (1, 2 or 4 row tiles of 32 per
 // workgroup, 0 = its own choice) selecting its row tiling; above, the 128 x 128 kernel (natural

@@ -229,7 +229,8 @@ def write_bert_model(path: str, seed: int = 0x6A5E0010, n_layer: int = 4, layers
     """A synthetic BERT GGUF with the tensor contract of src/gsv_bert.cpp:398-431 (keys bert.*,
     tensors bert.word_emb .. bert.l{i}.out_ln_b; projection weights in `wtype`, the rest F32, as
     tools/export_gguf/convert_bert.py writes them). Returns (path, weights): the fp32 values the
-    loader holds (F16 rounded, Q8_0 dequantised), for the oracle."""
+    loader holds (F16 rounded, Q8_0 dequantised; for Q8_0 also the blocks, under name + "#q8"),
+    for the oracle."""
     rng = np.random.Generator(np.random.PCG64(seed))
     D, F = hidden, inter
 
@@ -260,6 +261,7 @@ def write_bert_model(path: str, seed: int = 0x6A5E0010, n_layer: int = 4, layers
             blocks = q8_quantize_ref(a)
             w.add_tensor(name, a.shape, GGML_Q8_0, blocks.tobytes())
             W[name] = q8_dequant(blocks, a.shape[-1]).reshape(a.shape)
+            W[name + "#q8"] = blocks          # the blocks themselves (an oracle that quantises activations)
         else:
             w.add_tensor(name, a.shape, GGML_F32, f32(a))
             W[name] = a.astype(np.float32)

@@ -54,10 +54,40 @@ def attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float) -> np.n
     return p @ np.asarray(v, np.float64)
 
 
-def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float, act_f16: bool = False) -> np.ndarray:
+def q8_quantize_x86(x32: np.ndarray):
+    """ggml-cpu's x86 Q8_0 quantisation of float32 rows [R][K] (K % 32 == 0): per block of 32,
+    d = fp16(amax / 127), q = round-half-even(x * (127 / amax)) in float32 (0 for an all-zero block).
+    Returns (q int8 [R][K/32][32], d float64 [R][K/32])."""
+    x32 = np.asarray(x32, np.float32)
+    R, K = x32.shape
+    xb = x32.reshape(R, K // 32, 32)
+    amax = np.abs(xb).max(axis=-1)
+    d = (amax / np.float32(127.0)).astype(np.float16).astype(np.float64)
+    with np.errstate(divide="ignore"):
+        idv = np.where(amax != 0, np.float32(127.0) / amax, np.float32(0.0)).astype(np.float32)
+    q = np.rint(xb * idv[..., None]).astype(np.int8)
+    return q, d
+
+
+def q8_matmul(x: np.ndarray, blocks: np.ndarray, n: int, k: int) -> np.ndarray:
+    """ggml mul_mat of Q8_0 weights (GGUF blocks of an [n][k] matrix) with float activations:
+    the activations are quantised (q8_quantize_x86 of their float32 values, ggml-cpu's vec_dot type
+    for Q8_0), then y[m][n] = sum over blocks of d_x d_w (exact integer block dot), in float64."""
+    qx, dx = q8_quantize_x86(np.asarray(x, np.float64).astype(np.float32))
+    b = np.asarray(blocks, np.uint8).reshape(n, k // 32, 34)
+    dw = b[:, :, 0:2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    qw = b[:, :, 2:].view(np.int8).astype(np.int32)
+    s = np.einsum("mbk,nbk->mnb", qx.astype(np.int32), qw)
+    return np.einsum("mnb,mb,nb->mn", s.astype(np.float64), dx, dw)
+
+
+def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float, act_f16: bool = False,
+           act_q8: bool = False) -> np.ndarray:
     """One sequence of token ids -> [hidden][T] after n_layers layers (0: the embedding LN).
     act_f16: the projections' inputs are rounded to fp16 first, as ggml-cpu does for F16 weights
-    (their vec_dot type is F16: ggml_cpu_fp32_to_fp16 of the activations, then F16 x F16 dots)."""
+    (their vec_dot type is F16: ggml_cpu_fp32_to_fp16 of the activations, then F16 x F16 dots).
+    act_q8: Q8_0 weights (W holds their blocks under name + "#q8"), multiplied as ggml-cpu does:
+    activations quantised to Q8_0 (x86), exact integer block dots (q8_matmul)."""
     ids = np.asarray(ids, np.int64)
     T = len(ids)
     D, hd = hidden, hidden // heads
@@ -66,15 +96,22 @@ def encode(W: dict, ids, n_layers: int, hidden: int, heads: int, eps: float, act
     x = layernorm(x, g("bert.emb_ln_w"), g("bert.emb_ln_b"), eps)
     scale = 1.0 / math.sqrt(hd)
     r = (lambda a: a.astype(np.float32).astype(np.float16).astype(np.float64)) if act_f16 else (lambda a: a)
+
+    def mm(a, name):   # a . W^T of the projection `name`
+        if act_q8:
+            n_, k_ = W[name].shape
+            return q8_matmul(a, W[name + "#q8"], n_, k_)
+        return r(a) @ g(name).T
+
     for li in range(n_layers):
         p = f"bert.l{li}."
-        qkv = r(x) @ g(p + "qkv_w").T + g(p + "qkv_b")
+        qkv = mm(x, p + "qkv_w") + g(p + "qkv_b")
         a = np.empty((T, D))
         for h in range(heads):
             sl = slice(h * hd, (h + 1) * hd)
             a[:, sl] = attention(qkv[:, sl], qkv[:, D:2 * D][:, sl], qkv[:, 2 * D:][:, sl], scale)
-        x = layernorm(x + r(a) @ g(p + "attn_out_w").T + g(p + "attn_out_b"), g(p + "attn_ln_w"),
+        x = layernorm(x + mm(a, p + "attn_out_w") + g(p + "attn_out_b"), g(p + "attn_ln_w"),
                       g(p + "attn_ln_b"), eps)
-        hh = gelu_erf(r(x) @ g(p + "ff1_w").T + g(p + "ff1_b"))
-        x = layernorm(x + r(hh) @ g(p + "ff2_w").T + g(p + "ff2_b"), g(p + "out_ln_w"), g(p + "out_ln_b"), eps)
+        hh = gelu_erf(mm(x, p + "ff1_w") + g(p + "ff1_b"))
+        x = layernorm(x + mm(hh, p + "ff2_w") + g(p + "ff2_b"), g(p + "out_ln_w"), g(p + "out_ln_b"), eps)
     return x.T.copy()

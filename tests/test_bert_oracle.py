@@ -90,3 +90,36 @@ def test_encode_f16_activations_round_each_projection_input(tmp_path):
     assert 1e-6 < d < 1e-2
     np.testing.assert_array_equal(BO.encode(W, ids, 0, 1024, 16, 1e-12, act_f16=True),
                                   BO.encode(W, ids, 0, 1024, 16, 1e-12))
+
+
+def test_q8_quantiser_is_the_pinned_x86_one():
+    """bert_oracle.q8_quantize_x86 (numpy) against the C oracle's orc_q8_quantize_x86, itself pinned
+    by known-answer blocks (tests/test_oracle_pins.py): same quants and fp16 scales, ties
+    included."""
+    import oracle as O
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((7, 256)).astype(np.float32)
+    x[0, :32] = 0.0                                     # all-zero block
+    x[1, :32] = np.linspace(-1, 1, 32)                  # +-amax
+    x[2, :32] = np.arange(32, dtype=np.float32) - 15.5  # halves: exact ties after the scale
+    q, d = BO.q8_quantize_x86(x)
+    blocks = O.q8_quantize_x86(x).reshape(7, 8, 34)
+    np.testing.assert_array_equal(q, blocks[:, :, 2:].view(np.int8))
+    np.testing.assert_array_equal(d, blocks[:, :, 0:2].copy().view(np.float16)[:, :, 0].astype(np.float64))
+
+
+def test_q8_matmul_is_exact_block_products():
+    """q8_matmul against an independent evaluation: dequantised operands (d q, exact in float64)
+    multiplied in float64 give the same sums of exact block products to within fp64 rounding,
+    and against the plain float product to within the quantisation error."""
+    rng = np.random.default_rng(22)
+    n, k = 64, 128
+    w = (rng.standard_normal((n, k)) * 0.03).astype(np.float32)
+    blocks = sm.q8_quantize_ref(w)
+    x = rng.standard_normal((5, k))
+    y = BO.q8_matmul(x, blocks, n, k)
+    qx, dx = BO.q8_quantize_x86(x.astype(np.float32))
+    xd = (qx.astype(np.float64) * dx[..., None]).reshape(5, k)
+    wd = sm.q8_dequant(blocks, k).reshape(n, k).astype(np.float64)
+    np.testing.assert_allclose(y, xd @ wd.T, rtol=0, atol=1e-12 * np.abs(xd @ wd.T).max())
+    assert np.abs(y - x @ w.T.astype(np.float64)).max() <= 0.02 * np.abs(x @ w.T).max()
