@@ -13,12 +13,14 @@
 //
 // Tiling: workgroup 256 threads = 4 waves, output tile 128 (rows m) x 128 (columns n); wave w
 // owns rows 64*(w/2).. and columns 64*(w%2).., i.e. 2 x 2 MFMA tiles. K is staged through LDS in
-// chunks of 2 blocks (64 values) by direct global -> LDS loads, double buffered: the next
-// chunk streams in while the current one is multiplied, with no staging registers, and the
-// 35 KB of LDS and <= 168 VGPRs let 3 workgroups share a CU. Operands arrive with their quants
-// in natural order (q[row][k]; scales apart), so a chunk of a row is half a 128-byte line. A
-// lane's MFMA operand is one half (16 values) of a block of one row; A and B use the same halves,
-// so the product sums over the block whatever order the hardware assigns to the bytes.
+// chunks of 4 blocks (128 values) by direct global -> LDS loads, double buffered: the next
+// chunk streams in while the current one is multiplied, with no staging registers (70 KB of LDS
+// and <= 256 VGPRs: 2 workgroups per CU, 2 waves per SIMD). Operands arrive with their quants in
+// natural order (q[row][k]; scales apart). A lane's MFMA operand is one half (16 values) of a
+// block of one row; A and B use the same halves, so the product sums over the block whatever
+// order the hardware assigns to the bytes. Per block a wave issues the MFMA pair of a tile two
+// tiles ahead of the vector work that consumes it, so that the matrix cores and the vector ALUs
+// run side by side.
 //
 // Epilogue (the options of the decoder's GEMV, layer.h LayerOut): bias, ReLU, fp32 store of
 // columns < n_store, the fp16 K/V append, or the Q8_0 quantisation of each 32-column block (in
@@ -32,11 +34,8 @@ namespace {
 constexpr int GM_THREADS = 256;
 constexpr int GM_BM = 128;                 // rows (m) per workgroup
 constexpr int GM_BN = 128;                 // columns (n) per workgroup
-constexpr int GM_KC = 2;                   // blocks per K chunk
+constexpr int GM_KC = 4;                   // blocks per K chunk
 constexpr int GM_NBUF = 2;                 // chunk buffers (a chunk streams in while one is used)
-constexpr int GM_ROWB = GM_KC * 32;        // LDS bytes per row and chunk
-constexpr int GM_SLOTS = GM_ROWB / 16;     // 16-byte slots per row and chunk
-constexpr int GM_SWZ = GM_SLOTS - 1;       // slot swizzle mask
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -45,15 +44,19 @@ typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef __attribute__((address_space(3))) void lds_void;
 }  // namespace
 
-// K chunk buffers, filled by direct global -> LDS loads (no staging registers). A row's chunk is
-// 64 bytes = 4 slots of 16 bytes; piece p of row r sits in slot p ^ (r & 3), so that the 16-byte
-// operand reads of consecutive rows fall in different banks.
+// K chunk buffers, filled by direct global -> LDS loads (no staging registers), block-major:
+// a[buf][block][row] is the row's 32 quants of that block. Half h (16 bytes) of row r sits in
+// slot h ^ gemm_swz(r), so that the 16-byte operand reads of a wave (lane (i, g) reads half g of
+// row i) cover every bank once per 8 and per 16 lanes, and every operand address of a wave is
+// one base register plus a constant.
 struct GemmLds {
-    int8_t a[GM_NBUF][GM_BM * GM_ROWB];
-    int8_t b[GM_NBUF][GM_BN * GM_ROWB];
+    int8_t a[GM_NBUF][GM_KC][GM_BM][32];
+    int8_t b[GM_NBUF][GM_KC][GM_BN][32];
     float da[GM_NBUF][GM_BM * GM_KC];      // activation scales [row][block]
     uint16_t db[GM_NBUF][GM_BN * GM_KC];   // weight scales (fp16) [col][block]
 };
+
+__device__ __forceinline__ int gemm_swz(int r) { return ((r >> 2) ^ (r >> 3)) & 1; }
 
 // The chunk buffers during the K loop; half of the fp32 output tile (64 rows, padded by 4 floats)
 // in the epilogue.
@@ -71,42 +74,104 @@ __device__ __forceinline__ void lds_dma4(const void * g, void * lds) {
 // (a direct load places lane L's data at 4 * L for the 1-, 2- and 4-byte forms: the fp16 weight
 // scales travel in pairs)
 
+// Per-lane offsets of a wave's direct loads, fixed over the K loop (32-bit: m * k < 2^31 is
+// checked at launch). Wave w loads rows [32 w, 32 w + 32) of the tile: lane L the half of row
+// 32 w + L / 2 that belongs in its 16-byte LDS slot.
+struct GemmIssue {
+    uint32_t xo, wo;          // quants: row offset + half
+    uint32_t xdo[GM_KC / 2];  // activation scales: 256 (row, block) pairs per instruction
+    uint32_t wdo;             // weight scales: a pair of blocks of one column per lane
+};
+
+template <int NBLK>
+__device__ __forceinline__ GemmIssue gemm_issue_offsets(int m, int m0, int n0, int wave, int lane) {
+    GemmIssue o;
+    const int r = 32 * wave + lane / 2;
+    const uint32_t half = (uint32_t) ((lane & 1) ^ gemm_swz(r));
+    o.xo = (uint32_t) min(m0 + r, m - 1) * (NBLK * 32) + half * 16;
+    o.wo = (uint32_t) (n0 + r) * (NBLK * 32) + half * 16;
+#pragma unroll
+    for (int u = 0; u < GM_KC / 2; u++) {
+        const int i = u * 256 + wave * 64 + lane;
+        o.xdo[u] = (uint32_t) min(m0 + i / GM_KC, m - 1) * NBLK + i % GM_KC;
+    }
+    const int i = wave * 64 + lane;
+    o.wdo = (uint32_t) (n0 + i / (GM_KC / 2)) * NBLK + 2 * (i % (GM_KC / 2));
+    return o;
+}
+
 // Issue the direct loads of one K chunk into buffer buf. A wave's load instruction writes 64
-// consecutive 16-byte (or 4-byte) LDS slots, lane L the L-th; the global address of each lane is
-// chosen so that the slot receives what the layout above puts there.
+// consecutive 16-byte (or 4-byte) LDS slots, lane L the L-th.
 template <int NBLK>
 __device__ __forceinline__ void gemm_issue(const int8_t * __restrict__ xs, const float * __restrict__ xd,
                                            const int8_t * __restrict__ ws, const uint16_t * __restrict__ wd,
-                                           int m, int m0, int n0, int chunk, int wave, int lane, GemmLds & s,
-                                           int buf) {
+                                           const GemmIssue & o, int chunk, int wave, GemmLds & s, int buf) {
     const int blk0 = chunk * GM_KC;
-    constexpr int ROWS_PER_SEG = 64 / GM_SLOTS;   // rows covered by one wave instruction (1 KB)
 #pragma unroll
     for (int u = 0; u < GM_KC; u++) {
-        const int seg = u * 4 + wave;
-        const int r = seg * ROWS_PER_SEG + lane / GM_SLOTS;
-        const int p = (lane % GM_SLOTS) ^ (r & GM_SWZ);   // the piece that belongs in this slot
-        const int mm = min(m0 + r, m - 1);
-        lds_dma16(xs + (int64_t) mm * NBLK * 32 + blk0 * 32 + p * 16, &s.a[buf][seg * 1024]);
-        lds_dma16(ws + (int64_t) (n0 + r) * NBLK * 32 + blk0 * 32 + p * 16, &s.b[buf][seg * 1024]);
+        lds_dma16(xs + (blk0 + u) * 32 + o.xo, &s.a[buf][u][32 * wave][0]);
+        lds_dma16(ws + (blk0 + u) * 32 + o.wo, &s.b[buf][u][32 * wave][0]);
     }
 #pragma unroll
-    for (int u = 0; u < GM_KC / 2; u++) {          // 128 rows x GM_KC scales, 256 per instruction
-        const int i = u * 256 + wave * 64 + lane;
-        const int mm = min(m0 + i / GM_KC, m - 1);
-        lds_dma4(xd + (int64_t) mm * NBLK + blk0 + i % GM_KC, &s.da[buf][u * 256 + wave * 64]);
+    for (int u = 0; u < GM_KC / 2; u++) lds_dma4(xd + blk0 + o.xdo[u], &s.da[buf][u * 256 + wave * 64]);
+    // 128 columns x GM_KC fp16 scales, two per 4-byte lane: 64 * GM_KC lanes
+    static_assert(GM_BN * GM_KC / 2 == 256, "one weight-scale load per wave");
+    lds_dma4(wd + blk0 + o.wdo, &s.db[buf][2 * (wave * 64)]);
+}
+
+// One block's MFMA operands for a wave: 16 quants of each of its two row groups (A) and
+// column groups (B), and the raw scales of those rows and columns (see gemm_scales).
+struct GemmOps {
+    v4i fa[2], fb[2];
+    float dx[2];
+    uint32_t dw[2];   // fp16 bits
+};
+
+__device__ __forceinline__ GemmOps gemm_ops(const GemmLds & s, int buf, int bb, int wm, int wn, int li, int lg) {
+    GemmOps o;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        const int ra = wm + 32 * h + li, rb = wn + 32 * h + li;
+        o.fa[h] = *reinterpret_cast<const v4i *>(&s.a[buf][bb][ra][16 * (lg ^ gemm_swz(li))]);
+        o.fb[h] = *reinterpret_cast<const v4i *>(&s.b[buf][bb][rb][16 * (lg ^ gemm_swz(li))]);
+        o.dx[h] = s.da[buf][ra * GM_KC + bb];
+        o.dw[h] = s.db[buf][rb * GM_KC + bb];
     }
-    // 128 columns x GM_KC fp16 scales, two per 4-byte lane
-    constexpr int DB_LANES = GM_BN * GM_KC / 2;
-    if (wave * 64 < DB_LANES) {
-        const int i = wave * 64 + lane;
-        const int col = i / (GM_KC / 2), pair = i % (GM_KC / 2);
-        lds_dma4(wd + (int64_t) (n0 + col) * NBLK + blk0 + 2 * pair, &s.db[buf][2 * (wave * 64)]);
+    return o;
+}
+
+// The scales as fp16 MFMA operands holding dx (A) or dw (B) in their first K slot and zeros
+// elsewhere (the caller keeps the zeros; only slot 0 is written). Every lane carries its row's or
+// column's scale, so the K sum holds two equal terms (one per lane half) and the fp16 MFMA
+// returns 2 * dx * dw, exactly (both are fp16 values, so dx * dw is exact in fp32 and doubling
+// it is too). The accumulators thus hold exactly twice the sum; the epilogue halves them, which
+// is exact as well.
+__device__ __forceinline__ void gemm_scales(const GemmOps & o, v8h (&adx)[2], v8h (&bdw)[2]) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        adx[h][0] = (_Float16) o.dx[h];
+        bdw[h][0] = __builtin_bit_cast(_Float16, (uint16_t) o.dw[h]);
     }
 }
 
+// acc += float(c) * sc over a tile's 16 values per lane (c: exact integer sums of one block; sc:
+// twice the scale products)
+__device__ __forceinline__ void gemm_fold(float (&acc)[16], const v16i & c, const v16f & sc) {
+#pragma unroll
+    for (int v = 0; v < 16; v++) acc[v] = __builtin_fmaf((float) c[v], sc[v], acc[v]);
+}
+
+// The maximum over each aligned group of 8 lanes, by DPP: quad swaps (1 0 3 2) and (2 3 0 1),
+// then the half-row mirror (lane i <-> 7 - i of the 8), which pairs the two quads.
+__device__ __forceinline__ float max8_lanes(float v) {
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false)));
+    v = fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false)));
+    return v;
+}
+
 template <int NBLK>
-__global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restrict__ ws,
+__global__ void __launch_bounds__(GM_THREADS) __attribute__((amdgpu_waves_per_eu(2))) k_q8_gemm(const int8_t * __restrict__ ws,
                                                            const uint16_t * __restrict__ wd, int n, int m,
                                                            const int8_t * __restrict__ xs,
                                                            const float * __restrict__ xd, LayerOut out) {
@@ -116,8 +181,19 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int n0 = blockIdx.x * GM_BN;
-    const int m0 = blockIdx.y * GM_BM;
+    // The hardware deals workgroup ids round-robin to the 8 XCDs. Renumbered so that each XCD
+    // takes a contiguous run of tiles (column tiles fastest), the column tiles of a row tile run
+    // on one XCD and share its L2 copy of the activation rows.
+    int n0, m0;
+    {
+        const int total = (int) gridDim.x, b = (int) blockIdx.x;
+        const int per = (total + 7) / 8, tall = total % 8 == 0 ? 8 : total % 8;
+        const int xcd = b % 8, loc = b / 8;
+        const int t = xcd < tall ? xcd * per + loc : tall * per + (xcd - tall) * (per - 1) + loc;
+        const int nx = n / GM_BN;
+        n0 = (t % nx) * GM_BN;
+        m0 = (t / nx) * GM_BM;
+    }
     if (out.row_pad) {   // a tile of padding rows only: zeros out, no products (uniform branch)
         bool all_pad = true;
         const int S = out.rows_per_seq;
@@ -147,63 +223,90 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
     const int li = lane & 31;          // MFMA: row of A / column of B held by this lane
     const int lg = lane >> 5;          // MFMA: which half of the block
 
-    float acc[4][16];                  // tile t = 2 * ta + tb
+    float acc[4][16];                  // tile t = 2 * ta + tb; twice the output (see gemm_ops)
 #pragma unroll
     for (int t = 0; t < 4; t++)
 #pragma unroll
         for (int v = 0; v < 16; v++) acc[t][v] = 0.0f;
 
+    const GemmIssue io = gemm_issue_offsets<NBLK>(m, m0, n0, wave, lane);
 #pragma unroll
     for (int c = 0; c < GM_NBUF - 1; c++)
-        if (c < NCH) gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, c, wave, lane, s, c);
+        if (c < NCH) gemm_issue<NBLK>(xs, xd, ws, wd, io, c, wave, s, c);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
+#pragma unroll 1
     for (int ch = 0; ch < NCH; ch++) {
         const int buf = ch % GM_NBUF;
         // the chunk GM_NBUF - 1 ahead streams into the buffer read before the previous barrier
         if (ch + GM_NBUF - 1 < NCH)
-            gemm_issue<NBLK>(xs, xd, ws, wd, m, m0, n0, ch + GM_NBUF - 1, wave, lane, s, (ch + GM_NBUF - 1) % GM_NBUF);
-#pragma unroll 1
+            gemm_issue<NBLK>(xs, xd, ws, wd, io, ch + GM_NBUF - 1, wave, s, (ch + GM_NBUF - 1) % GM_NBUF);
+        GemmOps op = gemm_ops(s, buf, 0, wm, wn, li, lg);
+        v8h adx[2] = {v8h{}, v8h{}}, bdw[2] = {v8h{}, v8h{}};
+        // Per block: the four tiles' MFMA pairs are issued two tiles ahead of the vector work that
+        // consumes them, so that the matrix cores run while the vector ALUs fold the previous
+        // tile; the next block's operands are read from LDS under the last two folds. The
+        // scheduling barriers keep the compiler from regrouping the pairs (it would otherwise
+        // serialise every tile on one result register set).
+#pragma unroll
         for (int bb = 0; bb < GM_KC; bb++) {
-            // operands: piece 2 * bb + lg (16 values) of the wave's rows / columns
-            v4i fa[2], fb[2];
-            v8h adx[2], bdw[2];
-#pragma unroll
-            for (int h = 0; h < 2; h++) {
-                const int ra = wm + 32 * h + li, rb = wn + 32 * h + li;
-                fa[h] = *reinterpret_cast<const v4i *>(&s.a[buf][ra * GM_ROWB + (((2 * bb + lg) ^ (ra & GM_SWZ)) << 4)]);
-                fb[h] = *reinterpret_cast<const v4i *>(&s.b[buf][rb * GM_ROWB + (((2 * bb + lg) ^ (rb & GM_SWZ)) << 4)]);
-                // the scale-product MFMA: A = dx of the tile's rows, B = dw of its columns, in one
-                // K slot of lanes 0-31, every other slot zero. Both scales are fp16 values (the
-                // activation scale is rounded to fp16 when it is made), so their product is exact
-                // in the fp16 MFMA's fp32 result, as in a vector multiply.
-                adx[h] = v8h{};
-                bdw[h] = v8h{};
-                if (lg == 0) {
-                    adx[h][0] = (_Float16) s.da[buf][ra * GM_KC + bb];
-                    bdw[h][0] = __builtin_bit_cast(_Float16, s.db[buf][rb * GM_KC + bb]);
-                }
-            }
-            // per tile: the exact integer sum of the block, the products dx * dw, then
-            // acc += float(C) * (dx * dw) on the vector ALUs
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const v16i c = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[t >> 1], fb[t & 1], v16i{}, 0, 0, 0);
-                const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[t >> 1], bdw[t & 1], v16f{}, 0, 0, 0);
-#pragma unroll
-                for (int v = 0; v < 16; v++) acc[t][v] = __builtin_fmaf((float) c[v], sc[v], acc[t][v]);
-            }
+            gemm_scales(op, adx, bdw);
+            const v16i c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(op.fa[0], op.fb[0], v16i{}, 0, 0, 0);
+            const v16f s0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[0], bdw[0], v16f{}, 0, 0, 0);
+            const v16i c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(op.fa[0], op.fb[1], v16i{}, 0, 0, 0);
+            const v16f s1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[0], bdw[1], v16f{}, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm_fold(acc[0], c0, s0);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(op.fa[1], op.fb[0], v16i{}, 0, 0, 0);
+            const v16f s2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[1], bdw[0], v16f{}, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm_fold(acc[1], c1, s1);
+            __builtin_amdgcn_sched_barrier(0);
+            const v16i c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(op.fa[1], op.fb[1], v16i{}, 0, 0, 0);
+            const v16f s3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(adx[1], bdw[1], v16f{}, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (bb + 1 < GM_KC) op = gemm_ops(s, buf, bb + 1, wm, wn, li, lg);
+            __builtin_amdgcn_sched_barrier(0);
+            gemm_fold(acc[2], c2, s2);
+            gemm_fold(acc[3], c3, s3);
+            __builtin_amdgcn_sched_barrier(0);
         }
         __builtin_amdgcn_s_waitcnt(0);   // the chunks issued so far have landed
         __syncthreads();                 // and every wave is done with this one
     }
 
-    // ---- epilogue: each half of the 128 x 128 tile goes through LDS so that each thread then
-    // owns a 32-column block of a row: coalesced stores and an in-register Q8_0 quantisation ----
+    // ---- epilogue: each half of the 128 x 128 tile goes through LDS; then a wave takes 16 of
+    // its rows, two per step, lane l the 4 columns 4 (l % 32).. of row 2 i + l / 32, so that every
+    // store instruction writes whole rows (fp32: 512 bytes, Q8_0: 128 bytes, K/V: 64 bytes per
+    // head) and a Q8_0 block is 8 lanes (its absmax: three exchanges) ----
     int kvcol0 = 0;
     if (out.kc) kvcol0 = *out.col_ptr + out.col_add;
     const int nblk_out = n / 32;
+    const int c4 = lane & 31;
+    const int col = n0 + 4 * c4;
+    float4 b4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (out.bias) b4 = *reinterpret_cast<const float4 *>(out.bias + col);
+    const bool store_y = out.y && col < out.n_store;
+    const bool q8_only = out.yq && !out.y && !out.kc;
+    const int colq = n0 + 16 * (lane & 7);
+    float bq[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) bq[k] = 0.0f;
+    if (q8_only && out.bias) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const float4 f = *reinterpret_cast<const float4 *>(out.bias + colq + 4 * j);
+            bq[4 * j] = f.x; bq[4 * j + 1] = f.y; bq[4 * j + 2] = f.z; bq[4 * j + 3] = f.w;
+        }
+    }
+    // K/V append: the 32-column block of this lane's columns is one head of K or V
+    uint16_t * kv_head = nullptr;
+    if (out.kc && (col & ~31) >= out.kv_row0) {
+        const int rr = (col & ~31) - out.kv_row0;
+        kv_head = (rr / out.d_model == 0 ? out.kc : out.vc) + ((rr % out.d_model) >> 5) * out.lstride * 32 + (col & 31);
+    }
 #pragma unroll 1
     for (int half = 0; half < 2; half++) {
         if (half) __syncthreads();       // the first half has been read
@@ -213,73 +316,84 @@ __global__ void __launch_bounds__(GM_THREADS) k_q8_gemm(const int8_t * __restric
                 const int ta = t >> 1, tb = t & 1;
 #pragma unroll
                 for (int v = 0; v < 16; v++)
-                    sm.y[32 * ta + 8 * (v >> 2) + 4 * lg + (v & 3)][wn + 32 * tb + li] = acc[t][v];
+                    sm.y[32 * ta + 8 * (v >> 2) + 4 * lg + (v & 3)][wn + 32 * tb + li] = 0.5f * acc[t][v];
             }
         }
         __syncthreads();
-        const int r = tid >> 2, cb = tid & 3;      // 64 rows x 4 blocks of 32 columns
-        const int row = m0 + 64 * half + r;
-        if (row >= m) continue;
-        const int col0 = n0 + 32 * cb;
-        float y[32];
+        if (q8_only) {
+            // Q8_0 output alone: lane l takes the 16 columns 16 (l % 8).. of row l / 8 of a group
+            // of 8 rows, so a block is a lane pair (one exchange for its absmax) and its quants are
+            // one 16-byte store per lane
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const float4 f = *reinterpret_cast<const float4 *>(&sm.y[r][32 * cb + 4 * j]);
-            y[4 * j] = f.x; y[4 * j + 1] = f.y; y[4 * j + 2] = f.z; y[4 * j + 3] = f.w;
-        }
-        if (out.bias) {
+            for (int it = 0; it < 2; it++) {
+                const int r = 16 * wave + 8 * it + (lane >> 3);
+                const int row = m0 + 64 * half + r;
+                float y[16];
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float4 b4 = *reinterpret_cast<const float4 *>(out.bias + col0 + 4 * j);
-                y[4 * j] = y[4 * j] + b4.x; y[4 * j + 1] = y[4 * j + 1] + b4.y;
-                y[4 * j + 2] = y[4 * j + 2] + b4.z; y[4 * j + 3] = y[4 * j + 3] + b4.w;
+                for (int j = 0; j < 4; j++) {
+                    const float4 f = *reinterpret_cast<const float4 *>(&sm.y[r][16 * (lane & 7) + 4 * j]);
+                    y[4 * j] = f.x; y[4 * j + 1] = f.y; y[4 * j + 2] = f.z; y[4 * j + 3] = f.w;
+                }
+                if (out.bias) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) y[k] = y[k] + bq[k];
+                }
+                if (out.act == 1) {
+#pragma unroll
+                    for (int k = 0; k < 16; k++) y[k] = y[k] > 0.0f ? y[k] : 0.0f;
+                }
+                float amax = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 16; k++) amax = fmaxf(amax, fabsf(y[k]));
+                amax = fmaxf(amax, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, amax), 0xB1, 0xF, 0xF, false)));
+                const float d = amax / 127.0f;
+                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+                int w[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    w[j] = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; t++) w[j] |= (((int) __builtin_rintf(y[4 * j + t] * id)) & 0xff) << (8 * t);
+                }
+                if (row < m) {
+                    *reinterpret_cast<int4 *>(out.yq + (int64_t) row * n + colq) = make_int4(w[0], w[1], w[2], w[3]);
+                    if ((lane & 1) == 0) out.yd[(int64_t) row * nblk_out + (colq >> 5)] = h2f(f2h(d));
+                }
             }
+            continue;
         }
-        if (out.act == 1) {
+        float4 yv[8];
 #pragma unroll
-            for (int k = 0; k < 32; k++) y[k] = y[k] > 0.0f ? y[k] : 0.0f;
-        }
-        if (out.y && col0 < out.n_store) {
-            float * yr = out.y + (int64_t) row * out.y_stride + col0;
+        for (int i = 0; i < 8; i++) yv[i] = *reinterpret_cast<const float4 *>(&sm.y[16 * wave + 2 * i + (lane >> 5)][4 * c4]);
 #pragma unroll
-            for (int j = 0; j < 8; j++)
-                *reinterpret_cast<float4 *>(yr + 4 * j) = make_float4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
-        }
-        if (out.yq) {
-            float amax = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 32; k++) amax = fmaxf(amax, fabsf(y[k]));
-            const float d = amax / 127.0f;
-            const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-            const int blk = col0 >> 5;
-            int w[8];
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                w[j] = 0;
-#pragma unroll
-                for (int t = 0; t < 4; t++) w[j] |= (((int) __builtin_rintf(y[4 * j + t] * id)) & 0xff) << (8 * t);
+        for (int i = 0; i < 8; i++) {
+            const int row = m0 + 64 * half + 16 * wave + 2 * i + (lane >> 5);
+            float4 y = yv[i];
+            if (out.bias) { y.x = y.x + b4.x; y.y = y.y + b4.y; y.z = y.z + b4.z; y.w = y.w + b4.w; }
+            if (out.act == 1) {
+                y.x = y.x > 0.0f ? y.x : 0.0f; y.y = y.y > 0.0f ? y.y : 0.0f;
+                y.z = y.z > 0.0f ? y.z : 0.0f; y.w = y.w > 0.0f ? y.w : 0.0f;
             }
-            int4 * qr = reinterpret_cast<int4 *>(out.yq + (int64_t) row * n + col0);   // natural order
-            qr[0] = make_int4(w[0], w[1], w[2], w[3]);
-            qr[1] = make_int4(w[4], w[5], w[6], w[7]);
-            out.yd[(int64_t) row * nblk_out + blk] = h2f(f2h(d));
-        }
-        if (out.kc && col0 >= out.kv_row0) {
-            // one 32-column block = one head of K or V
-            const int rr = col0 - out.kv_row0;
-            const int which = rr / out.d_model;
-            const int h = (rr % out.d_model) >> 5;
-            const int b = row / out.rows_per_seq;
-            const int kcol = kvcol0 + row % out.rows_per_seq;
-            uint16_t * cache = (which == 0 ? out.kc : out.vc) + (((int64_t) b * out.n_head + h) * out.lstride + kcol) * 32;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                uint4 w;
-                w.x = (uint32_t) f2h(y[8 * j + 0]) | ((uint32_t) f2h(y[8 * j + 1]) << 16);
-                w.y = (uint32_t) f2h(y[8 * j + 2]) | ((uint32_t) f2h(y[8 * j + 3]) << 16);
-                w.z = (uint32_t) f2h(y[8 * j + 4]) | ((uint32_t) f2h(y[8 * j + 5]) << 16);
-                w.w = (uint32_t) f2h(y[8 * j + 6]) | ((uint32_t) f2h(y[8 * j + 7]) << 16);
-                *reinterpret_cast<uint4 *>(cache + 8 * j) = w;
+            const bool valid = row < m;
+            if (valid && store_y) *reinterpret_cast<float4 *>(out.y + (int64_t) row * out.y_stride + col) = y;
+            if (out.yq) {
+                const float amax = max8_lanes(fmaxf(fmaxf(fabsf(y.x), fabsf(y.y)), fmaxf(fabsf(y.z), fabsf(y.w))));
+                const float d = amax / 127.0f;
+                const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+                const int w = (((int) __builtin_rintf(y.x * id)) & 0xff) | ((((int) __builtin_rintf(y.y * id)) & 0xff) << 8) |
+                              ((((int) __builtin_rintf(y.z * id)) & 0xff) << 16) | ((((int) __builtin_rintf(y.w * id)) & 0xff) << 24);
+                if (valid) {
+                    *reinterpret_cast<int *>(out.yq + (int64_t) row * n + col) = w;   // natural order
+                    if ((lane & 7) == 0) out.yd[(int64_t) row * nblk_out + (col >> 5)] = h2f(f2h(d));
+                }
+            }
+            if (kv_head && valid) {
+                const int b = row / out.rows_per_seq;
+                const int kcol = kvcol0 + row % out.rows_per_seq;
+                uint2 w;
+                w.x = (uint32_t) f2h(y.x) | ((uint32_t) f2h(y.y) << 16);
+                w.y = (uint32_t) f2h(y.z) | ((uint32_t) f2h(y.w) << 16);
+                *reinterpret_cast<uint2 *>(kv_head + ((int64_t) b * out.n_head * out.lstride + kcol) * 32) = w;
             }
         }
     }
@@ -516,11 +630,13 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
     GSVK_REQUIRE(tile_rows == 0, "q8_gemm: row tiles are a choice of the small-batch kernel (m <= %lld)",
                  (long long) GS_MAX_ROWS);
     GSVK_REQUIRE(!out.row_pad || out.rows_per_seq > 0, "q8_gemm: padding rows need rows_per_seq");
+    GSVK_REQUIRE(m * k < ((int64_t) 1 << 31) && n * k < ((int64_t) 1 << 31),
+                 "q8_gemm: operands above 2 GiB (m=%lld n=%lld k=%lld)", (long long) m, (long long) n, (long long) k);
     GSVK_REQUIRE(x_layout == Q8_NATURAL && (!out.yq || out.yq_layout == Q8_NATURAL),
                  "q8_gemm: above %lld rows the operands are in natural order", (long long) GS_MAX_ROWS);
     const int8_t * ws = w.qn;
     const uint16_t * wd = w.dn;
-    const dim3 grid((unsigned) (n / GM_BN), (unsigned) ((m + GM_BM - 1) / GM_BM));
+    const dim3 grid((unsigned) (n / GM_BN * ((m + GM_BM - 1) / GM_BM)));
     if (k == 512)
         hipLaunchKernelGGL(k_q8_gemm<16>, grid, dim3(GM_THREADS), 0, stream, ws, wd, (int) n, (int) m, xs, xd, out);
     else if (k == 1024)

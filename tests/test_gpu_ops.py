@@ -453,6 +453,47 @@ def test_q8_gemm_matches_oracle(gpu, n, k, m):
     assert np.abs(y2.cpu().numpy() - ref2).max() <= 2e-6 * scale
 
 
+@pytest.mark.parametrize("n,k", [(2048, 512), (512, 2048), (1024, 4096)])
+@pytest.mark.parametrize("m", [300, 1024])
+@pytest.mark.parametrize("with_y", [True, False])
+def test_q8_gemm_large_q8_out(gpu, n, k, m, with_y):
+    """The 128 x 128 GEMM (above 256 rows) with bias + ReLU: the fp32 rows within 2e-6 of the
+    oracle's scale, the Q8_0 rows the x86 quantisation of those fp32 rows bit for bit, rows past m
+    untouched. Two epilogues: fp32 + Q8_0 (a block is 8 lanes of 4 columns) and Q8_0 alone (a
+    block is 2 lanes of 16 columns; its fp32 rows then come from a second call with fp32 only)."""
+    import torch
+    rng = np.random.default_rng(7200 + n + k + m)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    X[1, :] = 0.0                       # an all-zero row: zero blocks (scale 0) in the output
+    wb = sm.q8_quantize_ref(W).ravel()
+    wq_n, wd_n = blocks_to_split(wb, n, k)
+    xq_n, xd_n = blocks_to_split(O.q8_quantize_x86(X), m, k)
+    wq, wd = _dev(wq_n, torch), _dev(wd_n.view(np.int16), torch)
+    xq, xd = _dev(xq_n, torch), _dev(xd_n.view(np.float16).astype(np.float32), torch)
+    b = rng.standard_normal(n).astype(np.float32) * 0.02
+    b[:32] = 0.0                        # with row 1 at zero: a block of exact zeros
+    bias = _dev(b, torch)
+    y = torch.full((m + 1, n), 7.0, dtype=torch.float32, device="cuda")
+    yq = torch.full((m + 1, n), 5, dtype=torch.int8, device="cuda")
+    yd = torch.full((m + 1, n // 32), 3.0, dtype=torch.float32, device="cuda")
+    if with_y:
+        gpu.op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, 1, y, yq, yd)
+    else:
+        gpu.op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, 1, None, yq, yd)
+        gpu.op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, 1, y, None, None)
+    torch.cuda.synchronize()
+    y, yq, yd = y.cpu().numpy(), yq.cpu().numpy(), yd.cpu().numpy()
+    assert (y[m] == 7.0).all() and (yq[m] == 5).all() and (yd[m] == 3.0).all()
+    y, yq, yd = y[:m], yq[:m], yd[:m]
+    ref = np.maximum(O.q8_matmul(wb, n, k, X) + b[None, :], 0.0)
+    assert np.abs(y - ref).max() <= 2e-6 * np.abs(ref).max()
+    assert (yd[1, 0] == 0.0) and (yq[1, :32] == 0).all()
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(y), m, n)
+    assert np.array_equal(yq, q_ref.reshape(m, n))
+    assert np.array_equal(yd, d_ref.view(np.float16).astype(np.float32).reshape(m, n // 32))
+
+
 @pytest.mark.parametrize("n,k", [(1536, 512), (512, 2048), (2048, 512)])
 @pytest.mark.parametrize("m", [1, 64, 100, 128, 256])
 def test_q8_gemm_small_tiles(gpu, n, k, m):
