@@ -34,14 +34,23 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
     float v[MAXC][8];
     double s = 0.0, s2 = 0.0;
     // 16-byte loads, all issued before the first use; the branches are uniform
-    float4 xv[MAXC][2], rv[MAXC][2], bv[MAXC][2];
+    // (the LayerNorm weight and bias too: they are not needed until after the reductions, but a
+    // load issued then would be a second memory round trip)
+    float4 xv[MAXC][2], rv[MAXC][2], bv[MAXC][2], wv[MAXC][2], cv[MAXC][2];
 #pragma unroll
     for (int c = 0; c < MAXC; c++) {
         const int base = (lane + 64 * c) * 8;
         const bool act = lane + 64 * c < nchunk;
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        xv[c][0] = act ? *reinterpret_cast<const float4 *>(xr + base) : z;
-        xv[c][1] = act ? *reinterpret_cast<const float4 *>(xr + base + 4) : z;
+        xv[c][0] = xv[c][1] = wv[c][0] = wv[c][1] = cv[c][0] = cv[c][1] = z;
+        if (act) {   // (an explicit branch: a select of the load would become per-word loads)
+            xv[c][0] = *reinterpret_cast<const float4 *>(xr + base);
+            xv[c][1] = *reinterpret_cast<const float4 *>(xr + base + 4);
+            wv[c][0] = *reinterpret_cast<const float4 *>(wb + base);
+            wv[c][1] = *reinterpret_cast<const float4 *>(wb + base + 4);
+            cv[c][0] = *reinterpret_cast<const float4 *>(wb + n + base);
+            cv[c][1] = *reinterpret_cast<const float4 *>(wb + n + base + 4);
+        }
         rv[c][0] = rv[c][1] = bv[c][0] = bv[c][1] = z;
         if (rr && act) {
             rv[c][0] = *reinterpret_cast<const float4 *>(rr + base);
@@ -75,8 +84,6 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
     const float mean = (float) (s / (double) n);
     const float var = __builtin_fmaf(-mean, mean, (float) (s2 / (double) n));
     const float inv = 1.0f / __builtin_sqrtf(var + eps);
-    const float * w = wb;
-    const float * b = wb + n;
     float * yr = y + (int64_t) row * n;
     const int nblk = n / QK;
 #pragma unroll
@@ -86,12 +93,17 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
         float o[8];
         if (act) {
             const int base = ch * 8;
+            const float ws[8] = {wv[c][0].x, wv[c][0].y, wv[c][0].z, wv[c][0].w,
+                                 wv[c][1].x, wv[c][1].y, wv[c][1].z, wv[c][1].w};
+            const float bs[8] = {cv[c][0].x, cv[c][0].y, cv[c][0].z, cv[c][0].w,
+                                 cv[c][1].x, cv[c][1].y, cv[c][1].z, cv[c][1].w};
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                o[i] = __builtin_fmaf((v[c][i] - mean) * inv, w[base + i], b[base + i]);
-                yr[base + i] = o[i];
+                o[i] = __builtin_fmaf((v[c][i] - mean) * inv, ws[i], bs[i]);
                 if constexpr (F16OUT) y16[(int64_t) row * n + base + i] = f2h(o[i]);   // fp16 copy, nearest even
             }
+            *reinterpret_cast<float4 *>(yr + base) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4 *>(yr + base + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
         if (yq && (64 * c) < nchunk) {   // uniform across the wave
             if (!act) {
@@ -175,7 +187,7 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     GSVK_REQUIRE((yq == nullptr) == (yd == nullptr), "layernorm: yq and yd go together");
     GSVK_REQUIRE(layout >= Q8_SLICED && layout <= Q8_TILED, "layernorm: bad layout %d", layout);
     auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
-    GSVK_REQUIRE(al16(x) && al16(r) && al16(bias) && al16(wb), "layernorm: operands must be 16-byte aligned");
+    GSVK_REQUIRE(al16(x) && al16(r) && al16(bias) && al16(wb) && al16(y), "layernorm: operands must be 16-byte aligned");
     if (rows == 0) return GSVK_OK;
     // 4 rows (waves) per workgroup from 512 rows on: 16384 one-wave workgroups (a 16 x 1024
     // prefill) launch slower than the rows take; below, one-wave workgroups spread the rows over
