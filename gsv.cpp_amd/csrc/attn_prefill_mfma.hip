@@ -6,8 +6,10 @@
 // keys [pad_b, max_len) when it is a text row (s < max_len, bidirectional over the text) and the
 // keys [pad_b, s] when it is a semantic row (causal); no valid key gives 0.
 //
-// Work: workgroup = (128 queries, head, sequence), 4 waves of 32 queries. Key tiles of 32 are
-// staged through LDS (double buffered) as fp16 pairs hi + lo (x = hi + lo to ~2^-22 relative),
+// Work: workgroup = (256 queries, head, sequence), 8 waves of 32 queries. Key tiles of 64 are
+// staged through LDS (double buffered; one fetch and barrier per 64 keys, the 8 waves sharing
+// it), each wave consuming a tile as two halves of 32 keys, as fp16 pairs hi + lo (x = hi + lo
+// to ~2^-22 relative),
 // and every product is formed as hi*lo + lo*hi + hi*hi in three v_mfma_f32_32x32x16_f16 with
 // fp32 accumulation, so the scores and the weighted sum carry about fp32 accuracy (the reference
 // computes in fp32; plain fp16 operands would cost ~1e-3 relative).
@@ -33,10 +35,10 @@ int launch_attn_prefill(const float * qkv, int B, int S, int max_len, const int3
 
 namespace {
 constexpr int PM_Q = 32;                 // queries per wave
-constexpr int PM_WAVES = 4;
-constexpr int PM_KT = 32;                // keys per tile
+constexpr int PM_WAVES = 8;
+constexpr int PM_KT = 64;                // keys per LDS tile (two halves of 32 for the MFMAs)
 constexpr int PM_KROW = 32 * 2 + 16;     // LDS bytes per key row of K (32 fp16, padded)
-constexpr int PM_VROW = PM_KT * 2 + 16;  // LDS bytes per dim row of V^T (32 keys fp16, padded)
+constexpr int PM_VROW = PM_KT * 2 + 16;  // LDS bytes per dim row of V^T (64 keys fp16, padded)
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
@@ -166,14 +168,17 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
         const bool more = k0 + PM_KT < ke_g;   // uniform over the workgroup
         PmRegs nxt{};
         if (more) nxt = pm_fetch(base, rs, d_model, h, S, k0 + PM_KT, tid);
-        if (k0 < ke_w) {   // uniform per wave
-            const PmTile & t = tiles[buf];
+        const PmTile & t = tiles[buf];
+#pragma unroll
+        for (int hf = 0; hf < PM_KT / 32; hf++) {
+            const int kk = k0 + 32 * hf;   // the half's first key
+            if (kk >= ke_w) break;         // uniform per wave
             // S^T = K . Q^T over the 32 dims (2 chunks of 16)
             v16f sc = {};
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                const v8h kh = *reinterpret_cast<const v8h *>(&t.khi[li * PM_KROW + (16 * c + 8 * lh) * 2]);
-                const v8h kl = *reinterpret_cast<const v8h *>(&t.klo[li * PM_KROW + (16 * c + 8 * lh) * 2]);
+                const v8h kh = *reinterpret_cast<const v8h *>(&t.khi[(32 * hf + li) * PM_KROW + (16 * c + 8 * lh) * 2]);
+                const v8h kl = *reinterpret_cast<const v8h *>(&t.klo[(32 * hf + li) * PM_KROW + (16 * c + 8 * lh) * 2]);
                 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, ql[c], sc, 0, 0, 0);
                 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kl, qh[c], sc, 0, 0, 0);
                 sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(kh, qh[c], sc, 0, 0, 0);
@@ -181,7 +186,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
             // Softmax step in log2 units. A tile that every query of the wave sees whole (the
             // usual case: all but the last tile or two of a row) skips the masks; otherwise
             // invisible keys get -inf.
-            const bool full = k0 + PM_KT <= ke_min_w;   // uniform per wave (tiles start at pb)
+            const bool full = kk + 32 <= ke_min_w;   // uniform per wave (tiles start at pb)
             float p[16];
             float f, psum = 0.0f;
             if (full) {
@@ -201,7 +206,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
                 float rmax = -INFINITY;
 #pragma unroll
                 for (int v = 0; v < 16; v++) {
-                    const int key = k0 + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    const int key = kk + 8 * (v >> 2) + 4 * lh + (v & 3);
                     if (!(key >= pb && key < ke)) sc[v] = -INFINITY;
                     rmax = fmaxf(rmax, sc[v]);
                 }
@@ -235,7 +240,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
                     pl[i] = lo[0]; pl[i + 1] = lo[1];
                 }
                 // V^T rows: dim li, keys 16c + 4*lh + [0,4) and 16c + 8 + 4*lh + [0,4)
-                const int kA = 16 * c + 4 * lh, kB = 16 * c + 8 + 4 * lh;
+                const int kA = 32 * hf + 16 * c + 4 * lh, kB = 32 * hf + 16 * c + 8 + 4 * lh;
                 const v4h a0 = *reinterpret_cast<const v4h *>(&t.vhi[li * PM_VROW + kA * 2]);
                 const v4h a1 = *reinterpret_cast<const v4h *>(&t.vhi[li * PM_VROW + kB * 2]);
                 const v4h b0 = *reinterpret_cast<const v4h *>(&t.vlo[li * PM_VROW + kA * 2]);
