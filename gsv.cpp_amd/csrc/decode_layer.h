@@ -10,6 +10,17 @@ namespace gsvk {
 // hidden units of one sequence and their share of FFN2, written as one partial row of 512.
 constexpr int DEC_FFN_GROUPS = 16;
 
+// Largest batch the two-launch layer takes (its grids are 16 x B workgroups; nothing else in it
+// depends on the batch).
+constexpr int DEC_MAX_BATCH = 64;
+
+// Largest batch the library's default choice runs on the two-launch layer; above, the matrix-core
+// GEMMs are faster. Whole step, 24 layers, the batch-16 request shape, two-launch against
+// matrix-core: batch 24 0.68 / 0.82 ms, batch 32 0.71 / 0.84, batch 36 0.93 / 0.90, batch 48
+// 0.97 / 0.91, batch 64 1.24 / 0.95. (16 x 32 workgroups are two per CU; from batch 33 a launch
+// takes a third round.)
+constexpr int DEC_AUTO_MAX_BATCH = 32;
+
 // Launch 1 of a layer, workgroup (head h, sequence b):
 //   input row  x = LN2((res + parts[0] + ... + parts[NP-1]) + bias) (the previous layer's LN1
 //              output, FFN2 partials and b_2), or emb[tok] + alpha * PE[pos] for layer 0;

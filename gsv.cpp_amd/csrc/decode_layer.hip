@@ -1,4 +1,5 @@
-// Decode step at small batch (up to 16 sequences) in two launches per decoder layer, for gfx950.
+// Decode step at small batch (up to DEC_MAX_BATCH = 64 sequences) in two launches per decoder layer,
+// for gfx950.
 //
 // The decoder layer of src/gsv_ar.cpp:392-413 (QKV, K/V append, flash_attn_ext, out projection,
 // LN1, FFN1 + ReLU, FFN2, LN2) has three all-to-all dependencies inside a sequence's row: the out
@@ -442,12 +443,12 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
 }
 
 bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys) {
-    return B >= 1 && B <= 16 && nh == DL_NH && d_model == DL_K && ffn == DL_FFN &&
+    return B >= 1 && B <= DEC_MAX_BATCH && nh == DL_NH && d_model == DL_K && ffn == DL_FFN &&
            attn_nsplit(B, nh, max_keys) == 1;
 }
 
 int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream) {
-    GSVK_REQUIRE(a.B >= 1 && a.B <= 16, "dec_attn: batch %d out of range (1..16)", a.B);
+    GSVK_REQUIRE(a.B >= 1 && a.B <= DEC_MAX_BATCH, "dec_attn: batch %d out of range (1..%d)", a.B, DEC_MAX_BATCH);
     GSVK_REQUIRE(a.wq && a.wd && a.bqkv && a.kc && a.vc && a.kv_begin && a.col_ptr && a.woq && a.wod && a.p1,
                  "dec_attn: null pointer");
     GSVK_REQUIRE(a.lstride > 0, "dec_attn: bad cache stride");
@@ -464,7 +465,7 @@ int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream) {
 }
 
 int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream) {
-    GSVK_REQUIRE(a.B >= 1 && a.B <= 16, "dec_ffn: batch %d out of range (1..16)", a.B);
+    GSVK_REQUIRE(a.B >= 1 && a.B <= DEC_MAX_BATCH, "dec_ffn: batch %d out of range (1..%d)", a.B, DEC_MAX_BATCH);
     GSVK_REQUIRE(a.res && a.p1 && a.bo && a.wb1 && a.n1_out && a.w1q && a.w1d && a.b1 && a.w2q && a.w2d && a.p2,
                  "dec_ffn: null pointer");
     hipLaunchKernelGGL(k_dec_ffn<DEC_FFN_GROUPS>, dim3(DEC_FFN_GROUPS, (unsigned) a.B), dim3(DL_THREADS), 0,

@@ -741,7 +741,7 @@ int enqueue_decode_body(gsvk_model * m) {
     case GSVK_DECODE_MFMA:
         return enqueue_decode_mfma(m);
     default:
-        if (m->B < DECODE_GEMM_MIN_BATCH && fused_decode_ok(m)) return enqueue_decode_fused(m);
+        if (m->B <= DEC_AUTO_MAX_BATCH && fused_decode_ok(m)) return enqueue_decode_fused(m);
         break;
     }
     if (m->B >= DECODE_GEMM_MIN_BATCH) return enqueue_decode_mfma(m);

@@ -143,11 +143,11 @@ int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_s
 int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out);
 
 /* Which kernels run a decode step (the arithmetic of src/gsv_ar.cpp:380-467 in every case):
- *  GSVK_DECODE_AUTO  the library's choice (default): up to 16 sequences the two-launch layer,
- *                    from 17 the matrix-core GEMMs;
+ *  GSVK_DECODE_AUTO  the library's choice (default): up to 32 sequences the two-launch layer,
+ *                    from 33 the matrix-core GEMMs (the faster of the two at each batch);
  *  GSVK_DECODE_GEMV  up to 16 sequences the GEMV chain whose projections and LayerNorms are
  *                    bit-exact with ggml-cpu's x86 order (4 launches per layer);
- *  GSVK_DECODE_FUSED up to 16 sequences two launches per layer (attention + out-projection
+ *  GSVK_DECODE_FUSED up to 64 sequences two launches per layer (attention + out-projection
  *                    partial rows per head; LN1 + FFN1 + FFN2 partial rows per group of hidden
  *                    units): the same int32 block dots, fp32 sums over heads and groups in a fixed
  *                    order (agrees with the GEMV chain to fp32 rounding);
@@ -375,7 +375,7 @@ int gsvk_op_attn_exact(const float * q, const uint16_t * k, const uint16_t * v, 
  * exponential of gsvk_op_attn_exact; replaces the libm call inside ggml's softmax). */
 int gsvk_op_expf_exact(const float * x, int64_t n, float * y, void * stream);
 
-/* The decode layer of up to 16 sequences in two launches (GSVK_DECODE_FUSED; d_model 512, 16
+/* The decode layer of up to 64 sequences in two launches (GSVK_DECODE_FUSED; d_model 512, 16
  * heads of 32, FFN 2048). Launch 1, per (head, sequence): the input row x = LayerNorm((res +
  * parts[0] + ... + parts[15]) + ln_bias) with ln_wb = [w; b] (parts [16][B][512]: the previous
  * layer's FFN2 partial rows), or, when res is NULL, emb[tok[b]] + alpha * pe[*pos + pos_add]

@@ -64,6 +64,58 @@ def test_fused_layer_matches_gemv_chain(gpu, model4_path, B):
     assert np.array_equal(ka, kb) and np.array_equal(va, vb)
 
 
+@pytest.mark.parametrize("B", [17, 32, 64])
+def test_fused_layer_matches_mfma_path(gpu, model4_path, B):
+    """Above 16 sequences (where the GEMV chain does not run) the two-launch layer against the
+    matrix-core path: logits of every step equal to fp32 rounding at the median, within 1e-2 of
+    the row's scale at the worst step (re-quantisation flips, as against the GEMV chain); the
+    prefill is the same kernels."""
+    rng = np.random.default_rng(80 + B)
+    reqs = _reqs(81 + B, rng.integers(3, 40, B), 16)
+    steps = 10
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    g = gpu.Model(model4_path)
+    try:
+        print(f"fused vs matrix-core path, batch {B}", flush=True)
+        a = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_MFMA)
+        b = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_FUSED)
+    finally:
+        g.close()
+    assert np.array_equal(a[0], b[0])
+    rel = np.abs(a - b).max(axis=2) / np.abs(a).max(axis=2)
+    assert np.median(rel[1:]) <= 1e-5, np.median(rel[1:])
+    assert rel.max() <= 1e-2, rel.max()
+
+
+@pytest.mark.parametrize("B", [32, 64])
+def test_fused_decode_kv_matches_oracle_large_batch(gpu, model4_path, B):
+    """The two-launch layer at 32 and 64 sequences: the layer-0 K/V rows of every decode step are
+    the oracle's cache bit for bit (the embedding at PE position P + idx and its QKV in the x86
+    order), as at batch 16."""
+    rng = np.random.default_rng(90 + B)
+    reqs = _reqs(91 + B, rng.integers(3, 24, B), 16)
+    steps = 6
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    g = gpu.Model(model4_path)
+    o = O.Model(model4_path)
+    try:
+        print(f"fused decode K/V, batch {B}", flush=True)
+        g.set_decode_path(gpu.GSVK_DECODE_FUSED)
+        g.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced, flags=1)
+        k0, v0 = g.kv_read(0)
+        ref = o.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, kv_layer=0)
+    finally:
+        g.close()
+        o.close()
+    rk, rv = ref["kv"]
+    S = max(len(r["phones"]) for r in reqs) + 16
+    sl = slice(S, S + steps)
+    for b in range(B):
+        assert np.array_equal(k0[b, :, sl].view(np.float16).astype(np.float32), rk[b, :, sl]), b
+        assert np.array_equal(v0[b, :, sl].view(np.float16).astype(np.float32), rv[b, :, sl]), b
+
+
 @pytest.mark.parametrize("path", ["GEMV", "FUSED"])
 def test_decode_kv_cache_matches_oracle(gpu, model4_path, path):
     """The K/V rows every decode step appends (layer 0: the embedding at PE position P + idx, its
