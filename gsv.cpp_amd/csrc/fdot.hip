@@ -285,75 +285,7 @@ __global__ void __launch_bounds__(256) k_fdot_tinyblas(const WT * __restrict__ W
         if (m0 + t < m) Y[(int64_t) (m0 + t) * ys + row] = acc[t];
 }
 
-// MODE 2 — fp32 on the matrix cores (v_mfma_f32_32x32x2_f32), for the prefill's BERT projection
-// outside the exact mode: Y[m][n] = sum_k X[m][k] W[n][k] with fp32 products and accumulation in
-// the matrix cores' order (not ggml's; the results agree with it to fp32 rounding).
-// Workgroup 4 waves, tile 64 rows x 64 columns, wave (wr, wc) one 32 x 32 tile. For a K chunk of
-// 32, lane (i, g) holds row i's and column i's values [16 g, 16 g + 16) of the chunk (four 16-byte
-// loads each); MFMA step j multiplies element j of both, so the two lane halves sum k = j and
-// k = 16 + j: A and B use the same K order, which is all the product needs. Operands stream from
-// global memory (L1/L2) into registers two chunks ahead. Needs k % 32 == 0, n % 64 == 0 and
-// 16-byte aligned rows.
-namespace {
-constexpr int FG_WAVES = 4;
-typedef float v16f_fg __attribute__((ext_vector_type(16)));
-
-struct FgOps {
-    float4 x[4], w[4];
-};
-
-__device__ __forceinline__ void fg_load(FgOps & o, const float * __restrict__ xr, const float * __restrict__ wr, int k0) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        o.x[j] = *reinterpret_cast<const float4 *>(xr + k0 + 4 * j);
-        o.w[j] = *reinterpret_cast<const float4 *>(wr + k0 + 4 * j);
-    }
-}
-
-__device__ __forceinline__ v16f_fg fg_step(const FgOps & o, v16f_fg acc) {
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.x[j].x, o.w[j].x, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.x[j].y, o.w[j].y, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.x[j].z, o.w[j].z, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(o.x[j].w, o.w[j].w, acc, 0, 0, 0);
-    }
-    return acc;
-}
-}  // namespace
-
-__global__ void __launch_bounds__(FG_WAVES * 64) k_fgemm_mfma(const float * __restrict__ W, int n, int k,
-                                                             const float * __restrict__ X, int64_t xs, int m,
-                                                             float * __restrict__ Y, int64_t ys) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int li = lane & 31, lg = lane >> 5;
-    const int r0 = blockIdx.y * 64 + 32 * (wave >> 1);
-    const int c0 = blockIdx.x * 64 + 32 * (wave & 1);
-    const float * xr = X + (int64_t) min(r0 + li, m - 1) * xs + 16 * lg;
-    const float * wr = W + (int64_t) (c0 + li) * k + 16 * lg;
-    const int nch = k / 32;
-    v16f_fg acc = {};
-    FgOps a, b;
-    fg_load(a, xr, wr, 0);
-    if (nch > 1) fg_load(b, xr, wr, 32);
-    for (int c = 0; c < nch; c += 2) {
-        acc = fg_step(a, acc);
-        if (c + 2 < nch) fg_load(a, xr, wr, 32 * (c + 2));
-        if (c + 1 < nch) {
-            acc = fg_step(b, acc);
-            if (c + 3 < nch) fg_load(b, xr, wr, 32 * (c + 3));
-        }
-    }
-    // lane (i, g) holds rows 8 (v / 4) + 4 g + v % 4 of column i
-#pragma unroll
-    for (int v = 0; v < 16; v++) {
-        const int row = r0 + 8 * (v >> 2) + 4 * lg + (v & 3);
-        if (row < m) Y[(int64_t) row * ys + c0 + li] = acc[v];
-    }
-}
-
-// wtype: 0 = F32, 1 = F16. mode: 0 = ggml vec_dot, 1 = tinyBLAS (falls back to 0 if k % 8),
-// 2 = fp32 matrix cores (F32 only; k % 32 == 0, n % 64 == 0).
+// wtype: 0 = F32, 1 = F16. mode: 0 = ggml vec_dot, 1 = tinyBLAS (falls back to 0 if k % 8).
 int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
                 int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream) {
     GSVK_REQUIRE(W && X && Y && (wtype == 0 || wtype == 1), "fdot: bad arguments");
@@ -362,17 +294,6 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
                  "fdot: bad shape n=%lld k=%lld m=%lld", (long long) n, (long long) k,
                  (long long) m);
     constexpr int MT = 4;
-    if (mode == 2) {
-        GSVK_REQUIRE(wtype == 0 && k % 32 == 0 && n % 64 == 0 && xs % 4 == 0 && ((uintptr_t) X & 15) == 0 &&
-                         ((uintptr_t) W & 15) == 0,
-                     "fdot: the matrix-core mode needs F32 weights, k %% 32 == 0, n %% 64 == 0 and 16-byte "
-                     "aligned rows (n=%lld k=%lld)", (long long) n, (long long) k);
-        const dim3 grid((unsigned) (n / 64), (unsigned) ((m + 63) / 64));
-        hipLaunchKernelGGL(k_fgemm_mfma, grid, dim3(FG_WAVES * 64), 0, stream, (const float *) W, (int) n,
-                           (int) k, X, xs, (int) m, Y, ys);
-        GSVK_LAUNCH_CHECK();
-        return GSVK_OK;
-    }
     if (mode == 1 && k % 8 == 0) {
         const dim3 grid((unsigned) ((n + 31) / 32), (unsigned) ((m + MT - 1) / MT));
         if (wtype == 1)

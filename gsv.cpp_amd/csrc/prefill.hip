@@ -45,16 +45,14 @@ __global__ void __launch_bounds__(64) k_build_xy(const float * __restrict__ text
 __global__ void k_bert_feat(const float * __restrict__ bert, const int64_t * __restrict__ boff,
                             const int32_t * __restrict__ row_b, const int32_t * __restrict__ row_t,
                             const int32_t * __restrict__ tlen, int bert_dim, int R,
-                            float * __restrict__ feat, int stride) {
+                            float * __restrict__ feat) {
     const int r = blockIdx.x;
     if (r >= R) return;
     const int b = row_b[r], t = row_t[r], T = tlen[b];
     const float * src = boff[b] >= 0 ? bert + boff[b] : nullptr;
-    float * dst = feat + (int64_t) r * stride;
-    // (columns past bert_dim, up to the row stride, are zero: the matrix-core projection runs
-    // over a K padded to a multiple of 32 with zero weights there)
-    for (int k = threadIdx.x; k < stride; k += blockDim.x)
-        dst[k] = k == bert_dim ? 1.0f : (k < bert_dim && src ? src[(int64_t) k * T + t] : 0.0f);
+    float * dst = feat + (int64_t) r * (bert_dim + 1);
+    for (int k = threadIdx.x; k <= bert_dim; k += blockDim.x)
+        dst[k] = k == bert_dim ? 1.0f : (src ? src[(int64_t) k * T + t] : 0.0f);
 }
 
 // cur[b][pad_b + t] = xy + proj[r] (ggml_add(x, mul_mat(bert_aug, feat)), src/gsv_ar.cpp:241).
@@ -214,11 +212,10 @@ int launch_build_xy(const float * text_emb, const float * audio_emb, const float
 
 int launch_bert_feat(const float * bert, const int64_t * boff, const int32_t * row_b,
                      const int32_t * row_t, const int32_t * tlen, int bert_dim, int R, float * feat,
-                     int stride, hipStream_t stream) {
+                     hipStream_t stream) {
     if (R == 0) return GSVK_OK;
-    GSVK_REQUIRE(stride > bert_dim, "bert_feat: row stride %d too small", stride);
     hipLaunchKernelGGL(k_bert_feat, dim3((unsigned) R), dim3(256), 0, stream, bert, boff, row_b,
-                       row_t, tlen, bert_dim, R, feat, stride);
+                       row_t, tlen, bert_dim, R, feat);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

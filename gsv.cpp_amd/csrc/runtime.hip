@@ -32,7 +32,7 @@ int launch_build_xy(const float * text_emb, const float * audio_emb, const float
                     int S, int max_len, int d, float ta, float aa, float * xy, hipStream_t stream);
 int launch_bert_feat(const float * bert, const int64_t * boff, const int32_t * row_b,
                      const int32_t * row_t, const int32_t * tlen, int bert_dim, int R, float * feat,
-                     int stride, hipStream_t stream);
+                     hipStream_t stream);
 int launch_add_proj(float * xy, const float * proj, const float * bias, const int32_t * row_b,
                     const int32_t * row_t, const int32_t * pad, int S, int d, int R, int R1,
                     hipStream_t stream);
@@ -137,8 +137,6 @@ struct gsvk_model {
     Lin head_q8;                  // Q8_0 head
     float * text_emb = nullptr, * audio_emb = nullptr, * bert_aug = nullptr, * pe = nullptr;
     float * bert_b = nullptr;     // bias column of bert_aug, contiguous [D]
-    float * bert_aug_p = nullptr; // bert_aug with rows padded by zeros to bert_kp columns
-    int bert_kp = 0;              // BERT + 1 rounded up to a multiple of 32
     uint64_t * rng_jump = nullptr, * rng_adv = nullptr;
     int rng_chunk = 17;
     // KV cache
@@ -890,16 +888,10 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(launch_build_xy(m->text_emb, m->audio_emb, m->pe, d_phones, d_pad, d_prompt, B, S,
                              max_len, D, m->text_alpha, m->audio_alpha, cur.x, st));
     if (R1) {
-        // exact mode: ggml's F32 dot order; otherwise the fp32 matrix cores over K padded to a
-        // multiple of 32 (zero weights and features past the bias column)
-        const int KP = m->exact ? BD + 1 : m->bert_kp;
-        GSVK_TRY(tmp.alloc(feat, (size_t) R1 * KP));
+        GSVK_TRY(tmp.alloc(feat, (size_t) R1 * (BD + 1)));
         GSVK_TRY(tmp.alloc(proj, (size_t) R1 * D));
-        GSVK_TRY(launch_bert_feat(d_bert, d_boff, d_rowb, d_rowt, d_tlen, BD, R1, feat, KP, st));
-        if (m->exact)
-            GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R1, proj, D, 0, st));
-        else
-            GSVK_TRY(launch_fdot(m->bert_aug_p, 0, D, KP, feat, KP, R1, proj, D, 2, st));
+        GSVK_TRY(launch_bert_feat(d_bert, d_boff, d_rowb, d_rowt, d_tlen, BD, R1, feat, st));
+        GSVK_TRY(launch_fdot(m->bert_aug, 0, D, BD + 1, feat, BD + 1, R1, proj, D, 0, st));
     }
     if (R) GSVK_TRY(launch_add_proj(cur.x, proj, m->bert_b, d_rowb, d_rowt, d_pad, S, D, R, R1, st));
     // projections on the matrix-core GEMMs from GEMM_MIN_ROWS rows on, except in exact mode (the
@@ -1245,13 +1237,6 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
         }
         GSVK_TRY(m->wmem.alloc(m->bert_aug, aug.size()));
         GSVK_HIP(hipMemcpy(m->bert_aug, aug.data(), aug.size() * 4, hipMemcpyHostToDevice));
-        m->bert_kp = (m->BERT + 1 + 31) / 32 * 32;
-        std::vector<float> augp((size_t) m->D * m->bert_kp, 0.0f);
-        for (int d = 0; d < m->D; d++)
-            std::copy(aug.begin() + (size_t) d * (m->BERT + 1), aug.begin() + (size_t) (d + 1) * (m->BERT + 1),
-                      augp.begin() + (size_t) d * m->bert_kp);
-        GSVK_TRY(m->wmem.alloc(m->bert_aug_p, augp.size()));
-        GSVK_HIP(hipMemcpy(m->bert_aug_p, augp.data(), augp.size() * 4, hipMemcpyHostToDevice));
         GSVK_TRY(m->wmem.alloc(m->bert_b, bv.size()));
         GSVK_HIP(hipMemcpy(m->bert_b, bv.data(), bv.size() * 4, hipMemcpyHostToDevice));
     }

@@ -304,10 +304,7 @@ int gsvk_op_add_act(const float * a, const float * b, int64_t n, int64_t ne0, in
 
 /* Dot products of F16 (wtype 1) or F32 (wtype 0) weight rows W [n][k] with fp32 rows x [m][k]:
  * y[m][n], in ggml-cpu's x86 summation order (mode 0: ggml_vec_dot_f16/_f32, 4x8 lanes;
- * mode 1: tinyBLAS, 8 lanes, k % 8 == 0). F16 weights take fp16-rounded activations.
- * Mode 2: F32 only, on the fp32 matrix cores in their own summation order (agrees with mode 0
- * to fp32 rounding); k % 32 == 0, n % 64 == 0, 16-byte aligned w and x. The BERT projection of
- * src/gsv_ar.cpp:241 runs on it outside the exact mode. */
+ * mode 1: tinyBLAS, 8 lanes, k % 8 == 0). F16 weights take fp16-rounded activations. */
 int gsvk_op_fdot(const void * w, int wtype, int64_t n, int64_t k, const float * x, int64_t m,
                  float * y, int mode, void * stream);
 

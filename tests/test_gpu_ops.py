@@ -252,31 +252,6 @@ def test_fdot_bert_projection_bitexact(gpu, m):
     assert np.array_equal(y.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("m", [1, 63, 64, 333, 4100])
-def test_fdot_matrix_cores(gpu, m):
-    """Mode 2 (fp32 matrix cores, the BERT projection outside the exact mode): K = 1056 (bert_aug
-    padded with zero columns), rows past m untouched; within 2e-6 of the output scale of the
-    fp64 product and close to ggml's order (mode 0 on the unpadded K = 1025)."""
-    import torch
-    rng = np.random.default_rng(30 + m)
-    W = np.zeros((512, 1056), np.float32)
-    W[:, :1025] = rng.standard_normal((512, 1025)).astype(np.float32) * 0.02
-    X = np.zeros((m, 1056), np.float32)
-    X[:, :1024] = rng.uniform(-1, 1, (m, 1024)).astype(np.float32)
-    X[:, 1024] = 1.0
-    y = torch.full((m + 1, 512), 9.0, dtype=torch.float32, device="cuda")
-    gpu.op_fdot(_dev(W, torch), 0, _dev(X, torch), y[:m], 2)
-    torch.cuda.synchronize()
-    got = y.cpu().numpy()
-    assert (got[m] == 9.0).all()
-    got = got[:m]
-    ref = X.astype(np.float64) @ W.astype(np.float64).T
-    scale = np.abs(ref).max()
-    assert np.abs(got - ref).max() <= 2e-6 * scale, np.abs(got - ref).max() / scale
-    ggml = O.f32_matmul(np.ascontiguousarray(W[:, :1025]), np.ascontiguousarray(X[:, :1025]), 0)
-    assert np.abs(got - ggml).max() <= 2e-6 * scale
-
-
 def _attn_case(rng, B, nh, lstride, begins, ends):
     q = rng.standard_normal((B, nh, 32)).astype(np.float32)
     k = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16).view(np.uint16)
