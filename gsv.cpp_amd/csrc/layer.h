@@ -87,15 +87,14 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
 // Row count from which the prefill projections run on launch_q8_gemm rather than the GEMV.
 constexpr int64_t GEMM_MIN_ROWS = 64;
 
-// Batch from which the decode step runs its projections on launch_q8_gemm (with the LayerNorms
-// and the embedding as launches of their own) rather than on the fused GEMVs, whose weight
-// re-reads grow with the batch. The GEMVs are faster up to batch 64 but run only up to batch 16,
-// where they are tested: one batch-32 run of the GEMV path ended in a GPU memory fault whose
-// cause has not been found.
-#ifndef GSVK_DECODE_GEMM_MIN_BATCH
-#define GSVK_DECODE_GEMM_MIN_BATCH 17
-#endif
-constexpr int DECODE_GEMM_MIN_BATCH = GSVK_DECODE_GEMM_MIN_BATCH;
+// The decode's GEMV chain (the fused QKV + attention and the layer GEMVs, one activation row per
+// sequence) runs up to 16 sequences: one batch-32 decode run of it ended in a GPU memory fault
+// whose cause has not been found, so the decode refuses it above (a constant, not a build
+// option; the kernels themselves are tested at up to 64 rows one launch at a time). From
+// DECODE_GEMM_MIN_BATCH the matrix-core path takes the projections when the two-launch layer
+// does not run.
+constexpr int GEMV_DECODE_MAX_BATCH = 16;
+constexpr int DECODE_GEMM_MIN_BATCH = GEMV_DECODE_MAX_BATCH + 1;
 
 // Prefill self-attention on the matrix cores (attn_prefill_mfma.hip): qkv rows [B][S][3*d_model],
 // head_dim 32, 16-byte aligned qkv and out; used from GEMM_MIN_ROWS rows on, like the GEMM.

@@ -568,8 +568,9 @@ int enqueue_decode_mfma(gsvk_model * m) {
 // was measured slower, 0.57 -> 0.78 / 1.41 ms per step: the graph ran every branch on one
 // hardware queue, one after the other.)
 int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
-    // the GEMV chain runs (and is tested) up to DECODE_GEMM_MIN_BATCH - 1 rows only
-    GSVK_REQUIRE(n >= 1 && n < DECODE_GEMM_MIN_BATCH, "decode: %d rows on the GEMV path", n);
+    // the GEMV chain decodes (and is tested at) up to GEMV_DECODE_MAX_BATCH rows only
+    GSVK_REQUIRE(n >= 1 && n <= GEMV_DECODE_MAX_BATCH, "decode: %d rows on the GEMV path (at most %d)", n,
+                 GEMV_DECODE_MAX_BATCH);
     const int B = m->B, D = m->D, F = m->FFN;
     const float scale = 1.0f / std::sqrt((float) m->HD);
     const size_t row_kv = (size_t) m->NH * m->lstride * m->HD;
