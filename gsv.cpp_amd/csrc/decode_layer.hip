@@ -169,8 +169,14 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     __shared__ __align__(16) int8_t s_a[DL_WAVES][ATT_HD];
 
     // ---- loads, in the order their data is needed, with no branch between them ----
-    const int col = *a.col_ptr + a.col_add;   // column of this step's key
-    int beg = a.kv_begin[b];
+    // The key range first, as vector loads (an index the compiler cannot see to be zero): a
+    // scalar load's value would be consumed right after it (the compiler places its wait there),
+    // holding back every load below; a vector load's wait is placed at its first use, after the
+    // scheduling barrier below.
+    int vz;
+    asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
+    const int col_ld = a.col_ptr[vz];
+    const int beg_ld = a.kv_begin[b + vz];
     float xr = 0.0f, xb = 0.0f, xw = 0.0f, xc = 0.0f, xe = 0.0f, xpe = 0.0f;
     float xp[NP];
     int pos = 0;
@@ -216,6 +222,10 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
         wo[u] = *reinterpret_cast<const int4 *>(a.woq + (((int64_t) t * DL_NBLK + h) << 10) + lane * 16);
         wos[u] = a.wod[(((int64_t) t * DL_NBLK + h) << 5) + (lane & 31)];
     }
+    // (the key range arrived first: its loads were issued first and retire in order)
+    __builtin_amdgcn_sched_barrier(0);
+    const int col = __builtin_amdgcn_readfirstlane(col_ld) + a.col_add;   // column of this step's key
+    int beg = __builtin_amdgcn_readfirstlane(beg_ld);
     // the first block of cached keys [beg, col) (the new key is substituted later); a wave past
     // the last block loads that block again and does not use it
     const bool col_ok = col >= 0 && col < a.lstride;

@@ -120,8 +120,30 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
     __shared__ float s_bestv[1];
     __shared__ int s_besti[1];
 
-    // every load that does not depend on another is issued here, before the first use: the
-    // loop index, this row's state, its logits, the jump matrices and the advance columns
+    // Every load is issued here, before the first use, those whose addresses depend on no loaded
+    // value first: the logits and the first 4096 history entries (the penalty window whenever the
+    // row holds at most 4096 tokens). The scheduling barrier keeps them ahead of the scalar loads
+    // of the row's state, whose values the compiler would otherwise wait for right away.
+    constexpr int LV = SMP_SORT / SMP_THREADS;
+    float lv[LV];
+#pragma unroll
+    for (int r = 0; r < LV; r++) {
+        const int v = tid + r * SMP_THREADS;
+        lv[r] = v < V ? a.logits[(int64_t) b * V + v] : 0.0f;
+    }
+    constexpr int HW = 4096 / SMP_THREADS;   // the window: the last <= 4096 tokens, 16 per thread
+    const int hspec_n = (a.rep != 1.0f && a.ny) ? (a.hist_stride < 4096 ? a.hist_stride : 4096) : 0;
+    int htok[HW];
+    {
+        const int32_t * h = a.hist + (int64_t) b * a.hist_stride;
+#pragma unroll
+        for (int r = 0; r < HW; r++) {
+            const int i = tid + r * SMP_THREADS;
+            htok[r] = i < hspec_n ? h[i] : -1;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the loop index, this row's state, the jump matrices and the advance columns
     const int gidx = a.step ? *a.step : 11;   // no loop state: past the EOS-mask window
     const int idx = gidx - (a.row_start ? a.row_start[b] : 0);   // this row's own step
     const int rmax = a.row_max ? a.row_max[b] : a.max_steps;
@@ -137,21 +159,23 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
             s_next ^= a.adv[p * 256 + byte];
         }
     }
-    // the repetition-penalty window: the last <= 4096 tokens, at most 16 per thread
-    constexpr int HW = 4096 / SMP_THREADS;
     const int np = a.rep != 1.0f ? (n_hist < 4096 ? n_hist : 4096) : 0;
-    int htok[HW];
-    {
+    if (n_hist > 4096 && np > 0) {   // a longer row: its window starts at n_hist - 4096 (uniform)
         const int32_t * h = a.hist + (int64_t) b * a.hist_stride + (n_hist - np);
 #pragma unroll
-        for (int r = 0; r < HW; r++) {
-            const int i = tid + r * SMP_THREADS;
-            htok[r] = i < np ? h[i] : -1;
-        }
+        for (int r = 0; r < HW; r++) htok[r] = h[tid + r * SMP_THREADS];
+    } else {
+#pragma unroll
+        for (int r = 0; r < HW; r++)
+            if (tid + r * SMP_THREADS >= np) htok[r] = -1;
     }
-    for (int v = tid; v < V; v += SMP_THREADS) {
-        lg[v] = a.logits[(int64_t) b * V + v];
-        cnt[v] = 0;
+#pragma unroll
+    for (int r = 0; r < LV; r++) {
+        const int v = tid + r * SMP_THREADS;
+        if (v < V) {
+            lg[v] = lv[r];
+            cnt[v] = 0;
+        }
     }
     asm volatile("" ::"v"(st0), "v"(s_next));   // the table loads complete here, not at first use
     __syncthreads();
