@@ -293,20 +293,32 @@ def cpu_baseline(reqs, steps, min_s=10.0):
 
 def prefill_line(g, torch):
     """Prefill of batch 16 x 1024 rows (valid lengths U[512, 1024], 256 prompt codes), 24 layers:
-    median wall time of 3 calls after one warm-up, and TFLOP/s over prefill_flops."""
+    median wall time of 3 calls after one warm-up, and TFLOP/s over prefill_flops; the same in the
+    fp16 mode (projections on fp16 operands, gsvk_model_set_prefill_f16; its weight copies are made
+    in the warm-up call)."""
     pr = prefill_requests()
-    g.first_logits(pr)
-    torch.cuda.synchronize()
-    t = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        g.first_logits(pr)
-        t.append(time.perf_counter() - t0)
-    pf_s = float(np.median(t))
     fl = prefill_flops(pr)
+
+    def timed():
+        g.first_logits(pr)
+        torch.cuda.synchronize()
+        t = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            g.first_logits(pr)
+            t.append(time.perf_counter() - t0)
+        return float(np.median(t))
+
+    pf_s = timed()
+    g.set_prefill_f16(True)
+    try:
+        f16_s = timed()
+    finally:
+        g.set_prefill_f16(False)
     return {"ms": round(pf_s * 1e3, 2), "tflops": round(fl / pf_s / 1e12, 1),
             "frac_fp16_peak": round(fl / pf_s / 1e12 / MFMA_F16_PEAK_TFLOPS, 4),
             "algorithmic_tflop": round(fl / 1e12, 3),
+            "fp16_mode_ms": round(f16_s * 1e3, 2), "fp16_mode_tflops": round(fl / f16_s / 1e12, 1),
             "workload": "16 x 1024 rows, valid U[512,1024], 256 prompt codes, wall time of the whole "
                         "prefill call incl. head logits"}
 

@@ -84,6 +84,17 @@ int launch_q8_gemm(const Q8Weights & w, int64_t n, int64_t k, int64_t m, const i
                    const float * xd, int x_layout, const LayerOut & out, hipStream_t stream,
                    int tile_rows = 0);
 
+// w16[n][k] = fp16(d * q) (nearest even) of a natural-order Q8_0 matrix (gemm.hip).
+int launch_q8_dequant_f16(const int8_t * q, const uint16_t * d, int64_t n, int64_t k, uint16_t * w16,
+                          hipStream_t stream);
+
+// The same projection on the fp16 matrix cores (gemm.hip): the Q8_0 activations (natural order)
+// taken as fp16(d * q) times the fp16 weights w16 [n][k] of launch_q8_dequant_f16, fp32
+// accumulation, the epilogue of launch_q8_gemm's 128 x 128 kernel (natural-order Q8_0 output);
+// n % 128 == 0, k 512 or 2048.
+int launch_q8h_gemm(const uint16_t * w16, int64_t n, int64_t k, int64_t m, const int8_t * xs, const float * xd,
+                    const LayerOut & out, hipStream_t stream);
+
 // Row count from which the prefill projections run on launch_q8_gemm rather than the GEMV.
 constexpr int64_t GEMM_MIN_ROWS = 64;
 

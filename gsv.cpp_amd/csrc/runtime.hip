@@ -101,6 +101,7 @@ struct Lin {
     uint16_t * d = nullptr;
     int8_t * qt = nullptr;    // quants and scales in the matrix-core operand order (GEMM, small
     uint16_t * dt = nullptr;  // batch); rows % 32 == 0 only
+    uint16_t * w16 = nullptr; // fp16(d * q) [n][k]: the prefill's fp16 mode (made at its first use)
     float * b = nullptr;
     int n = 0, k = 0;
 };
@@ -156,6 +157,8 @@ struct gsvk_model {
     float * p1 = nullptr, * p2 = nullptr;   // partial rows of the two-launch decode layer
     int decode_path = GSVK_DECODE_AUTO;
     bool exact = false;   // gsvk_model_set_exact: ggml-cpu's arithmetic order throughout
+    bool prefill_f16 = false;   // gsvk_model_set_prefill_f16: prefill projections on fp16 matrix cores
+    DevArena w16mem;            // the fp16 weight copies of that mode
     void * attn_ws = nullptr;
     int32_t * kv_begin = nullptr, * kv_end = nullptr;
     int32_t * d_step = nullptr, * hist = nullptr, * ny = nullptr, * fin_step = nullptr,
@@ -420,9 +423,31 @@ int head_logits(gsvk_model * m, const Act & x, int B, int mode, float * out, hip
 // LN2 (cur' = LN2(n1 + h2 + b2)) is the input stage of the next layer's QKV or of final_ln().
 Q8Weights q8w(const Lin & l) { return Q8Weights{l.qn, l.d, l.qt, l.dt}; }
 
+// The fp16 copies of the four projections of every layer (gsvk_model_set_prefill_f16), made once.
+int ensure_w16(gsvk_model * m) {
+    for (LayerW & w : m->L)
+        for (Lin * l : {&w.qkv, &w.out, &w.f1, &w.f2})
+            if (!l->w16) {
+                GSVK_TRY(m->w16mem.alloc(l->w16, (size_t) l->n * l->k));
+                GSVK_TRY(launch_q8_dequant_f16(l->qn, l->d, l->n, l->k, l->w16, m->stream));
+            }
+    return GSVK_OK;
+}
+
+// A projection of the prefill's rows on the matrix cores: the int8 GEMM, or in the fp16 mode the
+// fp16 GEMM on the dequantised weights (the shapes it takes: above 256 rows, n % 128 == 0, k 512
+// or 2048).
+int prefill_gemm(const gsvk_model * m, const Lin & l, int64_t rows, const int8_t * xs, const float * xd,
+                 const LayerOut & out, hipStream_t st) {
+    if (m->prefill_f16 && l.w16 && rows > 256 && l.n % 128 == 0 && (l.k == 512 || l.k == 2048))
+        return launch_q8h_gemm(l.w16, l.n, l.k, rows, xs, xd, out, st);
+    return launch_q8_gemm(q8w(l), l.n, l.k, rows, xs, xd, Q8_NATURAL, out, st);
+}
+
 int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, const float * cur_x, const Act & attn,
                float * o, float * n1x, Act & hq, float * h2, Act * n1 = nullptr,
-               int layout = Q8_NATURAL, const int32_t * row_pad = nullptr, int rows_per_seq = 0) {
+               int layout = Q8_NATURAL, const int32_t * row_pad = nullptr, int rows_per_seq = 0,
+               bool prefill = false) {
     const int D = m->D, F = m->FFN;
     if (n1) {
         // many rows (the caller's choice): the projections on the matrix cores, LN1 as its own
@@ -434,7 +459,13 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
         oo.n_store = D;
         oo.row_pad = row_pad;           // (prefill: tiles of left-padding rows are skipped)
         oo.rows_per_seq = rows_per_seq;
-        GSVK_TRY(launch_q8_gemm(q8w(w.out), D, D, R, attn.q, attn.d, layout, oo, st));
+        // (prefill: natural order; prefill_gemm picks the int8 or the fp16 GEMM)
+        auto gemm = [&](const Lin & l, int64_t n, int64_t k, const int8_t * xs, const float * xd,
+                        const LayerOut & out) {
+            return prefill ? prefill_gemm(m, l, R, xs, xd, out, st)
+                           : launch_q8_gemm(q8w(l), n, k, R, xs, xd, layout, out, st);
+        };
+        GSVK_TRY(gemm(w.out, D, D, attn.q, attn.d, oo));
         GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout));
         LayerOut ho{};
         ho.bias = w.f1.b;
@@ -444,14 +475,14 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
         ho.yq_layout = layout;
         ho.row_pad = row_pad;
         ho.rows_per_seq = rows_per_seq;
-        GSVK_TRY(launch_q8_gemm(q8w(w.f1), F, D, R, n1->q, n1->d, layout, ho, st));
+        GSVK_TRY(gemm(w.f1, F, D, n1->q, n1->d, ho));
         LayerOut h2o{};
         h2o.y = h2;
         h2o.y_stride = D;
         h2o.n_store = D;
         h2o.row_pad = row_pad;
         h2o.rows_per_seq = rows_per_seq;
-        return launch_q8_gemm(q8w(w.f2), D, F, R, hq.q, hq.d, layout, h2o, st);
+        return gemm(w.f2, D, F, hq.q, hq.d, h2o);
     }
     LayerIn qin{};
     qin.mode = IN_Q8;
@@ -898,6 +929,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     // projections on the matrix-core GEMMs from GEMM_MIN_ROWS rows on, except in exact mode (the
     // GEMV chain in ggml-cpu's order and the sequential attention at any row count)
     const bool gemm = !m->exact && rows >= GEMM_MIN_ROWS;
+    if (gemm && m->prefill_f16) GSVK_TRY(ensure_w16(m));
     // the layer-0 QKV reads this copy: natural order for the GEMM, sliced for the GEMV
     GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, gemm ? Q8_NATURAL : Q8_SLICED));
     int32_t * zero = nullptr;
@@ -916,7 +948,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             }
             LayerOut qo = qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0);
             qo.row_pad = d_pad;   // row tiles of left padding only: zeros, no K/V (never attended)
-            GSVK_TRY(launch_q8_gemm(q8w(w.qkv), 3 * D, D, rows, cur.q, cur.d, Q8_NATURAL, qo, st));
+            GSVK_TRY(prefill_gemm(m, w.qkv, rows, cur.q, cur.d, qo, st));
         } else {
             LayerIn in{};
             if (li == 0) {
@@ -945,7 +977,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
         GSVK_TRY(layer_tail(m, st, w, rows, cur.x, attn, o, n1.x, hq, h2, gemm ? &n1 : nullptr,
-                            Q8_NATURAL, d_pad, S));
+                            Q8_NATURAL, d_pad, S, true));
     }
     GSVK_TRY(final_ln(m, st, rows, n1.x, h2, cur));
     GSVK_TRY(launch_gather_last(cur.x, B, S, D, last, st));
@@ -1333,6 +1365,13 @@ extern "C" int gsvk_model_set_exact(gsvk_model * m, int on) {
     cb_drop(m);
     drop_graph(m);
     m->exact = on != 0;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_model_set_prefill_f16(gsvk_model * m, int on) {
+    GSVK_REQUIRE(m, "null model");
+    DeviceGuard guard(m->device);
+    m->prefill_f16 = on != 0;   // (the prefill builds no graph; the weight copies are made at its next call)
     return GSVK_OK;
 }
 

@@ -30,7 +30,8 @@ EXPORTS = [
     "gsvk_cb_open", "gsvk_cb_add", "gsvk_cb_step", "gsvk_cb_take", "gsvk_cb_close",
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
-    "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact",
+    "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact", "gsvk_model_set_prefill_f16",
+    "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
@@ -102,6 +103,7 @@ def lib():
         L.gsvk_release_cache.argtypes = [vp]
         L.gsvk_model_set_decode_path.argtypes = [vp, i32]
         L.gsvk_model_set_exact.argtypes = [vp, i32]
+        L.gsvk_model_set_prefill_f16.argtypes = [vp, i32]
         L.gsvk_op_attn_exact.argtypes = [vp, vp, vp, i32, i32, i64, vp, vp, f32, vp, vp, vp, vp]
         L.gsvk_op_expf_exact.argtypes = [vp, i64, vp, vp]
         L.gsvk_op_dec_attn.argtypes = [i32, vp, vp, vp, vp, vp, vp, vp, vp, i32, f32, i32, i32, vp, vp, vp, vp, vp,
@@ -136,6 +138,8 @@ def lib():
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
         L.gsvk_op_q8_gemm.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
         L.gsvk_op_q8_gemm_ex.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp, vp, i32, i32, vp]
+        L.gsvk_op_q8_dequant_f16.argtypes = [vp, vp, i64, i64, vp, vp]
+        L.gsvk_op_q8h_gemm.argtypes = [vp, i64, i64, vp, vp, i64, vp, i32, vp, vp, vp, vp]
         L.gsvk_op_attn_prefill.argtypes = [vp, i32, i32, i32, vp, i32, i32, f32, i32, vp, vp, vp, vp]
         L.gsvk_sample_workspace_bytes.argtypes = [i32]
         L.gsvk_sample_workspace_bytes.restype = C.c_size_t
@@ -205,6 +209,15 @@ def op_q8_gemm_ex(wq, wd, n, k, xq, xd, m, bias, act, y=None, yq=None, yd=None, 
                   stream=None):
     check(lib().gsvk_op_q8_gemm_ex(_p(wq), _p(wd), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y), _p(yq),
                                    _p(yd), tile_rows, 1 if tiled else 0, _stream(stream)), "q8_gemm_ex")
+
+
+def op_q8_dequant_f16(wq, wd, n, k, w16, stream=None):
+    check(lib().gsvk_op_q8_dequant_f16(_p(wq), _p(wd), n, k, _p(w16), _stream(stream)), "q8_dequant_f16")
+
+
+def op_q8h_gemm(w16, n, k, xq, xd, m, bias, act, y=None, yq=None, yd=None, stream=None):
+    check(lib().gsvk_op_q8h_gemm(_p(w16), n, k, _p(xq), _p(xd), m, _p(bias), act, _p(y), _p(yq), _p(yd),
+                                 _stream(stream)), "q8h_gemm")
 
 
 def op_ln_gemv(wq, wd, n, res, r, ln_bias, wb, bias, act, y, ln_out=None, stream=None):
@@ -401,6 +414,10 @@ class Model:
     def set_decode_path(self, path: int):
         """GSVK_DECODE_AUTO / _GEMV / _FUSED / _MFMA (include/gsvk.h)."""
         check(lib().gsvk_model_set_decode_path(self.h, path), "set_decode_path")
+
+    def set_prefill_f16(self, on: bool = True):
+        """Prefill projections on the fp16 matrix cores (include/gsvk.h gsvk_model_set_prefill_f16)."""
+        check(lib().gsvk_model_set_prefill_f16(self.h, 1 if on else 0), "set_prefill_f16")
 
     def set_exact(self, on: bool = True):
         """Exact mode (include/gsvk.h gsvk_model_set_exact): ggml-cpu's arithmetic order throughout."""

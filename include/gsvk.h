@@ -169,6 +169,17 @@ int gsvk_model_set_decode_path(gsvk_model * m, int path);
  * its exact tokens and for tests. */
 int gsvk_model_set_exact(gsvk_model * m, int on);
 
+/* Prefill on the fp16 matrix cores (on != 0): the projections of a prefill with enough rows for
+ * the matrix-core GEMMs multiply the Q8_0 activations, turned into fp16(d * q), by copies of the
+ * Q8_0 weights dequantised once to fp16 (fp16(d * q), made at the first such prefill and kept
+ * with the model, 2 bytes per weight) on v_mfma_f32_32x32x16_f16 instead of the int8 products
+ * and their per-block fp32 scaling. Both operands are rounded to fp16, so the projections are
+ * within about 6e-4 of their row's scale of ggml's (north_star's bar is 2e-3) instead of fp32
+ * rounding, and so are the K/V rows the prefill writes. No effect on the decode or in exact mode.
+ * Off by default; no counterpart in the reference (an option for callers that prefer a faster
+ * prefill to agreement within fp32 rounding). */
+int gsvk_model_set_prefill_f16(gsvk_model * m, int on);
+
 /* Free the resident KV cache: replaces gsv_ar::release_cache (:826). */
 int gsvk_release_cache(gsvk_model * m);
 
@@ -282,6 +293,21 @@ int gsvk_op_q8_gemm(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k
 int gsvk_op_q8_gemm_ex(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k,
                        const int8_t * xq, const float * xd, int64_t m, const float * bias, int act,
                        float * y, int8_t * yq, float * yd, int tile_rows, int tiled, void * stream);
+
+/* w16[n][k] = fp16(d * q) (nearest even) of a Q8_0 matrix in natural order (quants wq [n][k],
+ * fp16 scales wd [n][k/32]): the weights of the prefill's fp16 mode (gsvk_model_set_prefill_f16).
+ * wq and w16 16-byte aligned. */
+int gsvk_op_q8_dequant_f16(const int8_t * wq, const uint16_t * wd, int64_t n, int64_t k, uint16_t * w16,
+                           void * stream);
+
+/* The projection of the prefill's fp16 mode: y = act(X . W^T + bias) with X the Q8_0 activations
+ * (xq [m][k] natural order, fp32 scales xd [m][k/32] holding fp16 values) taken as fp16(d * q) and
+ * W the fp16 weights w16 [n][k] of gsvk_op_q8_dequant_f16, on the fp16 matrix cores with fp32
+ * accumulation; y and/or yq/yd (the Q8_0 quantisation of each 32-column block of the output) as
+ * in gsvk_op_q8_gemm_ex. n a multiple of 128, k 512 or 2048. Replaces the same mul_mat nodes as
+ * gsvk_op_q8_gemm (src/gsv_ar.cpp:245-260) within fp16 operand rounding. */
+int gsvk_op_q8h_gemm(const uint16_t * w16, int64_t n, int64_t k, const int8_t * xq, const float * xd,
+                     int64_t m, const float * bias, int act, float * y, int8_t * yq, float * yd, void * stream);
 
 /* y = W . Q8_0(LayerNorm((res + r) + ln_bias) * wb[0:512] + wb[512:1024]) (+ bias) then act:
  * the decoder's fused kernel with its LayerNorm input stage (rows of 512; n % 32 == 0). The

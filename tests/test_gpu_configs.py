@@ -80,6 +80,53 @@ def test_prefill_16x1024(gpu, model24_path):
     assert rel <= 2e-2, rel
 
 
+def test_prefill_16x1024_fp16_mode(gpu, model24_path):
+    """The prefill's fp16 mode (gsvk_model_set_prefill_f16: the projections on fp16 operands) at
+    the same shape: a sequence prefilled alone gives the logits it has in the batch, bit for bit;
+    its layer-0 K/V rows are within 2e-3 of each row's largest magnitude of the oracle's (the
+    projections' bar: fp16 operands plus the fp16 cache); its first logits agree with the oracle
+    as the default mode's do (2e-2 of their scale after 24 layers of Q8_0 requantisation), with the
+    same greedy token; switching the mode off gives the default mode's logits back."""
+    P = 256
+    L = _lengths(0x6A5E0004, 16, 512, 1024)
+    reqs = sm.synth_requests(0x6A5E0004, 16, P, L - P)
+    short = int(np.argmin(L))
+    g = gpu.Model(model24_path)
+    try:
+        default = g.first_logits([reqs[short]])
+        g.set_prefill_f16(True)
+        batch = g.first_logits(reqs)
+        assert np.all(np.isfinite(batch))
+        print(f"fp16 mode, prefill alone: sequence {short}, {L[short]} rows", flush=True)
+        alone = g.first_logits([reqs[short]])
+        assert np.array_equal(batch[short], alone[0])
+        _, S = g.prefill([reqs[short]])
+        k_dev, v_dev = g.kv_read(0)
+        g.set_prefill_f16(False)
+        back = g.first_logits([reqs[short]])
+    finally:
+        g.close()
+    assert np.array_equal(back, default)
+    o = O.Model(model24_path)
+    try:
+        ref = o.first_logits([reqs[short]])
+        k_ref, v_ref, _ = o.prefill_kv([reqs[short]], 0, flags=O.ORC_KV_F16)
+    finally:
+        o.close()
+    for dev, r in ((k_dev, k_ref), (v_dev, v_ref)):
+        d = dev[:, :, :S, :].view(np.float16).astype(np.float32)
+        # rows (sequence, column) over all heads and dims
+        dr = np.moveaxis(d, 2, 1).reshape(d.shape[0], S, -1)
+        rr = np.moveaxis(r, 2, 1).reshape(r.shape[0], S, -1)
+        row_scale = np.maximum(np.abs(rr).max(axis=2), 1e-6)
+        rel = (np.abs(dr - rr).max(axis=2) / row_scale).max()
+        print(f"fp16 mode: layer-0 K/V within {rel:.2e} of the row scale", flush=True)
+        assert rel <= 2e-3, rel
+    assert int(alone[0].argmax()) == int(ref[0].argmax())
+    rel = np.abs(alone[0] - ref[0]).max() / np.abs(ref[0]).max()
+    assert rel <= 2e-2, rel
+
+
 def test_decode_batch128_long_kv(gpu, model24_path):
     P, steps = 64, 6
     L = _lengths(0x6A5E0005, 128, 1024, 4096)

@@ -494,6 +494,58 @@ def test_q8_gemm_large_q8_out(gpu, n, k, m, with_y):
     assert np.array_equal(yd, d_ref.view(np.float16).astype(np.float32).reshape(m, n // 32))
 
 
+@pytest.mark.parametrize("n,k", [(1536, 512), (2048, 512), (512, 2048)])
+@pytest.mark.parametrize("m", [300, 1000])
+def test_q8h_gemm_fp16_mode(gpu, n, k, m):
+    """The projection of the prefill's fp16 mode: the weights dequantised to fp16(d * q) bit for
+    bit (numpy's float16 conversion rounds to nearest even); the GEMM is the fp32-accumulated
+    product of the activations fp16(dx * qx) and those weights (within 2e-5 of the row's scale of
+    a float64 product of the same fp16 operands), and within 2e-3 of the row's scale of ggml's
+    Q8_0 product (the oracle), with bias + ReLU; rows past m untouched; its Q8_0 output is the x86
+    quantisation of its own fp32 output."""
+    import torch
+    rng = np.random.default_rng(7300 + n + k + m)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.standard_normal((m, k)).astype(np.float32)
+    X[1, :] = 0.0
+    wb = sm.q8_quantize_ref(W).ravel()
+    wq_n, wd_n = blocks_to_split(wb, n, k)
+    xq_n, xd_n = blocks_to_split(O.q8_quantize_x86(X), m, k)
+    wq, wd = _dev(wq_n, torch), _dev(wd_n.view(np.int16), torch)
+    xq, xd = _dev(xq_n, torch), _dev(xd_n.view(np.float16).astype(np.float32), torch)
+    b = rng.standard_normal(n).astype(np.float32) * 0.02
+    bias = _dev(b, torch)
+    w16 = torch.zeros(n * k, dtype=torch.int16, device="cuda")
+    gpu.op_q8_dequant_f16(wq, wd, n, k, w16)
+
+    def deq(q, d, rows):
+        return (q.reshape(rows, k // 32, 32).astype(np.float32) *
+                d.view(np.float16).astype(np.float32).reshape(rows, k // 32, 1)).astype(np.float16).reshape(rows, k)
+
+    w16_ref = deq(wq_n, wd_n, n)
+    torch.cuda.synchronize()
+    assert np.array_equal(w16.cpu().numpy().reshape(n, k), w16_ref.view(np.int16))
+    y = torch.full((m + 1, n), 7.0, dtype=torch.float32, device="cuda")
+    yq = torch.full((m + 1, n), 5, dtype=torch.int8, device="cuda")
+    yd = torch.full((m + 1, n // 32), 3.0, dtype=torch.float32, device="cuda")
+    gpu.op_q8h_gemm(w16, n, k, xq, xd, m, bias, 1, y=y)
+    gpu.op_q8h_gemm(w16, n, k, xq, xd, m, bias, 1, yq=yq, yd=yd)
+    torch.cuda.synchronize()
+    y, yq, yd = y.cpu().numpy(), yq.cpu().numpy(), yd.cpu().numpy()
+    assert (y[m] == 7.0).all() and (yq[m] == 5).all() and (yd[m] == 3.0).all()
+    y, yq, yd = y[:m], yq[:m], yd[:m]
+    ref16 = np.maximum(deq(xq_n, xd_n, m).astype(np.float64) @ w16_ref.astype(np.float64).T + b[None, :], 0.0)
+    ref = np.maximum(O.q8_matmul(wb, n, k, X) + b[None, :], 0.0)
+    scale = np.maximum(np.abs(ref).max(axis=1), 1e-6)
+    err16 = (np.abs(y - ref16).max(axis=1) / scale).max()
+    err = (np.abs(y - ref).max(axis=1) / scale).max()
+    print(f"fp16 GEMM n={n} k={k} m={m}: vs the same fp16 operands {err16:.2e}, vs ggml's Q8_0 product {err:.2e}")
+    assert err16 <= 2e-5 and err <= 2e-3
+    q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(y), m, n)
+    assert np.array_equal(yq, q_ref.reshape(m, n))
+    assert np.array_equal(yd, d_ref.view(np.float16).astype(np.float32).reshape(m, n // 32))
+
+
 @pytest.mark.parametrize("n,k", [(1536, 512), (512, 2048), (2048, 512)])
 @pytest.mark.parametrize("m", [1, 64, 100, 128, 256])
 def test_q8_gemm_small_tiles(gpu, n, k, m):
