@@ -23,6 +23,10 @@
 //        read from LDS in the same key order, so the product sums over the right keys.
 // The online softmax runs in log2 units (exp2); the output is divided by the final sum. Key tiles
 // start at the sequence's first valid key, so left padding changes no result bit.
+// In the prefill's fp16 mode (PV_HILO false) the weighted sum is one product of fp16(P) and
+// fp16(V) (about 2^-11 relative, 5e-4 of the output's scale): V's remainder is neither split nor
+// staged and P is rounded instead of split; the scores keep their three products (their error
+// would pass through the exponential).
 #include "common.h"
 #include "layer.h"
 
@@ -92,23 +96,31 @@ __device__ __forceinline__ PmRegs pm_fetch(const float * __restrict__ base, int6
     return r;
 }
 
-// split the fetched values into fp16 hi + lo and store them
+// split the fetched values into fp16 hi + lo and store them (V: hi only without PV_HILO)
+template <bool PV_HILO>
 __device__ __forceinline__ void pm_store(const PmRegs & r, int tid, PmTile & t) {
     const int key = tid >> 3, dq = (tid & 7) * 4;
     const int vd = tid & 31, vk = (tid >> 5) * 4;
-    v2h k0h, k0l, k1h, k1l, v0h, v0l, v1h, v1l;
+    v2h k0h, k0l, k1h, k1l;
     split_pair(r.k.x, r.k.y, k0h, k0l);
     split_pair(r.k.z, r.k.w, k1h, k1l);
-    split_pair(r.v[0], r.v[1], v0h, v0l);
-    split_pair(r.v[2], r.v[3], v1h, v1l);
     const v4h kh = {k0h[0], k0h[1], k1h[0], k1h[1]}, kl = {k0l[0], k0l[1], k1l[0], k1l[1]};
-    const v4h vh = {v0h[0], v0h[1], v1h[0], v1h[1]}, vl = {v0l[0], v0l[1], v1l[0], v1l[1]};
     *reinterpret_cast<v4h *>(&t.khi[key * PM_KROW + dq * 2]) = kh;
     *reinterpret_cast<v4h *>(&t.klo[key * PM_KROW + dq * 2]) = kl;
-    *reinterpret_cast<v4h *>(&t.vhi[vd * PM_VROW + vk * 2]) = vh;
-    *reinterpret_cast<v4h *>(&t.vlo[vd * PM_VROW + vk * 2]) = vl;
+    if constexpr (PV_HILO) {
+        v2h v0h, v0l, v1h, v1l;
+        split_pair(r.v[0], r.v[1], v0h, v0l);
+        split_pair(r.v[2], r.v[3], v1h, v1l);
+        const v4h vh = {v0h[0], v0h[1], v1h[0], v1h[1]}, vl = {v0l[0], v0l[1], v1l[0], v1l[1]};
+        *reinterpret_cast<v4h *>(&t.vhi[vd * PM_VROW + vk * 2]) = vh;
+        *reinterpret_cast<v4h *>(&t.vlo[vd * PM_VROW + vk * 2]) = vl;
+    } else {
+        const v4h vh = {(_Float16) r.v[0], (_Float16) r.v[1], (_Float16) r.v[2], (_Float16) r.v[3]};
+        *reinterpret_cast<v4h *>(&t.vhi[vd * PM_VROW + vk * 2]) = vh;
+    }
 }
 
+template <bool PV_HILO>
 __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const float * __restrict__ qkv, int S, int max_len, const int32_t * __restrict__ pad, int nh, int d_model,
     float scale_log2, float * __restrict__ out, int8_t * __restrict__ oq, float * __restrict__ od) {
@@ -160,7 +172,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     v16f o = {};               // O^T: this lane's query, dims 8*(v/4) + 4*lh + v%4
     float m = -INFINITY, l = 0.0f;
 
-    if (kt0 < ke_g) pm_store(pm_fetch(base, rs, d_model, h, S, kt0, tid), tid, tiles[0]);
+    if (kt0 < ke_g) pm_store<PV_HILO>(pm_fetch(base, rs, d_model, h, S, kt0, tid), tid, tiles[0]);
     __syncthreads();
     int buf = 0;
     for (int k0 = kt0; k0 < ke_g; k0 += PM_KT, buf ^= 1) {
@@ -231,32 +243,42 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
             // O^T += V^T . P^T, keys in the register order (two chunks of 16)
 #pragma unroll
             for (int c = 0; c < 2; c++) {
-                v8h ph, pl;
-#pragma unroll
-                for (int i = 0; i < 8; i += 2) {
-                    v2h hi, lo;
-                    split_pair(p[8 * c + i], p[8 * c + i + 1], hi, lo);
-                    ph[i] = hi[0]; ph[i + 1] = hi[1];
-                    pl[i] = lo[0]; pl[i + 1] = lo[1];
-                }
                 // V^T rows: dim li, keys 16c + 4*lh + [0,4) and 16c + 8 + 4*lh + [0,4)
                 const int kA = 32 * hf + 16 * c + 4 * lh, kB = 32 * hf + 16 * c + 8 + 4 * lh;
                 const v4h a0 = *reinterpret_cast<const v4h *>(&t.vhi[li * PM_VROW + kA * 2]);
                 const v4h a1 = *reinterpret_cast<const v4h *>(&t.vhi[li * PM_VROW + kB * 2]);
-                const v4h b0 = *reinterpret_cast<const v4h *>(&t.vlo[li * PM_VROW + kA * 2]);
-                const v4h b1 = *reinterpret_cast<const v4h *>(&t.vlo[li * PM_VROW + kB * 2]);
-                v8h vh, vl;
+                v8h vh;
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     vh[i] = a0[i]; vh[4 + i] = a1[i];
-                    vl[i] = b0[i]; vl[4 + i] = b1[i];
                 }
-                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl, o, 0, 0, 0);
-                o = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, o, 0, 0, 0);
+                v8h ph;
+                if constexpr (PV_HILO) {
+                    v8h pl;
+#pragma unroll
+                    for (int i = 0; i < 8; i += 2) {
+                        v2h hi, lo;
+                        split_pair(p[8 * c + i], p[8 * c + i + 1], hi, lo);
+                        ph[i] = hi[0]; ph[i + 1] = hi[1];
+                        pl[i] = lo[0]; pl[i + 1] = lo[1];
+                    }
+                    const v4h b0 = *reinterpret_cast<const v4h *>(&t.vlo[li * PM_VROW + kA * 2]);
+                    const v4h b1 = *reinterpret_cast<const v4h *>(&t.vlo[li * PM_VROW + kB * 2]);
+                    v8h vl;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        vl[i] = b0[i]; vl[4 + i] = b1[i];
+                    }
+                    o = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, pl, o, 0, 0, 0);
+                    o = __builtin_amdgcn_mfma_f32_32x32x16_f16(vl, ph, o, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) ph[i] = (_Float16) p[8 * c + i];
+                }
                 o = __builtin_amdgcn_mfma_f32_32x32x16_f16(vh, ph, o, 0, 0, 0);
             }
         }
-        if (more) pm_store(nxt, tid, tiles[buf ^ 1]);
+        if (more) pm_store<PV_HILO>(nxt, tid, tiles[buf ^ 1]);
         __syncthreads();
     }
 
@@ -296,15 +318,20 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
 }
 
 int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
-                             int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream) {
+                             int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream,
+                             bool pv_f16) {
     GSVK_REQUIRE(qkv && pad && out && B > 0 && S > 0 && nh * 32 == d_model && max_len <= S,
                  "attn_prefill_mfma: bad arguments");
     GSVK_REQUIRE((oq == nullptr) == (od == nullptr), "attn_prefill_mfma: oq and od go together");
     GSVK_REQUIRE(((uintptr_t) qkv & 15) == 0 && ((uintptr_t) out & 15) == 0,
                  "attn_prefill_mfma: qkv and out must be 16-byte aligned");
     const dim3 grid((unsigned) ((S + PM_Q * PM_WAVES - 1) / (PM_Q * PM_WAVES)), (unsigned) nh, (unsigned) B);
-    hipLaunchKernelGGL(k_attn_prefill_mfma, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad, nh,
-                       d_model, scale * 1.4426950408889634f, out, oq, od);
+    if (pv_f16)
+        hipLaunchKernelGGL(k_attn_prefill_mfma<false>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od);
+    else
+        hipLaunchKernelGGL(k_attn_prefill_mfma<true>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -315,11 +342,11 @@ extern "C" int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len
                                     int hd, float scale, int path, float * out, int8_t * oq, float * od,
                                     void * stream) {
     GSVK_REQUIRE(hd == 32, "attn_prefill: head_dim must be 32");
-    GSVK_REQUIRE(path >= 0 && path <= 2, "attn_prefill: path must be 0 (auto), 1 or 2");
-    const bool mfma = path == 2 || (path == 0 && gsvk::attn_prefill_uses_mfma((int64_t) B * S));
+    GSVK_REQUIRE(path >= 0 && path <= 3, "attn_prefill: path must be 0 (auto), 1, 2 or 3");
+    const bool mfma = path >= 2 || (path == 0 && gsvk::attn_prefill_uses_mfma((int64_t) B * S));
     if (mfma)
         return gsvk::launch_attn_prefill_mfma(qkv, B, S, max_len, pad, nh, nh * hd, scale, out, oq, od,
-                                              (hipStream_t) stream);
+                                              (hipStream_t) stream, path == 3);
     return gsvk::launch_attn_prefill(qkv, B, S, max_len, pad, nh, nh * hd, scale, out, oq, od,
                                      (hipStream_t) stream);
 }

@@ -972,7 +972,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                                                attn.d, st));
         else if (attn_prefill_uses_mfma(rows))
             GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
-                                              attn.d, st));
+                                              attn.d, st, gemm && m->prefill_f16));
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));

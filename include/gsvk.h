@@ -173,9 +173,10 @@ int gsvk_model_set_exact(gsvk_model * m, int on);
  * the matrix-core GEMMs multiply the Q8_0 activations, turned into fp16(d * q), by copies of the
  * Q8_0 weights dequantised once to fp16 (fp16(d * q), made at the first such prefill and kept
  * with the model, 2 bytes per weight) on v_mfma_f32_32x32x16_f16 instead of the int8 products
- * and their per-block fp32 scaling. Both operands are rounded to fp16, so the projections are
- * within about 6e-4 of their row's scale of ggml's (north_star's bar is 2e-3) instead of fp32
- * rounding, and so are the K/V rows the prefill writes. No effect on the decode or in exact mode.
+ * and their per-block fp32 scaling, and the attention's weighted sum is one fp16 product
+ * (gsvk_op_attn_prefill path 3). Both operands are rounded to fp16, so the projections are within
+ * about 6e-4 of their row's scale of ggml's (the bar for them is 2e-3) instead of fp32 rounding,
+ * and so are the K/V rows the prefill writes. No effect on the decode or in exact mode.
  * Off by default; no counterpart in the reference (an option for callers that prefer a faster
  * prefill to agreement within fp32 rounding). */
 int gsvk_model_set_prefill_f16(gsvk_model * m, int on);
@@ -431,8 +432,10 @@ int gsvk_op_dec_ffn(int B, const float * res, const float * p1, const float * bo
  * s < max_len, else [pad[b], s]. out fp32 [B][S][nh*hd]; oq/od (both or neither) its Q8_0 copy
  * (fp32 scales; the quants in the layout of the projection that reads them: sliced from the
  * lane-per-query kernel, natural order from the matrix-core kernel). path 0 picks the kernel the
- * prefill uses for B*S rows, 1 the lane-per-query kernel, 2 the matrix-core kernel. hd must be
- * 32; qkv and out 16-byte aligned. */
+ * prefill uses for B*S rows, 1 the lane-per-query kernel, 2 the matrix-core kernel, 3 the
+ * matrix-core kernel with the weighted sum as one product of fp16 probabilities and fp16 values
+ * (the prefill's fp16 mode, gsvk_model_set_prefill_f16; about 5e-4 of the output's scale). hd must
+ * be 32; qkv and out 16-byte aligned. */
 int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                          int hd, float scale, int path, float * out, int8_t * oq, float * od,
                          void * stream);

@@ -603,10 +603,11 @@ def test_q8_gemm_small_tiles(gpu, n, k, m):
     (2, 33, 20, [19, 3], "a one-key text span; 33 rows"),
     (2, 1024, 300, [0, 123], "long prompt (1024 rows of which 724 semantic)"),
 ])
-@pytest.mark.parametrize("path", [1, 2])
+@pytest.mark.parametrize("path", [1, 2, 3])
 def test_attn_prefill_matches_oracle(gpu, B, S, max_len, pads, what, path):
     """Both prefill-attention kernels (1: lane per query, 2: matrix cores with fp16 hi + lo
-    operands) against the oracle; the Q8_0 copy is the x86 quantisation of the fp32 output."""
+    operands; 3: the same with the weighted sum of fp16 probabilities and values, the prefill's
+    fp16 mode) against the oracle; the Q8_0 copy is the x86 quantisation of the fp32 output."""
     import torch
     nh, D = 16, 512
     rng = np.random.default_rng(40 + S + path)
@@ -622,8 +623,10 @@ def test_attn_prefill_matches_oracle(gpu, B, S, max_len, pads, what, path):
     got = out.cpu().numpy().reshape(B, S, D)
     ref = O.attn_prefill(qkv, max_len, pad, nh, scale)
     rel = np.abs(got - ref).max() / np.abs(ref).max()
+    print(f"attention path {path}, {what}: {rel:.2e} of the output's scale")
     assert rel <= 2e-3, rel
-    assert rel <= 2e-5, rel   # fp32 (or hi + lo split) products with fp32 accumulation
+    if path != 3:
+        assert rel <= 2e-5, rel   # fp32 (or hi + lo split) products with fp32 accumulation
     q_ref, d_ref = blocks_to_split(O.q8_quantize_x86(got.reshape(B * S, D)), B * S, D)
     q_got = oq.cpu().numpy()
     # quants in the layout of the projection that reads them: sliced (GEMV) or natural (GEMM)
