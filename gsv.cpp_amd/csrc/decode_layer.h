@@ -6,9 +6,16 @@
 
 namespace gsvk {
 
-// Hidden-unit groups of the FFN launch: each workgroup computes FFN1 for 2048 / DEC_FFN_GROUPS
-// hidden units of one sequence and their share of FFN2, written as one partial row of 512.
-constexpr int DEC_FFN_GROUPS = 16;
+// Hidden-unit groups of the FFN launch: each workgroup computes FFN1 for 2048 / groups hidden
+// units of one sequence and their share of FFN2, written as one partial row of 512 that the next
+// launch sums. 32 groups of 64 units while the 32 x B workgroups fit the 256 CUs (up to batch 8:
+// half the weight bytes per workgroup, twice the partial rows for the next LayerNorm), 16 groups
+// of 128 above. Whole step, 24 layers, 16 / 32 groups: batch 1 0.340 / 0.313 ms, batch 2 0.347 /
+// 0.322, batch 4 0.352 / 0.329, batch 8 0.371 / 0.349, batch 10 0.384 / 0.402, batch 16 0.406 /
+// 0.436.
+constexpr int DEC_FFN_GROUPS = 16;       // the C-ABI ops (gsvk_op_dec_attn / _ffn) and above batch 8
+constexpr int DEC_FFN_GROUPS_MAX = 32;
+inline int dec_ffn_groups(int B) { return B <= 8 ? DEC_FFN_GROUPS_MAX : DEC_FFN_GROUPS; }
 
 // Largest batch the two-launch layer takes (its grids are 16 x B workgroups; nothing else in it
 // depends on the batch).
@@ -30,7 +37,8 @@ constexpr int DEC_AUTO_MAX_BATCH = 32;
 struct DecAttnArgs {
     int mode;                 // IN_LN or IN_EMB
     const float * res;        // IN_LN: [B][512]
-    const float * parts;      // IN_LN: [DEC_FFN_GROUPS][B][512]
+    const float * parts;      // IN_LN: [nparts][B][512]
+    int nparts;               // IN_LN: the previous FFN launch's groups (16 or 32)
     const float * bias;       // IN_LN: [512]
     const float * wb;         // IN_LN: [w; b], 1024
     const float * emb;        // IN_EMB: embedding table [vocab][512]
@@ -63,7 +71,7 @@ struct DecAttnArgs {
 
 // Launch 2 of a layer, workgroup (hidden group g, sequence b):
 //   n1 = LN1((res + p1[0] + ... + p1[15]) + bo), stored by the group-0 workgroups;
-//   the group's 2048 / DEC_FFN_GROUPS hidden units h = relu(W1 . n1 + b1) (x86 Q8_0 dot),
+//   the group's 2048 / groups hidden units h = relu(W1 . n1 + b1) (x86 Q8_0 dot),
 //   quantised to Q8_0 blocks, times the matching columns of W2: partial row p2[g][b][0:512].
 struct DecFfnArgs {
     const float * res;        // [B][512] (x_out of launch 1)
@@ -76,7 +84,8 @@ struct DecFfnArgs {
     const float * b1;
     const int8_t * w2q;       // FFN2 [512][2048] in the Q8_TILED order
     const uint16_t * w2d;
-    float * p2;               // [DEC_FFN_GROUPS][B][512]
+    float * p2;               // [groups][B][512]
+    int groups;               // 16 or 32 (dec_ffn_groups)
     int B;
 };
 

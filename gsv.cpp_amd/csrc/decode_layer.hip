@@ -9,7 +9,7 @@
 //
 //   k_dec_attn, workgroup (head h, sequence b), 8 waves:
 //     every thread loads element `tid` of the input row's operands (the previous layer's LN1
-//     output, its DEC_FFN_GROUPS FFN2 partial rows, b_2, LN2's w and b), every wave its share of
+//     output, its 16 or 32 FFN2 partial rows, b_2, LN2's w and b), every wave its share of
 //     head h's 96 QKV weight rows and of the 512 x 32 out-projection slice of head h, and its
 //     first block of cached keys, all before any of them is used;
 //     LN2 over the workgroup (double sums, one value per thread), the x86 Q8_0 quantisation of
@@ -19,7 +19,7 @@
 //     the head's 32 outputs quantised to one Q8_0 block (the block the out projection's activation
 //     quantisation gives them: head h is block h of the row) and multiplied by the slice: for
 //     output n, (d_w d_a) * (exact int32 block dot), the partial row p1[h][b].
-//   k_dec_ffn, workgroup (hidden group g of 128 units, sequence b), 8 waves:
+//   k_dec_ffn, workgroup (hidden group g of 128 or 64 units, sequence b), 8 waves:
 //     LN1((x + sum_h p1[h]) + b_o), quantised; FFN1 + b_1 + ReLU for the group's 128 units (the
 //     8-lane dot), quantised to 4 Q8_0 blocks (those of FFN2's activation row), and the 512 x 128
 //     slice of FFN2: p2[g][b][n] = sum over the 4 blocks of (d_w d_h) * (int32 block dot).
@@ -141,10 +141,9 @@ __device__ __forceinline__ int tile_dot(const int4 & w, const int8_t * a_blk, in
 
 }  // namespace
 
-template <int MODE>
+template <int MODE, int NP>   // NP: the FFN2 partial rows of the input stage (IN_LN)
 __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     constexpr int NW = DL_WAVES;
-    constexpr int NP = DEC_FFN_GROUPS;
     constexpr int PASSES = (DL_QKV_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     constexpr int WO_T = DL_NBLK / NW;                        // out-projection tiles per wave
     const int h = blockIdx.x;
@@ -465,11 +464,15 @@ int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream) {
     GSVK_REQUIRE(a.mode == IN_LN ? (a.res && a.parts && a.bias && a.wb)
                                  : (a.mode == IN_EMB && a.emb && a.pe && a.tok && a.pos_ptr),
                  "dec_attn: bad input stage");
+    GSVK_REQUIRE(a.mode != IN_LN || a.nparts == 16 || a.nparts == 32, "dec_attn: %d partial rows (16 or 32)",
+                 a.nparts);
     const dim3 grid(DL_NH, (unsigned) a.B);
-    if (a.mode == IN_LN)
-        hipLaunchKernelGGL(k_dec_attn<IN_LN>, grid, dim3(DL_THREADS), 0, stream, a);
+    if (a.mode == IN_LN && a.nparts == 32)
+        hipLaunchKernelGGL((k_dec_attn<IN_LN, 32>), grid, dim3(DL_THREADS), 0, stream, a);
+    else if (a.mode == IN_LN)
+        hipLaunchKernelGGL((k_dec_attn<IN_LN, 16>), grid, dim3(DL_THREADS), 0, stream, a);
     else
-        hipLaunchKernelGGL(k_dec_attn<IN_EMB>, grid, dim3(DL_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_dec_attn<IN_EMB, 16>), grid, dim3(DL_THREADS), 0, stream, a);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -478,8 +481,11 @@ int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream) {
     GSVK_REQUIRE(a.B >= 1 && a.B <= DEC_MAX_BATCH, "dec_ffn: batch %d out of range (1..%d)", a.B, DEC_MAX_BATCH);
     GSVK_REQUIRE(a.res && a.p1 && a.bo && a.wb1 && a.n1_out && a.w1q && a.w1d && a.b1 && a.w2q && a.w2d && a.p2,
                  "dec_ffn: null pointer");
-    hipLaunchKernelGGL(k_dec_ffn<DEC_FFN_GROUPS>, dim3(DEC_FFN_GROUPS, (unsigned) a.B), dim3(DL_THREADS), 0,
-                       stream, a);
+    GSVK_REQUIRE(a.groups == 16 || a.groups == 32, "dec_ffn: %d hidden groups (16 or 32)", a.groups);
+    if (a.groups == 32)
+        hipLaunchKernelGGL(k_dec_ffn<32>, dim3(32, (unsigned) a.B), dim3(DL_THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k_dec_ffn<16>, dim3(16, (unsigned) a.B), dim3(DL_THREADS), 0, stream, a);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -498,6 +504,7 @@ extern "C" int gsvk_op_dec_attn(int B, const float * res, const float * parts, c
     a.mode = res ? IN_LN : IN_EMB;
     a.res = res;
     a.parts = parts;
+    a.nparts = DEC_FFN_GROUPS;
     a.bias = ln_bias;
     a.wb = ln_wb;
     a.emb = emb;
@@ -542,6 +549,7 @@ extern "C" int gsvk_op_dec_ffn(int B, const float * res, const float * p1, const
     a.w2q = w2q;
     a.w2d = w2d;
     a.p2 = p2;
+    a.groups = DEC_FFN_GROUPS;
     a.B = B;
     return launch_dec_ffn(a, (hipStream_t) stream);
 }

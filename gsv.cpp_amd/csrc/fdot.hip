@@ -365,7 +365,7 @@ int launch_head_ln_parts(const void * W, int wtype, int64_t n, const float * res
                          int nparts, int64_t pstride, const float * bias, const float * wb, int64_t m,
                          float * Y, int64_t ys, hipStream_t stream) {
     GSVK_REQUIRE(W && res && parts && wb && Y && (wtype == 0 || wtype == 1) && n > 0 && n < (1 << 30) &&
-                     m > 0 && m < (1 << 30) && ys >= n && nparts == 16 && pstride >= m * 512,
+                     m > 0 && m < (1 << 30) && ys >= n && (nparts == 16 || nparts == 32) && pstride >= m * 512,
                  "head_ln_parts: bad arguments");
     auto al16 = [](const void * p) { return ((uintptr_t) p & 15) == 0; };
     GSVK_REQUIRE(al16(res) && al16(parts) && al16(bias) && al16(wb) && pstride % 4 == 0,
@@ -373,12 +373,15 @@ int launch_head_ln_parts(const void * W, int wtype, int64_t n, const float * res
     constexpr int MTK = 4;
     const dim3 grid((unsigned) ((n + 7) / 8), (unsigned) ((m + MTK - 1) / MTK));
     const LnSrc ln{res, nullptr, bias, wb, parts, pstride};
-    if (wtype == 1)
-        hipLaunchKernelGGL((k_fdot_ggml_k<uint16_t, MTK, 16, true, 16>), grid, dim3(256), 0, stream,
-                           (const uint16_t *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
-    else
-        hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16, true, 16>), grid, dim3(256), 0, stream,
-                           (const float *) W, (int) n, nullptr, 512, (int) m, Y, ys, ln);
+#define GSVK_HEAD(WT, NP)                                                                           \
+    hipLaunchKernelGGL((k_fdot_ggml_k<WT, MTK, 16, true, NP>), grid, dim3(256), 0, stream, (const WT *) W, (int) n, \
+                       nullptr, 512, (int) m, Y, ys, ln)
+    if (wtype == 1) {
+        if (nparts == 32) GSVK_HEAD(uint16_t, 32); else GSVK_HEAD(uint16_t, 16);
+    } else {
+        if (nparts == 32) GSVK_HEAD(float, 32); else GSVK_HEAD(float, 16);
+    }
+#undef GSVK_HEAD
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

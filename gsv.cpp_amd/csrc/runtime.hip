@@ -358,7 +358,7 @@ int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
     GSVK_TRY(a.alloc(m->h2, (size_t) B * D));
     GSVK_TRY(a.alloc(m->logits, (size_t) B * m->V));
     GSVK_TRY(a.alloc(m->p1, (size_t) m->NH * B * D));
-    GSVK_TRY(a.alloc(m->p2, (size_t) DEC_FFN_GROUPS * B * D));
+    GSVK_TRY(a.alloc(m->p2, (size_t) DEC_FFN_GROUPS_MAX * B * D));
     char * ws = nullptr;
     GSVK_TRY(a.alloc(ws, attn_workspace_bytes(B, m->NH, m->lstride)));
     GSVK_HIP(hipMemset(ws, 0, attn_workspace_bytes(B, m->NH, m->lstride)));
@@ -682,6 +682,7 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
 // layer's partials in its LayerNorm input stage.
 int enqueue_decode_fused(gsvk_model * m) {
     const int B = m->B, D = m->D;
+    const int G = dec_ffn_groups(B);   // hidden groups of the FFN launch = partial rows of the next LN
     const float scale = 1.0f / std::sqrt((float) m->HD);
     hipStream_t st = m->stream;
     for (int li = 0; li < m->NL; li++) {
@@ -706,6 +707,7 @@ int enqueue_decode_fused(gsvk_model * m) {
             aa.mode = IN_LN;
             aa.res = m->n1.x;
             aa.parts = m->p2;
+            aa.nparts = G;
             aa.bias = p.f2.b;
             aa.wb = p.ln2;
         }
@@ -737,13 +739,13 @@ int enqueue_decode_fused(gsvk_model * m) {
         fa.w2q = w.f2.qt;
         fa.w2d = w.f2.dt;
         fa.p2 = m->p2;
+        fa.groups = G;
         fa.B = B;
         GSVK_TRY(launch_dec_ffn(fa, st));
     }
     const LayerW & last = m->L[m->NL - 1];
     return launch_head_ln_parts(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, m->n1.x, m->p2,
-                                DEC_FFN_GROUPS, (int64_t) B * D, last.f2.b, last.ln2, B, m->logits, m->V,
-                                st);
+                                G, (int64_t) B * D, last.f2.b, last.ln2, B, m->logits, m->V, st);
 }
 
 // The two-launch layer covers the shape and the weights it reads (tiled out / FFN2 copies, an
