@@ -236,16 +236,18 @@ def test_fdot_head_bitexact(gpu, wtype, mode):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"max {np.abs(got - ref).max():.3e}"
 
 
-@pytest.mark.parametrize("m", [9, 70, 333])
-def test_fdot_bert_projection_bitexact(gpu, m):
-    """K = 1025 (bert_aug = [W | b]): ggml_vec_dot_f32 with a fused leftover; from 64 rows the
-    kernel that keeps 4 weight rows x 16 activation rows per thread, the same chains."""
+@pytest.mark.parametrize("m,k,n", [(9, 1025, 512), (70, 1025, 512), (333, 1025, 512), (2050, 1025, 512),
+                                   (96, 1024, 512), (130, 1025, 200)])
+def test_fdot_bert_projection_bitexact(gpu, m, k, n):
+    """K = 1025 (bert_aug = [W | b]): ggml_vec_dot_f32 with a fused leftover. From 64 rows, n % 32
+    == 0: the fp32 matrix-core kernel (one product per instruction and output, the same chains);
+    n = 200: the kernel that keeps 4 weight rows x 16 activation rows per thread."""
     import torch
-    rng = np.random.default_rng(20 + m)
-    W = rng.standard_normal((512, 1025)).astype(np.float32) * 0.02
-    X = rng.uniform(-1, 1, (m, 1025)).astype(np.float32)
-    X[:, 1024] = 1.0
-    y = torch.zeros((m, 512), dtype=torch.float32, device="cuda")
+    rng = np.random.default_rng(20 + m + k + n)
+    W = rng.standard_normal((n, k)).astype(np.float32) * 0.02
+    X = rng.uniform(-1, 1, (m, k)).astype(np.float32)
+    X[:, k - 1] = 1.0
+    y = torch.zeros((m, n), dtype=torch.float32, device="cuda")
     gpu.op_fdot(_dev(W, torch), 0, _dev(X, torch), y, 0)
     torch.cuda.synchronize()
     ref = O.f32_matmul(W, X, 0)
