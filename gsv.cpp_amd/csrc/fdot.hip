@@ -135,133 +135,6 @@ __global__ void __launch_bounds__(256) k_fdot_ggml_t(const WT * __restrict__ W, 
         }
 }
 
-// MODE 0 for many activation rows of F32 weights (the prefill's BERT projection) on the fp32
-// matrix cores. v_mfma_f32_32x32x1_2b_f32 adds one product to each output of each block per
-// instruction, rounded once like an fma, so the chain of slice p, acc_p = fma(w[32i+p],
-// x[32i+p], acc_p) for i = 0, 1, ..., runs unchanged as a sequence of these instructions.
-// Workgroup: 32 activation rows x 32 weight rows, 8 waves; wave v owns the slices 4v..4v+3 in
-// two accumulators: acc0 holds slice 4v (block 0, lanes 0-31) and 4v+2 (block 1, lanes 32-63),
-// acc1 slices 4v+1 and 4v+3. Both 32-row tiles are staged through LDS 128 columns (4 steps) at a
-// time (k & ~31 a multiple of 128), with the next chunk's loads in flight during the products;
-// the rows are padded to 130 floats, so the 8-byte reads of 32 lanes (32 rows) cover the 64
-// banks once. The
-// butterfly over the slices (xor 16, 8, 4, 1, 2) becomes: waves v and v+4, then v and v+2, then
-// waves 0 and 1 (through LDS), then acc0 + acc1, then block 0 + block 1 in wave 0, which fuses
-// the k % 32 leftovers and stores.
-typedef float v32f __attribute__((ext_vector_type(32)));
-
-namespace {
-constexpr int FM_CH = 128;          // columns per staged chunk (4 steps of 32)
-constexpr int FM_ROW = FM_CH + 2;   // LDS floats per staged row
-}  // namespace
-
-// (at least 4 waves per SIMD: two workgroups per CU)
-__global__ void __launch_bounds__(512, 4)
-k_fdot_ggml_mfma(const float * __restrict__ W, int n, int k, const float * __restrict__ X, int64_t xs, int m,
-                 float * __restrict__ Y, int64_t ys) {
-    // the staged tiles (x rows, then w rows), reused as red[4][32][64] for the slice sums
-    __shared__ __align__(16) float lds[2 * 32 * FM_ROW];
-    __shared__ float left[2][32][33];   // columns np..k-1 of the 32 activation rows, the 32 weight rows
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6;
-    const int l = tid & 63;
-    // Workgroup g runs on XCD g % 8 (round-robin dispatch); XCD x takes a contiguous run of
-    // tiles, n-tile fastest, so the n / 32 workgroups that read one activation tile share an L2.
-    const int G = gridDim.x, g = blockIdx.x;
-    const int per = G >> 3, rem = G & 7, xcd = g & 7;
-    const int t = (xcd < rem ? xcd * (per + 1) : rem * (per + 1) + (xcd - rem) * per) + (g >> 3);
-    const int n0 = (t % (n >> 5)) * 32;
-    const int m0 = (t / (n >> 5)) * 32;
-    const int np = k & ~31;
-    // staging: thread t copies column t % 128 of rows 4e + t / 128 (e = 0..7) of both tiles, so
-    // each load instruction reads 4 rows x 512 contiguous bytes; activation rows past m repeat
-    // row m - 1 (their outputs are not stored)
-    const int srow = tid >> 7, scol = tid & 127;
-    const float * xg = X + (int64_t) m0 * xs + scol;
-    const float * wg = W + (int64_t) n0 * k + scol;
-    const int xlim = m - 1 - m0;
-    float * sl = lds + srow * FM_ROW + scol;
-    // products: lane l reads row l % 32 at its slice pair
-    const int slice = 4 * wv + 2 * (l >> 5);
-    const float * xr = lds + (l & 31) * FM_ROW + slice;
-    const float * wr = lds + (32 + (l & 31)) * FM_ROW + slice;
-    v32f acc0, acc1;
-#pragma unroll
-    for (int r = 0; r < 32; r++) {
-        acc0[r] = 0.0f;
-        acc1[r] = 0.0f;
-    }
-    float xv[8], wv8[8];
-    auto fetch = [&](int c0) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            xv[e] = xg[min(4 * e + srow, xlim) * (int) xs + c0];
-            wv8[e] = wg[(4 * e + srow) * k + c0];
-        }
-    };
-    fetch(0);
-    // the k % 32 leftover columns, read once here for the last step of wave 0 (made visible by
-    // the first barrier of the loop)
-    for (int e = tid; e < 2 * 32 * 32; e += 512) {
-        const int side = e >> 10, row = (e >> 5) & 31, col = e & 31;
-        if (np + col < k)
-            left[side][row][col] = side ? W[(int64_t) (n0 + row) * k + np + col]
-                                        : X[(int64_t) min(m0 + row, m - 1) * xs + np + col];
-    }
-    for (int c0 = 0; c0 < np; c0 += FM_CH) {   // np % FM_CH == 0
-        __syncthreads();   // the previous chunk's reads are done
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-            sl[4 * e * FM_ROW] = xv[e];
-            sl[(32 + 4 * e) * FM_ROW] = wv8[e];
-        }
-        __syncthreads();
-        if (c0 + FM_CH < np) fetch(c0 + FM_CH);
-#pragma unroll
-        for (int st = 0; st < FM_CH / 32; st++) {
-            const float2 x2 = *reinterpret_cast<const float2 *>(xr + 32 * st);
-            const float2 w2 = *reinterpret_cast<const float2 *>(wr + 32 * st);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x1f32(x2.x, w2.x, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x1f32(x2.y, w2.y, acc1, 0, 0, 0);
-        }
-    }
-    // slice p + slice (p ^ 4 * lvl) for lvl = 4, 2, 1: wave v += wave v + lvl, one accumulator at
-    // a time through red[v][reg][lane]
-    float (*red)[32][64] = reinterpret_cast<float (*)[32][64]>(lds);
-#pragma unroll
-    for (int lvl = 4; lvl >= 1; lvl >>= 1) {
-#pragma unroll
-        for (int a = 0; a < 2; a++) {
-            __syncthreads();
-            if (wv >= lvl && wv < 2 * lvl) {
-#pragma unroll
-                for (int r = 0; r < 32; r++) red[wv - lvl][r][l] = a ? acc1[r] : acc0[r];
-            }
-            __syncthreads();
-            if (wv < lvl) {
-#pragma unroll
-                for (int r = 0; r < 32; r++) {
-                    if (a) acc1[r] = acc1[r] + red[wv][r][l];
-                    else acc0[r] = acc0[r] + red[wv][r][l];
-                }
-            }
-        }
-    }
-    if (wv != 0) return;
-    // xor 1: slice 0 + slice 1 and slice 2 + slice 3; xor 2: the two blocks. Output (i, j) of a
-    // block sits in lane j + 32 * ((i / 4) % 2), register 4 * (i / 8) + i % 4 (+ 16 for block 1).
-    const int j = l & 31;
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-        const float v0 = acc0[r] + acc1[r];
-        const float v1 = acc0[16 + r] + acc1[16 + r];
-        float v = v0 + v1;
-        const int i = (r & 3) + 4 * (l >> 5) + 8 * (r >> 2);
-        for (int kk = 0; kk < k - np; kk++) v = __builtin_fmaf(left[1][j][kk], left[0][i][kk], v);
-        if (m0 + i < m) Y[(int64_t) (m0 + i) * ys + n0 + j] = v;
-    }
-}
-
 // MODE 0 with K = 32 * NI known at compile time (the decode head, K = 512): the same arithmetic
 // as k_fdot_ggml, with every load issued up front. The MT activation rows (rounded to fp16 for
 // F16 weights) are staged once per workgroup in LDS with 16-byte loads; each lane loads its NI
@@ -412,6 +285,10 @@ __global__ void __launch_bounds__(256) k_fdot_tinyblas(const WT * __restrict__ W
         if (m0 + t < m) Y[(int64_t) (m0 + t) * ys + row] = acc[t];
 }
 
+// MODE 0 on the fp32 matrix cores for many activation rows of F32 weights (fdot_mfma.hip)
+int launch_fdot_mfma(const float * W, int64_t n, int64_t k, const float * X, int64_t xs, int64_t m, float * Y,
+                     int64_t ys, hipStream_t stream);
+
 // wtype: 0 = F32, 1 = F16. mode: 0 = ggml vec_dot, 1 = tinyBLAS (falls back to 0 if k % 8).
 int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X, int64_t xs,
                 int64_t m, float * Y, int64_t ys, int mode, hipStream_t stream) {
@@ -438,11 +315,9 @@ int launch_fdot(const void * W, int wtype, int64_t n, int64_t k, const float * X
         else
             hipLaunchKernelGGL((k_fdot_ggml_k<float, MTK, 16>), grid, dim3(256), 0, stream,
                                (const float *) W, (int) n, X, xs, (int) m, Y, ys, LnSrc{});
-    } else if (m >= 64 && wtype == 0 && n % 32 == 0 && k >= 128 && (k & ~31) % 128 == 0 &&
+    } else if (m >= 64 && wtype == 0 && n % 32 == 0 && k >= 64 && (k & ~31) % 64 == 0 &&
                (n / 32) * ((m + 31) / 32) < (1LL << 31)) {
-        const dim3 grid((unsigned) ((n / 32) * ((m + 31) / 32)));
-        hipLaunchKernelGGL(k_fdot_ggml_mfma, grid, dim3(512), 0, stream, (const float *) W, (int) n, (int) k,
-                           X, xs, (int) m, Y, ys);
+        return launch_fdot_mfma((const float *) W, n, k, X, xs, m, Y, ys, stream);
     } else if (m >= 64) {
         constexpr int RN = 4, MTT = 16;
         const dim3 grid((unsigned) ((n + 8 * RN - 1) / (8 * RN)), (unsigned) ((m + MTT - 1) / MTT));

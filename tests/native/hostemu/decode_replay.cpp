@@ -35,6 +35,13 @@ void set_error(const char * fmt, ...) {
 const char * get_error() { return g_err.c_str(); }
 int launch_head_ln(const void * W, int wtype, int64_t n, const float * res, const float * r, const float * bias,
                    const float * wb, int64_t m, float * Y, int64_t ys, hipStream_t stream);
+// the prefill's many-row projection on the matrix cores (fdot_mfma.hip) is not part of the decode
+// step: linked here, never run
+int launch_fdot_mfma(const float *, int64_t, int64_t, const float *, int64_t, int64_t, float *, int64_t,
+                     hipStream_t) {
+    std::fprintf(stderr, "hostemu: matrix-core kernel not emulated\n");
+    std::abort();
+}
 }  // namespace gsvk
 
 using namespace gsvk;

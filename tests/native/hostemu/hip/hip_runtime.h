@@ -117,14 +117,6 @@ inline int __builtin_amdgcn_ds_swizzle(int v, int pattern) { return ::emu::ds_sw
 
 // ---- arithmetic builtins ----
 inline float __builtin_amdgcn_exp2f(float x) { return std::exp2(x); }
-// the fp32 matrix-core kernel of the prefill's many-row projection is not part of the decode
-// step: compiled here, never run
-typedef float emu_v32f __attribute__((ext_vector_type(32)));
-inline emu_v32f __builtin_amdgcn_mfma_f32_32x32x1f32(float, float, emu_v32f c, int, int, int) {
-    std::fprintf(stderr, "hostemu: matrix-core kernel not emulated\n");
-    std::abort();
-    return c;
-}
 inline int __builtin_amdgcn_sdot4(int a, int b, int c, bool) {
     int s = c;
     for (int i = 0; i < 4; i++) s += (int) (int8_t) (a >> (8 * i)) * (int) (int8_t) (b >> (8 * i));
