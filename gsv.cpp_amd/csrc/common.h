@@ -281,10 +281,13 @@ int launch_q8_repack(const void * blocks, int64_t rows, int64_t k, int8_t * qs, 
 // rows % 32 == 0): the load of a pre-swizzled GGUF
 int launch_q8_untile(const int8_t * qt, const uint16_t * dt, int64_t rows, int64_t k, int8_t * qs, uint16_t * d,
                      int8_t * qn, hipStream_t stream);
-// (y16: optional fp16 copy of y, rounded to nearest even)
+// (y16: optional fp16 copy of y, rounded to nearest even; row_pad: left-padding rows per sequence
+// of rows_per_seq rows, or null: padding rows are neither read nor written, their outputs keep
+// what they held)
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, int layout = Q8_SLICED, uint16_t * y16 = nullptr);
+                     hipStream_t stream, int layout = Q8_SLICED, uint16_t * y16 = nullptr,
+                     const int32_t * row_pad = nullptr, int rows_per_seq = 0);
 int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, int vocab,
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
                     int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, const int32_t * pos_sub,

@@ -23,10 +23,12 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
                                                   float eps, float * __restrict__ y,
                                                   int8_t * __restrict__ yq,
                                                   float * __restrict__ yd, int layout,
-                                                  uint16_t * __restrict__ y16) {
+                                                  uint16_t * __restrict__ y16,
+                                                  const int32_t * __restrict__ row_pad, int rows_per_seq) {
     // one wave per row, up to 4 rows per workgroup (the waves are independent: no barrier)
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
+    if (row_pad && row % rows_per_seq < row_pad[row / rows_per_seq]) return;   // a padding row
     const int lane = threadIdx.x & 63;
     const int nchunk = n / 8;
     const float * xr = x + (int64_t) row * n;
@@ -179,8 +181,9 @@ __global__ void __launch_bounds__(64) k_embed_pe(const float * __restrict__ emb,
 
 int launch_layernorm(const float * x, const float * r, const float * bias, const float * wb,
                      int64_t rows, int64_t n, float eps, float * y, int8_t * yq, float * yd,
-                     hipStream_t stream, int layout, uint16_t * y16) {
+                     hipStream_t stream, int layout, uint16_t * y16, const int32_t * row_pad, int rows_per_seq) {
     GSVK_REQUIRE(x && wb && y, "layernorm: null pointer");
+    GSVK_REQUIRE(!row_pad || (rows_per_seq > 0 && rows % rows_per_seq == 0), "layernorm: bad padding rows");
     GSVK_REQUIRE(rows >= 0 && rows < (1 << 30) && n > 0 && n % 32 == 0 && n <= 4096,
                  "layernorm: unsupported shape rows=%lld n=%lld (n %% 32 == 0, n <= 4096)",
                  (long long) rows, (long long) n);
@@ -197,7 +200,7 @@ int launch_layernorm(const float * x, const float * r, const float * bias, const
     // (the fp16 copy is a separate instantiation: the kernel without it stays as it was)
 #define GSVK_LN(C, H)                                                                              \
     hipLaunchKernelGGL((k_layernorm<C, H>), grid, block, 0, stream, x, r, bias, wb, (int) rows, (int) n, eps, \
-                       y, yq, yd, layout, y16)
+                       y, yq, yd, layout, y16, row_pad, rows_per_seq)
     if (n <= 512) {
         if (y16) GSVK_LN(1, true); else GSVK_LN(1, false);
     } else if (n <= 1024) {

@@ -466,7 +466,10 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
                            : launch_q8_gemm(q8w(l), n, k, R, xs, xd, layout, out, st);
         };
         GSVK_TRY(gemm(w.out, D, D, attn.q, attn.d, oo));
-        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout));
+        // (prefill: the left-padding rows are skipped; no valid row reads their LN1 rows, and
+        // their FFN rows stay in those rows)
+        GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout, nullptr,
+                                  row_pad, rows_per_seq));
         LayerOut ho{};
         ho.bias = w.f1.b;
         ho.act = 1;
@@ -942,11 +945,13 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
         if (gemm) {
-            // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy
+            // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy; the
+            // left-padding rows are skipped and keep their layer-0 input (zeros: finite K/V rows
+            // that no query attends)
             if (li > 0) {
                 const LayerW & p = m->L[li - 1];
                 GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st,
-                                          Q8_NATURAL));
+                                          Q8_NATURAL, nullptr, d_pad, S));
             }
             LayerOut qo = qkv_out(m, w, loff, qkv, 3 * D, S, zero, col0);
             qo.row_pad = d_pad;   // row tiles of left padding only: zeros, no K/V (never attended)
