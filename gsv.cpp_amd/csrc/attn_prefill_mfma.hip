@@ -123,13 +123,18 @@ __device__ __forceinline__ void pm_store(const PmRegs & r, int tid, PmTile & t) 
 template <bool PV_HILO>
 __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const float * __restrict__ qkv, int S, int max_len, const int32_t * __restrict__ pad, int nh, int d_model,
-    float scale_log2, float * __restrict__ out, int8_t * __restrict__ oq, float * __restrict__ od) {
-    const int h = blockIdx.y, b = blockIdx.z;
+    float scale_log2, float * __restrict__ out, int8_t * __restrict__ oq, float * __restrict__ od,
+    const int32_t * __restrict__ seq_order) {
+    // seq_order (or null): the sequences in dispatch order, and each sequence's query blocks from
+    // the last (the most keys) down, so that the longest workgroups start first
+    const int h = blockIdx.y;
+    const int b = seq_order ? seq_order[blockIdx.z] : blockIdx.z;
+    const int qb = seq_order ? gridDim.x - 1 - blockIdx.x : blockIdx.x;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int li = lane & 31, lh = lane >> 5;
-    const int q0w = blockIdx.x * (PM_Q * PM_WAVES);      // first query of the workgroup
+    const int q0w = qb * (PM_Q * PM_WAVES);             // first query of the workgroup
     const int qw = q0w + wave * PM_Q;                     // first query of this wave
     const int q = qw + li;                                // this lane's query
     const int pb = pad[b];
@@ -319,7 +324,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
 
 int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                              int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream,
-                             bool pv_f16) {
+                             bool pv_f16, const int32_t * seq_order) {
     GSVK_REQUIRE(qkv && pad && out && B > 0 && S > 0 && nh * 32 == d_model && max_len <= S,
                  "attn_prefill_mfma: bad arguments");
     GSVK_REQUIRE((oq == nullptr) == (od == nullptr), "attn_prefill_mfma: oq and od go together");
@@ -328,10 +333,10 @@ int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const
     const dim3 grid((unsigned) ((S + PM_Q * PM_WAVES - 1) / (PM_Q * PM_WAVES)), (unsigned) nh, (unsigned) B);
     if (pv_f16)
         hipLaunchKernelGGL(k_attn_prefill_mfma<false>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od);
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order);
     else
         hipLaunchKernelGGL(k_attn_prefill_mfma<true>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od);
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }

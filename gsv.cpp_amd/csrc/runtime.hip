@@ -888,6 +888,13 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(tmp.alloc(d_boff, B));
     GSVK_TRY(upload(d_phones, phones.data(), phones.size() * 4, st));
     GSVK_TRY(upload(d_pad, pad.data(), (size_t) B * 4, st));
+    // the attention's sequence order: fewest padding rows (longest) first
+    std::vector<int32_t> order(B);
+    for (int b = 0; b < B; b++) order[b] = b;
+    std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return pad[a] < pad[c]; });
+    int32_t * d_order;
+    GSVK_TRY(tmp.alloc(d_order, B));
+    GSVK_TRY(upload(d_order, order.data(), (size_t) B * 4, st));
     if (P) GSVK_TRY(upload(d_prompt, reqs[0].prompt, (size_t) P * 4, st));
     if (R) {
         GSVK_TRY(upload(d_rowb, row_b.data(), (size_t) R * 4, st));
@@ -979,7 +986,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                                                attn.d, st));
         else if (attn_prefill_uses_mfma(rows))
             GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
-                                              attn.d, st, gemm && m->prefill_f16));
+                                              attn.d, st, gemm && m->prefill_f16, d_order));
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));
