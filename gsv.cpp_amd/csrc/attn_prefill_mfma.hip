@@ -124,7 +124,7 @@ template <bool PV_HILO>
 __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const float * __restrict__ qkv, int S, int max_len, const int32_t * __restrict__ pad, int nh, int d_model,
     float scale_log2, float * __restrict__ out, int8_t * __restrict__ oq, float * __restrict__ od,
-    const int32_t * __restrict__ seq_order) {
+    const int32_t * __restrict__ seq_order, int skip_pad) {
     // seq_order (or null): the sequences in dispatch order, and each sequence's query blocks from
     // the last (the most keys) down, so that the longest workgroups start first
     const int h = blockIdx.y;
@@ -154,6 +154,10 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const int ke_g = min(key_end(qlast_g), S);
     // tiles start at the first valid key: a sequence's arithmetic does not depend on its left pad
     const int kt0 = pb;
+    // skip_pad: queries of left-padding rows are not computed (their rows get zeros). A wave of
+    // padding queries only helps stage the tiles; a workgroup of them stages none (uniform).
+    const bool idle = skip_pad && qw + PM_Q <= pb;
+    const int kend = skip_pad && q0w + PM_Q * PM_WAVES <= pb ? kt0 : ke_g;
 
     // Q^T operand (B): query q, dims 16c + 8*lh + [0, 8), split hi + lo
     v8h qh[2], ql[2];
@@ -177,19 +181,19 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     v16f o = {};               // O^T: this lane's query, dims 8*(v/4) + 4*lh + v%4
     float m = -INFINITY, l = 0.0f;
 
-    if (kt0 < ke_g) pm_store<PV_HILO>(pm_fetch(base, rs, d_model, h, S, kt0, tid), tid, tiles[0]);
+    if (kt0 < kend) pm_store<PV_HILO>(pm_fetch(base, rs, d_model, h, S, kt0, tid), tid, tiles[0]);
     __syncthreads();
     int buf = 0;
-    for (int k0 = kt0; k0 < ke_g; k0 += PM_KT, buf ^= 1) {
+    for (int k0 = kt0; k0 < kend; k0 += PM_KT, buf ^= 1) {
         // the next tile is fetched into registers before this one is used, and stored after
-        const bool more = k0 + PM_KT < ke_g;   // uniform over the workgroup
+        const bool more = k0 + PM_KT < kend;   // uniform over the workgroup
         PmRegs nxt{};
         if (more) nxt = pm_fetch(base, rs, d_model, h, S, k0 + PM_KT, tid);
         const PmTile & t = tiles[buf];
 #pragma unroll
         for (int hf = 0; hf < PM_KT / 32; hf++) {
             const int kk = k0 + 32 * hf;   // the half's first key
-            if (kk >= ke_w) break;         // uniform per wave
+            if (kk >= ke_w || idle) break; // uniform per wave
             // S^T = K . Q^T over the 32 dims (2 chunks of 16)
             v16f sc = {};
 #pragma unroll
@@ -333,10 +337,10 @@ int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const
     const dim3 grid((unsigned) ((S + PM_Q * PM_WAVES - 1) / (PM_Q * PM_WAVES)), (unsigned) nh, (unsigned) B);
     if (pv_f16)
         hipLaunchKernelGGL(k_attn_prefill_mfma<false>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order);
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) (seq_order != nullptr));
     else
         hipLaunchKernelGGL(k_attn_prefill_mfma<true>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order);
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) (seq_order != nullptr));
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
