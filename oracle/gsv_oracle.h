@@ -35,8 +35,11 @@
  *   orc_first_logits                      zero / exact-identity projections give float64 closed
  *                                         forms of the input rows (BERT projection, PE positions,
  *                                         alphas, padding), the LayerNorm chain with b_o and b_2,
- *                                         the head over the last row, the attention masks, the
- *                                         decode embedding position and K/V cache column; plus
+ *                                         the head over the last row, the prefill attention masks,
+ *                                         the decode embedding position and K/V cache column, the
+ *                                         decode attention's key range [pad, len] (new key
+ *                                         included) and 1/sqrt(32) scale, and the ReLU between
+ *                                         FFN1 and FFN2 (exactly quantisable activations); plus
  *                                         left-padding invariance and EOS / early-stop traces
  * Parity unpinned: the ORDER of ggml-cpu's floating-point arithmetic (the x86 activation
  * rounding mode, the 8-lane Q8_0 and F16 dot orders, flash_attn_ext's online-softmax order and

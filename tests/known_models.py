@@ -69,11 +69,15 @@ def params(seed: int, n_layer: int):
     return p, perm, scale
 
 
-def write(path, seed, layers):
+def write(path, seed, layers, edit=None):
     """layers: per layer a dict of {"qkv", "out", "ffn1", "ffn2"} -> "zero" | "id" | cols array
-    (see synth_model.q8_blocks); missing entries are zero. Returns (path, tensors, perm, scale)."""
+    (see synth_model.q8_blocks); missing entries are zero. edit(p), if given, changes the random
+    non-projection tensors in place before the file is written. Returns (path, tensors, perm,
+    scale)."""
     n_layer = len(layers)
     p, perm, scale = params(seed, n_layer)
+    if edit is not None:
+        edit(p)
     shapes = {"qkv": (3 * D, D), "out": (D, D), "ffn1": (FFN, D), "ffn2": (D, FFN)}
     for li, spec in enumerate(layers):
         for name, (n, k) in shapes.items():

@@ -344,3 +344,176 @@ def test_bert_encoder_composition(ident, n_layers):
     np.testing.assert_allclose(got, ref, rtol=1e-9, atol=1e-9)
     for drop in ("b_o", "b_2"):
         assert np.max(np.abs(got - _bert_closed(W, ids, n_layers, ident, drop))) > 1e-2
+
+
+# ---------------------------------------------------------------------------- decode attention
+
+def _dec_attn_model(tmp_path_factory, name, seed, k_ident):
+    """1 layer: Wq = 0 (q = b_q), Wk = I (k = the quantised input + b_k) or 0 (k = b_k), Wv = I,
+    Wo = I; FFN zero. The head reads LN2(LN1(x + quant(attention) + b_o) + b_2)."""
+    d = tmp_path_factory.mktemp("km")
+    kcols = np.arange(KM.D) if k_ident else np.full(KM.D, -1)
+    cols = np.concatenate([np.full(KM.D, -1), kcols, np.arange(KM.D)])
+    return KM.write(str(d / name), seed, [{"qkv": cols, "out": "id"}])
+
+
+@pytest.fixture(scope="module")
+def dec_mean(tmp_path_factory):
+    """q and k constant: decode attention is the plain mean of the visible V rows."""
+    return _dec_attn_model(tmp_path_factory, "dec_mean.gguf", 14, False)
+
+
+@pytest.fixture(scope="module")
+def dec_soft(tmp_path_factory):
+    """k varies per key: the softmax weights exp(scale * b_q . k_j) depend on the scale."""
+    return _dec_attn_model(tmp_path_factory, "dec_soft.gguf", 15, True)
+
+
+def _dec_attn_logits64(p, perm, scale, x, K0, V0, b, keys, sc):
+    """Logits of a decode row of sequence b whose layer input is x: per head h, softmax over the
+    cache columns `keys` of sc * (b_q[h] . K0[b, h, j]), times V0[b, h, j]; o = quant(attention);
+    x' = LN2(LN1(x + o + b_o) + b_2) (zero FFN); then the head. float64 from the layer-0 cache
+    (whose values the K/V tests above pin)."""
+    b0 = "transformer.block0"
+    bq = p[f"{b0}.qkv_b"][:KM.D].astype(np.float32).astype(np.float64)
+    keys = np.asarray(list(keys))
+    a = np.zeros(KM.D)
+    for h in range(KM.NH):
+        sl = slice(h * KM.HD, (h + 1) * KM.HD)
+        Kh = K0[b, h, keys].astype(np.float64)
+        Vh = V0[b, h, keys].astype(np.float64)
+        s = sc * (Kh @ bq[sl])
+        w = np.exp(s - s.max())
+        a[sl] = (w / w.sum()) @ Vh
+    n1 = KM.ln64(x + _q8(a) + p[f"{b0}.out_b"], p[f"{b0}.norm1_w"], p[f"{b0}.norm1_b"])
+    return KM.head64(KM.ln64(n1 + p[f"{b0}.ffn2_b"], p[f"{b0}.norm2_w"], p[f"{b0}.norm2_b"]), perm, scale)
+
+
+def _close_frac(got, ref):
+    """Fraction of logits within the fp16-head bound of the closed form. The closed form models the
+    attention output's quantisation with the pinned quantiser; fp32 rounding moves a value across
+    a quantisation boundary for a few elements in a thousand, so the bar is a fraction."""
+    got = np.asarray(got, np.float64)
+    return float(np.mean(np.abs(got - ref) <= 2.0 ** -10 * np.abs(ref) + 1e-5))
+
+
+@pytest.mark.parametrize("model", ["dec_mean", "dec_soft"])
+def test_decode_attention_keys_scale_and_new_key(model, request):
+    """Decode step idx of sequence b attends over cache columns [pad_b, S + idx]: the left-pad
+    columns (whose V is the bias alone, x = 0) are hidden, the first valid column is seen, and the
+    key just appended at column S + idx is included; scores are scaled by 1/sqrt(32)
+    (src/gsv_ar.cpp:404-405 flash_attn_ext scale, :445-452 the decode mask)."""
+    path, p, perm, scale = request.getfixturevalue(model)
+    m = O.Model(path)
+    pe = KM.pe(64)
+    P = 5
+    reqs = _reqs(26, [3, 8, 6], P, bert=(True, False, True))
+    forced = np.array([40, 1001, 7, 300, 12, 999], np.int32)
+    n = len(forced)
+    flags = O.ORC_EOS_MASK_ALL | (O.ORC_KV_F16 if model == "dec_soft" else 0)
+    r = m.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=n, oracle=forced, seeds=[3, 4, 5],
+                   flags=flags, nthreads=N_THREADS, want_logits=True, kv_layer=0)
+    lg = r["logits"]
+    K0, V0 = r["kv"]
+    max_len = max(len(q["phones"]) for q in reqs)
+    S = max_len + P
+    assert K0.shape[2] == S + n
+    pads = [max_len - len(q["phones"]) for q in reqs]
+    assert pads[0] > 0 and pads[1] == 0
+    sc = 1.0 / np.sqrt(32.0)
+    miss = {}
+    for idx in range(n - 1):
+        x = KM.decode_input64(p, forced[idx], P + idx, pe)
+        col = S + idx
+        for b in range(len(reqs)):
+            got = lg[idx + 1, b]
+            ref = _dec_attn_logits64(p, perm, scale, x, K0, V0, b, range(pads[b], col + 1), sc)
+            assert _close_frac(got, ref) >= 0.99, (model, idx, b)
+            alts = {"pad columns visible": (range(0, col + 1), sc),
+                    "first valid column dropped": (range(pads[b] + 1, col + 1), sc),
+                    "new key excluded": (range(pads[b], col), sc),
+                    "keys up to the prefill only": (range(pads[b], S), sc)}
+            if model == "dec_soft":
+                alts["scale 1"] = (range(pads[b], col + 1), 1.0)
+                alts["scale 1/32"] = (range(pads[b], col + 1), 1.0 / 32.0)
+            for what, (keys, s2) in alts.items():
+                if list(keys) == list(range(pads[b], col + 1)) and s2 == sc:
+                    continue                     # identical to the reference for this row (pad 0)
+                alt = _dec_attn_logits64(p, perm, scale, x, K0, V0, b, keys, s2)
+                miss.setdefault(what, []).append(_close_frac(got, alt))
+    expect = {"pad columns visible", "first valid column dropped", "new key excluded",
+              "keys up to the prefill only"} | ({"scale 1", "scale 1/32"} if model == "dec_soft" else set())
+    assert set(miss) == expect
+    for what, fr in miss.items():
+        assert max(fr) < 0.5, (model, what, max(fr))
+
+
+# ---------------------------------------------------------------------------- FFN activation
+
+def _ffn_exact_edit(seed):
+    """Layer 0 with LN1 weight 0, so n1 = LN1(.) = norm1_b exactly, and norm1_b, b_1 multiples of
+    1/16 whose every 32-block (of n1, and of the hidden row h = relu(n1[r % 512] + b_1[r])) has
+    amax exactly 127/16: the x86 quantiser then maps each of those rows to itself (127/amax = 16,
+    d = 2^-4), the identity FFN1 and FFN2 are exact, and the pre-activations take both signs."""
+    def edit(p):
+        rng = np.random.default_rng(seed)
+        b = "transformer.block0"
+        n1 = rng.integers(-40, 41, KM.D).astype(np.float64)
+        pos = rng.integers(0, 32, KM.D // 32)
+        n1[np.arange(KM.D // 32) * 32 + pos] = 127.0
+        m = rng.integers(-20, 21, KM.FFN).astype(np.float64)
+        r = np.arange(KM.FFN)
+        m[(r % 32) == pos[(r % KM.D) // 32]] = 0.0
+        p[f"{b}.norm1_w"] = np.zeros(KM.D, np.float32)
+        p[f"{b}.norm1_b"] = (n1 / 16.0).astype(np.float32)
+        p[f"{b}.ffn1_b"] = (m / 16.0).astype(np.float32)
+    return edit
+
+
+@pytest.fixture(scope="module")
+def ffn_exact(tmp_path_factory):
+    """1 layer: attention and out projection zero, FFN1 = FFN2 = identity (exact, see the edit)."""
+    d = tmp_path_factory.mktemp("km")
+    return KM.write(str(d / "ffn_exact.gguf"), 16, [{"ffn1": "id", "ffn2": "id"}], edit=_ffn_exact_edit(17))
+
+
+def _ffn_logits64(p, perm, scale, act="relu", drop=None):
+    import math
+    b = "transformer.block0"
+    n1 = p[f"{b}.norm1_b"].astype(np.float64)
+    pre = n1 + (0.0 if drop == "b_1" else p[f"{b}.ffn1_b"][:KM.D].astype(np.float64))
+    if act == "relu":
+        f = np.maximum(pre, 0.0)
+    elif act == "gelu":
+        f = np.array([0.5 * t * (1.0 + math.erf(t / math.sqrt(2.0))) for t in pre])
+    else:
+        f = pre
+    res = 0.0 if drop == "n1 residual" else n1
+    x = KM.ln64(res + f + p[f"{b}.ffn2_b"], p[f"{b}.norm2_w"], p[f"{b}.norm2_b"])
+    return KM.head64(x, perm, scale)
+
+
+def test_ffn_relu_between_the_projections(ffn_exact):
+    """x' = LN2(n1 + W2 . relu(W1 . n1 + b_1) + b_2): the FFN activation is ReLU (ggml ADD_ACT,
+    PATCH:1586-1620; src/gsv_ar.cpp:262, :408), with b_1 inside it and n1 as the residual. Checked
+    on the prefill's last row and on every decode row (the layer output does not depend on the row
+    here, since n1 = norm1_b)."""
+    path, p, perm, scale = ffn_exact
+    m = O.Model(path)
+    reqs = _reqs(27, [4, 9], 6)
+    ref = _ffn_logits64(p, perm, scale)
+    bound = 2.0 ** -10 * np.abs(ref) + 1e-6
+    got = m.first_logits(reqs, nthreads=N_THREADS)
+    forced = np.array([5, 600, 1000], np.int32)
+    r = m.generate(reqs, sampler=(1, 1.0, 1.0, 1.0), max_steps=len(forced), oracle=forced, seeds=[1, 2],
+                   flags=O.ORC_EOS_MASK_ALL | O.ORC_KV_F16, nthreads=N_THREADS, want_logits=True)
+    rows = [got[0], got[1]] + [r["logits"][i, b] for i in range(1, len(forced)) for b in range(2)]
+    for row in rows:
+        assert _excess(row, ref, bound) <= 1.0
+    pre = p["transformer.block0.norm1_b"].astype(np.float64) + p["transformer.block0.ffn1_b"][:KM.D]
+    assert (pre < -0.5).sum() > 100 and (pre > 0.5).sum() > 100     # both signs, away from 0
+    for what, alt in {"GELU": _ffn_logits64(p, perm, scale, "gelu"),
+                      "no activation": _ffn_logits64(p, perm, scale, "none"),
+                      "b_1 dropped": _ffn_logits64(p, perm, scale, drop="b_1"),
+                      "n1 residual dropped": _ffn_logits64(p, perm, scale, drop="n1 residual")}.items():
+        assert _excess(rows[0], alt, bound) > 10, what
