@@ -18,7 +18,10 @@ of the two-launch layer at batch <= 16) alone with HIP events on the stream it r
 mid-run shape of the line's own steps, rotating through buffers larger than the 256 MB MALL; its
 traffic is the HBM-counter ratio of profiles/decode_layer_b16_hbm.md times those algorithmic
 bytes. cpu_baseline times the oracle (the CPU restatement of the reference path) on this host's
-cores on the same requests and the same steps, repeated to at least 10 s of decode.
+cores on the same requests and the same steps, repeated to at least 10 s of decode; with the
+oracle as the checker it also counts, under teacher forcing, the steps whose device choice differs
+from the oracle's (default path and exact mode, batch 16 and batch 1). extra.exact_mode times
+exact mode (ggml-cpu's arithmetic order, the oracle's logits to the bit) on the same workloads.
 """
 from __future__ import annotations
 
@@ -291,6 +294,43 @@ def cpu_baseline(reqs, steps, min_s=10.0):
                       f"untimed); F32 KV cache, OpenMP over {nthreads} threads"}
 
 
+def token_parity(g, reqs, cfg, steps, seeds):
+    """Token identity against the oracle (the checker, fp16 KV as on the device) on the same
+    requests, sampler, seeds and steps. The oracle runs freely; its sequence-0 tokens are then
+    forced on both sides (the reference's oracle_tokens), so that every step of every sequence
+    sees the same history, and the device's choice before the override is compared with the
+    oracle's at every step. Reported for the default path and for exact mode, plus whether exact
+    mode's free run gives the oracle's free-run tokens."""
+    import gsvk
+    import oracle
+    import synth_model as sm
+    path = sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER)
+    o = oracle.Model(path)
+    fl = oracle.ORC_KV_F16 | oracle.ORC_EOS_MASK_ALL
+    try:
+        free = o.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=fl)
+        forced = free["sampled"][:, 0].astype(np.int32)
+        ref = o.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, oracle=forced, flags=fl)
+    finally:
+        o.close()
+    flags = gsvk.GSVK_GEN_EOS_MASK_ALL
+    out = {"choices": len(reqs) * steps}
+    for mode in ("default", "exact"):
+        g.set_exact(mode == "exact")
+        try:
+            r = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, oracle=forced, flags=flags,
+                           want_sampled=True)
+            d = {"teacher_forced_differ": int((r["sampled"] != ref["sampled"][:steps]).sum())}
+            if mode == "exact":
+                rf = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=flags)
+                d["free_run_tokens_equal"] = all(np.array_equal(rf["tokens"][b], free["tokens"][b])
+                                                 for b in range(len(reqs)))
+        finally:
+            g.set_exact(False)
+        out[mode] = d
+    return out
+
+
 def prefill_line(g, torch):
     """Prefill of batch 16 x 1024 rows (valid lengths U[512, 1024], 256 prompt codes), 24 layers:
     median wall time of 3 calls after one warm-up, and TFLOP/s over prefill_flops; the same in the
@@ -455,13 +495,32 @@ def main():
              "step_bytes_mb": round(step_bytes / 1e6, 1),
              "step_hbm_frac": round(step_bytes / (ms_step / 1e3) / 1e9 / HBM_PEAK_GBS, 4)}
     # batch 1 as the reference's single-sequence case: 128 phones + 64 prompt codes (prefill 192),
-    # 300 greedy steps with EOS masked
+    # 300 greedy steps (repetition penalty 1.35) with EOS masked
     r1 = sm.synth_requests(0x6A5E0001, 1, 64, [128])
-    g.generate(r1, sampler=(1, 1.0, 1.0, 1.0), max_steps=8, seeds=[1], flags=flags)
-    rb = g.generate(r1, sampler=(1, 1.0, 1.0, 1.0), max_steps=300, seeds=[1], flags=flags)
+    cfg1 = (1, 1.0, 1.0, 1.35)
+    g.generate(r1, sampler=cfg1, max_steps=8, seeds=[1], flags=flags)
+    rb = g.generate(r1, sampler=cfg1, max_steps=300, seeds=[1], flags=flags)
     extra["tok_s_b1"] = round(300 / (rb["decode_ms"] / 1e3), 1)
     extra["ms_per_step_b1"] = round(rb["decode_ms"] / 300, 4)
-    extra["b1_workload"] = "1 sequence, 128 phones + 64 prompt codes, 300 greedy steps"
+    extra["b1_workload"] = "1 sequence, 128 phones + 64 prompt codes, 300 greedy steps, repetition penalty 1.35"
+    # exact mode (ggml-cpu's arithmetic order throughout: the oracle's logits to the bit) on the same
+    # two workloads
+    g.set_exact(True)
+    try:
+        if B > 16:
+            raise SystemExit("exact mode decodes at most 16 sequences")
+        g.generate(r1, sampler=cfg1, max_steps=8, seeds=[1], flags=flags)
+        rx1 = g.generate(r1, sampler=cfg1, max_steps=300, seeds=[1], flags=flags)
+        g.generate(reqs, sampler=cfg, max_steps=max(args.warmup, 1), seeds=list(range(1, B + 1)), flags=flags)
+        rx = g.generate(reqs, sampler=cfg, max_steps=args.steps, seeds=list(range(1, B + 1)), flags=flags)
+    finally:
+        g.set_exact(False)
+    extra["exact_mode"] = {"tok_s": round(B * args.steps / (rx["decode_ms"] / 1e3), 1),
+                           "ms_per_step": round(rx["decode_ms"] / args.steps, 4),
+                           "tok_s_b1": round(300 / (rx1["decode_ms"] / 1e3), 1),
+                           "ms_per_step_b1": round(rx1["decode_ms"] / 300, 4),
+                           "what": "gsvk_model_set_exact: the same workloads with ggml-cpu's arithmetic "
+                                   "order throughout (logits equal to the oracle's to the bit)"}
     # batch 64: the batch-16 workload's request shape at 64 sequences, 200 steps
     _, rb, _ = run(64, 200, 8)
     extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)
@@ -495,6 +554,16 @@ def main():
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(reqs, args.steps)
+        g = gsvk.Model(path, device=0)
+        try:
+            cpu["token_parity"] = {
+                "batch16": token_parity(g, reqs, cfg, args.steps, list(range(1, B + 1))),
+                "batch1": token_parity(g, r1, cfg1, 300, [1]),
+                "what": "the oracle (fp16 KV) as the checker: its tokens forced on both sides, the "
+                        "device's choice before the override compared at every step; default path "
+                        "and exact mode"}
+        finally:
+            g.close()
 
     line = {
         "metric": "AR decode tokens/sec at batch 1/16/64; attn+Q8_0 GEMV % of HBM roofline",

@@ -27,6 +27,9 @@
 // fp16(V) (about 2^-11 relative, 5e-4 of the output's scale): V's remainder is neither split nor
 // staged and P is rounded instead of split; the scores keep their three products (their error
 // would pass through the exponential).
+#include <algorithm>
+#include <vector>
+
 #include "common.h"
 #include "layer.h"
 
@@ -154,8 +157,9 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
     const int ke_g = min(key_end(qlast_g), S);
     // tiles start at the first valid key: a sequence's arithmetic does not depend on its left pad
     const int kt0 = pb;
-    // skip_pad: queries of left-padding rows are not computed (their rows get zeros). A wave of
-    // padding queries only helps stage the tiles; a workgroup of them stages none (uniform).
+    // skip_pad: a wave whose 32 queries are all left-padding rows computes nothing (those rows
+    // get zeros); it only helps stage the tiles, and a workgroup of such waves stages none
+    // (uniform). Padding queries in a wave with valid ones are computed as the masks give them.
     const bool idle = skip_pad && qw + PM_Q <= pb;
     const int kend = skip_pad && q0w + PM_Q * PM_WAVES <= pb ? kt0 : ke_g;
 
@@ -328,7 +332,7 @@ __global__ void __launch_bounds__(PM_WAVES * 64) k_attn_prefill_mfma(
 
 int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                              int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream,
-                             bool pv_f16, const int32_t * seq_order) {
+                             bool pv_f16, const int32_t * seq_order, bool skip_pad) {
     GSVK_REQUIRE(qkv && pad && out && B > 0 && S > 0 && nh * 32 == d_model && max_len <= S,
                  "attn_prefill_mfma: bad arguments");
     GSVK_REQUIRE((oq == nullptr) == (od == nullptr), "attn_prefill_mfma: oq and od go together");
@@ -337,10 +341,10 @@ int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const
     const dim3 grid((unsigned) ((S + PM_Q * PM_WAVES - 1) / (PM_Q * PM_WAVES)), (unsigned) nh, (unsigned) B);
     if (pv_f16)
         hipLaunchKernelGGL(k_attn_prefill_mfma<false>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) (seq_order != nullptr));
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) skip_pad);
     else
         hipLaunchKernelGGL(k_attn_prefill_mfma<true>, grid, dim3(PM_WAVES * 64), 0, stream, qkv, S, max_len, pad,
-                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) (seq_order != nullptr));
+                           nh, d_model, scale * 1.4426950408889634f, out, oq, od, seq_order, (int) skip_pad);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -351,7 +355,29 @@ extern "C" int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len
                                     int hd, float scale, int path, float * out, int8_t * oq, float * od,
                                     void * stream) {
     GSVK_REQUIRE(hd == 32, "attn_prefill: head_dim must be 32");
-    GSVK_REQUIRE(path >= 0 && path <= 3, "attn_prefill: path must be 0 (auto), 1, 2 or 3");
+    GSVK_REQUIRE(path >= 0 && path <= 4, "attn_prefill: path must be 0 (auto), 1, 2, 3 or 4");
+    if (path == 4) {
+        // the decoder prefill's dispatch: sequences longest first (the fewest padding rows; equal
+        // pads in index order), each sequence's query blocks from the last, waves of padding
+        // queries skipped. The order is built on the host from pad and lives in a temporary
+        // device array; the stream is synchronised before it is freed.
+        GSVK_REQUIRE(B > 0 && pad, "attn_prefill: bad arguments");
+        hipStream_t st = (hipStream_t) stream;
+        std::vector<int32_t> hp((size_t) B), order((size_t) B);
+        GSVK_HIP(hipMemcpyAsync(hp.data(), pad, (size_t) B * 4, hipMemcpyDeviceToHost, st));
+        GSVK_HIP(hipStreamSynchronize(st));
+        for (int b = 0; b < B; b++) order[(size_t) b] = b;
+        std::stable_sort(order.begin(), order.end(), [&](int a, int c) { return hp[(size_t) a] < hp[(size_t) c]; });
+        int32_t * d_order = nullptr;
+        GSVK_HIP(hipMalloc(&d_order, (size_t) B * 4));
+        int rc = hipMemcpyAsync(d_order, order.data(), (size_t) B * 4, hipMemcpyHostToDevice, st) == hipSuccess
+                     ? gsvk::launch_attn_prefill_mfma(qkv, B, S, max_len, pad, nh, nh * hd, scale, out, oq, od, st,
+                                                      false, d_order, true)
+                     : GSVK_ERR_HIP;
+        if (hipStreamSynchronize(st) != hipSuccess && rc == GSVK_OK) rc = GSVK_ERR_HIP;
+        (void) hipFree(d_order);
+        return rc;
+    }
     const bool mfma = path >= 2 || (path == 0 && gsvk::attn_prefill_uses_mfma((int64_t) B * S));
     if (mfma)
         return gsvk::launch_attn_prefill_mfma(qkv, B, S, max_len, pad, nh, nh * hd, scale, out, oq, od,

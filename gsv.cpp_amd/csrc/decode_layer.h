@@ -90,7 +90,8 @@ struct DecFfnArgs {
 };
 
 // 1 when the two-launch layer covers this shape: d_model 512, 16 heads of 32, FFN 2048, at most
-// 16 sequences, and rows the attention takes in one workgroup per (sequence, head).
+// DEC_MAX_BATCH (64) sequences (the library's default choice up to DEC_AUTO_MAX_BATCH, 32), and rows
+// the attention takes in one workgroup per (sequence, head).
 bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys);
 int launch_dec_attn(const DecAttnArgs & a, hipStream_t stream);
 int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream);

@@ -110,12 +110,13 @@ constexpr int DECODE_GEMM_MIN_BATCH = GEMV_DECODE_MAX_BATCH + 1;
 // Prefill self-attention on the matrix cores (attn_prefill_mfma.hip): qkv rows [B][S][3*d_model],
 // head_dim 32, 16-byte aligned qkv and out; used from GEMM_MIN_ROWS rows on, like the GEMM.
 // pv_f16: the weighted sum as one fp16 product (the prefill's fp16 mode) instead of hi/lo pairs.
-// seq_order: a permutation of the B sequences, dispatched in that order (longest first), or null;
-// with it, the queries of left-padding rows are not computed and their rows get zeros (the
-// decoder's prefill, where no valid row reads them).
+// seq_order: a permutation of the B sequences, dispatched in that order (longest first), or null
+// (index order); the order changes only the dispatch, not a value. skip_pad: a wave whose 32 queries
+// are all left-padding rows computes nothing and those rows get zeros (the decoder's prefill, where
+// no valid row reads them); padding queries sharing a wave with valid ones are computed.
 int launch_attn_prefill_mfma(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                              int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream,
-                             bool pv_f16 = false, const int32_t * seq_order = nullptr);
+                             bool pv_f16 = false, const int32_t * seq_order = nullptr, bool skip_pad = false);
 inline bool attn_prefill_uses_mfma(int64_t rows) { return rows >= GEMM_MIN_ROWS; }
 
 // n % 32 == 0, k in {512, 2048}; IN_LN and IN_EMB need k == 512.

@@ -28,7 +28,10 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
     // one wave per row, up to 4 rows per workgroup (the waves are independent: no barrier)
     const int row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (row >= rows) return;
-    if (row_pad && row % rows_per_seq < row_pad[row / rows_per_seq]) return;   // a padding row
+    // a left-padding row (prefill) is normalised from zeros instead of its stale input: its
+    // output is the LayerNorm bias, finite, without reading the row (no valid row reads it, but
+    // the matrix-core tiles that mix padding and valid rows multiply it)
+    const bool pad_row = row_pad && row % rows_per_seq < row_pad[row / rows_per_seq];
     const int lane = threadIdx.x & 63;
     const int nchunk = n / 8;
     const float * xr = x + (int64_t) row * n;
@@ -45,20 +48,22 @@ __global__ void __launch_bounds__(256) k_layernorm(const float * __restrict__ x,
         const bool act = lane + 64 * c < nchunk;
         const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         xv[c][0] = xv[c][1] = wv[c][0] = wv[c][1] = cv[c][0] = cv[c][1] = z;
-        if (act) {   // (an explicit branch: a select of the load would become per-word loads)
+        if (act && !pad_row) {   // (an explicit branch: a select of the load would become per-word loads)
             xv[c][0] = *reinterpret_cast<const float4 *>(xr + base);
             xv[c][1] = *reinterpret_cast<const float4 *>(xr + base + 4);
+        }
+        if (act) {
             wv[c][0] = *reinterpret_cast<const float4 *>(wb + base);
             wv[c][1] = *reinterpret_cast<const float4 *>(wb + base + 4);
             cv[c][0] = *reinterpret_cast<const float4 *>(wb + n + base);
             cv[c][1] = *reinterpret_cast<const float4 *>(wb + n + base + 4);
         }
         rv[c][0] = rv[c][1] = bv[c][0] = bv[c][1] = z;
-        if (rr && act) {
+        if (rr && act && !pad_row) {
             rv[c][0] = *reinterpret_cast<const float4 *>(rr + base);
             rv[c][1] = *reinterpret_cast<const float4 *>(rr + base + 4);
         }
-        if (bias && act) {
+        if (bias && act && !pad_row) {
             bv[c][0] = *reinterpret_cast<const float4 *>(bias + base);
             bv[c][1] = *reinterpret_cast<const float4 *>(bias + base + 4);
         }

@@ -466,8 +466,9 @@ int layer_tail(gsvk_model * m, hipStream_t st, const LayerW & w, int64_t R, cons
                            : launch_q8_gemm(q8w(l), n, k, R, xs, xd, layout, out, st);
         };
         GSVK_TRY(gemm(w.out, D, D, attn.q, attn.d, oo));
-        // (prefill: the left-padding rows are skipped; no valid row reads their LN1 rows, and
-        // their FFN rows stay in those rows)
+        // (prefill: the left-padding rows are normalised from zeros, without reading their
+        // rows: no valid row reads them, and the FFN GEMM tiles that mix them with valid rows get
+        // finite values)
         GSVK_TRY(launch_layernorm(cur_x, o, w.out.b, w.ln1, R, D, 1e-5f, n1x, n1->q, n1->d, st, layout, nullptr,
                                   row_pad, rows_per_seq));
         LayerOut ho{};
@@ -766,13 +767,16 @@ int enqueue_decode_body(gsvk_model * m) {
                      DECODE_GEMM_MIN_BATCH - 1, m->B);
         return enqueue_decode_rows(m, 0, m->B, m->stream);
     }
+    // an explicit choice runs as asked or fails: it never falls back to another path
     switch (m->decode_path) {
     case GSVK_DECODE_GEMV:
-        if (m->B < DECODE_GEMM_MIN_BATCH) return enqueue_decode_rows(m, 0, m->B, m->stream);
-        break;
+        GSVK_REQUIRE(m->B < DECODE_GEMM_MIN_BATCH, "decode path GEMV: %d sequences (it decodes at most %d)",
+                     m->B, DECODE_GEMM_MIN_BATCH - 1);
+        return enqueue_decode_rows(m, 0, m->B, m->stream);
     case GSVK_DECODE_FUSED:
-        if (fused_decode_ok(m)) return enqueue_decode_fused(m);
-        break;
+        GSVK_REQUIRE(fused_decode_ok(m), "decode path FUSED: not available for %d sequences (at most %d) "
+                     "or for this model (it needs an F16 or F32 head)", m->B, DEC_MAX_BATCH);
+        return enqueue_decode_fused(m);
     case GSVK_DECODE_MFMA:
         return enqueue_decode_mfma(m);
     default:
@@ -953,8 +957,8 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
         const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
         if (gemm) {
             // LN2 of the previous layer as its own launch, then the QKV GEMM on its Q8_0 copy; the
-            // left-padding rows are skipped and keep their layer-0 input (zeros: finite K/V rows
-            // that no query attends)
+            // left-padding rows are normalised from zeros (the LayerNorm bias: finite K/V rows that
+            // no query attends)
             if (li > 0) {
                 const LayerW & p = m->L[li - 1];
                 GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st,
@@ -986,7 +990,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
                                                attn.d, st));
         else if (attn_prefill_uses_mfma(rows))
             GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
-                                              attn.d, st, gemm && m->prefill_f16, d_order));
+                                              attn.d, st, gemm && m->prefill_f16, d_order, true));
         else
             GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, attn.q,
                                          attn.d, st));

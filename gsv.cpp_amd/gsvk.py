@@ -300,7 +300,8 @@ def op_dec_ffn(B, res, p1, bo, ln1_wb, n1_out, w1q, w1d, b1, w2q, w2d, p2, strea
 
 def op_attn_prefill(qkv, max_len, pad, nh, scale, out, oq=None, od=None, path=0, stream=None):
     """qkv [B][S][3*D] fp32, pad int32 [B] (device); out [B][S][D]; path 0 auto, 1 lane-per-query,
-    2 matrix cores, 3 matrix cores with the weighted sum on fp16 operands (the fp16 prefill mode)."""
+    2 matrix cores, 3 matrix cores with the weighted sum on fp16 operands (the fp16 prefill mode),
+    4 matrix cores in the decoder prefill's dispatch (longest first, padding-only waves skipped)."""
     B, S, three_d = qkv.shape
     hd = three_d // 3 // nh
     check(lib().gsvk_op_attn_prefill(_p(qkv), B, S, max_len, _p(pad), nh, hd, scale, path, _p(out), _p(oq),

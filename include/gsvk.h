@@ -152,8 +152,9 @@ int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * 
  *                    units): the same int32 block dots, fp32 sums over heads and groups in a fixed
  *                    order (agrees with the GEMV chain to fp32 rounding);
  *  GSVK_DECODE_MFMA  the matrix-core GEMMs at any batch.
- * A choice that does not cover the batch (or model) falls back to AUTO's. No counterpart in the
- * reference (it has one CPU path); for tests and benchmarks. */
+ * An explicit choice that does not cover the batch (or model: FUSED needs an F16 / F32 head) makes
+ * the decode fail with an error naming it; it never falls back to another path. No counterpart
+ * in the reference (it has one CPU path); for tests and benchmarks. */
 #define GSVK_DECODE_AUTO   0
 #define GSVK_DECODE_GEMV   1
 #define GSVK_DECODE_FUSED  2
@@ -434,8 +435,11 @@ int gsvk_op_dec_ffn(int B, const float * res, const float * p1, const float * bo
  * lane-per-query kernel, natural order from the matrix-core kernel). path 0 picks the kernel the
  * prefill uses for B*S rows, 1 the lane-per-query kernel, 2 the matrix-core kernel, 3 the
  * matrix-core kernel with the weighted sum as one product of fp16 probabilities and fp16 values
- * (the prefill's fp16 mode, gsvk_model_set_prefill_f16; about 5e-4 of the output's scale). hd must
- * be 32; qkv and out 16-byte aligned. */
+ * (the prefill's fp16 mode, gsvk_model_set_prefill_f16; about 5e-4 of the output's scale), 4 the
+ * matrix-core kernel as the decoder's prefill dispatches it (sequences longest first; a wave whose
+ * 32 queries are all left-padding rows computes nothing and those rows are zero; the other rows
+ * equal path 2's to the bit; it reads pad to the host and synchronises the stream). hd must be 32;
+ * qkv and out 16-byte aligned. */
 int gsvk_op_attn_prefill(const float * qkv, int B, int S, int max_len, const int32_t * pad, int nh,
                          int hd, float scale, int path, float * out, int8_t * oq, float * od,
                          void * stream);

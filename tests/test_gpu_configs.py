@@ -12,13 +12,14 @@ that hold at any size and an oracle check on the sequence the oracle finishes in
   appears with the bit-exact GEMV and the lane-per-query attention, so the bound below (2e-2) is
   that of the model's re-quantisation, not of the matrix-core kernels, whose own outputs are
   checked to 2e-3 (in practice ~1e-6) op by op.
-* Decode at batch 128 with KV lengths U[1024, 4096] (27 GB fp16 KV cache): teacher-forced greedy
-  steps; the shortest sequence's sampled tokens equal the oracle's run of that sequence alone,
-  except where the oracle's top two logits are within 2e-3 of each other.
+* Decode at batch 128 with KV lengths U[1024, 4096] (27 GB fp16 KV cache): 32 teacher-forced
+  greedy steps; the three shortest sequences' choices equal the oracle's run of each sequence
+  alone, except at fragile steps (tests/fragile.py).
 """
 import numpy as np
 import pytest
 
+import fragile as FR
 import oracle as O
 import synth_model as sm
 
@@ -30,17 +31,6 @@ def _lengths(seed, B, lo, hi):
     L = rng.integers(lo, hi + 1, B)
     L[0] = hi
     return L
-
-
-def _penalised_top2(logits, hist, rep=1.35, mask_eos=None):
-    row = logits.astype(np.float32).copy()
-    if mask_eos is not None:
-        row[mask_eos] = -np.inf
-    for t in hist[-4096:]:
-        s = row[t]
-        row[t] = s * np.float32(rep) if s < 0 else s / np.float32(rep)
-    o = np.argsort(-row, kind="stable")
-    return o[0], float(row[o[0]] - row[o[1]]), float(np.abs(row[np.isfinite(row)]).max())
 
 
 def test_prefill_16x1024(gpu, model24_path):
@@ -128,29 +118,38 @@ def test_prefill_16x1024_fp16_mode(gpu, model24_path):
 
 
 def test_decode_batch128_long_kv(gpu, model24_path):
-    P, steps = 64, 6
+    """Batch 128, KV lengths U[1024, 4096], 32 teacher-forced greedy steps (repetition penalty
+    1.35): the generate graph's choices equal those of the per-step path's logits, and for the
+    three shortest sequences (each run alone by the oracle) every choice is the oracle's except at
+    a fragile step (one whose measured logit drift could change it)."""
+    P, steps = 64, 32
     L = _lengths(0x6A5E0005, 128, 1024, 4096)
     reqs = sm.synth_requests(0x6A5E0005, 128, P, L - P, bert=False)
     forced = np.random.default_rng(12).integers(0, 1024, steps).astype(np.int32)
     greedy = (1, 1.0, 1.0, 1.35)
+    seeds = list(range(1, 129))
     g = gpu.Model(model24_path)
     try:
-        print("decode: batch 128, KV lengths U[1024, 4096]", flush=True)
-        res = g.generate(reqs, sampler=greedy, max_steps=steps, oracle=forced, flags=1, want_sampled=True)
+        print("decode: batch 128, KV lengths U[1024, 4096], generate", flush=True)
+        res = g.generate(reqs, sampler=greedy, max_steps=steps, oracle=forced, seeds=seeds, flags=1,
+                         want_sampled=True)
+        print("decode: batch 128, per-step logits", flush=True)
+        dev = FR.device_step_logits(g, reqs, forced, steps)
         g.release_cache()
     finally:
         g.close()
     assert res["n_steps"] == steps
-    short = int(np.argmin(L))
     o = O.Model(model24_path)
     try:
-        ref = o.generate([reqs[short]], sampler=greedy, max_steps=steps, oracle=forced,
-                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+        for s in np.argsort(L, kind="stable")[:3]:
+            print(f"oracle: sequence {s} alone, {L[s]} rows, {steps} steps", flush=True)
+            ref = o.generate([reqs[s]], sampler=greedy, max_steps=steps, oracle=forced, seeds=[seeds[s]],
+                             flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+            assert np.array_equal(res["tokens"][s], ref["tokens"][0])
+            n_mis, n_fr, worst = FR.check_choices([reqs[s]], greedy, forced, [seeds[s]], ref,
+                                                  {"sampled": res["sampled"][:, [s]]}, dev[:, [s]], steps)
+            print(f"sequence {s}: {n_mis} of {steps} choices differ, {n_fr} fragile, drift {worst:.2e}",
+                  flush=True)
+            assert worst <= 3e-2, worst
     finally:
         o.close()
-    assert np.array_equal(res["tokens"][short], ref["tokens"][0])
-    for i in range(steps):
-        if res["sampled"][i, short] != ref["sampled"][i, 0]:
-            hist = np.concatenate([reqs[short]["prompt"], forced[:i]])
-            _, margin, scale = _penalised_top2(ref["logits"][i, 0], hist, mask_eos=1024)
-            assert margin <= 2e-3 * scale, (i, margin, scale)

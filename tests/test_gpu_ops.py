@@ -354,16 +354,29 @@ def test_attn_decode_empty_and_constant(gpu):
 
 
 def test_attn_decode_microbench_shape(gpu):
-    """The decode-attention microkernel configuration at reduced batch: 16 heads x 32,
-    KV lengths uniform 256-2048, one query per sequence."""
+    """The decode-attention microkernel configuration at its own shape and launch, as the
+    benchmark times it: batch 64 x 16 heads x 32, one query per sequence, KV lengths uniform
+    256-2048 from the benchmark's seed, fp16 K/V ~ N(0,1), planned for 2048 keys (one workgroup
+    per (sequence, head), 8 waves, no split), fp32 output and its fp16 copy."""
     import torch
-    rng = np.random.default_rng(32)
-    B, nh, lstride = 16, 16, 2048
+    rng = np.random.Generator(np.random.PCG64(0x6A5E0003))
+    B, nh, lstride = 64, 16, 2048
     L = rng.integers(256, 2049, B)
-    q, k, v, kb, ke = _attn_case(rng, B, nh, lstride, np.zeros(B), L)
-    got, scale, _ = _run_attn(gpu, torch, q, k, v, kb, ke, lstride)
+    q, k, v, kb, ke = _attn_case(np.random.default_rng(32), B, nh, lstride, np.zeros(B), L)
+    scale = np.float32(1.0) / np.sqrt(np.float32(32.0))
+    out = torch.zeros((B, nh * 32), dtype=torch.float32, device="cuda")
+    out16 = torch.zeros((B, nh * 32), dtype=torch.float16, device="cuda")
+    ws = torch.zeros(gpu.attn_workspace_bytes(B, nh, lstride), dtype=torch.uint8, device="cuda")
+    gpu.op_attn_decode(_dev(q, torch), _dev(k, torch), _dev(v, torch), _dev(kb, torch), _dev(ke, torch), lstride,
+                       float(scale), out, out16=out16, ws=ws)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
     ref = O.attn_decode_f16(q, k, v, kb, ke, scale)
-    assert np.abs(got - ref).max() / np.abs(ref).max() <= 2e-3
+    rel = np.abs(got - ref).max() / np.abs(ref).max()
+    assert rel <= 2e-3, rel
+    assert rel <= 1e-5, rel
+    # the fp16 output is the fp32 output rounded to nearest even
+    assert np.array_equal(out16.cpu().numpy(), got.astype(np.float16))
 
 
 @pytest.mark.parametrize("B,lstride", [(16, 1000), (3, 300), (40, 200), (64, 700), (1, 64)])
@@ -636,3 +649,42 @@ def test_attn_prefill_matches_oracle(gpu, B, S, max_len, pads, what, path):
     assert np.array_equal(q_got, q_ref)
     d_ref32 = d_ref.view(np.float16).astype(np.float32)
     assert np.array_equal(od.cpu().numpy().reshape(B * S, -1).view(np.uint32), d_ref32.view(np.uint32))
+
+
+def test_attn_prefill_decoder_dispatch(gpu):
+    """Path 4, the matrix-core prefill attention as the decoder's prefill dispatches it (sequences
+    longest first, query blocks last first, waves of 32 padding queries skipped), with left pads
+    that do not fall on a 32-query wave or a 256-query workgroup boundary: every row of a valid
+    query and every padding row that shares a wave with one equals path 2's to the bit (and the
+    oracle within 2e-5); the rows of padding-only waves are zero."""
+    import torch
+    nh, D = 16, 512
+    B, S, max_len = 5, 384, 320
+    pads = np.array([0, 17, 33, 255, 300], np.int32)
+    rng = np.random.default_rng(77)
+    qkv = rng.standard_normal((B, S, 3 * D)).astype(np.float32)
+    qkv[:, :, :D] *= 2.0
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(32)))
+    outs = {}
+    for path in (2, 4):
+        out = torch.zeros(B * S * D, dtype=torch.float32, device="cuda")
+        oq = torch.zeros(B * S * D, dtype=torch.int8, device="cuda")
+        od = torch.zeros(B * S * D // 32, dtype=torch.float32, device="cuda")
+        gpu.op_attn_prefill(_dev(qkv, torch), max_len, _dev(pads, torch), nh, scale, out, oq, od, path=path)
+        torch.cuda.synchronize()
+        outs[path] = (out.cpu().numpy().reshape(B, S, D), oq.cpu().numpy().reshape(B, S, D),
+                      od.cpu().numpy().reshape(B, S, D // 32))
+    ref = O.attn_prefill(qkv, max_len, pads, nh, scale)
+    a, b4 = outs[2], outs[4]
+    n_zero = 0
+    for b in range(B):
+        for s in range(S):
+            if (s // 32) * 32 + 32 <= pads[b]:          # a wave of padding queries only
+                assert np.all(b4[0][b, s] == 0.0), (b, s)
+                n_zero += 1
+            else:
+                assert np.array_equal(b4[0][b, s].view(np.uint32), a[0][b, s].view(np.uint32)), (b, s)
+                assert np.array_equal(b4[1][b, s], a[1][b, s]) and np.array_equal(b4[2][b, s], a[2][b, s]), (b, s)
+    assert n_zero == sum(int(p) // 32 * 32 for p in pads)
+    valid = np.concatenate([ref[b, pads[b]:] - b4[0][b, pads[b]:] for b in range(B)])
+    assert np.abs(valid).max() / np.abs(ref).max() <= 2e-5

@@ -1,7 +1,8 @@
 """A model loaded from the pre-swizzled GGUF (gsv.cpp_amd/gguf_tiled.py: layer projections in
 the matrix-core operand order, the sliced and natural copies derived on the device) computes the
 same bits as the one loaded from the Q8_0 block form: prefill and step logits and the K/V cache,
-on the two-launch layer, the GEMV chain and the matrix-core path (batch 20), and in exact mode."""
+on the two-launch layer, the GEMV chain and the matrix-core path (batch 20), and in exact mode;
+in exact mode the tiled file also gives the oracle's logits to the bit."""
 import numpy as np
 import pytest
 
@@ -53,3 +54,25 @@ def test_tiled_file_gives_the_same_bits(gpu, model4_path, tiled4, B, path, exact
     b = _run(gpu, tiled4, reqs, forced, steps, pid, exact)
     assert np.array_equal(a[0].view(np.uint32), b[0].view(np.uint32))
     assert np.array_equal(a[1], b[1]) and np.array_equal(a[2], b[2])
+
+
+def test_tiled_file_exact_mode_equals_the_oracle(gpu, model4_path, tiled4):
+    """The pre-swizzled file, loaded in exact mode, gives the oracle's logits (the oracle reading
+    the reference exporter's Q8_0 block form, tools/export_gguf/convert_ar.py:76-130) to the bit:
+    the prefill's last-row logits and those entering every teacher-forced decode step."""
+    import oracle as O
+    rng = np.random.default_rng(950)
+    B = 3
+    reqs = sm.synth_requests(951, B, 16, rng.integers(3, 40, B))
+    steps = 8
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    o = O.Model(model4_path)
+    try:
+        ref = o.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+    finally:
+        o.close()
+    print("tiled file, exact mode, batch 3 against the oracle", flush=True)
+    got, _, _ = _run(gpu, tiled4, reqs, forced, steps, None, True)
+    assert np.array_equal(got.view(np.uint32), ref["logits"][:steps].view(np.uint32)), \
+        np.abs(got - ref["logits"][:steps]).max()

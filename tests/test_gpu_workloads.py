@@ -30,65 +30,11 @@ oracle's free run's tokens, every one of every sequence.
 import numpy as np
 import pytest
 
+import fragile as FR
 import oracle as O
 import synth_model as sm
 
 pytestmark = pytest.mark.gpu
-
-V, EOS = 1025, 1024
-
-
-def _penalised(cfg, z, hist):
-    """The sampler's row after EOS masking (every step here), the repetition penalty and the
-    temperature (top_k = V and top_p = 1 leave it whole): the oracle's own pinned function."""
-    row = np.array(z, np.float32)
-    row[EOS] = -np.inf
-    out, _ = O.logits_to_probs((V, 1.0, cfg[2], cfg[3]), row, hist)
-    return out
-
-
-def _decision(cfg, z, hist, q):
-    """The sampler's choice for the logits z entering a step, with the step's exponential draws q:
-    the oracle's pinned gsv_logits_to_probs and argmax p / q (EOS masked first)."""
-    row = np.array(z, np.float32)
-    row[EOS] = -np.inf
-    _, probs = O.logits_to_probs(cfg, row, hist)
-    return int(O.lib().orc_argmax_probs_over_q(probs, np.ascontiguousarray(q, np.float32), V))
-
-
-def _fragile(cfg, zrow, q, e, tok):
-    """Could a perturbation of every logit by at most e change the choice tok? Either tok can
-    leave the top-k set (it is within 2e of the (k+1)-th largest), or another token that can be in
-    that set (within 2e of the k-th largest) scores z - log q within 2e of tok's (greedy: the top
-    two within 2e)."""
-    k = cfg[0]
-    fin = np.isfinite(zrow)
-    zs = np.sort(zrow[fin])[::-1]
-    kk = min(k, int(fin.sum()))
-    zk = zs[kk - 1]
-    zk1 = zs[kk] if kk < len(zs) else -np.inf
-    cand = fin & (zrow >= zk - 2 * e)
-    cand[tok] = False
-    if not cand.any():
-        return False
-    if zrow[tok] <= zk1 + 2 * e:
-        return True
-    score = zrow.astype(np.float64) - np.log(q.astype(np.float64))
-    return bool(np.any(score[cand] >= score[tok] - 2 * e - 1e-6))
-
-
-def _device_step_logits(g, reqs, forced, steps):
-    """Prefill + steps - 1 decode steps fed the forced tokens: the logits entering each step."""
-    import gsvk
-    B = len(reqs)
-    S = max(len(r["phones"]) for r in reqs) + len(reqs[0]["prompt"])
-    gsvk.check(gsvk.lib().gsvk_kv_alloc(g.h, B, S + steps + 8), "kv_alloc")
-    lg, _ = g.prefill(reqs)
-    out = np.zeros((steps, B, V), np.float32)
-    out[0] = lg
-    for i in range(steps - 1):
-        out[i + 1] = g.decode_step(np.full(B, forced[i], np.int32))
-    return out
 
 
 def _check_workload(gpu, model24_path, reqs, cfg, steps, seeds):
@@ -108,34 +54,13 @@ def _check_workload(gpu, model24_path, reqs, cfg, steps, seeds):
     try:
         print("device: generate and step logits", flush=True)
         res = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, oracle=forced, flags=1, want_sampled=True)
-        dev = _device_step_logits(g, reqs, forced, steps)
+        dev = FR.device_step_logits(g, reqs, forced, steps)
     finally:
         g.close()
     assert res["n_steps"] == ref["n_steps"] == steps
     for b in range(B):
         assert np.array_equal(res["tokens"][b], ref["tokens"][b])            # the forced histories
-    draws = [O.rng_exponential_n(s, steps * V).reshape(steps, V) for s in seeds]
-    n_mis = n_fragile = 0
-    worst = 0.0
-    for b in range(B):
-        hist = np.concatenate([reqs[b]["prompt"], forced]).astype(np.int32)
-        for i in range(steps):
-            h = hist[:P + i]
-            zo = _penalised(cfg, ref["logits"][i, b], h)
-            zd = _penalised(cfg, dev[i, b], h)
-            fin = np.isfinite(zo)
-            e = float(np.abs(zd[fin] - zo[fin]).max())
-            worst = max(worst, e / float(np.abs(zo[fin]).max()))
-            q = draws[b][i]
-            tok_o = _decision(cfg, ref["logits"][i, b], h, q)
-            tok_d = _decision(cfg, dev[i, b], h, q)
-            assert tok_o == ref["sampled"][i, b], (b, i)            # the oracle's own choice
-            assert tok_d == res["sampled"][i, b], (b, i)            # the device's own choice
-            fragile = _fragile(cfg, zo, q, e, tok_o)
-            n_fragile += fragile
-            if tok_d != tok_o:
-                n_mis += 1
-                assert fragile, (b, i, tok_d, tok_o, e)
+    n_mis, n_fragile, worst = FR.check_choices(reqs, cfg, forced, seeds, ref, res, dev, steps)
     print(f"batch {B}: {B * steps} choices, {n_mis} differ from the oracle's, all at fragile steps "
           f"({n_fragile} fragile); worst logit drift {worst:.2e} of the scale", flush=True)
     assert worst <= 3e-2, worst
@@ -145,7 +70,7 @@ def _check_workload(gpu, model24_path, reqs, cfg, steps, seeds):
         g.set_exact(True)
         print("device, exact mode: free run and step logits", flush=True)
         res_x = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=1, want_sampled=True)
-        dev_x = _device_step_logits(g, reqs, forced, steps)
+        dev_x = FR.device_step_logits(g, reqs, forced, steps)
     finally:
         g.close()
     assert np.array_equal(dev_x.view(np.uint32), ref["logits"][:steps].view(np.uint32)), \
