@@ -19,6 +19,7 @@ struct QkvAttnArgs {
     int col_add;
     int n_head;
     float scale_log2;          // softmax scale * log2(e)
+    float scale;               // softmax scale (exact mode's scores: q.k * scale, as ggml)
     float * out;               // attention output fp32 [B][512]
     int8_t * oq;               // and its Q8_0 copy (sliced) + scales [B][16], or null
     float * od;
@@ -29,6 +30,8 @@ struct QkvAttnArgs {
 bool qkv_attn_supported(int B, int nh, int64_t max_keys);
 // what the decode's GEMV chain uses: supported, and fewer than DECODE_GEMM_MIN_BATCH sequences
 bool qkv_attn_preferred(int B, int nh, int64_t max_keys);
-int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream);
+// exact: the attention in ggml-cpu's order (flash_attn_ext's sequential online softmax with
+// glibc's expf), bit for bit with the oracle; any row length (no split needed)
+int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream, bool exact = false);
 
 }  // namespace gsvk

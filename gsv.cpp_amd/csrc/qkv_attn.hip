@@ -16,7 +16,20 @@
 //
 // head h's workgroups are blockIdx.x = b * nh + h: with nh a multiple of 8 they all run on one
 // XCD, so the 52 KB of weights of head h are read from HBM once per XCD L2.
+//
+// Exact mode (EXACT): step 4 is flash_attn_ext's sequential online softmax in ggml-cpu's order
+// (src/gsv_ar.cpp:404; the oracle's orc_attn_row), bit for bit, in chunks of 256 keys:
+//   a. thread t of the 4 waves takes key c0 + t: its score q.k in ggml_vec_dot_f32's order times
+//      the scale, and its V row into LDS as fp32 (plus 1.0 for S's chain); the next chunk's K/V
+//      rows are loaded now;
+//   b. the maximum before each key (an exclusive prefix max over the chunk, seeded with the
+//      running maximum) gives each key's ms and vs (glibc's expf): ms = expf(before - s), vs = 1
+//      for a new maximum, else ms = 1, vs = expf(s - before);
+//   c. wave 0 runs the chains, one dependent fma per key: lanes 0..31 acc_d = fma(v_d, vs,
+//      acc_d * ms), lane 32 S = fma(S, ms, vs); with ms = 1 (no new maximum among 8 keys, a
+//      ballot per key) both are fma(x, vs, acc) with x = v_d or 1.
 #include "attn_dev.h"
+#include "expf_exact.h"
 #include "layer.h"
 #include "layer_dev.h"
 #include "qkv_attn.h"
@@ -28,10 +41,185 @@ constexpr int QA_K = 512;                // d_model
 constexpr int QA_NBLK = QA_K / 32;
 constexpr int QA_NB4 = QA_K / 128;       // int4 weight loads per slice lane
 constexpr int QA_ROWS = 3 * ATT_HD;      // rows of one head: q, k, v
+
+constexpr int QX_C = 256;    // keys per chunk of the exact attention: one per thread of 4 waves
+constexpr int QX_XS = 36;    // floats per key row in LDS: 32 V values, 1.0 (S's chain), padding
+
+struct QxLds {
+    float x[QX_C + 8][QX_XS];    // (8 rows past the chunk: read ahead by the chain, never used)
+    float vs[QX_C + 8];
+    float ms[QX_C];
+    float wmax[QX_C / 64];
+    uint8_t nm[QX_C / 8 + 8];    // per group of 8 keys: the bits of the keys that set a new maximum
+};
+
+__constant__ uint64_t qx_exp2_tab[32] = GSVK_EXP2_TAB32;
+
+// the K and V rows (64 bytes each) of key j of one (sequence, head); a key past `last` reads key
+// `last` (in the buffer; not used)
+__device__ __forceinline__ void qx_load(const uint16_t * __restrict__ kb, const uint16_t * __restrict__ vb, int j,
+                                        int last, KV8 & r) {
+    const int key = j < last ? j : last;
+    const uint4 * kp = reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
+    const uint4 * vp = reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        r.k[p] = kp[p];
+        r.v[p] = vp[p];
+    }
+}
+
+// Exact attention of one (sequence, head) over keys [beg, end), end - 1 == col (the new key, in
+// s_kv); 256 threads; r holds the rows of key beg + tid on entry. Returns dimension `lane` of the
+// output in wave 0's lanes 0..31.
+__device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * __restrict__ kb,
+                                           const uint16_t * __restrict__ vb, int beg, int end, int col,
+                                           int last_old, const float * s_q, const uint16_t (*s_kv)[ATT_HD],
+                                           float scale, int tid) {
+    __shared__ __align__(16) QxLds L;
+    const int lane = tid & 63, wave = tid >> 6;
+    float qv[32];
+#pragma unroll
+    for (int c = 0; c < 8; c++) {
+        const float4 q4 = *reinterpret_cast<const float4 *>(&s_q[4 * c]);
+        qv[4 * c] = q4.x; qv[4 * c + 1] = q4.y; qv[4 * c + 2] = q4.z; qv[4 * c + 3] = q4.w;
+    }
+    const int dl = lane < 32 ? lane : 32;
+    float M = -INFINITY;   // running maximum, uniform
+    float acc = 0.0f;      // wave 0: lanes 0..31 the output dimensions, lane 32 (and above) S
+    uint4 rk0 = first.k[0], rk1 = first.k[1], rk2 = first.k[2], rk3 = first.k[3];
+    uint4 rv0 = first.v[0], rv1 = first.v[1], rv2 = first.v[2], rv3 = first.v[3];
+    for (int c0 = beg; c0 < end; c0 += QX_C) {   // uniform
+        const int n = min(QX_C, end - c0);
+        const int j = c0 + tid;
+        // the new key from LDS (the loaded slot holds the old contents)
+        const bool nw = j == col;
+        const uint4 * nk = reinterpret_cast<const uint4 *>(&s_kv[0][0]);
+        const uint4 * nv = reinterpret_cast<const uint4 *>(&s_kv[1][0]);
+        const uint4 kw[4] = {nw ? nk[0] : rk0, nw ? nk[1] : rk1, nw ? nk[2] : rk2, nw ? nk[3] : rk3};
+        const uint4 vw[4] = {nw ? nv[0] : rv0, nw ? nv[1] : rv1, nw ? nv[2] : rv2, nw ? nv[3] : rv3};
+        if (c0 + QX_C < end) {   // the next chunk's rows (uniform)
+            const int key = j + QX_C < last_old ? j + QX_C : last_old;
+            const uint4 * kp = reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
+            const uint4 * vp = reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+            rk0 = kp[0]; rk1 = kp[1]; rk2 = kp[2]; rk3 = kp[3];
+            rv0 = vp[0]; rv1 = vp[1]; rv2 = vp[2]; rv3 = vp[3];
+        }
+        float s = -INFINITY;
+        if (tid < n) {
+            float kf[32], vf[32];
+#pragma unroll
+            for (int p = 0; p < 4; p++) {
+                float t8[8];
+                h8_to_f(kw[p], t8);
+#pragma unroll
+                for (int i = 0; i < 8; i++) kf[8 * p + i] = t8[i];
+                h8_to_f(vw[p], t8);
+#pragma unroll
+                for (int i = 0; i < 8; i++) vf[8 * p + i] = t8[i];
+            }
+            // ggml_vec_dot_f32 (32 elements): 4 x 8 partial products, (0 + 2) + (1 + 3), hsum
+            float s0[8];
+#pragma unroll
+            for (int l = 0; l < 8; l++) {
+                const float p0 = __builtin_fmaf(kf[l], qv[l], 0.0f), p1 = __builtin_fmaf(kf[8 + l], qv[8 + l], 0.0f);
+                const float p2 = __builtin_fmaf(kf[16 + l], qv[16 + l], 0.0f), p3 = __builtin_fmaf(kf[24 + l], qv[24 + l], 0.0f);
+                s0[l] = (p0 + p2) + (p1 + p3);
+            }
+            const float t0 = s0[0] + s0[4], t1 = s0[1] + s0[5], t2 = s0[2] + s0[6], t3 = s0[3] + s0[7];
+            s = ((t0 + t1) + (t2 + t3)) * scale;
+            float4 * xr = reinterpret_cast<float4 *>(&L.x[tid][0]);
+#pragma unroll
+            for (int c = 0; c < 8; c++) xr[c] = make_float4(vf[4 * c], vf[4 * c + 1], vf[4 * c + 2], vf[4 * c + 3]);
+            xr[8] = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+        }
+        // the maximum before each key: inclusive scan within the wave, the waves' maxima, seeded
+        // with the running maximum (max is exact in any order)
+        float incl = s;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float o = __shfl_up(incl, off, 64);
+            if (lane >= off) incl = fmaxf(incl, o);
+        }
+        float excl = __shfl_up(incl, 1, 64);
+        if (lane == 0) excl = -INFINITY;
+        if (lane == 63) L.wmax[wave] = incl;
+        __syncthreads();
+        float before = M, mn = M;
+#pragma unroll
+        for (int w = 0; w < QX_C / 64; w++) {
+            const float wm = L.wmax[w];
+            if (w < wave) before = fmaxf(before, wm);
+            mn = fmaxf(mn, wm);
+        }
+        before = fmaxf(before, excl);
+        float ms = 1.0f, vs = 1.0f;
+        if (tid < n) {
+            if (s > before) ms = expf_glibc(before - s, qx_exp2_tab);
+            else vs = expf_glibc(s - before, qx_exp2_tab);
+        }
+        L.ms[tid] = ms;
+        L.vs[tid] = vs;
+        const uint64_t nm = __ballot(ms != 1.0f);
+        if (lane == 0) *reinterpret_cast<uint64_t *>(&L.nm[8 * wave]) = nm;
+        M = mn;
+        __syncthreads();
+        // the chains (wave 0): groups of 8 keys, the next group's LDS reads issued before the
+        // current group's fmas
+        if (wave == 0) {
+            float xa[8], va[8];
+            int ga;
+            auto group = [&](int t0, float (&xs)[8], float (&vs8)[8], int & g) {
+#pragma unroll
+                for (int i = 0; i < 8; i++) xs[i] = L.x[t0 + i][dl];
+                const float4 v0 = *reinterpret_cast<const float4 *>(&L.vs[t0]);
+                const float4 v1 = *reinterpret_cast<const float4 *>(&L.vs[t0 + 4]);
+                vs8[0] = v0.x; vs8[1] = v0.y; vs8[2] = v0.z; vs8[3] = v0.w;
+                vs8[4] = v1.x; vs8[5] = v1.y; vs8[6] = v1.z; vs8[7] = v1.w;
+                g = L.nm[t0 >> 3];
+            };
+            group(0, xa, va, ga);
+            int t = 0;
+            for (; t + 8 <= n; t += 8) {
+                float xb[8], vbn[8];
+                int gb;
+                group(t + 8, xb, vbn, gb);
+                if (__builtin_amdgcn_readfirstlane(ga) == 0) {   // no new maximum: ms = 1
+#pragma unroll
+                    for (int i = 0; i < 8; i++) acc = __builtin_fmaf(xa[i], va[i], acc);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; i++) {
+                        const float m1 = L.ms[t + i];
+                        const float lo = __builtin_fmaf(xa[i], va[i], acc * m1);
+                        const float hs = __builtin_fmaf(acc, m1, va[i]);
+                        acc = lane >= 32 ? hs : lo;
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    xa[i] = xb[i];
+                    va[i] = vbn[i];
+                }
+                ga = gb;
+            }
+            for (; t < n; t++) {
+                const float x1 = L.x[t][dl], v1 = L.vs[t], m1 = L.ms[t];
+                const float lo = __builtin_fmaf(x1, v1, acc * m1);
+                const float hs = __builtin_fmaf(acc, m1, v1);
+                acc = lane >= 32 ? hs : lo;
+            }
+        }
+        __syncthreads();
+    }
+    const float S = __shfl(acc, 32, 64);
+    return acc * (S == 0.0f ? 0.0f : 1.0f / S);
+}
 }  // namespace
 
-template <int NW, int MODE>
+template <int NW, int MODE, bool EXACT>
 __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
+    static_assert(!EXACT || NW * 64 == QX_C, "exact mode: one key of a chunk per thread");
     constexpr int PASSES = (QA_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     const int nh = a.n_head;
     const int bh = blockIdx.x;
@@ -131,7 +319,10 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     last_old = last_old < a.lstride ? last_old : (int) a.lstride - 1;
     int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
     KV8 cur;
-    load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+    if constexpr (EXACT)   // the rows of key beg + tid (the first chunk)
+        qx_load(a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg + tid, last_old, cur);
+    else
+        load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
     __syncthreads();
     if (!col_ok) {   // the new key is outside the cache: write nothing to it, output 0
         if (wave == 0) attn_store_out(0.0f, lane, pair, nh, a.out, nullptr, a.oq, a.od);
@@ -175,6 +366,12 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     // 4. attention over [beg, col]
     if (nkeys == 0) {   // (col < beg: nothing valid; ggml returns 0)
         if (wave == 0) attn_store_out(0.0f, lane, pair, nh, a.out, nullptr, a.oq, a.od);
+        return;
+    }
+    if constexpr (EXACT) {
+        const float val = qx_attend(cur, a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg,
+                                    end, col, last_old, s_q, s_kv, a.scale, tid);
+        if (wave == 0) attn_store_out(val, lane, pair, nh, a.out, nullptr, a.oq, a.od);
         return;
     }
     float qv[8];
@@ -238,7 +435,7 @@ bool qkv_attn_preferred(int B, int nh, int64_t max_keys) {
     return B < DECODE_GEMM_MIN_BATCH && qkv_attn_supported(B, nh, max_keys);
 }
 
-int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream) {
+int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t stream, bool exact) {
     GSVK_REQUIRE(a.ws && a.wd && a.bias && a.kc && a.vc && a.kv_begin && a.col_ptr && a.out,
                  "qkv_attn: null pointer");
     GSVK_REQUIRE(a.n_head * ATT_HD == QA_K && B > 0 && a.lstride > 0 && max_keys <= a.lstride,
@@ -247,10 +444,19 @@ int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t 
                                                                 a.in.tok && a.in.pos_ptr),
                  "qkv_attn: bad input stage");
     GSVK_REQUIRE((a.oq == nullptr) == (a.od == nullptr), "qkv_attn: oq and od go together");
+    const dim3 grid((unsigned) ((int64_t) B * a.n_head));
+    if (exact) {   // any row length: the chunks cover it
+        GSVK_REQUIRE(B <= 65535 * 16 && a.scale > 0.0f, "qkv_attn: bad exact-mode arguments");
+        if (a.in.mode == IN_LN)
+            hipLaunchKernelGGL((k_qkv_attn<4, IN_LN, true>), grid, dim3(256), 0, stream, a);
+        else
+            hipLaunchKernelGGL((k_qkv_attn<4, IN_EMB, true>), grid, dim3(256), 0, stream, a);
+        GSVK_LAUNCH_CHECK();
+        return GSVK_OK;
+    }
     GSVK_REQUIRE(qkv_attn_supported(B, a.n_head, max_keys), "qkv_attn: rows this long need the split path");
     const int nw = attn_waves(B, a.n_head, max_keys);
-    const dim3 grid((unsigned) ((int64_t) B * a.n_head));
-#define GSVK_QA(W, MODE) hipLaunchKernelGGL((k_qkv_attn<W, MODE>), grid, dim3(W * 64), 0, stream, a)
+#define GSVK_QA(W, MODE) hipLaunchKernelGGL((k_qkv_attn<W, MODE, false>), grid, dim3(W * 64), 0, stream, a)
     if (a.in.mode == IN_LN) {
         if (nw == 8) GSVK_QA(8, IN_LN);
         else GSVK_QA(4, IN_LN);
@@ -265,11 +471,11 @@ int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t 
 
 }  // namespace gsvk
 
-extern "C" int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
-                                const float * r, const float * ln_bias, const float * wb, int B, int nh,
-                                uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
-                                const int32_t * col, float scale, float * out, int8_t * oq, float * od,
-                                float * ln_out, void * stream) {
+namespace {
+int op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res, const float * r,
+                const float * ln_bias, const float * wb, int B, int nh, uint16_t * k, uint16_t * v, int64_t lstride,
+                const int32_t * kv_begin, const int32_t * col, float scale, float * out, int8_t * oq, float * od,
+                float * ln_out, void * stream, bool exact) {
     using namespace gsvk;
     GSVK_REQUIRE(res && wb, "qkv_attn: null pointer");
     QkvAttnArgs a{};
@@ -290,10 +496,30 @@ extern "C" int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const fl
     a.col_add = 0;
     a.n_head = nh;
     a.scale_log2 = scale * LOG2E;
+    a.scale = scale;
     a.out = out;
     a.oq = oq;
     a.od = od;
-    return launch_qkv_attn(a, B, lstride, (hipStream_t) stream);
+    return launch_qkv_attn(a, B, lstride, (hipStream_t) stream, exact);
+}
+}  // namespace
+
+extern "C" int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
+                                const float * r, const float * ln_bias, const float * wb, int B, int nh,
+                                uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                                const int32_t * col, float scale, float * out, int8_t * oq, float * od,
+                                float * ln_out, void * stream) {
+    return op_qkv_attn(wq, wd, bias, res, r, ln_bias, wb, B, nh, k, v, lstride, kv_begin, col, scale, out, oq, od,
+                       ln_out, stream, false);
+}
+
+extern "C" int gsvk_op_qkv_attn_exact(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
+                                      const float * r, const float * ln_bias, const float * wb, int B, int nh,
+                                      uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
+                                      const int32_t * col, float scale, float * out, int8_t * oq, float * od,
+                                      float * ln_out, void * stream) {
+    return op_qkv_attn(wq, wd, bias, res, r, ln_bias, wb, B, nh, k, v, lstride, kv_begin, col, scale, out, oq, od,
+                       ln_out, stream, true);
 }
 
 extern "C" int gsvk_qkv_attn_supported(int B, int nh, int64_t max_keys) {

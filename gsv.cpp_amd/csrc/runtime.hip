@@ -641,15 +641,17 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
             in.wb = p.ln2;
         }
         in.out_x = x.x;
-        if (m->exact) {
+        const bool exact_fused = m->exact && m->NH * m->HD == 512 && m->HD == 32;
+        if (m->exact && !exact_fused) {
             // the GEMV QKV, then attention in ggml-cpu's sequential order with glibc's expf
             GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, n, in,
                                        qkv_out(m, w, loff, qkv, D, 1, m->d_step, m->S - 1), st));
             GSVK_TRY(launch_attn_exact_decode(qkv, D, m->kc + loff, m->vc + loff, n, m->NH, m->lstride,
                                               m->kv_begin + r0, m->kv_end + r0, scale, attn.x, attn.q, attn.d, st,
                                               Q8_SLICED));
-        } else if (qkv_attn_preferred(n, m->NH, m->lstride)) {
-            // QKV + attention in one launch per layer
+        } else if (exact_fused || qkv_attn_preferred(n, m->NH, m->lstride)) {
+            // QKV + attention in one launch per layer (exact mode: the attention in ggml-cpu's
+            // sequential order with glibc's expf)
             QkvAttnArgs qa{};
             qa.ws = w.qkv.qs;
             qa.wd = w.qkv.d;
@@ -663,10 +665,11 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
             qa.col_add = m->S - 1;
             qa.n_head = m->NH;
             qa.scale_log2 = scale * 1.4426950408889634f;
+            qa.scale = scale;
             qa.out = attn.x;
             qa.oq = attn.q;
             qa.od = attn.d;
-            GSVK_TRY(launch_qkv_attn(qa, n, m->lstride, st));
+            GSVK_TRY(launch_qkv_attn(qa, n, m->lstride, st, exact_fused));
         } else {
             GSVK_TRY(launch_layer_gemv(w.qkv.qs, w.qkv.d, 3 * D, D, n, in,
                                        qkv_out(m, w, loff, qkv, D, 1, m->d_step, m->S - 1), st));

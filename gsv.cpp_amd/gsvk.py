@@ -31,7 +31,7 @@ EXPORTS = [
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
     "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact", "gsvk_model_set_prefill_f16",
-    "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm",
+    "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
@@ -135,6 +135,7 @@ def lib():
                                                   vp, vp, vp]
         L.gsvk_op_qkv_attn.argtypes = [vp, vp, vp, vp, vp, vp, vp, i32, i32, vp, vp, i64, vp, vp, f32, vp, vp,
                                        vp, vp, vp]
+        L.gsvk_op_qkv_attn_exact.argtypes = L.gsvk_op_qkv_attn.argtypes
         L.gsvk_qkv_attn_supported.argtypes = [i32, i32, i64]
         L.gsvk_op_q8_gemm.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp]
         L.gsvk_op_q8_gemm_ex.argtypes = [vp, vp, i64, i64, vp, vp, i64, vp, i32, vp, vp, vp, i32, i32, vp]
@@ -313,12 +314,13 @@ def qkv_attn_supported(B, nh, max_keys) -> bool:
 
 
 def op_qkv_attn(wq, wd, bias, res, r, ln_bias, wb, k, v, kv_begin, col, scale, out, oq=None, od=None,
-                ln_out=None, stream=None):
+                ln_out=None, stream=None, exact=False):
+    """exact=True: gsvk_op_qkv_attn_exact (the attention in ggml-cpu's sequential order)."""
     B = res.shape[0]
     _, nh, lstride, _ = k.shape
-    check(lib().gsvk_op_qkv_attn(_p(wq), _p(wd), _p(bias), _p(res), _p(r), _p(ln_bias), _p(wb), B, nh, _p(k),
-                                 _p(v), lstride, _p(kv_begin), _p(col), scale, _p(out), _p(oq), _p(od),
-                                 _p(ln_out), _stream(stream)), "qkv_attn")
+    fn = lib().gsvk_op_qkv_attn_exact if exact else lib().gsvk_op_qkv_attn
+    check(fn(_p(wq), _p(wd), _p(bias), _p(res), _p(r), _p(ln_bias), _p(wb), B, nh, _p(k), _p(v), lstride,
+             _p(kv_begin), _p(col), scale, _p(out), _p(oq), _p(od), _p(ln_out), _stream(stream)), "qkv_attn")
 
 
 def op_sample(logits, cfg, rng, tok_out, hist=None, n_hist=None, probs_out=None, ws=None, stream=None):

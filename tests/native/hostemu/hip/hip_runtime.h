@@ -102,6 +102,11 @@ template <typename T>
 inline T __shfl_xor(T v, int mask, int width = 64) { return ::emu::shfl_xor(v, mask, width); }
 template <typename T>
 inline T __shfl(T v, int src, int width = 64) { return ::emu::shfl(v, src, width); }
+template <typename T>
+inline T __shfl_up(T v, unsigned delta, int width = 64) {   // 1-D workgroups: lane = threadIdx.x % 64
+    const int lane = (int) (threadIdx.x & 63), base = lane & ~(width - 1), src = lane - (int) delta;
+    return ::emu::shfl(v, src >= base ? src : lane, 64);
+}
 inline unsigned long long __ballot(int pred) { return ::emu::ballot(pred != 0); }
 inline int __any(int pred) { return ::emu::ballot(pred != 0) != 0; }
 inline int __all(int pred) { return ::emu::ballot(pred != 0) == ::emu::live_mask(); }

@@ -5,6 +5,8 @@
 * gsvk_op_attn_exact: flash_attn_ext's sequential online softmax against orc_attn_decode_f16 on
   ragged rows (empty, one key, chunk edges, the whole cache), scores that set a new maximum at
   every key, ties, and scores spread over +-80.
+* gsvk_op_qkv_attn_exact (exact mode's fused decode kernel) against the GEMV's q and the oracle's
+  attention over the appended cache, bit for bit.
 * A model in exact mode: the prefill's K/V (every column, at a row count where the default path
   runs the matrix-core GEMM), the logits entering every teacher-forced decode step and the decode
   K/V columns of layers 0 and 3 equal the oracle's to the bit; a decode of 17 sequences is refused.
@@ -90,6 +92,59 @@ def test_attn_exact_op_matches_oracle(gpu, B, lstride):
     q_ref = blocks[:, :, 2:].view(np.int8).reshape(B, nh * 32)
     qs = oq.cpu().numpy().reshape(B, 8, nh, 4).transpose(0, 2, 1, 3).reshape(B, nh * 32)
     assert np.array_equal(qs, q_ref)
+
+
+@pytest.mark.parametrize("B,lstride", [(4, 300), (16, 1100)])
+def test_qkv_attn_exact_op_matches_oracle(gpu, B, lstride):
+    """Exact mode's fused decode kernel (gsvk_op_qkv_attn_exact: LN input, QKV, K/V append and the
+    attention in ggml-cpu's order in chunks of 256 keys) against the LN-input GEMV (bit-exact with
+    ggml's dot) and the oracle's attention over the appended cache: output bit for bit, the same K/V
+    rows; a row of the new key only, one that reaches column 0, and one whose every key sets a new
+    maximum."""
+    import torch
+    from test_gpu_ops import _dev as dev
+    rng = np.random.default_rng(420 + B)
+    D, nh, n = 512, 16, 1536
+    W = rng.standard_normal((n, D)).astype(np.float32) * 0.02
+    wq = torch.zeros(n * D, dtype=torch.int8, device="cuda")
+    wd = torch.zeros(n * D // 32, dtype=torch.int16, device="cuda")
+    gpu.op_q8_repack(dev(sm.q8_quantize_ref(W).ravel(), torch), n, D, wq, wd)
+    bias = dev(rng.standard_normal(n).astype(np.float32) * 0.02, torch)
+    res = dev(rng.standard_normal((B, D)).astype(np.float32), torch)
+    r = dev(rng.standard_normal((B, D)).astype(np.float32) * 0.5, torch)
+    lb = dev(rng.standard_normal(D).astype(np.float32) * 0.02, torch)
+    wb = dev(np.concatenate([1 + 0.05 * rng.standard_normal(D), 0.05 * rng.standard_normal(D)]).astype(np.float32),
+             torch)
+    qkv = torch.zeros((B, n), dtype=torch.float32, device="cuda")
+    gpu.op_ln_gemv(wq, wd, n, res, r, lb, wb, bias, 0, qkv)
+    torch.cuda.synchronize()
+    q = qkv[:, :D].cpu().numpy().reshape(B, nh, 32)
+    k = rng.standard_normal((B, nh, lstride, 32)).astype(np.float32)
+    v = rng.standard_normal((B, nh, lstride, 32)).astype(np.float16)
+    ramp = np.linspace(0.0, 6.0, lstride, dtype=np.float32)     # sequence 2: rising scores
+    k[2] = q[2][:, None, :] * ramp[None, :, None] / np.maximum((q[2] ** 2).sum(-1), 1e-3)[:, None, None]
+    k = k.astype(np.float16)
+    col = lstride - 3
+    begins = rng.integers(0, col + 1, B).astype(np.int32)
+    begins[0], begins[1], begins[2] = col, 0, 0
+    kc, vc = dev(k, torch), dev(v, torch)
+    col_d = torch.tensor([col], dtype=torch.int32, device="cuda")
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(32.0)))
+    out = torch.zeros((B, D), dtype=torch.float32, device="cuda")
+    print(f"qkv_attn_exact B={B} lstride={lstride}", flush=True)
+    gpu.op_qkv_attn(wq, wd, bias, res, r, lb, wb, kc, vc, dev(begins, torch), col_d, scale, out, exact=True)
+    torch.cuda.synchronize()
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, col, :] = qkv[:, D:2 * D].cpu().numpy().reshape(B, nh, 32).astype(np.float16)
+    v2[:, :, col, :] = qkv[:, 2 * D:].cpu().numpy().reshape(B, nh, 32).astype(np.float16)
+    assert np.array_equal(kc.cpu().numpy().view(np.uint16), k2.view(np.uint16))
+    assert np.array_equal(vc.cpu().numpy().view(np.uint16), v2.view(np.uint16))
+    ends = np.full(B, col + 1, np.int32)
+    ref = O.attn_decode_f16(q, k2.view(np.uint16), v2.view(np.uint16), begins, ends, scale)
+    got = out.cpu().numpy()
+    bad = np.argwhere(got.view(np.uint32) != ref.view(np.uint32))
+    assert bad.size == 0, (len(bad), bad[:4], np.abs(got - ref).max())
+    assert np.array_equal(got[0], v2[0, :, col, :].astype(np.float32).reshape(-1))   # one key: its V row
 
 
 def _forced_logits(g, reqs, forced, steps):

@@ -52,3 +52,18 @@ def test_planted_cache_overflow_is_reported(replay):
     r = _run(replay, [32, 400, 500, 7, 23], plant=True)
     assert r.returncode != 0
     assert "heap-buffer-overflow" in r.stderr and "k_qkv_attn" in r.stderr, r.stderr[-4000:]
+
+
+CHECK = os.path.join(ROOT, "_build", "hostemu", "exact_attn_check")
+
+
+@pytest.mark.parametrize("args", [(3, 300, 40, 1), (4, 700, 650, 2), (5, 1200, 1100, 3)])
+def test_exact_fused_kernel_equals_the_two_launches(replay, args):
+    """Exact mode's fused decode kernel (QKV + K/V append + ggml-order attention in chunks of 256
+    keys) against the QKV GEMV + one-wave exact attention it replaces, on the CPU under
+    AddressSanitizer: outputs, Q8_0 copies and appended K/V equal to the bit, no access outside a
+    buffer; rows of 1 key (only the new one) up to 1101 keys (5 chunks)."""
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0")
+    r = subprocess.run([CHECK] + [str(a) for a in args], capture_output=True, text=True, env=env, timeout=900)
+    assert r.returncode == 0, (r.stdout + r.stderr)[-4000:]
+    assert "equal to the bit" in r.stdout
