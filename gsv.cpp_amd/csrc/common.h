@@ -292,6 +292,12 @@ int launch_embed_pe(const float * emb, const float * pe, const int32_t * tok, in
                     const int32_t * pos_ptr, int pos_add, float alpha, int d, int B, float * x,
                     int8_t * xq, float * xd, int32_t * kv_end, int kv_end_add, const int32_t * pos_sub,
                     int pe_rows, hipStream_t stream, int layout = Q8_SLICED);
+int launch_add_act(const float * a, const float * b, int64_t n, int64_t ne0, int act, float * y, hipStream_t stream);
+// QKV rows [rows][3 * d_model] of an F16 / F32 projection: + bias in place, K and V (fp16) appended
+// at column *col_ptr + col_add + r % rows_per_seq of sequence r / rows_per_seq
+int launch_bias_kv(float * y, const float * bias, int64_t rows, int d_model, uint16_t * kc, uint16_t * vc,
+                   int n_head, int64_t lstride, int rows_per_seq, const int32_t * col_ptr, int col_add,
+                   hipStream_t stream);
 size_t attn_workspace_bytes(int B, int nh, int64_t max_keys);
 int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, const uint16_t * v,
                        int B, int nh, int hd, int64_t lstride, const int32_t * kv_begin,

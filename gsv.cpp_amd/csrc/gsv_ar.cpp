@@ -136,9 +136,20 @@ gsv_ar_result gsv_ar::generate(const std::vector<gsv_ar_request> & reqs,
         fprintf(stderr, "[gsv_ar] generate failed: %s\n", gsvk_last_error());
         return res;   // empty: callers check tokens.size() == reqs.size()
     }
-    if (p->profile)
-        printf("[prof:decode] B=%d steps=%d total=%.1f ms (%.3f ms/step incl. prefill)\n", B,
-               out.n_steps, now_ms() - t0, (now_ms() - t0) / std::max(1, out.n_steps));
+    if (p->profile) {
+        // the reference's three report lines (src/gsv_ar.cpp:33-42); the embedding, masks and
+        // sampling run on the device inside `compute`, so the host buckets are zero
+        gsvk_profile pr{};
+        gsvk_model_get_profile(p->m, &pr);
+        const int n = std::max(1, pr.steps);
+        printf("[prof:decode] prefill(build/copy/compute/io) = %.1f/%.1f/%.1f/%.1f ms\n", pr.pf_build_ms,
+               pr.pf_copy_ms, pr.pf_compute_ms, pr.pf_io_ms);
+        printf("[prof:decode] steps=%d build=%.1fms copy=%.1fms compute=%.1fms other=%.1fms (per-step: %.2f/%.2f/%.2f)\n",
+               pr.steps, pr.dec_build_ms, pr.dec_copy_ms, pr.dec_compute_ms, pr.dec_other_ms, pr.dec_build_ms / n,
+               pr.dec_copy_ms / n, pr.dec_compute_ms / n);
+        printf("[prof:decode] host per-step: mask=%.3fms sampling=%.3fms emb+pe=%.3fms\n", 0.0, 0.0, 0.0);
+        printf("[prof:decode] B=%d total=%.1f ms\n", B, now_ms() - t0);
+    }
     res.tokens.resize(B);
     for (int b = 0; b < B; b++)
         res.tokens[b].assign(tokens.begin() + (size_t) b * stride, tokens.begin() + (size_t) b * stride + tok_len[b]);

@@ -145,6 +145,54 @@ __global__ void k_add_act(const float * __restrict__ a, const float * __restrict
     y[i] = apply_act(a[i] + b[i % ne0], act);
 }
 
+int launch_add_act(const float * a, const float * b, int64_t n, int64_t ne0, int act, float * y, hipStream_t stream) {
+    GSVK_REQUIRE(a && b && y && n >= 0 && ne0 > 0 && act >= 0 && act <= 3, "add_act: bad arguments");
+    if (n == 0) return GSVK_OK;
+    hipLaunchKernelGGL(k_add_act, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream, a, b, n, ne0, act, y);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+// ---------------------------------------------------------------------------------------
+// QKV rows of an F16 / F32 projection (src/gsv_ar.cpp:244-255, :271-275, :392-399): y += bias in
+// place (the ggml_add after the mul_mat), and the K and V parts, rounded to fp16, appended to the
+// caches: row r belongs to sequence r / rows_per_seq and goes to column
+// *col_ptr + col_add + r % rows_per_seq. One thread per element of a row of 3 * d_model.
+// ---------------------------------------------------------------------------------------
+
+__global__ void k_bias_kv(float * __restrict__ y, const float * __restrict__ bias, int64_t rows, int d_model,
+                          uint16_t * __restrict__ kc, uint16_t * __restrict__ vc, int n_head, int64_t lstride,
+                          int rows_per_seq, const int32_t * __restrict__ col_ptr, int col_add) {
+    const int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x;
+    const int w = 3 * d_model;
+    if (i >= rows * w) return;
+    const int64_t r = i / w;
+    const int c = (int) (i - r * w);
+    const float v = y[i] + bias[c];
+    y[i] = v;
+    if (c < d_model) return;
+    const int which = c / d_model, j = c - which * d_model;
+    const int64_t seq = r / rows_per_seq;
+    const int64_t col = (int64_t) *col_ptr + col_add + r % rows_per_seq;
+    if (col < 0 || col >= lstride) return;
+    uint16_t * dst = which == 1 ? kc : vc;
+    dst[((seq * n_head + j / 32) * lstride + col) * 32 + (j & 31)] = f2h(v);
+}
+
+int launch_bias_kv(float * y, const float * bias, int64_t rows, int d_model, uint16_t * kc, uint16_t * vc,
+                   int n_head, int64_t lstride, int rows_per_seq, const int32_t * col_ptr, int col_add,
+                   hipStream_t stream) {
+    GSVK_REQUIRE(y && bias && kc && vc && col_ptr && rows >= 0 && rows_per_seq > 0 && n_head * 32 == d_model &&
+                     lstride > 0 && rows * 3 * d_model < ((int64_t) 1 << 40),
+                 "bias_kv: bad arguments");
+    const int64_t n = rows * 3 * d_model;
+    if (n == 0) return GSVK_OK;
+    hipLaunchKernelGGL(k_bias_kv, dim3((unsigned) ((n + 255) / 256)), dim3(256), 0, stream, y, bias, rows, d_model,
+                       kc, vc, n_head, lstride, rows_per_seq, col_ptr, col_add);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
 // ---------------------------------------------------------------------------------------
 // embedding + PE (src/gsv_ar.cpp:798-807): x[b] = emb[tok[b]] + alpha * pe[*pos_ptr + pos_add],
 // with its Q8_0 copy (in the given layout), and kv_end[b] = *pos_ptr + kv_end_add

@@ -104,6 +104,8 @@ struct Lin {
     uint16_t * w16 = nullptr; // fp16(d * q) [n][k]: the prefill's fp16 mode (made at its first use)
     float * b = nullptr;
     int n = 0, k = 0;
+    int type = GGML_Q8_0;     // GGML_Q8_0, or GGML_F16 / GGML_F32 with the rows [n][k] in wf
+    void * wf = nullptr;
 };
 
 struct LayerW {
@@ -155,6 +157,8 @@ struct gsvk_model {
     Act x, attn, n1, hq;
     float * qkv = nullptr, * o = nullptr, * h2 = nullptr, * logits = nullptr;
     float * p1 = nullptr, * p2 = nullptr;   // partial rows of the two-launch decode layer
+    float * hx = nullptr;                   // FFN1 output rows (F16 / F32 projections)
+    bool generic = false;   // some projection is F16 / F32: the per-op path (enqueue_decode_generic)
     int decode_path = GSVK_DECODE_AUTO;
     bool exact = false;   // gsvk_model_set_exact: ggml-cpu's arithmetic order throughout
     bool prefill_f16 = false;   // gsvk_model_set_prefill_f16: prefill projections on fp16 matrix cores
@@ -171,6 +175,10 @@ struct gsvk_model {
     // mapped pinned word (d_unfinished_host: its device address); one event per step in flight
     int32_t * h_unfinished = nullptr, * d_unfinished_host = nullptr;
     hipEvent_t step_ev[2] = {nullptr, nullptr};
+    // GSV_AR_PROFILE buckets of the last prefill / generate (gsvk_model_get_profile); the prefill's
+    // device phases are timed with these events (uploads, kernels, logits read-back)
+    hipEvent_t pf_ev[4] = {nullptr, nullptr, nullptr, nullptr};
+    gsvk_profile prof{};
     // sequence state
     int prompt_len = 0, S = 0, max_len = 0, B = 0, host_step = 0;
     bool prefilled = false;
@@ -195,6 +203,8 @@ struct gsvk_model {
         if (h_pinned) (void) hipHostFree(h_pinned);
         if (h_unfinished) (void) hipHostFree(h_unfinished);
         for (hipEvent_t & e : step_ev)
+            if (e) (void) hipEventDestroy(e);
+        for (hipEvent_t & e : pf_ev)
             if (e) (void) hipEventDestroy(e);
         if (stream) (void) hipStreamDestroy(stream);
     }
@@ -359,6 +369,7 @@ int ensure_state(gsvk_model * m, int B, int hist_len, int max_steps) {
     GSVK_TRY(a.alloc(m->logits, (size_t) B * m->V));
     GSVK_TRY(a.alloc(m->p1, (size_t) m->NH * B * D));
     GSVK_TRY(a.alloc(m->p2, (size_t) DEC_FFN_GROUPS_MAX * B * D));
+    GSVK_TRY(a.alloc(m->hx, (size_t) B * m->FFN));
     char * ws = nullptr;
     GSVK_TRY(a.alloc(ws, attn_workspace_bytes(B, m->NH, m->lstride)));
     GSVK_HIP(hipMemset(ws, 0, attn_workspace_bytes(B, m->NH, m->lstride)));
@@ -755,16 +766,84 @@ int enqueue_decode_fused(gsvk_model * m) {
                                 G, (int64_t) B * D, last.f2.b, last.ln2, B, m->logits, m->V, st);
 }
 
+// y[R][n] = W[n][k] . x[R][k] of one projection in ggml-cpu's order: a Q8_0 weight through the GEMV
+// on the sliced Q8_0 copy of x (xq, xd); an F16 / F32 weight through ggml_vec_dot (mode 0) or
+// tinyBLAS (mode 1) on the fp32 rows x, F16 with the activations rounded to fp16.
+int proj_rows(const Lin & l, const float * x, const int8_t * xq, const float * xd, int64_t R, float * y, int mode,
+              hipStream_t st) {
+    if (l.type == GGML_Q8_0) {
+        LayerIn qin{};
+        qin.mode = IN_Q8;
+        qin.xs = xq;
+        qin.xd = xd;
+        LayerOut o{};
+        o.y = y;
+        o.y_stride = l.n;
+        o.n_store = l.n;
+        return launch_layer_gemv(l.qs, l.d, l.n, l.k, R, qin, o, st);
+    }
+    return launch_fdot(l.wf, l.type == GGML_F16 ? 1 : 0, l.n, l.k, x, l.k, R, y, l.n, mode, st);
+}
+
+// Decode step of a model with F16 / F32 projections (the reference exporter's attn= / ffn=
+// options; the engine's fallback model): one launch per op of src/gsv_ar.cpp:380-467, each in
+// ggml-cpu's order (the projections as proj_rows, the LayerNorms as the Q8_0 path's), the attention
+// the default decode kernel or, in exact mode, ggml's sequential one.
+int enqueue_decode_generic(gsvk_model * m) {
+    const int B = m->B, D = m->D, F = m->FFN;
+    const float scale = 1.0f / std::sqrt((float) m->HD);
+    hipStream_t st = m->stream;
+    const size_t row_kv = (size_t) m->NH * m->lstride * m->HD;
+    for (int li = 0; li < m->NL; li++) {
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * B * row_kv;
+        if (li == 0) {
+            GSVK_TRY(launch_embed_pe(m->audio_emb, m->pe, m->last_tok, m->V, m->d_step, m->prompt_len - 1,
+                                     m->audio_alpha, D, B, m->x.x, m->x.q, m->x.d, m->kv_end, m->S, m->row_start,
+                                     PE_MAX, st));
+        } else {
+            const LayerW & p = m->L[li - 1];
+            GSVK_TRY(launch_layernorm(m->n1.x, m->h2, p.f2.b, p.ln2, B, D, 1e-5f, m->x.x, m->x.q, m->x.d, st));
+        }
+        GSVK_TRY(proj_rows(w.qkv, m->x.x, m->x.q, m->x.d, B, m->qkv, 0, st));
+        GSVK_TRY(launch_bias_kv(m->qkv, w.qkv.b, B, D, m->kc + loff, m->vc + loff, m->NH, m->lstride, 1, m->d_step,
+                                m->S - 1, st));
+        if (m->exact)
+            GSVK_TRY(launch_attn_exact_decode(m->qkv, 3 * D, m->kc + loff, m->vc + loff, B, m->NH, m->lstride,
+                                              m->kv_begin, m->kv_end, scale, m->attn.x, m->attn.q, m->attn.d, st,
+                                              Q8_SLICED));
+        else
+            GSVK_TRY(launch_attn_decode(m->qkv, 3 * D, m->kc + loff, m->vc + loff, B, m->NH, m->HD, m->lstride,
+                                        m->kv_begin, m->kv_end, m->lstride, scale, m->attn.x, nullptr, m->attn.q,
+                                        m->attn.d, m->attn_ws, st));
+        GSVK_TRY(proj_rows(w.out, m->attn.x, m->attn.q, m->attn.d, B, m->o, 0, st));
+        GSVK_TRY(launch_layernorm(m->x.x, m->o, w.out.b, w.ln1, B, D, 1e-5f, m->n1.x, m->n1.q, m->n1.d, st));
+        GSVK_TRY(proj_rows(w.f1, m->n1.x, m->n1.q, m->n1.d, B, m->hx, 0, st));
+        GSVK_TRY(launch_add_act(m->hx, w.f1.b, (int64_t) B * F, F, 1, m->hx, st));
+        if (w.f2.type == GGML_Q8_0) GSVK_TRY(launch_q8_quantize(m->hx, B, F, m->hq.q, m->hq.d, st));
+        GSVK_TRY(proj_rows(w.f2, m->hx, m->hq.q, m->hq.d, B, m->h2, 0, st));
+    }
+    return decode_head(m, B, m->n1.x, m->h2, m->x, m->logits, st);
+}
+
 // The two-launch layer covers the shape and the weights it reads (tiled out / FFN2 copies, an
 // F16 / F32 head).
 bool fused_decode_ok(const gsvk_model * m) {
-    if (m->head_type == GGML_Q8_0 || !dec_layer_supported(m->B, m->NH, m->D, m->FFN, m->lstride)) return false;
+    if (m->generic || m->head_type == GGML_Q8_0 || !dec_layer_supported(m->B, m->NH, m->D, m->FFN, m->lstride))
+        return false;
     for (const LayerW & w : m->L)
         if (!w.out.qt || !w.f2.qt) return false;
     return true;
 }
 
 int enqueue_decode_body(gsvk_model * m) {
+    if (m->generic) {
+        GSVK_REQUIRE(m->decode_path == GSVK_DECODE_AUTO, "decode path %d: not available for a model with F16 / "
+                     "F32 projections (it has its own per-op path)", m->decode_path);
+        GSVK_REQUIRE(!m->exact || m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences (got %d)",
+                     DECODE_GEMM_MIN_BATCH - 1, m->B);
+        return enqueue_decode_generic(m);
+    }
     if (m->exact) {
         GSVK_REQUIRE(m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences (got %d)",
                      DECODE_GEMM_MIN_BATCH - 1, m->B);
@@ -828,6 +907,7 @@ int check_requests(gsvk_model * m, const gsvk_request * reqs, int B) {
 int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed, float * logits_host,
                int hist_len, int max_steps, int kv_slot = -1, int col0 = 0) {
     GSVK_TRY(check_requests(m, reqs, B));
+    const auto t_build = std::chrono::steady_clock::now();
     const int P = reqs[0].n_prompt;
     int max_len = 0;
     for (int b = 0; b < B; b++) max_len = std::max(max_len, reqs[b].n_phones);
@@ -893,6 +973,8 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(tmp.alloc(d_rowt, std::max(R, 1)));
     GSVK_TRY(tmp.alloc(d_tlen, B));
     GSVK_TRY(tmp.alloc(d_boff, B));
+    m->prof.pf_build_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_build).count();
+    GSVK_HIP(hipEventRecord(m->pf_ev[0], st));
     GSVK_TRY(upload(d_phones, phones.data(), phones.size() * 4, st));
     GSVK_TRY(upload(d_pad, pad.data(), (size_t) B * 4, st));
     // the attention's sequence order: fewest padding rows (longest) first
@@ -935,6 +1017,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(tmp.alloc(last, (size_t) B * D));
     GSVK_TRY(tmp.alloc(lg, (size_t) B * m->V));
 
+    GSVK_HIP(hipEventRecord(m->pf_ev[1], st));
     // inputs: xy, then + bert_aug . [feat; 1] on the text rows
     GSVK_TRY(launch_build_xy(m->text_emb, m->audio_emb, m->pe, d_phones, d_pad, d_prompt, B, S,
                              max_len, D, m->text_alpha, m->audio_alpha, cur.x, st));
@@ -947,7 +1030,7 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     if (R) GSVK_TRY(launch_add_proj(cur.x, proj, m->bert_b, d_rowb, d_rowt, d_pad, S, D, R, R1, st));
     // projections on the matrix-core GEMMs from GEMM_MIN_ROWS rows on, except in exact mode (the
     // GEMV chain in ggml-cpu's order and the sequential attention at any row count)
-    const bool gemm = !m->exact && rows >= GEMM_MIN_ROWS;
+    const bool gemm = !m->exact && !m->generic && rows >= GEMM_MIN_ROWS;
     if (gemm && m->prefill_f16) GSVK_TRY(ensure_w16(m));
     // the layer-0 QKV reads this copy: natural order for the GEMM, sliced for the GEMV
     GSVK_TRY(launch_q8_quantize(cur.x, rows, D, cur.q, cur.d, st, gemm ? Q8_NATURAL : Q8_SLICED));
@@ -955,7 +1038,41 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     GSVK_TRY(tmp.alloc(zero, 1));
     GSVK_HIP(hipMemsetAsync(zero, 0, 4, st));
     const float scale = 1.0f / std::sqrt((float) m->HD);
-    for (int li = 0; li < m->NL; li++) {
+    float * hx = nullptr;
+    if (m->generic) GSVK_TRY(tmp.alloc(hx, rows * F));
+    for (int li = 0; li < m->NL && m->generic; li++) {
+        // F16 / F32 projections: one launch per op (the decode's enqueue_decode_generic over the
+        // B * S rows), the projections in tinyBLAS order when S >= 2 as for the head; K/V of every
+        // row, padding rows included, at columns [col0, col0 + S)
+        const LayerW & w = m->L[li];
+        const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
+        const int mode = S >= 2 ? 1 : 0;
+        if (li > 0) {
+            const LayerW & p = m->L[li - 1];
+            GSVK_TRY(launch_layernorm(n1.x, h2, p.f2.b, p.ln2, rows, D, 1e-5f, cur.x, cur.q, cur.d, st, Q8_SLICED,
+                                      nullptr, d_pad, S));
+        }
+        GSVK_TRY(proj_rows(w.qkv, cur.x, cur.q, cur.d, rows, qkv, mode, st));
+        GSVK_TRY(launch_bias_kv(qkv, w.qkv.b, rows, D, m->kc + loff, m->vc + loff, m->NH, m->lstride, S, zero, col0,
+                                st));
+        if (m->exact)
+            GSVK_TRY(launch_attn_exact_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, nullptr, nullptr,
+                                               st));
+        else if (attn_prefill_uses_mfma(rows))
+            GSVK_TRY(launch_attn_prefill_mfma(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, nullptr, nullptr,
+                                              st, false, d_order, true));
+        else
+            GSVK_TRY(launch_attn_prefill(qkv, B, S, max_len, d_pad, m->NH, D, scale, attn.x, nullptr, nullptr, st));
+        if (w.out.type == GGML_Q8_0) GSVK_TRY(launch_q8_quantize(attn.x, rows, D, attn.q, attn.d, st));
+        GSVK_TRY(proj_rows(w.out, attn.x, attn.q, attn.d, rows, o, mode, st));
+        GSVK_TRY(launch_layernorm(cur.x, o, w.out.b, w.ln1, rows, D, 1e-5f, n1.x, n1.q, n1.d, st, Q8_SLICED, nullptr,
+                                  d_pad, S));
+        GSVK_TRY(proj_rows(w.f1, n1.x, n1.q, n1.d, rows, hx, mode, st));
+        GSVK_TRY(launch_add_act(hx, w.f1.b, rows * F, F, 1, hx, st));
+        if (w.f2.type == GGML_Q8_0) GSVK_TRY(launch_q8_quantize(hx, rows, F, hq.q, hq.d, st));
+        GSVK_TRY(proj_rows(w.f2, hx, hq.q, hq.d, rows, h2, mode, st));
+    }
+    for (int li = 0; li < m->NL && !m->generic; li++) {
         const LayerW & w = m->L[li];
         const size_t loff = (size_t) li * m->kv_B * m->NH * m->lstride * m->HD + slot_off;
         if (gemm) {
@@ -1011,12 +1128,21 @@ int do_prefill(gsvk_model * m, const gsvk_request * reqs, int B, int lmax_needed
     }
     // llamafile's tinyBLAS handles the head when the prefill has >= 2 columns
     GSVK_TRY(head_logits(m, lastq, B, S >= 2 ? 1 : 0, lg, st));
+    GSVK_HIP(hipEventRecord(m->pf_ev[2], st));
     GSVK_HIP(hipMemcpyAsync(m->logits + (slot_mode ? (size_t) kv_slot * m->V : 0), lg, (size_t) B * m->V * 4,
                             hipMemcpyDeviceToDevice, st));
     if (!slot_mode) GSVK_TRY(upload(m->kv_begin, pad.data(), (size_t) B * 4, st));
     if (logits_host)
         GSVK_HIP(hipMemcpyAsync(logits_host, lg, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
+    GSVK_HIP(hipEventRecord(m->pf_ev[3], st));
     GSVK_HIP(hipStreamSynchronize(st));
+    {
+        float t[3] = {0, 0, 0};
+        for (int i = 0; i < 3; i++) GSVK_HIP(hipEventElapsedTime(&t[i], m->pf_ev[i], m->pf_ev[i + 1]));
+        m->prof.pf_copy_ms = t[0];
+        m->prof.pf_compute_ms = t[1];
+        m->prof.pf_io_ms = t[2];
+    }
     if (tmp.need > m->pf_cap) {
         // grow the workspace for the next prefill of this size (nothing of it is in use now)
         if (m->pf_pool) (void) hipFree(m->pf_pool);
@@ -1135,7 +1261,9 @@ int validate_gguf(const GgufFile & g, Hparams & hp) {
     if (F <= 0 || F % 128 != 0) { set_error("ffn size %d must be a multiple of 128", F); return GSVK_ERR_FORMAT; }
     // a Q8_0 projection [n][k]: the GGUF tensor, or its tiled pair in a pre-swizzled file
     auto need_q8 = [&](const std::string & name, int64_t k, int64_t n) -> int {
-        if (!hp.tiled) return need(name, {GGML_Q8_0}, {k, n});
+        // F16 / F32 projections too (the reference exporter's attn= / ffn= options,
+        // tools/export_gguf/export.py:53-54); a pre-swizzled file holds Q8_0 only
+        if (!hp.tiled) return need(name, {GGML_Q8_0, GGML_F16, GGML_F32}, {k, n});
         GSVK_TRY(need(name + ".qt", {GGML_I8}, {k, n}));
         return need(name + ".dt", {GGML_F16}, {k / 32, n});
     };
@@ -1220,7 +1348,22 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
             } else {
                 const GgufTensor * t = g.tensor(nm);
                 if (!t) { set_error("missing tensor %s", nm); return GSVK_ERR_FORMAT; }
-                GSVK_TRY(load_q8(m.get(), g, t, *q.lin, staging, staging_bytes, host));
+                if (t->type == GGML_F16 || t->type == GGML_F32) {
+                    // kept as stored: ggml_mul_mat multiplies F16 / F32 rows as they are
+                    if (t->ne.size() != 2) { set_error("%s: expected a 2-D tensor", nm); return GSVK_ERR_FORMAT; }
+                    q.lin->type = (int) t->type;
+                    q.lin->k = (int) t->ne[0];
+                    q.lin->n = (int) t->ne[1];
+                    host.resize(t->nbytes);
+                    if (!g.read(*t, host.data())) { set_error("read of %s failed", nm); return GSVK_ERR_IO; }
+                    uint8_t * d = nullptr;
+                    GSVK_TRY(m->wmem.alloc(d, t->nbytes));
+                    GSVK_HIP(hipMemcpy(d, host.data(), t->nbytes, hipMemcpyHostToDevice));
+                    q.lin->wf = d;
+                    m->generic = true;
+                } else {
+                    GSVK_TRY(load_q8(m.get(), g, t, *q.lin, staging, staging_bytes, host));
+                }
             }
             if ((q.expect_n >= 0 && q.lin->n != q.expect_n) || (q.expect_k >= 0 && q.lin->k != q.expect_k)) {
                 set_error("%s: shape [%d, %d] does not match the model", nm, q.lin->n, q.lin->k);
@@ -1328,6 +1471,7 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
     GSVK_HIP(hipHostMalloc((void **) &m->h_unfinished, 64, hipHostMallocMapped | hipHostMallocCoherent));
     GSVK_HIP(hipHostGetDevicePointer((void **) &m->d_unfinished_host, m->h_unfinished, 0));
     for (hipEvent_t & e : m->step_ev) GSVK_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    for (hipEvent_t & e : m->pf_ev) GSVK_HIP(hipEventCreate(&e));
     GSVK_HIP(hipStreamSynchronize(m->stream));
     if (verbose)
         fprintf(stderr, "[gsvk] loaded %s on HIP device %d: D=%d heads=%d layers=%d vocab=%d EOS=%d "
@@ -1707,6 +1851,7 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     GSVK_TRY(do_prefill(m, reqs, B, S + max_steps + 8, nullptr, hist_len, max_steps));
     out->prefill_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_pf).count();
     hipStream_t st = m->stream;
+    const auto t_state = std::chrono::steady_clock::now();
     std::vector<int32_t> pad(B);
     for (int b = 0; b < B; b++) pad[b] = max_len - reqs[b].n_phones;
     // host state -> device
@@ -1731,6 +1876,8 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
         GSVK_TRY(upload(m->oracle, oracle, (size_t) std::min(n_oracle, max_steps) * 4, st));
     GSVK_HIP(hipMemsetAsync(m->sampled, 0xff, (size_t) std::max(max_steps, 1) * B * 4, st));
     GSVK_HIP(hipStreamSynchronize(st));
+    const auto t_graph = std::chrono::steady_clock::now();
+    m->prof.dec_copy_ms = std::chrono::duration<double, std::milli>(t_graph - t_state).count();
 
     // one step = sampler (loop index idx) + decode at idx; the graph is replayed max_steps times
     SampleArgs sa{};
@@ -1796,6 +1943,7 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     };
     GSVK_HIP(hipStreamSynchronize(st));
     const auto t_dec = std::chrono::steady_clock::now();
+    m->prof.dec_build_ms = std::chrono::duration<double, std::milli>(t_dec - t_graph).count();
     for (int idx = 0; idx < max_steps; idx++) {
         hipEvent_t & ev = m->step_ev[idx % STEPS_IN_FLIGHT];
         if (idx >= STEPS_IN_FLIGHT) {
@@ -1809,6 +1957,8 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     }
     GSVK_HIP(hipStreamSynchronize(st));
     out->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_dec).count();
+    m->prof.dec_compute_ms = out->decode_ms;
+    const auto t_res = std::chrono::steady_clock::now();
     // results
     GSVK_HIP(hipMemcpy(hist.data(), m->hist, hist.size() * 4, hipMemcpyDeviceToHost));
     GSVK_HIP(hipMemcpy(ny.data(), m->ny, (size_t) B * 4, hipMemcpyDeviceToHost));
@@ -1844,6 +1994,14 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     if ((flags & GSVK_GEN_PROB_DUMP) && out->probs0 && out->n_steps > 0)
         GSVK_HIP(hipMemcpy(out->probs0, m->probs_dump, (size_t) out->n_steps * m->V * 4,
                            hipMemcpyDeviceToHost));
+    m->prof.dec_other_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_res).count();
+    m->prof.steps = out->n_steps;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_model_get_profile(gsvk_model * m, gsvk_profile * out) {
+    GSVK_REQUIRE(m && out, "null argument");
+    *out = m->prof;
     return GSVK_OK;
 }
 

@@ -31,7 +31,7 @@ EXPORTS = [
     "gsvk_bert_load", "gsvk_bert_free", "gsvk_bert_get_info", "gsvk_bert_encode",
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
     "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact", "gsvk_model_set_prefill_f16",
-    "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact",
+    "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact", "gsvk_model_get_profile",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
@@ -59,6 +59,11 @@ class GenOut(C.Structure):
                 ("lens", C.c_void_p), ("finish_seq", C.c_void_p), ("probs0", C.c_void_p),
                 ("n_steps", C.c_int32), ("progress", PROGRESS_FN), ("progress_user", C.c_void_p),
                 ("prefill_ms", C.c_double), ("decode_ms", C.c_double)]
+
+
+class Profile(C.Structure):
+    _fields_ = [(n, C.c_double) for n in ("pf_build_ms", "pf_copy_ms", "pf_compute_ms", "pf_io_ms", "dec_build_ms",
+                                          "dec_copy_ms", "dec_compute_ms", "dec_other_ms")] + [("steps", C.c_int)]
 
 
 class ModelInfo(C.Structure):
@@ -421,6 +426,12 @@ class Model:
     def set_prefill_f16(self, on: bool = True):
         """Prefill projections on the fp16 matrix cores (include/gsvk.h gsvk_model_set_prefill_f16)."""
         check(lib().gsvk_model_set_prefill_f16(self.h, 1 if on else 0), "set_prefill_f16")
+
+    def profile(self):
+        """The GSV_AR_PROFILE buckets of the last generate (include/gsvk.h gsvk_model_get_profile)."""
+        pr = Profile()
+        check(lib().gsvk_model_get_profile(self.h, C.byref(pr)), "get_profile")
+        return {n: getattr(pr, n) for n, _ in Profile._fields_}
 
     def set_exact(self, on: bool = True):
         """Exact mode (include/gsvk.h gsvk_model_set_exact): ggml-cpu's arithmetic order throughout."""

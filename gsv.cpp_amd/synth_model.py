@@ -104,13 +104,17 @@ class _Writer:
 def write_model(path: str, seed: int = 0x6A5E0000, n_layer: int = 24, d_model: int = 512,
                 n_head: int = 16, ffn: int = 2048, vocab: int = 1025, phone_vocab: int = 732,
                 eos: int = 1024, head_type: str = "f16", bert_dim: int = 1024,
-                override: dict | None = None, text_alpha: float = 1.0, audio_alpha: float = 1.0) -> str:
+                override: dict | None = None, text_alpha: float = 1.0, audio_alpha: float = 1.0,
+                attn_type: str = "q8_0", ffn_type: str = "q8_0") -> str:
     """Write the synthetic model to ``path`` (returns path).
 
     override maps tensor names to the values to store instead of the random ones (the random
     stream is drawn as usual, so the other tensors do not change): fp32 arrays of the tensor's
     shape, stored in the tensor's type (Q8_0 through q8_quantize_ref, F16 rounded), or, for a
-    Q8_0 tensor, a uint8 array of ready GGUF blocks (exact scales, see q8_blocks)."""
+    Q8_0 tensor, a uint8 array of ready GGUF blocks (exact scales, see q8_blocks).
+
+    attn_type (qkv_w, out_w) and ffn_type (ffn1_w, ffn2_w): "q8_0", "f16" or "f32", the projection
+    types of the reference exporter's attn= / ffn= options (tools/export_gguf/export.py:53-54)."""
     rng = np.random.Generator(np.random.PCG64(seed))
     D = d_model
     override = override or {}
@@ -162,17 +166,19 @@ def write_model(path: str, seed: int = 0x6A5E0000, n_layer: int = 24, d_model: i
         put("ar.predict", (vocab, D), GGML_Q8_0, pred)
     else:
         raise ValueError("head_type must be f16, f32 or q8_0")
+    types = {"q8_0": GGML_Q8_0, "f16": GGML_F16, "f32": GGML_F32}
+    ta, tf = types[attn_type], types[ffn_type]
     for li in range(n_layer):
         p = f"transformer.block{li}"
-        put(f"{p}.qkv_w", (3 * D, D), GGML_Q8_0, normal((3 * D, D), 0.02))
+        put(f"{p}.qkv_w", (3 * D, D), ta, normal((3 * D, D), 0.02))
         put(f"{p}.qkv_b", (3 * D,), GGML_F32, normal((3 * D,), 0.02))
-        put(f"{p}.out_w", (D, D), GGML_Q8_0, normal((D, D), 0.02))
+        put(f"{p}.out_w", (D, D), ta, normal((D, D), 0.02))
         put(f"{p}.out_b", (D,), GGML_F32, normal((D,), 0.02))
         put(f"{p}.norm1_w", (D,), GGML_F32, 1.0 + normal((D,), 0.05))
         put(f"{p}.norm1_b", (D,), GGML_F32, normal((D,), 0.05))
-        put(f"{p}.ffn1_w", (ffn, D), GGML_Q8_0, normal((ffn, D), 0.02))
+        put(f"{p}.ffn1_w", (ffn, D), tf, normal((ffn, D), 0.02))
         put(f"{p}.ffn1_b", (ffn,), GGML_F32, normal((ffn,), 0.02))
-        put(f"{p}.ffn2_w", (D, ffn), GGML_Q8_0, normal((D, ffn), 0.02))
+        put(f"{p}.ffn2_w", (D, ffn), tf, normal((D, ffn), 0.02))
         put(f"{p}.ffn2_b", (D,), GGML_F32, normal((D,), 0.02))
         put(f"{p}.norm2_w", (D,), GGML_F32, 1.0 + normal((D,), 0.05))
         put(f"{p}.norm2_b", (D,), GGML_F32, normal((D,), 0.05))

@@ -79,7 +79,10 @@ typedef struct gsvk_model_info {
 } gsvk_model_info;
 
 /* Load a gsv AR GGUF (tools/export_gguf/convert_ar.py contract) onto HIP device `device`.
- * Replaces gsv_ar::load (src/gsv_ar.cpp:490-705). */
+ * Replaces gsv_ar::load (src/gsv_ar.cpp:490-705). The layer projections may be Q8_0, F16 or F32
+ * (the exporter's attn= / ffn= options, tools/export_gguf/export.py:53-54); a model with an F16 or
+ * F32 projection decodes on a per-op path (ggml's F16 / F32 dot orders, F16 with fp16-rounded
+ * activations) and ignores gsvk_model_set_decode_path's explicit choices (they fail). */
 int gsvk_model_load(const char * gguf_path, int device, int verbose, gsvk_model ** out);
 void gsvk_model_free(gsvk_model * m);
 int gsvk_model_get_info(const gsvk_model * m, gsvk_model_info * info);
@@ -131,6 +134,18 @@ typedef struct gsvk_gen_out {
     double    prefill_ms;
     double    decode_ms;
 } gsvk_gen_out;
+
+/* Time buckets of the last generate (prefill phases also after first_logits / prefill), the ones
+ * GSV_AR_PROFILE prints (src/gsv_ar.cpp:18-42: prof_report). Prefill: host packing of the requests,
+ * uploads, the kernels, the logits read-back (device phases timed with HIP events). Decode: the
+ * graph capture, the state uploads, the step loop (the GPU's decode, sampling and embedding
+ * included: they run on the device), the results read-back. */
+typedef struct {
+    double pf_build_ms, pf_copy_ms, pf_compute_ms, pf_io_ms;
+    double dec_build_ms, dec_copy_ms, dec_compute_ms, dec_other_ms;
+    int steps;
+} gsvk_profile;
+int gsvk_model_get_profile(gsvk_model * m, gsvk_profile * out);
 
 /* Full batched generation: replaces gsv_ar::generate (src/gsv_ar.cpp:719-824).
  * oracle (teacher forcing) may be NULL; seeds may be NULL (then seed_base + 0x9E3779B9*b). */

@@ -467,7 +467,8 @@ static size_t gg_nbytes(const gg_tensor * t) {
 }
 
 typedef struct {
-    const uint8_t * q8;   /* Q8_0 rows */
+    const void * w;       /* [N][K] rows: Q8_0 blocks, F16 or F32 */
+    int type;             /* 8 Q8_0, 1 F16, 0 F32 */
     const float * b;
 } lin_t;
 
@@ -562,15 +563,16 @@ orc_model * orc_model_load(const char * path, char * err, int errlen) {
         m->L = (layer_t *) calloc((size_t) m->NL, sizeof(layer_t));
         for (int li = 0; li < m->NL; li++) {
             layer_t * L = &m->L[li];
-#define GETW(field, suffix) do { snprintf(nm, sizeof nm, "transformer.block%d." suffix, li); gg_tensor * t = gg_find(ts, n, nm); \
-            if (!t) FAIL("missing tensor %s", nm); if (t->type != 8) FAIL("%s: projection weights must be Q8_0", nm); field = m->file + t->off; } while (0)
+#define GETW(lin, suffix) do { snprintf(nm, sizeof nm, "transformer.block%d." suffix, li); gg_tensor * t = gg_find(ts, n, nm); \
+            if (!t) FAIL("missing tensor %s", nm); if (t->type != 8 && t->type != 1 && t->type != 0) \
+            FAIL("%s: projection weights must be Q8_0, F16 or F32", nm); (lin).w = m->file + t->off; (lin).type = t->type; } while (0)
 #define GETF(field, suffix) do { snprintf(nm, sizeof nm, "transformer.block%d." suffix, li); gg_tensor * t = gg_find(ts, n, nm); \
             if (!t) FAIL("missing tensor %s", nm); if (t->type != 0) FAIL("%s must be F32", nm); field = (const float *) (m->file + t->off); } while (0)
             const float * n1w, * n1b, * n2w, * n2b;
-            GETW(L->qkv.q8, "qkv_w"); GETF(L->qkv.b, "qkv_b");
-            GETW(L->out.q8, "out_w"); GETF(L->out.b, "out_b");
-            GETW(L->f1.q8, "ffn1_w"); GETF(L->f1.b, "ffn1_b");
-            GETW(L->f2.q8, "ffn2_w"); GETF(L->f2.b, "ffn2_b");
+            GETW(L->qkv, "qkv_w"); GETF(L->qkv.b, "qkv_b");
+            GETW(L->out, "out_w"); GETF(L->out.b, "out_b");
+            GETW(L->f1, "ffn1_w"); GETF(L->f1.b, "ffn1_b");
+            GETW(L->f2, "ffn2_w"); GETF(L->f2.b, "ffn2_b");
             GETF(n1w, "norm1_w"); GETF(n1b, "norm1_b"); GETF(n2w, "norm2_w"); GETF(n2b, "norm2_b");
             if (li == 0) {
                 snprintf(nm, sizeof nm, "transformer.block0.ffn1_w");
@@ -653,15 +655,26 @@ static void head_logits(const orc_model * m, const float * x, int M, int mode, f
     else orc_q8_matmul((const uint8_t *) m->head, m->V, m->D, x, M, out, nt);
 }
 
+/* y[M][N] = W[N][K] . x[M][K], ggml_mul_mat of a projection (src/gsv_ar.cpp:244, :260-263, :392,
+ * :407-411): Q8_0 weights take the x86-quantised activations and the int8 block dot; F16 and F32
+ * weights ggml_vec_dot_f16 / _f32 (mode 0) or llamafile's tinyBLAS (mode 1, the prefill's
+ * multi-column products, as for the head), F16 with the activations rounded to fp16 (ggml's
+ * vec_dot_type). */
+static void proj(const lin_t * l, int64_t N, int64_t K, const float * x, int64_t M, float * y, int mode, int nt) {
+    if (l->type == 8) orc_q8_matmul((const uint8_t *) l->w, N, K, x, M, y, nt);
+    else if (l->type == 1) orc_f16_matmul((const uint16_t *) l->w, N, K, x, M, y, mode, nt);
+    else orc_f32_matmul((const float *) l->w, N, K, x, M, y, mode, nt);
+}
+
 /* one transformer layer over R rows after attention has produced attn[R][D] */
 static void layer_tail(const orc_model * m, const layer_t * L, float * cur, const float * attn,
-                       int64_t R, int nt, float * o, float * n1, float * h, float * h2) {
+                       int64_t R, int mode, int nt, float * o, float * n1, float * h, float * h2) {
     const int D = m->D, F = m->FFN;
-    orc_q8_matmul(L->out.q8, D, D, attn, R, o, nt);
+    proj(&L->out, D, D, attn, R, o, mode, nt);
     orc_layernorm(cur, o, L->out.b, L->ln1, R, D, 1e-5f, n1);
-    orc_q8_matmul(L->f1.q8, F, D, n1, R, h, nt);
+    proj(&L->f1, F, D, n1, R, h, mode, nt);
     orc_add_act(h, L->f1.b, R * F, F, 1, h);
-    orc_q8_matmul(L->f2.q8, D, F, h, R, h2, nt);
+    proj(&L->f2, D, F, h, R, h2, mode, nt);
     orc_layernorm(n1, h2, L->f2.b, L->ln2, R, D, 1e-5f, cur);
 }
 
@@ -733,7 +746,7 @@ static void prefill(const orc_model * m, const orc_request * reqs, int B, int S,
     const float scale = 1.0f / sqrtf((float) HD);
     for (int li = 0; li < m->NL; li++) {
         const layer_t * L = &m->L[li];
-        orc_q8_matmul(L->qkv.q8, 3 * D, D, cur, R, qkv, nt);
+        proj(&L->qkv, 3 * D, D, cur, R, qkv, S >= 2 ? 1 : 0, nt);
         for (int64_t r = 0; r < R; r++)
             for (int i = 0; i < 3 * D; i++) qkv[r * 3 * D + i] = qkv[r * 3 * D + i] + L->qkv.b[i];
         {
@@ -751,7 +764,7 @@ static void prefill(const orc_model * m, const orc_request * reqs, int B, int S,
                         c->k[cidx(m, c, li, b, hh, s) + d] = kv_round(row[D + hh * HD + d], flags);
                         c->v[cidx(m, c, li, b, hh, s) + d] = kv_round(row[2 * D + hh * HD + d], flags);
                     }
-        layer_tail(m, L, cur, attn, R, nt, o, n1, h, h2);
+        layer_tail(m, L, cur, attn, R, S >= 2 ? 1 : 0, nt, o, n1, h, h2);
     }
     /* logits of the last position (:266-269); tinyBLAS order for >= 2 columns */
     float * last = (float *) malloc(sizeof(float) * (size_t) B * D);
@@ -775,7 +788,7 @@ static void decode(const orc_model * m, const float * x_in, int B, const int * p
     const float scale = 1.0f / sqrtf((float) HD);
     for (int li = 0; li < m->NL; li++) {
         const layer_t * L = &m->L[li];
-        orc_q8_matmul(L->qkv.q8, 3 * D, D, cur, B, qkv, nt);
+        proj(&L->qkv, 3 * D, D, cur, B, qkv, 0, nt);
         for (int64_t r = 0; r < B; r++)
             for (int i = 0; i < 3 * D; i++) qkv[r * 3 * D + i] = qkv[r * 3 * D + i] + L->qkv.b[i];
         for (int b = 0; b < B; b++)
@@ -792,7 +805,7 @@ static void decode(const orc_model * m, const float * x_in, int B, const int * p
                              c->v + cidx(m, c, li, b, hh, L0), HD, HD, len + 1 - L0, NULL, scale,
                              attn + (size_t) b * D + hh * HD);
             }
-        layer_tail(m, L, cur, attn, B, nt, o, n1, h, h2);
+        layer_tail(m, L, cur, attn, B, 0, nt, o, n1, h, h2);
     }
     head_logits(m, cur, B, 0, logits, nt);
     free(cur); free(qkv); free(attn); free(o); free(n1); free(h); free(h2);

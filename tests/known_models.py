@@ -69,7 +69,7 @@ def params(seed: int, n_layer: int):
     return p, perm, scale
 
 
-def write(path, seed, layers, edit=None):
+def write(path, seed, layers, edit=None, **kw):
     """layers: per layer a dict of {"qkv", "out", "ffn1", "ffn2"} -> "zero" | "id" | cols array
     (see synth_model.q8_blocks); missing entries are zero. edit(p), if given, changes the random
     non-projection tensors in place before the file is written. Returns (path, tensors, perm,
@@ -79,9 +79,19 @@ def write(path, seed, layers, edit=None):
     if edit is not None:
         edit(p)
     shapes = {"qkv": (3 * D, D), "out": (D, D), "ffn1": (FFN, D), "ffn2": (D, FFN)}
+    fkind = {"qkv": kw.get("attn_type", "q8_0"), "out": kw.get("attn_type", "q8_0"),
+             "ffn1": kw.get("ffn_type", "q8_0"), "ffn2": kw.get("ffn_type", "q8_0")}
     for li, spec in enumerate(layers):
         for name, (n, k) in shapes.items():
             kind = spec.get(name, "zero")
+            if fkind[name] != "q8_0":      # F16 / F32 weights: the matrix itself (exact 1.0 and 0.0)
+                cols = None if isinstance(kind, str) else np.asarray(kind)
+                Wm = np.zeros((n, k), np.float32)
+                if not (isinstance(kind, str) and kind == "zero"):
+                    c = np.arange(n) % k if cols is None else cols
+                    Wm[np.arange(n)[c >= 0], c[c >= 0]] = 1.0
+                p[f"transformer.block{li}.{name}_w"] = Wm
+                continue
             if isinstance(kind, str) and kind == "zero":
                 blk = zero_q8(n, k)
             elif isinstance(kind, str) and kind == "id":
@@ -90,7 +100,7 @@ def write(path, seed, layers, edit=None):
                 blk = sm.q8_blocks(n, k, cols=kind)
             p[f"transformer.block{li}.{name}_w"] = blk
     sm.write_model(path, seed=seed, n_layer=n_layer, override=p, text_alpha=TEXT_ALPHA,
-                   audio_alpha=AUDIO_ALPHA)
+                   audio_alpha=AUDIO_ALPHA, **kw)
     return path, p, perm, scale
 
 
@@ -157,6 +167,12 @@ def zero_layers64(p, x, n_layer):
         n1 = ln64(x + p[f"{b}.out_b"], p[f"{b}.norm1_w"], p[f"{b}.norm1_b"])
         x = ln64(n1 + p[f"{b}.ffn2_b"], p[f"{b}.norm2_w"], p[f"{b}.norm2_b"])
     return x
+
+
+def head64_f32(x, perm, scale):
+    """F32 head of signed unit rows: exact products of the fp32 activations."""
+    xs = np.asarray(x, np.float64).astype(np.float32).astype(np.float64)
+    return xs[..., perm[np.arange(V) % D]] * scale
 
 
 def head64(x, perm, scale):

@@ -29,6 +29,33 @@ def test_reference_caller_runs_unchanged(gpu, small_model_path):
         assert float(r[-1]) > 0.0   # tok/s
 
 
+def test_profile_buckets(gpu, small_model_path):
+    """GSV_AR_PROFILE's buckets (src/gsv_ar.cpp:18-42): the reference caller prints the reference's
+    three report lines, and the buckets of a generate add up: the prefill's device phases are
+    positive, the decode's compute is the step loop's wall time, steps the steps that ran."""
+    import synth_model as sm
+    if os.path.exists(BIN):
+        env = dict(os.environ, GSV_AR_PROFILE="1")
+        p = subprocess.run([BIN, small_model_path, "vulkan", "16"], capture_output=True, text=True, timeout=180,
+                           env=env)
+        assert p.returncode == 0, p.stderr
+        assert re.search(r"\[prof:decode\] prefill\(build/copy/compute/io\) = [\d.]+/[\d.]+/[\d.]+/[\d.]+ ms", p.stdout)
+        assert re.search(r"\[prof:decode\] steps=\d+ build=[\d.]+ms copy=[\d.]+ms compute=[\d.]+ms other=[\d.]+ms", p.stdout)
+        assert "[prof:decode] host per-step: mask=" in p.stdout
+    g = gpu.Model(small_model_path)
+    try:
+        reqs = sm.synth_requests(77, 3, 16, [10, 20, 5])
+        r = g.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=12, seeds=[1, 2, 3], flags=1)
+        pr = g.profile()
+    finally:
+        g.close()
+    assert pr["steps"] == r["n_steps"] == 12
+    assert pr["pf_compute_ms"] > 0 and pr["pf_copy_ms"] >= 0 and pr["pf_io_ms"] >= 0 and pr["pf_build_ms"] >= 0
+    assert pr["pf_copy_ms"] + pr["pf_compute_ms"] + pr["pf_io_ms"] <= r["prefill_ms"] + 1e-3
+    assert abs(pr["dec_compute_ms"] - r["decode_ms"]) < 1e-9
+    assert pr["dec_build_ms"] > 0 and pr["dec_copy_ms"] > 0 and pr["dec_other_ms"] > 0
+
+
 def test_generate_ticks_the_engine_progress_counters(gpu, small_model_path):
     """gsv_ar::generate sets the engine's /progress counters (src/gsv_ar.cpp:761-763): stage 2 with
     the step budget as total, one tick per decode step, seen from the calling program (the

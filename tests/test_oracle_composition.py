@@ -517,3 +517,69 @@ def test_ffn_relu_between_the_projections(ffn_exact):
                       "b_1 dropped": _ffn_logits64(p, perm, scale, drop="b_1"),
                       "n1 residual dropped": _ffn_logits64(p, perm, scale, drop="n1 residual")}.items():
         assert _excess(rows[0], alt, bound) > 10, what
+
+
+# ---------------------------------------------------------------------------- F16 / F32 projections
+
+@pytest.fixture(scope="module", params=["f32", "f16"])
+def ffn_float(request, tmp_path_factory):
+    """1 layer of F16 or F32 projections (the exporter's attn= / ffn= options): attention and out
+    projection zero, FFN1 = FFN2 = identity (1.0 and 0.0, exact in both types); F32 head."""
+    d = tmp_path_factory.mktemp("kmf")
+    t = request.param
+    return t, KM.write(str(d / f"ffn_{t}.gguf"), 18, [{"ffn1": "id", "ffn2": "id"}], attn_type=t, ffn_type=t,
+                       head_type="f32")
+
+
+def _ffn_float_logits64(p, perm, scale, x, wtype, round16=True, act="relu"):
+    """x' = LN2(n1 + W2 . relu(W1 . n1 + b_1) + b_2) with n1 = LN1(x + b_o) and identity W1, W2:
+    F16 weights take their activations rounded to fp16 (n1 into FFN1, h into FFN2)."""
+    b = "transformer.block0"
+    n1 = KM.ln64(x + p[f"{b}.out_b"], p[f"{b}.norm1_w"], p[f"{b}.norm1_b"])
+    r16 = (lambda a: np.asarray(a).astype(np.float32).astype(np.float16).astype(np.float64)) \
+        if (wtype == "f16" and round16) else (lambda a: np.asarray(a).astype(np.float32).astype(np.float64))
+    pre = r16(n1) + p[f"{b}.ffn1_b"][:KM.D].astype(np.float64)
+    h = np.maximum(pre.astype(np.float32).astype(np.float64), 0.0) if act == "relu" else pre
+    xo = KM.ln64(n1 + r16(h) + p[f"{b}.ffn2_b"], p[f"{b}.norm2_w"], p[f"{b}.norm2_b"])
+    return KM.head64_f32(xo, perm, scale)
+
+
+def test_f16_f32_projections(ffn_float):
+    """Projections stored F16 or F32 (src/gsv_ar.cpp:244, :392 multiply them through ggml_mul_mat;
+    the engine's fallback F16 model, src/gsv_engine.cpp:216): F32 weights take the fp32
+    activations, F16 weights the activations rounded to fp16 (ggml's vec_dot_type), with no Q8_0
+    quantisation; checked through identity FFN matrices on the prefill's last row (tinyBLAS order)
+    and the decode rows (vec_dot order), where both orders are exact."""
+    wtype, (path, p, perm, scale) = ffn_float
+    m = O.Model(path)
+    pe = KM.pe(64)
+    P = 6
+    reqs = _reqs(28, [4, 9], P)
+    forced = np.array([5, 600, 1000, 77], np.int32)
+    got0 = m.first_logits(reqs, nthreads=N_THREADS)
+    r = m.generate(reqs, sampler=(1, 1.0, 1.0, 1.0), max_steps=len(forced), oracle=forced, seeds=[1, 2],
+                   flags=O.ORC_EOS_MASK_ALL, nthreads=N_THREADS, want_logits=True)
+    rows = [(got0[b], KM.decode_input64(p, reqs[b]["prompt"][P - 1], P - 1, pe)) for b in range(2)]
+    rows += [(r["logits"][i + 1, b], KM.decode_input64(p, forced[i], P + i, pe))
+             for i in range(len(forced) - 1) for b in range(2)]
+    for got, x in rows:
+        ref = _ffn_float_logits64(p, perm, scale, x, wtype)
+        close = np.abs(np.asarray(got, np.float64) - ref) <= 2e-6 * np.abs(ref) + 1e-6
+        assert close.mean() >= 0.99, (wtype, close.mean())
+        # the wrong compositions: Q8_0-style or no rounding of the activations, no activation
+        for what, alt in {"no fp16 rounding": _ffn_float_logits64(p, perm, scale, x, wtype, round16=False),
+                          "no activation": _ffn_float_logits64(p, perm, scale, x, wtype, act="none"),
+                          "Q8_0 activations": KM.head64_f32(KM.ln64(
+                              KM.ln64(x + p["transformer.block0.out_b"], p["transformer.block0.norm1_w"],
+                                      p["transformer.block0.norm1_b"]) * 0 + 0, np.ones(KM.D), np.zeros(KM.D)),
+                              perm, scale)}.items():
+            if what == "no fp16 rounding" and wtype == "f32":
+                continue
+            if what == "Q8_0 activations":
+                b0 = "transformer.block0"
+                n1 = KM.ln64(x + p[f"{b0}.out_b"], p[f"{b0}.norm1_w"], p[f"{b0}.norm1_b"])
+                h = np.maximum(_q8(n1) + p[f"{b0}.ffn1_b"][:KM.D], 0.0)
+                alt = KM.head64_f32(KM.ln64(n1 + _q8(h) + p[f"{b0}.ffn2_b"], p[f"{b0}.norm2_w"],
+                                            p[f"{b0}.norm2_b"]), perm, scale)
+            frac = np.mean(np.abs(np.asarray(got, np.float64) - alt) <= 2e-6 * np.abs(alt) + 1e-6)
+            assert frac < 0.9, (wtype, what, frac)   # the bar above is 0.99
