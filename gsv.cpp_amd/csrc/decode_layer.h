@@ -89,6 +89,28 @@ struct DecFfnArgs {
     int B;
 };
 
+// ---- the persistent decode: all layers of a step in one launch ----
+// 256 workgroups, 32 on each XCD (the dispatcher's round-robin; the hardware's XCC id names the
+// XCD a workgroup runs on); XCD x owns the sequences b = x, x + 8, ... and runs, per layer, launch 1's
+// work (head h of each of its sequences), a barrier among its 32 workgroups, launch 2's work
+// (group g of each), a barrier. The arithmetic is the two launches' to the bit. Each layer's
+// arguments are those of its two launches, kept in device memory (attn[n_layer], ffn[n_layer]).
+struct DecPersistArgs {
+    const DecAttnArgs * attn;   // [n_layer]: layer 0 IN_EMB, the others IN_LN with nparts = groups
+    const DecFfnArgs * ffn;     // [n_layer]
+    int n_layer;
+    int B;
+    int groups;                 // dec_ffn_groups(B)
+    const int32_t * step;       // the device step counter: the barrier's epoch
+    int * flags;                // [8][32] barrier words (zero before the first step of a run)
+    int * err;                  // 0, or 1 (a wait gave up) / 2 (an XCC id outside 0..7)
+};
+constexpr int DEC_PERSIST_WGS = 256;
+constexpr int DEC_PERSIST_MAX_BATCH = 32;   // 4 sequences per XCD
+int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream);
+// The device has the 256 CUs in 8 XCDs the kernel assumes, and one workgroup of it fits a CU.
+bool dec_persist_device_ok(int device);
+
 // 1 when the two-launch layer covers this shape: d_model 512, 16 heads of 32, FFN 2048, at most
 // DEC_MAX_BATCH (64) sequences (the library's default choice up to DEC_AUTO_MAX_BATCH, 32), and rows
 // the attention takes in one workgroup per (sequence, head).

@@ -139,15 +139,69 @@ __device__ __forceinline__ int tile_dot(const int4 & w, const int8_t * a_blk, in
     return s + (int) sw[1];
 }
 
+// ---- the persistent decode's barrier among the 32 workgroups of one XCD ----
+// Each workgroup owns one flag word and stores into it, after its stores of a phase are complete,
+// the count of phases it has finished (an epoch from the step counter plus the phase); a workgroup
+// that needs the results of a phase waits until all 32 words have reached it. The words and the
+// rows the phases exchange are written with plain stores (performed at the XCD's L2) and read
+// with device-scope loads (which bypass the CU's L1), so the L2 shared by the XCD carries them;
+// no atomic read-modify-write is involved. Every wait is bounded: a workgroup that gives up (or
+// finds the error word set) sets the error word and the kernel ends, the host then falls back.
+constexpr int XBAR_SPIN_MAX = 1 << 18;     // polls (each a round trip to L2): about 0.2 s
+struct XBar {
+    int * flags;    // the XCD's 32 flag words
+    int * err;      // error word (0: none)
+    int target;     // wait until every word >= target (0: no wait)
+};
+
+__device__ __forceinline__ bool xbar_wait(const XBar & x, int tid, int * s_ok) {
+    if (x.target == 0) return true;
+    if (tid < 64) {
+        bool ok = false;
+        for (int spins = 0; spins < XBAR_SPIN_MAX; spins++) {
+            const int v = tid < 32 ? __hip_atomic_load(&x.flags[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : x.target;
+            if (__all(v >= x.target)) {
+                ok = true;
+                break;
+            }
+            if ((spins & 255) == 255 &&
+                __hip_atomic_load(x.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
+                break;
+        }
+        if (tid == 0) {
+            *s_ok = ok;
+            if (!ok) __hip_atomic_store(x.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();
+    return *s_ok != 0;
+}
+
+__device__ __forceinline__ void xbar_signal(int * flag, int value, int tid) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);   // this thread's stores are performed
+    __syncthreads();
+    if (tid == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// a row element another workgroup of the XCD wrote in this kernel (PERSIST) or before it
+template <bool PERSIST>
+__device__ __forceinline__ float ld_row(const float * p) {
+    if constexpr (PERSIST) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    else return *p;
+}
+
 }  // namespace
 
-template <int MODE, int NP>   // NP: the FFN2 partial rows of the input stage (IN_LN)
-__global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
+// Launch 1's work for (head h, sequence b). PERSIST (the persistent decode): the loads that do not
+// depend on the previous phase go out first, then the wait on `bar`, then the input row's
+// operands, read with device-scope loads; returns false when the wait gave up.
+template <int MODE, int NP, bool PERSIST>
+__device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h, const int b, const XBar & bar) {
     constexpr int NW = DL_WAVES;
     constexpr int PASSES = (DL_QKV_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     constexpr int WO_T = DL_NBLK / NW;                        // out-projection tiles per wave
-    const int h = blockIdx.x;
-    const int b = blockIdx.y;
     const int B = a.B;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -166,6 +220,8 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     __shared__ float s_l[NW];
     __shared__ float s_o[NW][ATT_HD];
     __shared__ __align__(16) int8_t s_a[DL_WAVES][ATT_HD];
+    __shared__ int s_ok;
+    if constexpr (PERSIST) __syncthreads();   // the previous item's LDS reads are done
 
     // ---- loads, in the order their data is needed, with no branch between them ----
     // The key range first, as vector loads (an index the compiler cannot see to be zero): a
@@ -179,10 +235,13 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     float xr = 0.0f, xb = 0.0f, xw = 0.0f, xc = 0.0f, xe = 0.0f, xpe = 0.0f;
     float xp[NP];
     int pos = 0;
-    if constexpr (MODE == IN_LN) {
-        xr = a.res[(int64_t) b * DL_K + tid];
+    auto load_ln_rows = [&]() {
+        xr = ld_row<PERSIST>(a.res + (int64_t) b * DL_K + tid);
 #pragma unroll
-        for (int g = 0; g < NP; g++) xp[g] = a.parts[((int64_t) g * B + b) * DL_K + tid];
+        for (int g = 0; g < NP; g++) xp[g] = ld_row<PERSIST>(a.parts + ((int64_t) g * B + b) * DL_K + tid);
+    };
+    if constexpr (MODE == IN_LN) {
+        if constexpr (!PERSIST) load_ln_rows();
         xb = a.bias[tid];
         xw = a.wb[tid];
         xc = a.wb[DL_K + tid];
@@ -240,6 +299,10 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
     KV8 cur;
     load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+    if constexpr (PERSIST) {
+        if (!xbar_wait(bar, tid, &s_ok)) return false;
+        if constexpr (MODE == IN_LN) load_ln_rows();
+    }
 
     // ---- the input row: LN2 of the previous layer (or the embedding), quantised into LDS ----
     float x;
@@ -344,10 +407,17 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
         const float y = (h2f(wos[u]) * da) * (float) isum;
         if (lane < 32) prow[t * 32 + lane] = y;
     }
+    return true;
 }
 
-template <int G>
-__global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
+template <int MODE, int NP>   // NP: the FFN2 partial rows of the input stage (IN_LN)
+__global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
+    dec_attn_body<MODE, NP, false>(a, blockIdx.x, blockIdx.y, XBar{});
+}
+
+// Launch 2's work for (hidden group g, sequence b); PERSIST as for dec_attn_body.
+template <int G, bool PERSIST>
+__device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, const int b, const XBar & bar) {
     constexpr int NW = DL_WAVES;
     constexpr int U = DL_FFN / G;              // hidden units of the group
     constexpr int UB = U / 32;                 // their Q8_0 blocks
@@ -355,8 +425,6 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
     constexpr int W2_T = (DL_K / 32) / NW;     // FFN2 output tiles per wave
     constexpr int K2_NBLK = DL_FFN / 32;       // blocks of an FFN2 weight row
     static_assert(U % (8 * NW) == 0 && UB * 32 == U && W2_T * NW * 32 == DL_K, "group shape");
-    const int g = blockIdx.x;
-    const int b = blockIdx.y;
     const int B = a.B;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -370,12 +438,18 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
     __shared__ float s_h[U];
     __shared__ __align__(16) int8_t s_hq[U];
     __shared__ float s_hd[UB];
+    __shared__ int s_ok;
+    if constexpr (PERSIST) __syncthreads();   // the previous item's LDS reads are done
 
     // ---- loads: the LN1 operands of element tid, then the group's weights ----
-    const float xr = a.res[(int64_t) b * DL_K + tid];
+    float xr = 0.0f;
     float xp[DL_NH];
+    auto load_ln_rows = [&]() {
+        xr = ld_row<PERSIST>(a.res + (int64_t) b * DL_K + tid);
 #pragma unroll
-    for (int hh = 0; hh < DL_NH; hh++) xp[hh] = a.p1[((int64_t) hh * B + b) * DL_K + tid];
+        for (int hh = 0; hh < DL_NH; hh++) xp[hh] = ld_row<PERSIST>(a.p1 + ((int64_t) hh * B + b) * DL_K + tid);
+    };
+    if constexpr (!PERSIST) load_ln_rows();
     const float xb = a.bo[tid];
     const float xw = a.wb1[tid];
     const float xc = a.wb1[DL_K + tid];
@@ -405,6 +479,10 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
             w2[u][k] = *reinterpret_cast<const int4 *>(a.w2q + (tb << 10) + lane * 16);
             d2[u][k] = a.w2d[(tb << 5) + (lane & 31)];
         }
+    }
+    if constexpr (PERSIST) {
+        if (!xbar_wait(bar, tid, &s_ok)) return false;
+        load_ln_rows();
     }
 
     // ---- n1 = LN1((x + o) + b_o), quantised into LDS ----
@@ -449,6 +527,90 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
         }
         if (lane < 32) prow[t * 32 + lane] = acc;
     }
+    return true;
+}
+
+template <int G>
+__global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
+    dec_ffn_body<G, false>(a, blockIdx.x, blockIdx.y, XBar{});
+}
+
+// one layer's two phases of the persistent decode on this workgroup (MODE: layer 0's embedding
+// input or a LayerNorm of the previous layer's rows); false when a wait gave up
+template <int MODE, int G>
+__device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int li, int x, int w, int ns, int epoch,
+                                                  const XBar & bar, int * my, int tid) {
+    bool first = true;
+    for (int it = w; it < ns * DL_NH; it += 32) {   // uniform over the workgroup
+        XBar bw = bar;
+        bw.target = (MODE == IN_LN && first) ? epoch + 2 * li : 0;
+        if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(p.attn[li], it % DL_NH, x + 8 * (it / DL_NH), bw))
+            return false;
+        first = false;
+    }
+    xbar_signal(my, epoch + 2 * li + 1, tid);
+    first = true;
+    for (int it = w; it < ns * G; it += 32) {
+        XBar bw = bar;
+        bw.target = first ? epoch + 2 * li + 1 : 0;
+        if (!dec_ffn_body<G, true>(p.ffn[li], it % G, x + 8 * (it / G), bw)) return false;
+        first = false;
+    }
+    xbar_signal(my, epoch + 2 * li + 2, tid);
+    return true;
+}
+
+// Placement: the dispatcher hands consecutive workgroups to the 8 XCDs in turn, starting where the
+// previous dispatch stopped, so the workgroups on one XCD are 32 consecutive multiples of 8 apart:
+// (the XCD, blockIdx / 8) numbers them 0..31 within it. The XCD comes from the hardware (XCC_ID),
+// so the workgroups that exchange a sequence's rows share an L2 whatever the placement; a
+// placement other than 32 per XCD leaves some flag word unwritten and the waits give up.
+template <int G>
+__global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
+    const int tid = threadIdx.x;
+    int xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    const int x = xcc & 7, w = blockIdx.x >> 3;
+    __shared__ int s_go;
+    if (tid == 0) {
+        const bool placed = (xcc & 0xf) < 8;
+        if (!placed) __hip_atomic_store(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_go = placed && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+    }
+    __syncthreads();
+    if (!s_go) return;
+    const int ns = x < p.B ? (p.B - 1 - x) / 8 + 1 : 0;   // sequences x, x + 8, ...
+    const int epoch = __builtin_amdgcn_readfirstlane(*p.step) * 64;   // 2 phases per layer, < 64
+    const XBar bar{p.flags + x * 32, p.err, 0};
+    int * my = p.flags + x * 32 + w;
+    if (!dec_persist_layer<IN_EMB, G>(p, 0, x, w, ns, epoch, bar, my, tid)) return;
+    for (int li = 1; li < p.n_layer; li++)
+        if (!dec_persist_layer<IN_LN, G>(p, li, x, w, ns, epoch, bar, my, tid)) return;
+}
+
+int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
+    GSVK_REQUIRE(a.B >= 1 && a.B <= DEC_PERSIST_MAX_BATCH && a.groups == dec_ffn_groups(a.B) && a.n_layer >= 1 &&
+                     a.attn && a.ffn && a.flags && a.err && a.step,
+                 "dec_persist: bad arguments (batch %d, %d layers)", a.B, a.n_layer);
+    if (a.groups == 32)
+        hipLaunchKernelGGL(k_dec_persist<32>, dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+    else
+        hipLaunchKernelGGL(k_dec_persist<16>, dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+    GSVK_LAUNCH_CHECK();
+    return GSVK_OK;
+}
+
+bool dec_persist_device_ok(int device) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
+    int occ16 = 0, occ32 = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16, k_dec_persist<16>, DL_THREADS, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ32, k_dec_persist<32>, DL_THREADS, 0) != hipSuccess) {
+        (void) hipGetLastError();
+        return false;
+    }
+    return prop.multiProcessorCount == DEC_PERSIST_WGS && occ16 >= 1 && occ32 >= 1 &&
+           std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
 }
 
 bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys) {

@@ -158,6 +158,12 @@ struct gsvk_model {
     float * qkv = nullptr, * o = nullptr, * h2 = nullptr, * logits = nullptr;
     float * p1 = nullptr, * p2 = nullptr;   // partial rows of the two-launch decode layer
     float * hx = nullptr;                   // FFN1 output rows (F16 / F32 projections)
+    // the persistent decode (decode_layer.h k_dec_persist): per-layer launch arguments in device
+    // memory, its barrier words + error word; usable on this device; failed once (then not used)
+    DecAttnArgs * d_pattn = nullptr;
+    DecFfnArgs * d_pffn = nullptr;
+    int * d_pflags = nullptr;           // [8 * 32] flags, then the error word
+    bool persist_dev_ok = false, persist_failed = false, persist_now = false;
     bool generic = false;   // some projection is F16 / F32: the per-op path (enqueue_decode_generic)
     int decode_path = GSVK_DECODE_AUTO;
     bool exact = false;   // gsvk_model_set_exact: ggml-cpu's arithmetic order throughout
@@ -698,72 +704,98 @@ int enqueue_decode_rows(gsvk_model * m, int r0, int n, hipStream_t st) {
 // attention, out-projection partial rows per head) and the FFN launch (LN1 over those partials,
 // FFN1 + ReLU of a group of hidden units, FFN2 partial rows per group); the head sums the last
 // layer's partials in its LayerNorm input stage.
-int enqueue_decode_fused(gsvk_model * m) {
-    const int B = m->B, D = m->D;
+void dec_layer_args(const gsvk_model * m, int li, DecAttnArgs & aa, DecFfnArgs & fa) {
+    const int B = m->B;
     const int G = dec_ffn_groups(B);   // hidden groups of the FFN launch = partial rows of the next LN
     const float scale = 1.0f / std::sqrt((float) m->HD);
-    hipStream_t st = m->stream;
-    for (int li = 0; li < m->NL; li++) {
-        const LayerW & w = m->L[li];
-        const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
-        DecAttnArgs aa{};
-        if (li == 0) {
-            aa.mode = IN_EMB;
-            aa.emb = m->audio_emb;
-            aa.pe = m->pe;
-            aa.tok = m->last_tok;
-            aa.pos_ptr = m->d_step;
-            aa.pos_add = m->prompt_len - 1;
-            aa.pos_sub = m->row_start;
-            aa.pe_rows = PE_MAX;
-            aa.alpha = m->audio_alpha;
-            aa.vocab = m->V;
-            aa.kv_end = m->kv_end;
-            aa.kv_end_add = m->S;
-        } else {
-            const LayerW & p = m->L[li - 1];
-            aa.mode = IN_LN;
-            aa.res = m->n1.x;
-            aa.parts = m->p2;
-            aa.nparts = G;
-            aa.bias = p.f2.b;
-            aa.wb = p.ln2;
-        }
-        aa.x_out = m->x.x;
-        aa.wq = w.qkv.qs;
-        aa.wd = w.qkv.d;
-        aa.bqkv = w.qkv.b;
-        aa.kc = m->kc + loff;
-        aa.vc = m->vc + loff;
-        aa.lstride = m->lstride;
-        aa.kv_begin = m->kv_begin;
-        aa.col_ptr = m->d_step;
-        aa.col_add = m->S - 1;
-        aa.scale_log2 = scale * 1.4426950408889634f;
-        aa.woq = w.out.qt;
-        aa.wod = w.out.dt;
-        aa.p1 = m->p1;
-        aa.B = B;
-        GSVK_TRY(launch_dec_attn(aa, st));
-        DecFfnArgs fa{};
-        fa.res = m->x.x;
-        fa.p1 = m->p1;
-        fa.bo = w.out.b;
-        fa.wb1 = w.ln1;
-        fa.n1_out = m->n1.x;
-        fa.w1q = w.f1.qs;
-        fa.w1d = w.f1.d;
-        fa.b1 = w.f1.b;
-        fa.w2q = w.f2.qt;
-        fa.w2d = w.f2.dt;
-        fa.p2 = m->p2;
-        fa.groups = G;
-        fa.B = B;
-        GSVK_TRY(launch_dec_ffn(fa, st));
+    const LayerW & w = m->L[li];
+    const size_t loff = (size_t) li * B * m->NH * m->lstride * m->HD;
+    aa = DecAttnArgs{};
+    if (li == 0) {
+        aa.mode = IN_EMB;
+        aa.emb = m->audio_emb;
+        aa.pe = m->pe;
+        aa.tok = m->last_tok;
+        aa.pos_ptr = m->d_step;
+        aa.pos_add = m->prompt_len - 1;
+        aa.pos_sub = m->row_start;
+        aa.pe_rows = PE_MAX;
+        aa.alpha = m->audio_alpha;
+        aa.vocab = m->V;
+        aa.kv_end = m->kv_end;
+        aa.kv_end_add = m->S;
+    } else {
+        const LayerW & p = m->L[li - 1];
+        aa.mode = IN_LN;
+        aa.res = m->n1.x;
+        aa.parts = m->p2;
+        aa.nparts = G;
+        aa.bias = p.f2.b;
+        aa.wb = p.ln2;
     }
+    aa.x_out = m->x.x;
+    aa.wq = w.qkv.qs;
+    aa.wd = w.qkv.d;
+    aa.bqkv = w.qkv.b;
+    aa.kc = m->kc + loff;
+    aa.vc = m->vc + loff;
+    aa.lstride = m->lstride;
+    aa.kv_begin = m->kv_begin;
+    aa.col_ptr = m->d_step;
+    aa.col_add = m->S - 1;
+    aa.scale_log2 = scale * 1.4426950408889634f;
+    aa.woq = w.out.qt;
+    aa.wod = w.out.dt;
+    aa.p1 = m->p1;
+    aa.B = B;
+    fa = DecFfnArgs{};
+    fa.res = m->x.x;
+    fa.p1 = m->p1;
+    fa.bo = w.out.b;
+    fa.wb1 = w.ln1;
+    fa.n1_out = m->n1.x;
+    fa.w1q = w.f1.qs;
+    fa.w1d = w.f1.d;
+    fa.b1 = w.f1.b;
+    fa.w2q = w.f2.qt;
+    fa.w2d = w.f2.dt;
+    fa.p2 = m->p2;
+    fa.groups = G;
+    fa.B = B;
+}
+
+int decode_head_parts(gsvk_model * m) {
     const LayerW & last = m->L[m->NL - 1];
     return launch_head_ln_parts(m->head, m->head_type == GGML_F16 ? 1 : 0, m->V, m->n1.x, m->p2,
-                                G, (int64_t) B * D, last.f2.b, last.ln2, B, m->logits, m->V, st);
+                                dec_ffn_groups(m->B), (int64_t) m->B * m->D, last.f2.b, last.ln2, m->B, m->logits,
+                                m->V, m->stream);
+}
+
+int enqueue_decode_fused(gsvk_model * m) {
+    for (int li = 0; li < m->NL; li++) {
+        DecAttnArgs aa;
+        DecFfnArgs fa;
+        dec_layer_args(m, li, aa, fa);
+        GSVK_TRY(launch_dec_attn(aa, m->stream));
+        GSVK_TRY(launch_dec_ffn(fa, m->stream));
+    }
+    return decode_head_parts(m);
+}
+
+// The persistent decode: one launch for the 24 layers (the arguments prepare_persist uploaded),
+// then the head.
+int enqueue_decode_persist(gsvk_model * m) {
+    DecPersistArgs pa{};
+    pa.attn = m->d_pattn;
+    pa.ffn = m->d_pffn;
+    pa.n_layer = m->NL;
+    pa.B = m->B;
+    pa.groups = dec_ffn_groups(m->B);
+    pa.step = m->d_step;
+    pa.flags = m->d_pflags;
+    pa.err = m->d_pflags + 8 * 32;
+    GSVK_TRY(launch_dec_persist(pa, m->stream));
+    return decode_head_parts(m);
 }
 
 // y[R][n] = W[n][k] . x[R][k] of one projection in ggml-cpu's order: a Q8_0 weight through the GEMV
@@ -836,6 +868,53 @@ bool fused_decode_ok(const gsvk_model * m) {
     return true;
 }
 
+// The persistent decode covers the shape: the two-launch layer's range up to 32 sequences, the device
+// it assumes, no earlier failure, not in exact mode or a continuous-batching session.
+bool persist_decode_ok(const gsvk_model * m) {
+    return m->persist_dev_ok && !m->persist_failed && !m->exact && !m->cb_open && m->B <= DEC_PERSIST_MAX_BATCH &&
+           m->NL <= 64 && fused_decode_ok(m);
+}
+
+// Before the decode steps of a run (outside any graph capture): the persistent decode's per-layer
+// arguments for the current state uploaded and its barrier words cleared, when it will run.
+int prepare_persist(gsvk_model * m) {
+    m->persist_now = false;
+    const bool want = m->decode_path == GSVK_DECODE_PERSIST ||
+                      (m->decode_path == GSVK_DECODE_AUTO && m->B <= DEC_AUTO_MAX_BATCH);
+    if (!want || !persist_decode_ok(m)) return GSVK_OK;
+    if (!m->d_pattn) {
+        GSVK_TRY(m->wmem.alloc(m->d_pattn, (size_t) m->NL));
+        GSVK_TRY(m->wmem.alloc(m->d_pffn, (size_t) m->NL));
+        GSVK_TRY(m->wmem.alloc(m->d_pflags, 8 * 32 + 1));
+    }
+    std::vector<DecAttnArgs> aa((size_t) m->NL);
+    std::vector<DecFfnArgs> fa((size_t) m->NL);
+    for (int li = 0; li < m->NL; li++) dec_layer_args(m, li, aa[(size_t) li], fa[(size_t) li]);
+    GSVK_HIP(hipMemcpy(m->d_pattn, aa.data(), aa.size() * sizeof(DecAttnArgs), hipMemcpyHostToDevice));
+    GSVK_HIP(hipMemcpy(m->d_pffn, fa.data(), fa.size() * sizeof(DecFfnArgs), hipMemcpyHostToDevice));
+    GSVK_HIP(hipMemsetAsync(m->d_pflags, 0, (8 * 32 + 1) * sizeof(int), m->stream));
+    GSVK_HIP(hipStreamSynchronize(m->stream));
+    m->persist_now = true;
+    return GSVK_OK;
+}
+
+// After a run on the persistent decode: its error word. Nonzero (a barrier wait gave up: the
+// workgroups were not placed 32 per XCD, or one never ran): the run's results are not valid, the
+// persistent decode is not used again by this model, and the caller repeats the run.
+int persist_check(gsvk_model * m, bool * failed) {
+    *failed = false;
+    if (!m->persist_now) return GSVK_OK;
+    int err = 0;
+    GSVK_HIP(hipMemcpy(&err, m->d_pflags + 8 * 32, sizeof(int), hipMemcpyDeviceToHost));
+    if (err != 0) {
+        fprintf(stderr, "[gsvk] persistent decode failed (code %d): using the two-launch decode from now on\n", err);
+        m->persist_failed = true;
+        m->persist_now = false;
+        *failed = true;
+    }
+    return GSVK_OK;
+}
+
 int enqueue_decode_body(gsvk_model * m) {
     if (m->generic) {
         GSVK_REQUIRE(m->decode_path == GSVK_DECODE_AUTO, "decode path %d: not available for a model with F16 / "
@@ -859,9 +938,15 @@ int enqueue_decode_body(gsvk_model * m) {
         GSVK_REQUIRE(fused_decode_ok(m), "decode path FUSED: not available for %d sequences (at most %d) "
                      "or for this model (it needs an F16 or F32 head)", m->B, DEC_MAX_BATCH);
         return enqueue_decode_fused(m);
+    case GSVK_DECODE_PERSIST:
+        GSVK_REQUIRE(m->persist_now, "decode path PERSIST: not available (%d sequences, at most %d; it needs "
+                     "the 256-CU gfx950 device, an F16 or F32 head, and no earlier failure; not in exact mode or "
+                     "a continuous batch)", m->B, DEC_PERSIST_MAX_BATCH);
+        return enqueue_decode_persist(m);
     case GSVK_DECODE_MFMA:
         return enqueue_decode_mfma(m);
     default:
+        if (m->persist_now) return enqueue_decode_persist(m);
         if (m->B <= DEC_AUTO_MAX_BATCH && fused_decode_ok(m)) return enqueue_decode_fused(m);
         break;
     }
@@ -1316,6 +1401,7 @@ extern "C" int gsvk_model_load(const char * path, int device, int verbose, gsvk_
     m->verbose = verbose;
     GSVK_HIP(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
     if (getenv("GSVK_NO_GRAPH")) m->use_graph = false;
+    m->persist_dev_ok = !getenv("GSVK_NO_PERSIST") && dec_persist_device_ok(device);
     m->D = hp.D;
     m->NH = hp.NH;
     m->NL = hp.NL;
@@ -1516,7 +1602,7 @@ extern "C" int gsvk_kv_alloc(gsvk_model * m, int B, int lmax) {
 
 extern "C" int gsvk_model_set_decode_path(gsvk_model * m, int path) {
     GSVK_REQUIRE(m, "null model");
-    GSVK_REQUIRE(path >= GSVK_DECODE_AUTO && path <= GSVK_DECODE_MFMA, "bad decode path %d", path);
+    GSVK_REQUIRE(path >= GSVK_DECODE_AUTO && path <= GSVK_DECODE_PERSIST, "bad decode path %d", path);
     DeviceGuard guard(m->device);
     cb_drop(m);
     drop_graph(m);
@@ -1599,7 +1685,14 @@ extern "C" int gsvk_decode_step(gsvk_model * m, const int32_t * last_tok, float 
     GSVK_TRY(upload(m->last_tok, last_tok, (size_t) B * 4, st));
     GSVK_TRY(upload(m->d_step, &step1, 4, st));
     GSVK_HIP(hipStreamSynchronize(st));   // the host values above live on this stack frame
+    GSVK_TRY(prepare_persist(m));
     GSVK_TRY(enqueue_decode_body(m));
+    {
+        GSVK_HIP(hipStreamSynchronize(st));
+        bool failed = false;
+        GSVK_TRY(persist_check(m, &failed));
+        if (failed) GSVK_TRY(enqueue_decode_body(m));   // the same step on the two-launch decode
+    }
     if (logits) GSVK_HIP(hipMemcpyAsync(logits, m->logits, (size_t) B * m->V * 4, hipMemcpyDeviceToHost, st));
     GSVK_HIP(hipStreamSynchronize(st));
     m->host_step++;
@@ -1686,6 +1779,7 @@ extern "C" int gsvk_cb_open(gsvk_model * m, int capacity, int max_prefill, int m
     sa.row_start = m->row_start;
     sa.row_max = m->row_max;
     m->cb_open = true;
+    m->persist_now = false;
     m->cb_smax = max_prefill;
     m->cb_steps = max_steps;
     m->cb_step = 0;
@@ -1919,6 +2013,7 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
         return GSVK_OK;
     };
     drop_graph(m);
+    GSVK_TRY(prepare_persist(m));
     if (m->use_graph && max_steps > 1) {
         GSVK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
         const int rc = enqueue_step();
@@ -1957,6 +2052,13 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     }
     GSVK_HIP(hipStreamSynchronize(st));
     out->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_dec).count();
+    {
+        bool failed = false;
+        GSVK_TRY(persist_check(m, &failed));
+        if (failed)   // the run again, on the two-launch decode (prefill included: the cache was written)
+            return gsvk_generate(m, reqs, B, cfg, seed_base, early_stop_num, max_steps, oracle, n_oracle, seeds,
+                                 flags, out);
+    }
     m->prof.dec_compute_ms = out->decode_ms;
     const auto t_res = std::chrono::steady_clock::now();
     // results

@@ -34,7 +34,7 @@ EXPORTS = [
     "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact", "gsvk_model_get_profile",
 ]
 
-GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA = 0, 1, 2, 3
+GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA, GSVK_DECODE_PERSIST = 0, 1, 2, 3, 4
 
 
 class GsvkError(RuntimeError):
@@ -420,7 +420,7 @@ class Model:
         check(lib().gsvk_release_cache(self.h), "release_cache")
 
     def set_decode_path(self, path: int):
-        """GSVK_DECODE_AUTO / _GEMV / _FUSED / _MFMA (include/gsvk.h)."""
+        """GSVK_DECODE_AUTO / _GEMV / _FUSED / _MFMA / _PERSIST (include/gsvk.h)."""
         check(lib().gsvk_model_set_decode_path(self.h, path), "set_decode_path")
 
     def set_prefill_f16(self, on: bool = True):

@@ -158,15 +158,23 @@ int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_s
 int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out);
 
 /* Which kernels run a decode step (the arithmetic of src/gsv_ar.cpp:380-467 in every case):
- *  GSVK_DECODE_AUTO  the library's choice (default): up to 32 sequences the two-launch layer,
- *                    from 33 the matrix-core GEMMs (the faster of the two at each batch);
+ *  GSVK_DECODE_AUTO  the library's choice (default): up to 32 sequences the persistent decode
+ *                    where it runs (PERSIST), else the two-launch layer; from 33 the matrix-core
+ *                    GEMMs (the fastest at each batch);
  *  GSVK_DECODE_GEMV  up to 16 sequences the GEMV chain whose projections and LayerNorms are
  *                    bit-exact with ggml-cpu's x86 order (4 launches per layer);
  *  GSVK_DECODE_FUSED up to 64 sequences two launches per layer (attention + out-projection
  *                    partial rows per head; LN1 + FFN1 + FFN2 partial rows per group of hidden
  *                    units): the same int32 block dots, fp32 sums over heads and groups in a fixed
  *                    order (agrees with the GEMV chain to fp32 rounding);
- *  GSVK_DECODE_MFMA  the matrix-core GEMMs at any batch.
+ *  GSVK_DECODE_MFMA  the matrix-core GEMMs at any batch;
+ *  GSVK_DECODE_PERSIST up to 32 sequences, all 24 layers of a step in one launch: the two-launch
+ *                    layer's work and arithmetic (the same bits), each XCD running whole
+ *                    sequences with its 32 workgroups synchronised through per-workgroup flag
+ *                    words in its L2; needs the 256-CU gfx950 device (checked), not in exact mode
+ *                    or a continuous batch. A run whose workgroups could not synchronise (a
+ *                    bounded wait gave up) is repeated on the two-launch layer, which the model
+ *                    then keeps using; GSVK_NO_PERSIST in the environment turns it off.
  * An explicit choice that does not cover the batch (or model: FUSED needs an F16 / F32 head) makes
  * the decode fail with an error naming it; it never falls back to another path. No counterpart
  * in the reference (it has one CPU path); for tests and benchmarks. */
@@ -174,6 +182,7 @@ int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * 
 #define GSVK_DECODE_GEMV   1
 #define GSVK_DECODE_FUSED  2
 #define GSVK_DECODE_MFMA   3
+#define GSVK_DECODE_PERSIST 4
 int gsvk_model_set_decode_path(gsvk_model * m, int path);
 
 /* Exact mode (on != 0): every projection, LayerNorm, quantisation and attention row of the

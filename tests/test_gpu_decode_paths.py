@@ -6,6 +6,8 @@
   and FFN2 are summed over heads / hidden groups as partial rows, so they agree with the GEMV
   chain to fp32 rounding; everything before the first of those sums (the layer-0 input, QKV, the
   K/V append of layer 0) is unchanged and stays bit-exact.
+* GSVK_DECODE_PERSIST (the default up to 32 sequences where the device allows): the two-launch
+  layer's work in one launch per step, each XCD running whole sequences; the same bits as FUSED.
 """
 import numpy as np
 import pytest
@@ -342,3 +344,38 @@ def test_dec_ffn_op_matches_separate_kernels(gpu, B):
     yref = y.cpu().numpy().astype(np.float64)
     ysum = p2.cpu().numpy().astype(np.float64).sum(axis=0)
     assert np.abs(ysum - yref).max() <= 2e-6 * np.abs(yref).max()
+
+
+@pytest.mark.parametrize("B", [1, 3, 8, 9, 16, 17, 32])
+def test_persistent_decode_equals_two_launch_layer(gpu, model4_path, B):
+    """The persistent decode (all layers of a step in one launch, per-XCD barriers) against the
+    two launches per layer: the logits entering every teacher-forced step, the K/V of every layer
+    and the sampled tokens of a generate, all to the bit. Batches 1-8: one sequence per XCD, 32
+    FFN groups; 9-16: up to two; 17-32: up to four (two items per workgroup and phase)."""
+    rng = np.random.default_rng(500 + B)
+    reqs = _reqs(501 + B, rng.integers(3, 60, B), 16)
+    steps = 10
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
+    cfg = (15, 1.0, 1.0, 1.35)
+    seeds = list(range(1, B + 1))
+    g = gpu.Model(model4_path)
+    try:
+        print(f"persistent vs two-launch, batch {B}", flush=True)
+        a = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_FUSED)
+        kva = [g.kv_read(li) for li in (0, 3)]
+        ra = g.generate(reqs, sampler=cfg, max_steps=24, seeds=seeds, flags=1)
+        b = _step_logits(g, reqs, forced, steps, gpu.GSVK_DECODE_PERSIST)
+        kvb = [g.kv_read(li) for li in (0, 3)]
+        rb = g.generate(reqs, sampler=cfg, max_steps=24, seeds=seeds, flags=1)
+        g.set_decode_path(gpu.GSVK_DECODE_AUTO)
+        rc = g.generate(reqs, sampler=cfg, max_steps=24, seeds=seeds, flags=1)
+    finally:
+        g.close()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), np.abs(a - b).max()
+    ncol = max(len(r["phones"]) for r in reqs) + 16 + steps - 1    # the columns the steps wrote
+    for (ka, va), (kb, vb) in zip(kva, kvb):
+        assert np.array_equal(ka[:, :, :ncol], kb[:, :, :ncol]) and np.array_equal(va[:, :, :ncol], vb[:, :, :ncol])
+    for r in (rb, rc):
+        assert r["n_steps"] == ra["n_steps"]
+        for i in range(B):
+            assert np.array_equal(r["tokens"][i], ra["tokens"][i]), i
