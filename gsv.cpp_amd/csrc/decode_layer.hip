@@ -198,7 +198,8 @@ __device__ __forceinline__ float ld_row(const float * p) {
 // depend on the previous phase go out first, then the wait on `bar`, then the input row's
 // operands, read with device-scope loads; returns false when the wait gave up.
 template <int MODE, int NP, bool PERSIST>
-__device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h, const int b, const XBar & bar) {
+__device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h, const int b, const XBar & bar,
+                                              const int col_pre = 0, const int beg_pre = 0) {
     constexpr int NW = DL_WAVES;
     constexpr int PASSES = (DL_QKV_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     constexpr int WO_T = DL_NBLK / NW;                        // out-projection tiles per wave
@@ -228,10 +229,14 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     // scalar load's value would be consumed right after it (the compiler places its wait there),
     // holding back every load below; a vector load's wait is placed at its first use, after the
     // scheduling barrier below.
-    int vz;
-    asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
-    const int col_ld = a.col_ptr[vz];
-    const int beg_ld = a.kv_begin[b + vz];
+    // (PERSIST: *col_ptr and kv_begin[b] come in as col_pre, beg_pre, read once per launch)
+    int col_ld = col_pre, beg_ld = beg_pre;
+    if constexpr (!PERSIST) {
+        int vz;
+        asm volatile("v_mov_b32 %0, 0" : "=v"(vz));
+        col_ld = a.col_ptr[vz];
+        beg_ld = a.kv_begin[b + vz];
+    }
     float xr = 0.0f, xb = 0.0f, xw = 0.0f, xc = 0.0f, xe = 0.0f, xpe = 0.0f;
     float xp[NP];
     int pos = 0;
@@ -240,11 +245,16 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
 #pragma unroll
         for (int g = 0; g < NP; g++) xp[g] = ld_row<PERSIST>(a.parts + ((int64_t) g * B + b) * DL_K + tid);
     };
-    if constexpr (MODE == IN_LN) {
-        if constexpr (!PERSIST) load_ln_rows();
+    auto load_ln_params = [&]() {
         xb = a.bias[tid];
         xw = a.wb[tid];
         xc = a.wb[DL_K + tid];
+    };
+    if constexpr (MODE == IN_LN) {
+        if constexpr (!PERSIST) {
+            load_ln_rows();
+            load_ln_params();
+        }
     } else {
         pos = *a.pos_ptr;
         int tk = a.tok[b];
@@ -258,28 +268,36 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     int4 w[PASSES][4];
     uint2 dh[PASSES][4];
     float rbias[PASSES];
-#pragma unroll
-    for (int p = 0; p < PASSES; p++) {
-        const int rl = (p * NW + wave) * 8 + rsub;
-        const int rlc = rl < DL_QKV_ROWS ? rl : DL_QKV_ROWS - 1;
-        const int row = (rlc >> 5) * DL_K + h * ATT_HD + (rlc & 31);
-        const int4 * wsl = reinterpret_cast<const int4 *>(a.wq + ((int64_t) row * 8 + j) * DL_NBLK * 4);
-        const uint2 * wdr = reinterpret_cast<const uint2 *>(a.wd + (int64_t) row * DL_NBLK);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            w[p][i] = wsl[i];
-            dh[p][i] = wdr[i];
-        }
-        rbias[p] = a.bqkv[row];
-    }
     int4 wo[WO_T];
     uint16_t wos[WO_T];
+    auto load_qkv_weights = [&]() {
 #pragma unroll
-    for (int u = 0; u < WO_T; u++) {
-        const int t = wave + NW * u;    // 32-row tile of the out projection's 512 outputs
-        wo[u] = *reinterpret_cast<const int4 *>(a.woq + (((int64_t) t * DL_NBLK + h) << 10) + lane * 16);
-        wos[u] = a.wod[(((int64_t) t * DL_NBLK + h) << 5) + (lane & 31)];
-    }
+        for (int p = 0; p < PASSES; p++) {
+            const int rl = (p * NW + wave) * 8 + rsub;
+            const int rlc = rl < DL_QKV_ROWS ? rl : DL_QKV_ROWS - 1;
+            const int row = (rlc >> 5) * DL_K + h * ATT_HD + (rlc & 31);
+            const int4 * wsl = reinterpret_cast<const int4 *>(a.wq + ((int64_t) row * 8 + j) * DL_NBLK * 4);
+            const uint2 * wdr = reinterpret_cast<const uint2 *>(a.wd + (int64_t) row * DL_NBLK);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                w[p][i] = wsl[i];
+                dh[p][i] = wdr[i];
+            }
+            rbias[p] = a.bqkv[row];
+        }
+    };
+    auto load_out_weights = [&]() {
+#pragma unroll
+        for (int u = 0; u < WO_T; u++) {
+            const int t = wave + NW * u;    // 32-row tile of the out projection's 512 outputs
+            wo[u] = *reinterpret_cast<const int4 *>(a.woq + (((int64_t) t * DL_NBLK + h) << 10) + lane * 16);
+            wos[u] = a.wod[(((int64_t) t * DL_NBLK + h) << 5) + (lane & 31)];
+        }
+    };
+    // PERSIST: the QKV weights go out ahead of the barrier's poll; the loads that are needed
+    // later (cached keys, out projection) after the input row's, behind the wait
+    load_qkv_weights();
+    if constexpr (!PERSIST) load_out_weights();
     // (the key range arrived first: its loads were issued first and retire in order)
     __builtin_amdgcn_sched_barrier(0);
     const int col = __builtin_amdgcn_readfirstlane(col_ld) + a.col_add;   // column of this step's key
@@ -298,10 +316,16 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     last_old = last_old < a.lstride ? last_old : (int) a.lstride - 1;
     int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
     KV8 cur;
-    load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
-    if constexpr (PERSIST) {
+    if constexpr (!PERSIST) {
+        load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+    } else {
         if (!xbar_wait(bar, tid, &s_ok)) return false;
-        if constexpr (MODE == IN_LN) load_ln_rows();
+        if constexpr (MODE == IN_LN) {
+            load_ln_rows();
+            load_ln_params();
+        }
+        load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+        load_out_weights();
     }
 
     // ---- the input row: LN2 of the previous layer (or the embedding), quantised into LDS ----
@@ -449,40 +473,57 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
 #pragma unroll
         for (int hh = 0; hh < DL_NH; hh++) xp[hh] = ld_row<PERSIST>(a.p1 + ((int64_t) hh * B + b) * DL_K + tid);
     };
-    if constexpr (!PERSIST) load_ln_rows();
-    const float xb = a.bo[tid];
-    const float xw = a.wb1[tid];
-    const float xc = a.wb1[DL_K + tid];
+    float xb = 0.0f, xw = 0.0f, xc = 0.0f;
+    auto load_ln_params = [&]() {
+        xb = a.bo[tid];
+        xw = a.wb1[tid];
+        xc = a.wb1[DL_K + tid];
+    };
+    if constexpr (!PERSIST) {
+        load_ln_rows();
+        load_ln_params();
+    }
     int4 w1[PASSES][4];
     uint2 d1[PASSES][4];
     float rb1[PASSES];
-#pragma unroll
-    for (int p = 0; p < PASSES; p++) {
-        const int row = g * U + (p * NW + wave) * 8 + rsub;
-        const int4 * wsl = reinterpret_cast<const int4 *>(a.w1q + ((int64_t) row * 8 + j) * DL_NBLK * 4);
-        const uint2 * wdr = reinterpret_cast<const uint2 *>(a.w1d + (int64_t) row * DL_NBLK);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            w1[p][i] = wsl[i];
-            d1[p][i] = wdr[i];
-        }
-        rb1[p] = a.b1[row];
-    }
     int4 w2[W2_T][UB];
     uint16_t d2[W2_T][UB];
+    auto load_ffn1_weights = [&]() {
 #pragma unroll
-    for (int u = 0; u < W2_T; u++) {
-        const int t = wave + NW * u;
+        for (int p = 0; p < PASSES; p++) {
+            const int row = g * U + (p * NW + wave) * 8 + rsub;
+            const int4 * wsl = reinterpret_cast<const int4 *>(a.w1q + ((int64_t) row * 8 + j) * DL_NBLK * 4);
+            const uint2 * wdr = reinterpret_cast<const uint2 *>(a.w1d + (int64_t) row * DL_NBLK);
 #pragma unroll
-        for (int k = 0; k < UB; k++) {
-            const int64_t tb = (int64_t) t * K2_NBLK + g * UB + k;
-            w2[u][k] = *reinterpret_cast<const int4 *>(a.w2q + (tb << 10) + lane * 16);
-            d2[u][k] = a.w2d[(tb << 5) + (lane & 31)];
+            for (int i = 0; i < 4; i++) {
+                w1[p][i] = wsl[i];
+                d1[p][i] = wdr[i];
+            }
+            rb1[p] = a.b1[row];
         }
-    }
-    if constexpr (PERSIST) {
+    };
+    auto load_ffn2_weights = [&]() {
+#pragma unroll
+        for (int u = 0; u < W2_T; u++) {
+            const int t = wave + NW * u;
+#pragma unroll
+            for (int k = 0; k < UB; k++) {
+                const int64_t tb = (int64_t) t * K2_NBLK + g * UB + k;
+                w2[u][k] = *reinterpret_cast<const int4 *>(a.w2q + (tb << 10) + lane * 16);
+                d2[u][k] = a.w2d[(tb << 5) + (lane & 31)];
+            }
+        }
+    };
+    // PERSIST: FFN1's weights ahead of the barrier's poll, FFN2's after the input row's (as in
+    // dec_attn_body)
+    load_ffn1_weights();
+    if constexpr (!PERSIST) {
+        load_ffn2_weights();
+    } else {
         if (!xbar_wait(bar, tid, &s_ok)) return false;
         load_ln_rows();
+        load_ln_params();
+        load_ffn2_weights();
     }
 
     // ---- n1 = LN1((x + o) + b_o), quantised into LDS ----
@@ -537,24 +578,81 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_ffn(DecFfnArgs a) {
 
 // one layer's two phases of the persistent decode on this workgroup (MODE: layer 0's embedding
 // input or a LayerNorm of the previous layer's rows); false when a wait gave up
-template <int MODE, int G>
+// A layer's arguments, read through the constant address space (scalar loads into SGPRs: they do
+// not change during the launch) with every pointer in it declared a global-memory one, so that the
+// loads through them are global loads (counted by vmcnt alone) and not flat ones, whose completion
+// an LDS wait would also have to wait for.
+#define GSVK_GLOBAL_PTR(ptr) \
+    __builtin_assume(!__builtin_amdgcn_is_shared((const void *) (ptr)) && !__builtin_amdgcn_is_private((const void *) (ptr)))
+// (device pass only: the host pass sees a plain copy it never runs)
+__device__ __forceinline__ DecAttnArgs persist_attn_args(const DecAttnArgs * all, int li) {
+#if !defined(__HIP_DEVICE_COMPILE__)
+    return all[li];
+#else
+    DecAttnArgs a = ((const __attribute__((address_space(4))) DecAttnArgs *) all)[li];
+    GSVK_GLOBAL_PTR(a.res); GSVK_GLOBAL_PTR(a.parts); GSVK_GLOBAL_PTR(a.bias); GSVK_GLOBAL_PTR(a.wb);
+    GSVK_GLOBAL_PTR(a.emb); GSVK_GLOBAL_PTR(a.pe); GSVK_GLOBAL_PTR(a.tok); GSVK_GLOBAL_PTR(a.pos_ptr);
+    GSVK_GLOBAL_PTR(a.pos_sub); GSVK_GLOBAL_PTR(a.kv_end); GSVK_GLOBAL_PTR(a.x_out); GSVK_GLOBAL_PTR(a.wq);
+    GSVK_GLOBAL_PTR(a.wd); GSVK_GLOBAL_PTR(a.bqkv); GSVK_GLOBAL_PTR(a.kc); GSVK_GLOBAL_PTR(a.vc);
+    GSVK_GLOBAL_PTR(a.kv_begin); GSVK_GLOBAL_PTR(a.col_ptr); GSVK_GLOBAL_PTR(a.woq); GSVK_GLOBAL_PTR(a.wod);
+    GSVK_GLOBAL_PTR(a.p1);
+    return a;
+#endif
+}
+__device__ __forceinline__ DecFfnArgs persist_ffn_args(const DecFfnArgs * all, int li) {
+#if !defined(__HIP_DEVICE_COMPILE__)
+    return all[li];
+#else
+    DecFfnArgs a = ((const __attribute__((address_space(4))) DecFfnArgs *) all)[li];
+    GSVK_GLOBAL_PTR(a.res); GSVK_GLOBAL_PTR(a.p1); GSVK_GLOBAL_PTR(a.bo); GSVK_GLOBAL_PTR(a.wb1);
+    GSVK_GLOBAL_PTR(a.n1_out); GSVK_GLOBAL_PTR(a.w1q); GSVK_GLOBAL_PTR(a.w1d); GSVK_GLOBAL_PTR(a.b1);
+    GSVK_GLOBAL_PTR(a.w2q); GSVK_GLOBAL_PTR(a.w2d); GSVK_GLOBAL_PTR(a.p2);
+    return a;
+#endif
+}
+
+// The workgroup's attention items are (head it % 16, sequence x + 8 (it / 16)) for it = w, w + 32:
+// at most 2 (4 sequences per XCD), the same in every layer; col (the new key's column before
+// col_add) and beg[k] (item k's first key) were read at the launch's start. ONE: at most one
+// attention item and one FFN item per workgroup (up to 2 sequences per XCD, batch <= 16), written
+// without the item loops, which (with the loads each item issues ahead of its wait) cost the loop
+// form registers it spills.
+static_assert(DEC_PERSIST_MAX_BATCH / 8 * DL_NH <= 2 * 32, "two attention items per workgroup at most");
+
+template <int MODE, int G, bool ONE>
 __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int li, int x, int w, int ns, int epoch,
-                                                  const XBar & bar, int * my, int tid) {
-    bool first = true;
-    for (int it = w; it < ns * DL_NH; it += 32) {   // uniform over the workgroup
-        XBar bw = bar;
-        bw.target = (MODE == IN_LN && first) ? epoch + 2 * li : 0;
-        if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(p.attn[li], it % DL_NH, x + 8 * (it / DL_NH), bw))
-            return false;
-        first = false;
+                                                  const XBar & bar, int * my, int tid, int col, const int (&beg)[2]) {
+    const DecAttnArgs aa = persist_attn_args(p.attn, li);
+    if constexpr (ONE) {
+        if (w < ns * DL_NH) {   // uniform over the workgroup
+            XBar bw = bar;
+            bw.target = MODE == IN_LN ? epoch + 2 * li : 0;
+            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(aa, w % DL_NH, x + 8 * (w / DL_NH), bw, col, beg[0]))
+                return false;
+        }
+    } else {
+        for (int it = w, k = 0; it < ns * DL_NH; it += 32, k++) {
+            XBar bw = bar;
+            bw.target = (MODE == IN_LN && k == 0) ? epoch + 2 * li : 0;
+            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw, col,
+                                                                    k == 0 ? beg[0] : beg[1]))
+                return false;
+        }
     }
     xbar_signal(my, epoch + 2 * li + 1, tid);
-    first = true;
-    for (int it = w; it < ns * G; it += 32) {
-        XBar bw = bar;
-        bw.target = first ? epoch + 2 * li + 1 : 0;
-        if (!dec_ffn_body<G, true>(p.ffn[li], it % G, x + 8 * (it / G), bw)) return false;
-        first = false;
+    const DecFfnArgs fa = persist_ffn_args(p.ffn, li);
+    if constexpr (ONE) {
+        if (w < ns * G) {
+            XBar bw = bar;
+            bw.target = epoch + 2 * li + 1;
+            if (!dec_ffn_body<G, true>(fa, w % G, x + 8 * (w / G), bw)) return false;
+        }
+    } else {
+        for (int it = w; it < ns * G; it += 32) {
+            XBar bw = bar;
+            bw.target = it == w ? epoch + 2 * li + 1 : 0;
+            if (!dec_ffn_body<G, true>(fa, it % G, x + 8 * (it / G), bw)) return false;
+        }
     }
     xbar_signal(my, epoch + 2 * li + 2, tid);
     return true;
@@ -565,7 +663,7 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
 // (the XCD, blockIdx / 8) numbers them 0..31 within it. The XCD comes from the hardware (XCC_ID),
 // so the workgroups that exchange a sequence's rows share an L2 whatever the placement; a
 // placement other than 32 per XCD leaves some flag word unwritten and the waits give up.
-template <int G>
+template <int G, bool ONE>
 __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     const int tid = threadIdx.x;
     int xcc;
@@ -583,19 +681,30 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     const int epoch = __builtin_amdgcn_readfirstlane(*p.step) * 64;   // 2 phases per layer, < 64
     const XBar bar{p.flags + x * 32, p.err, 0};
     int * my = p.flags + x * 32 + w;
-    if (!dec_persist_layer<IN_EMB, G>(p, 0, x, w, ns, epoch, bar, my, tid)) return;
+    const DecAttnArgs a0 = persist_attn_args(p.attn, 0);
+    const int col = __builtin_amdgcn_readfirstlane(*a0.col_ptr);
+    int beg[2] = {0, 0};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        const int it = w + 32 * k;
+        if (it < ns * DL_NH) beg[k] = __builtin_amdgcn_readfirstlane(a0.kv_begin[x + 8 * (it / DL_NH)]);
+    }
+    if (!dec_persist_layer<IN_EMB, G, ONE>(p, 0, x, w, ns, epoch, bar, my, tid, col, beg)) return;
     for (int li = 1; li < p.n_layer; li++)
-        if (!dec_persist_layer<IN_LN, G>(p, li, x, w, ns, epoch, bar, my, tid)) return;
+        if (!dec_persist_layer<IN_LN, G, ONE>(p, li, x, w, ns, epoch, bar, my, tid, col, beg)) return;
 }
 
 int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
     GSVK_REQUIRE(a.B >= 1 && a.B <= DEC_PERSIST_MAX_BATCH && a.groups == dec_ffn_groups(a.B) && a.n_layer >= 1 &&
                      a.attn && a.ffn && a.flags && a.err && a.step,
                  "dec_persist: bad arguments (batch %d, %d layers)", a.B, a.n_layer);
+    // one item per workgroup and phase while the XCD holds at most 2 sequences (32 groups: 1)
     if (a.groups == 32)
-        hipLaunchKernelGGL(k_dec_persist<32>, dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_dec_persist<32, true>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+    else if (a.B <= 16)
+        hipLaunchKernelGGL((k_dec_persist<16, true>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
     else
-        hipLaunchKernelGGL(k_dec_persist<16>, dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+        hipLaunchKernelGGL((k_dec_persist<16, false>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -603,13 +712,14 @@ int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
 bool dec_persist_device_ok(int device) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
-    int occ16 = 0, occ32 = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16, k_dec_persist<16>, DL_THREADS, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ32, k_dec_persist<32>, DL_THREADS, 0) != hipSuccess) {
+    int occ16 = 0, occ32 = 0, occ16m = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16, k_dec_persist<16, true>, DL_THREADS, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16m, k_dec_persist<16, false>, DL_THREADS, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ32, k_dec_persist<32, true>, DL_THREADS, 0) != hipSuccess) {
         (void) hipGetLastError();
         return false;
     }
-    return prop.multiProcessorCount == DEC_PERSIST_WGS && occ16 >= 1 && occ32 >= 1 &&
+    return prop.multiProcessorCount == DEC_PERSIST_WGS && occ16 >= 1 && occ16m >= 1 && occ32 >= 1 &&
            std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
 }
 

@@ -880,7 +880,7 @@ bool persist_decode_ok(const gsvk_model * m) {
 int prepare_persist(gsvk_model * m) {
     m->persist_now = false;
     const bool want = m->decode_path == GSVK_DECODE_PERSIST ||
-                      (m->decode_path == GSVK_DECODE_AUTO && m->B <= DEC_AUTO_MAX_BATCH);
+                      (m->decode_path == GSVK_DECODE_AUTO && m->B <= DEC_PERSIST_AUTO_MAX_BATCH);
     if (!want || !persist_decode_ok(m)) return GSVK_OK;
     if (!m->d_pattn) {
         GSVK_TRY(m->wmem.alloc(m->d_pattn, (size_t) m->NL));
