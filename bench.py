@@ -138,7 +138,7 @@ def kernel_roofline(gsvk, torch, reqs, steps):
     res = {}
     rot = N_LAYER
     scale = 1.0 / np.sqrt(32.0)
-    small = B <= 32   # the two-launch layer's range in the library's default choice
+    small = B <= 32   # the two-launch layer's range (the library's default choice from batch 17)
     kc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
     vc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
     qkv_w = 3 * D * D // 32 * 34
@@ -174,11 +174,11 @@ def kernel_roofline(gsvk, torch, reqs, steps):
         ms = time_events(dec_attn, 240, torch)
         ab = kv_bytes + qkv_w + out_w
         res["dec_attn"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER,
-                           "in_decode": True}
+                           "in_decode": B > 16}
         ms = time_events(dec_ffn, 240, torch)
         fb = 2 * ffn_w
         res["dec_ffn"] = {"ms": ms, "bytes": fb, "gbs": fb / ms / 1e6, "launches_per_step": N_LAYER,
-                          "in_decode": True}
+                          "in_decode": B > 16}
         del wq, wd, woq, wod, w1q, w1d, w2q, w2d
     # the standalone decode attention (the matrix-core path's, from batch 33)
     q = torch.randn((B, NH, HD), dtype=torch.float32, device="cuda")
@@ -195,6 +195,24 @@ def kernel_roofline(gsvk, torch, reqs, steps):
                           "in_decode": not small}
     del kc, vc
     return res, sh
+
+
+def persist_kernel(g, reqs, steps, launches=100):
+    """The persistent decode's kernel (the 24 layers of a step in one launch, the decode's dominant
+    kernel up to batch 16) alone, at the mid-run state of a run of `steps` steps: a generate of
+    steps // 2 + 1 steps leaves the state of loop index steps // 2, whose kernel is then launched
+    `launches` times back to back and timed with HIP events on the model's stream
+    (gsvk_model_time_decode_kernel). Algorithmic bytes per launch: the 24 layers' Q8_0 weights,
+    biases and LayerNorm vectors, the valid K/V rows read and the new K/V rows written (the step's
+    head is another kernel)."""
+    mid = steps // 2
+    B = len(reqs)
+    g.generate(reqs, sampler=(15, 1.0, 1.0, 1.35), max_steps=mid + 1, seeds=list(range(1, B + 1)), flags=1)
+    ms = g.time_decode_kernel(launches)
+    b = decode_bytes_per_step(reqs, mid) - V * D * 2
+    sh = kernel_shape(reqs, steps)
+    return {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": 1, "in_decode": B <= 16,
+            "mid": mid, "nkeys": sh["nkeys"]}
 
 
 def attn_microkernel(gsvk, torch, seed=0x6A5E0003, B=64, sets=8):
@@ -237,22 +255,29 @@ def copy_probe(torch, nbytes=256 << 20):
     return nbytes
 
 
-PROFILE_HBM = os.path.join("profiles", "decode_layer_b16_hbm.md")
+PROFILES_HBM = (os.path.join("profiles", "decode_persist_b16_hbm.md"),
+                os.path.join("profiles", "decode_layer_b16_hbm.md"))
 
 
-def traffic_ratio(kernel):
-    """(HBM traffic / algorithmic bytes per launch, the shape it was measured at) of `kernel`
-    from the committed counter summary: two rocprofv3 --pmc passes (FETCH_SIZE, then WRITE_SIZE)
-    over `bench.py --kernels-only` at that shape, each scaled by what the counter reads for a
-    256 MiB copy. None when the summary does not hold the kernel."""
-    path = os.path.join(ROOT, PROFILE_HBM)
-    if not os.path.exists(path):
-        return None
-    for line in open(path):
-        f = line.split()
-        if len(f) >= 5 and f[0] == "traffic_ratio" and f[1] == kernel:
-            return float(f[2]), " ".join(f[4:])
-    return None
+def traffic_ratio(kernel, shape=None):
+    """(HBM traffic / algorithmic bytes per launch, the shape it was measured at, the summary) of
+    `kernel` from the committed counter summaries: two rocprofv3 --pmc passes (FETCH_SIZE, then
+    WRITE_SIZE) over `bench.py --kernels-only` at that shape, each scaled by what the counter reads
+    for a 256 MiB copy; the line measured at `shape` when there is one, else the first. None when
+    no summary holds the kernel."""
+    found = []
+    for rel in PROFILES_HBM:
+        path = os.path.join(ROOT, rel)
+        if not os.path.exists(path):
+            continue
+        for line in open(path):
+            f = line.split()
+            if len(f) >= 5 and f[0] == "traffic_ratio" and f[1] == kernel:
+                found.append((float(f[2]), " ".join(f[4:]), rel))
+    for t in found:
+        if t[1] == shape:
+            return t
+    return found[0] if found else None
 
 
 def physical_cores():
@@ -445,7 +470,14 @@ def main():
 
     assert torch.cuda.is_available(), "bench.py needs a HIP device"
     if args.kernels_only:
-        kr, sh = kernel_roofline(gsvk, torch, workload_requests(args.batch), args.steps)
+        kreqs = workload_requests(args.batch)
+        kr, sh = kernel_roofline(gsvk, torch, kreqs, args.steps)
+        if args.batch <= 16:
+            gk = gsvk.Model(sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER), device=0)
+            try:
+                kr["dec_persist"] = persist_kernel(gk, kreqs, args.steps)
+            finally:
+                gk.close()
         res = {k: {"us": round(v["ms"] * 1e3, 3), "bytes": v["bytes"], "GBs": round(v["gbs"], 1),
                    "in_decode": v["in_decode"]} for k, v in kr.items()}
         res["shape"] = {"batch": args.batch, "steps": args.steps, "mid_step": sh["mid"], "valid_keys": sh["nkeys"]}
@@ -521,6 +553,8 @@ def main():
                            "ms_per_step_b1": round(rx1["decode_ms"] / 300, 4),
                            "what": "gsvk_model_set_exact: the same workloads with ggml-cpu's arithmetic "
                                    "order throughout (logits equal to the oracle's to the bit)"}
+    # the decode's dominant kernel alone at the timed run's mid-run state (batch <= 16)
+    pk = persist_kernel(g, reqs, args.steps) if (not args.no_kernels and B <= 16) else None
     # batch 64: the batch-16 workload's request shape at 64 sequences, 200 steps
     _, rb, _ = run(64, 200, 8)
     extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)
@@ -536,21 +570,27 @@ def main():
     roof = None
     if not args.no_kernels:
         kr, sh = kernel_roofline(gsvk, torch, reqs, args.steps)
+        if pk is not None:
+            kr["dec_persist"] = pk
         extra["kernels"] = {k: {"us": round(v["ms"] * 1e3, 2), "GBs": round(v["gbs"], 1),
                                 "frac": round(v["gbs"] / HBM_PEAK_GBS, 4), "in_decode": v["in_decode"]}
                             for k, v in kr.items()}
         extra["attn_microkernel_b64"] = attn_microkernel(gsvk, torch)
         dom = max((k for k in kr if kr[k]["in_decode"]), key=lambda k: kr[k]["ms"] * kr[k]["launches_per_step"])
         d = kr[dom]
-        tr = traffic_ratio(dom)
+        shape = (f"batch {B}, mid-run of {args.steps} steps (loop index {sh['mid']}), "
+                 f"{sh['nkeys']} valid keys per head")
+        tr = traffic_ratio(dom, shape)
         roof = {"bound": "hbm", "kernel": dom, "achieved": round(d["gbs"], 1), "peak": HBM_PEAK_GBS,
                 "unit": "GB/s", "frac": round(d["gbs"] / HBM_PEAK_GBS, 4),
                 "traffic": None if tr is None else int(round(tr[0] * d["bytes"])),
                 "bytes_per_launch": int(d["bytes"]), "us_per_launch": round(d["ms"] * 1e3, 3),
-                "shape": f"batch {B}, mid-run of {args.steps} steps (loop index {sh['mid']}), "
-                         f"{sh['nkeys']} valid keys per head",
+                "shape": shape,
+                "timing": "HIP events around back-to-back launches on the launching stream"
+                          + (" (gsvk_model_time_decode_kernel)" if dom == "dec_persist" else
+                             " (one captured graph of 240 launches)"),
                 "traffic_basis": None if tr is None else
-                {"ratio": tr[0], "measured_at": tr[1], "profile": PROFILE_HBM}}
+                {"ratio": tr[0], "measured_at": tr[1], "profile": tr[2]}}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(reqs, args.steps)

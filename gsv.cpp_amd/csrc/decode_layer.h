@@ -102,6 +102,8 @@ struct DecPersistArgs {
     int B;
     int groups;                 // dec_ffn_groups(B)
     const int32_t * step;       // the device step counter: the barrier's epoch
+    int epoch_add;              // added to *step for the epoch (0; 0, 1, ... when the kernel of
+                                // one step is launched repeatedly, every launch's words above the last)
     int * flags;                // [8][32] barrier words (zero before the first step of a run)
     int * err;                  // 0, or 1 (a wait gave up) / 2 (an XCC id outside 0..7)
 };

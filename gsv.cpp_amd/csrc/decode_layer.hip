@@ -678,7 +678,7 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     __syncthreads();
     if (!s_go) return;
     const int ns = x < p.B ? (p.B - 1 - x) / 8 + 1 : 0;   // sequences x, x + 8, ...
-    const int epoch = __builtin_amdgcn_readfirstlane(*p.step) * 64;   // 2 phases per layer, < 64
+    const int epoch = (__builtin_amdgcn_readfirstlane(*p.step) + p.epoch_add) * 64;   // 2 phases per layer, < 64
     const XBar bar{p.flags + x * 32, p.err, 0};
     int * my = p.flags + x * 32 + w;
     const DecAttnArgs a0 = persist_attn_args(p.attn, 0);

@@ -784,7 +784,7 @@ int enqueue_decode_fused(gsvk_model * m) {
 
 // The persistent decode: one launch for the 24 layers (the arguments prepare_persist uploaded),
 // then the head.
-int enqueue_decode_persist(gsvk_model * m) {
+DecPersistArgs persist_args(const gsvk_model * m) {
     DecPersistArgs pa{};
     pa.attn = m->d_pattn;
     pa.ffn = m->d_pffn;
@@ -794,7 +794,11 @@ int enqueue_decode_persist(gsvk_model * m) {
     pa.step = m->d_step;
     pa.flags = m->d_pflags;
     pa.err = m->d_pflags + 8 * 32;
-    GSVK_TRY(launch_dec_persist(pa, m->stream));
+    return pa;
+}
+
+int enqueue_decode_persist(gsvk_model * m) {
+    GSVK_TRY(launch_dec_persist(persist_args(m), m->stream));
     return decode_head_parts(m);
 }
 
@@ -2098,6 +2102,50 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
                            hipMemcpyDeviceToHost));
     m->prof.dec_other_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_res).count();
     m->prof.steps = out->n_steps;
+    return GSVK_OK;
+}
+
+extern "C" int gsvk_model_time_decode_kernel(gsvk_model * m, int launches, float * ms_per_launch) {
+    GSVK_REQUIRE(m && ms_per_launch && launches >= 1 && launches <= 100000, "bad arguments");
+    if (!m->prefilled || m->cb_open) {
+        set_error("time_decode_kernel: no decode state (prefill or generate first; not in a continuous batch)");
+        return GSVK_ERR_STATE;
+    }
+    DeviceGuard guard(m->device);
+    GSVK_TRY(prepare_persist(m));
+    GSVK_REQUIRE(m->persist_now, "time_decode_kernel: the persistent decode does not run for this model and "
+                 "batch (%d sequences) on the current decode path", m->B);
+    hipStream_t st = m->stream;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    GSVK_HIP(hipEventCreate(&e0));
+    if (hipEventCreate(&e1) != hipSuccess) {
+        (void) hipEventDestroy(e0);
+        set_error("time_decode_kernel: hipEventCreate failed");
+        return GSVK_ERR_HIP;
+    }
+    DecPersistArgs pa = persist_args(m);
+    int rc = hipEventRecord(e0, st) == hipSuccess ? GSVK_OK : GSVK_ERR_HIP;
+    for (int i = 0; i < launches && rc == GSVK_OK; i++) {
+        pa.epoch_add = i;   // flags were cleared: every launch's epoch above the last's
+        rc = launch_dec_persist(pa, st);
+    }
+    float ms = 0.0f;
+    if (rc == GSVK_OK && (hipEventRecord(e1, st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+                          hipEventElapsedTime(&ms, e0, e1) != hipSuccess)) {
+        set_error("time_decode_kernel: event timing failed");
+        rc = GSVK_ERR_HIP;
+    }
+    (void) hipStreamSynchronize(st);
+    (void) hipEventDestroy(e0);
+    (void) hipEventDestroy(e1);
+    GSVK_TRY(rc);
+    int err = 0;
+    GSVK_HIP(hipMemcpy(&err, m->d_pflags + 8 * 32, sizeof(int), hipMemcpyDeviceToHost));
+    if (err != 0) {
+        set_error("time_decode_kernel: a barrier wait of the persistent decode gave up (code %d)", err);
+        return GSVK_ERR_STATE;
+    }
+    *ms_per_launch = ms / (float) launches;
     return GSVK_OK;
 }
 

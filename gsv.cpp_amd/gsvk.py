@@ -32,6 +32,7 @@ EXPORTS = [
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
     "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact", "gsvk_model_set_prefill_f16",
     "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact", "gsvk_model_get_profile",
+    "gsvk_model_time_decode_kernel",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA, GSVK_DECODE_PERSIST = 0, 1, 2, 3, 4
@@ -432,6 +433,13 @@ class Model:
         pr = Profile()
         check(lib().gsvk_model_get_profile(self.h, C.byref(pr)), "get_profile")
         return {n: getattr(pr, n) for n, _ in Profile._fields_}
+
+    def time_decode_kernel(self, launches: int = 50) -> float:
+        """Mean duration (ms) of the persistent decode's kernel at the current step, HIP events
+        around `launches` back-to-back launches (include/gsvk.h gsvk_model_time_decode_kernel)."""
+        ms = C.c_float(0.0)
+        check(lib().gsvk_model_time_decode_kernel(self.h, int(launches), C.byref(ms)), "time_decode_kernel")
+        return float(ms.value)
 
     def set_exact(self, on: bool = True):
         """Exact mode (include/gsvk.h gsvk_model_set_exact): ggml-cpu's arithmetic order throughout."""

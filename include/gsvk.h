@@ -147,6 +147,14 @@ typedef struct {
 } gsvk_profile;
 int gsvk_model_get_profile(gsvk_model * m, gsvk_profile * out);
 
+/* The persistent decode's kernel (GSVK_DECODE_PERSIST: all 24 layers of a step) at the model's
+ * current step, launched `launches` times back to back on the model's stream between two HIP
+ * events: its mean duration per launch. Every launch repeats that step's layers on the same inputs
+ * (writing the same K/V column the step writes); the head and the sampler do not run. Needs a
+ * decode state (after a prefill or generate) on a path and batch where the persistent decode runs.
+ * No counterpart in the reference; for benchmarks (the decode's dominant kernel, timed alone). */
+int gsvk_model_time_decode_kernel(gsvk_model * m, int launches, float * ms_per_launch);
+
 /* Full batched generation: replaces gsv_ar::generate (src/gsv_ar.cpp:719-824).
  * oracle (teacher forcing) may be NULL; seeds may be NULL (then seed_base + 0x9E3779B9*b). */
 int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_sampler_cfg * cfg,
