@@ -138,7 +138,7 @@ def kernel_roofline(gsvk, torch, reqs, steps):
     res = {}
     rot = N_LAYER
     scale = 1.0 / np.sqrt(32.0)
-    small = B <= 32   # the two-launch layer's range (the library's default choice from batch 17)
+    small = B <= 32   # the two-launch layer's range (the persistent decode's fallback there)
     kc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
     vc = torch.randn((rot, B, NH, lstride, HD), dtype=torch.float16, device="cuda").view(torch.int16)
     qkv_w = 3 * D * D // 32 * 34
@@ -174,11 +174,11 @@ def kernel_roofline(gsvk, torch, reqs, steps):
         ms = time_events(dec_attn, 240, torch)
         ab = kv_bytes + qkv_w + out_w
         res["dec_attn"] = {"ms": ms, "bytes": ab, "gbs": ab / ms / 1e6, "launches_per_step": N_LAYER,
-                           "in_decode": B > 16}
+                           "in_decode": False}
         ms = time_events(dec_ffn, 240, torch)
         fb = 2 * ffn_w
         res["dec_ffn"] = {"ms": ms, "bytes": fb, "gbs": fb / ms / 1e6, "launches_per_step": N_LAYER,
-                          "in_decode": B > 16}
+                          "in_decode": False}
         del wq, wd, woq, wod, w1q, w1d, w2q, w2d
     # the standalone decode attention (the matrix-core path's, from batch 33)
     q = torch.randn((B, NH, HD), dtype=torch.float32, device="cuda")
@@ -199,7 +199,7 @@ def kernel_roofline(gsvk, torch, reqs, steps):
 
 def persist_kernel(g, reqs, steps, launches=100):
     """The persistent decode's kernel (the 24 layers of a step in one launch, the decode's dominant
-    kernel up to batch 16) alone, at the mid-run state of a run of `steps` steps: a generate of
+    kernel up to batch 32) alone, at the mid-run state of a run of `steps` steps: a generate of
     steps // 2 + 1 steps leaves the state of loop index steps // 2, whose kernel is then launched
     `launches` times back to back and timed with HIP events on the model's stream
     (gsvk_model_time_decode_kernel). Algorithmic bytes per launch: the 24 layers' Q8_0 weights,
@@ -211,7 +211,7 @@ def persist_kernel(g, reqs, steps, launches=100):
     ms = g.time_decode_kernel(launches)
     b = decode_bytes_per_step(reqs, mid) - V * D * 2
     sh = kernel_shape(reqs, steps)
-    return {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": 1, "in_decode": B <= 16,
+    return {"ms": ms, "bytes": b, "gbs": b / ms / 1e6, "launches_per_step": 1, "in_decode": True,
             "mid": mid, "nkeys": sh["nkeys"]}
 
 
@@ -472,7 +472,7 @@ def main():
     if args.kernels_only:
         kreqs = workload_requests(args.batch)
         kr, sh = kernel_roofline(gsvk, torch, kreqs, args.steps)
-        if args.batch <= 16:
+        if args.batch <= 32:
             gk = gsvk.Model(sm.cached_model(os.path.join(ROOT, "_fixtures"), n_layer=N_LAYER), device=0)
             try:
                 kr["dec_persist"] = persist_kernel(gk, kreqs, args.steps)
@@ -554,7 +554,7 @@ def main():
                            "what": "gsvk_model_set_exact: the same workloads with ggml-cpu's arithmetic "
                                    "order throughout (logits equal to the oracle's to the bit)"}
     # the decode's dominant kernel alone at the timed run's mid-run state (batch <= 16)
-    pk = persist_kernel(g, reqs, args.steps) if (not args.no_kernels and B <= 16) else None
+    pk = persist_kernel(g, reqs, args.steps) if (not args.no_kernels and B <= 32) else None
     # batch 64: the batch-16 workload's request shape at 64 sequences, 200 steps
     _, rb, _ = run(64, 200, 8)
     extra["tok_s_b64"] = round(64 * 200 / (rb["decode_ms"] / 1e3), 1)

@@ -109,12 +109,12 @@ struct DecPersistArgs {
 };
 constexpr int DEC_PERSIST_WGS = 256;
 constexpr int DEC_PERSIST_MAX_BATCH = 32;   // 4 sequences per XCD
-// Largest batch the library's default choice runs on the persistent decode (one attention item and
-// one FFN item per workgroup and layer). Whole step, 24 layers, the batch-16 request shape (batch 1:
-// 128 phones), two-launch against persistent: batch 1 0.311 / 0.296 ms, 2 0.319 / 0.304, 4 0.325 /
-// 0.307, 8 0.345 / 0.335, 12 0.387 / 0.320, 16 0.405 / 0.332, 17 0.620 / 0.665, 20 0.638 / 0.664,
-// 24 0.664 / 0.719, 32 0.692 / 0.672 (above 16 a workgroup takes two items of a phase in turn).
-constexpr int DEC_PERSIST_AUTO_MAX_BATCH = 16;
+// Largest batch the library's default choice runs on the persistent decode (above 16 a workgroup
+// takes two items of a phase in turn). Whole step, 24 layers, the batch-16 request shape (batch 1:
+// 128 phones), two-launch against persistent: batch 1 0.310 / 0.297 ms, 2 0.319 / 0.307, 4 0.326 /
+// 0.308, 8 0.346 / 0.341, 12 0.385 / 0.319, 16 0.406 / 0.333, 17 0.621 / 0.561, 20 0.638 / 0.572,
+// 24 0.666 / 0.615, 32 0.689 / 0.597.
+constexpr int DEC_PERSIST_AUTO_MAX_BATCH = 32;
 int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream);
 // The device has the 256 CUs in 8 XCDs the kernel assumes, and one workgroup of it fits a CU.
 bool dec_persist_device_ok(int device);

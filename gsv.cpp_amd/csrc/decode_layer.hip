@@ -196,15 +196,21 @@ __device__ __forceinline__ float ld_row(const float * p) {
 
 // Launch 1's work for (head h, sequence b). PERSIST (the persistent decode): the loads that do not
 // depend on the previous phase go out first, then the wait on `bar`, then the input row's
-// operands, read with device-scope loads; returns false when the wait gave up.
-template <int MODE, int NP, bool PERSIST>
+// operands, read with device-scope loads; returns false when the wait gave up. OPAQUE: the thread
+// index is made opaque to the compiler per call, so that the indexing derived from it is
+// recomputed for each item instead of being hoisted out of the persistent decode's layer loop and
+// kept live across it (which the loop form spilled: 28 VGPRs; without spills it is 0.60 instead of
+// 0.67 ms per step at batch 17-24; the one-item form is faster without it).
+template <int MODE, int NP, bool PERSIST, bool OPAQUE = false>
 __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h, const int b, const XBar & bar,
                                               const int col_pre = 0, const int beg_pre = 0) {
     constexpr int NW = DL_WAVES;
     constexpr int PASSES = (DL_QKV_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     constexpr int WO_T = DL_NBLK / NW;                        // out-projection tiles per wave
     const int B = a.B;
-    const int tid = threadIdx.x;
+    int tid_v = threadIdx.x;
+    if constexpr (OPAQUE) asm volatile("" : "+v"(tid_v));
+    const int tid = tid_v;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int ks = lane >> 2;
@@ -439,8 +445,8 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_attn(DecAttnArgs a) {
     dec_attn_body<MODE, NP, false>(a, blockIdx.x, blockIdx.y, XBar{});
 }
 
-// Launch 2's work for (hidden group g, sequence b); PERSIST as for dec_attn_body.
-template <int G, bool PERSIST>
+// Launch 2's work for (hidden group g, sequence b); PERSIST and OPAQUE as for dec_attn_body.
+template <int G, bool PERSIST, bool OPAQUE = false>
 __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, const int b, const XBar & bar) {
     constexpr int NW = DL_WAVES;
     constexpr int U = DL_FFN / G;              // hidden units of the group
@@ -450,7 +456,9 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
     constexpr int K2_NBLK = DL_FFN / 32;       // blocks of an FFN2 weight row
     static_assert(U % (8 * NW) == 0 && UB * 32 == U && W2_T * NW * 32 == DL_K, "group shape");
     const int B = a.B;
-    const int tid = threadIdx.x;
+    int tid_v = threadIdx.x;
+    if constexpr (OPAQUE) asm volatile("" : "+v"(tid_v));
+    const int tid = tid_v;
     const int lane = tid & 63;
     const int wave = tid >> 6;
     const int rsub = lane >> 3;
@@ -615,8 +623,7 @@ __device__ __forceinline__ DecFfnArgs persist_ffn_args(const DecFfnArgs * all, i
 // at most 2 (4 sequences per XCD), the same in every layer; col (the new key's column before
 // col_add) and beg[k] (item k's first key) were read at the launch's start. ONE: at most one
 // attention item and one FFN item per workgroup (up to 2 sequences per XCD, batch <= 16), written
-// without the item loops, which (with the loads each item issues ahead of its wait) cost the loop
-// form registers it spills.
+// without the item loops; the loop form (batch 17-32) runs its bodies OPAQUE.
 static_assert(DEC_PERSIST_MAX_BATCH / 8 * DL_NH <= 2 * 32, "two attention items per workgroup at most");
 
 template <int MODE, int G, bool ONE>
@@ -634,8 +641,8 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
         for (int it = w, k = 0; it < ns * DL_NH; it += 32, k++) {
             XBar bw = bar;
             bw.target = (MODE == IN_LN && k == 0) ? epoch + 2 * li : 0;
-            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw, col,
-                                                                    k == 0 ? beg[0] : beg[1]))
+            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, true>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw,
+                                                                          col, k == 0 ? beg[0] : beg[1]))
                 return false;
         }
     }
@@ -651,7 +658,7 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
         for (int it = w; it < ns * G; it += 32) {
             XBar bw = bar;
             bw.target = it == w ? epoch + 2 * li + 1 : 0;
-            if (!dec_ffn_body<G, true>(fa, it % G, x + 8 * (it / G), bw)) return false;
+            if (!dec_ffn_body<G, true, true>(fa, it % G, x + 8 * (it / G), bw)) return false;
         }
     }
     xbar_signal(my, epoch + 2 * li + 2, tid);

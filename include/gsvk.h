@@ -166,9 +166,9 @@ int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_s
 int gsvk_first_logits(gsvk_model * m, const gsvk_request * reqs, int B, float * logits_out);
 
 /* Which kernels run a decode step (the arithmetic of src/gsv_ar.cpp:380-467 in every case):
- *  GSVK_DECODE_AUTO  the library's choice (default, the fastest at each batch): up to 16
- *                    sequences the persistent decode where it runs (PERSIST), else (and up to 32)
- *                    the two-launch layer; from 33 the matrix-core GEMMs;
+ *  GSVK_DECODE_AUTO  the library's choice (default, the fastest at each batch): up to 32
+ *                    sequences the persistent decode where it runs (PERSIST), else the two-launch
+ *                    layer; from 33 the matrix-core GEMMs;
  *  GSVK_DECODE_GEMV  up to 16 sequences the GEMV chain whose projections and LayerNorms are
  *                    bit-exact with ggml-cpu's x86 order (4 launches per layer);
  *  GSVK_DECODE_FUSED up to 64 sequences two launches per layer (attention + out-projection

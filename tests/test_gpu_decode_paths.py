@@ -2,13 +2,12 @@
 
 * GSVK_DECODE_GEMV: four launches per layer, projections and LayerNorms bit-exact with the
   oracle (ggml-cpu's x86 order).
-* GSVK_DECODE_FUSED (the default from 17 to 32 sequences): two launches per layer; the out projection
+* GSVK_DECODE_FUSED (the persistent decode's fallback up to 32 sequences): two launches per layer; the out projection
   and FFN2 are summed over heads / hidden groups as partial rows, so they agree with the GEMV
   chain to fp32 rounding; everything before the first of those sums (the layer-0 input, QKV, the
   K/V append of layer 0) is unchanged and stays bit-exact.
-* GSVK_DECODE_PERSIST (the default up to 16 sequences where the device allows; up to 32 when
-  chosen): the two-launch layer's work in one launch per step, each XCD running whole sequences;
-  the same bits as FUSED.
+* GSVK_DECODE_PERSIST (the default up to 32 sequences where the device allows): the two-launch
+  layer's work in one launch per step, each XCD running whole sequences; the same bits as FUSED.
 """
 import numpy as np
 import pytest
@@ -385,7 +384,7 @@ def test_persistent_decode_equals_two_launch_layer(gpu, model4_path, B):
 def test_decode_kernel_timing_leaves_the_state(gpu, model4_path):
     """gsvk_model_time_decode_kernel (the bench's timing of the persistent kernel alone) repeats the
     current step's kernel: a positive duration, and a generate afterwards gives the tokens it gave
-    before. Where the persistent decode does not run (batch 17 on the default path) it is an error."""
+    before. Where the persistent decode does not run (batch 33 on the default path) it is an error."""
     rng = np.random.default_rng(777)
     reqs = _reqs(778, rng.integers(3, 60, 4), 16)
     cfg = (15, 1.0, 1.0, 1.35)
@@ -394,8 +393,8 @@ def test_decode_kernel_timing_leaves_the_state(gpu, model4_path):
         r0 = g.generate(reqs, sampler=cfg, max_steps=12, seeds=[1, 2, 3, 4], flags=1)
         ms = g.time_decode_kernel(5)
         r1 = g.generate(reqs, sampler=cfg, max_steps=12, seeds=[1, 2, 3, 4], flags=1)
-        big = _reqs(779, rng.integers(3, 30, 17), 16)
-        g.generate(big, sampler=cfg, max_steps=4, seeds=list(range(1, 18)), flags=1)
+        big = _reqs(779, rng.integers(3, 30, 33), 16)
+        g.generate(big, sampler=cfg, max_steps=4, seeds=list(range(1, 34)), flags=1)
         with pytest.raises(gpu.GsvkError):
             g.time_decode_kernel(2)
     finally:
