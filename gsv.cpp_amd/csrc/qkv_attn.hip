@@ -165,10 +165,11 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
         M = mn;
         __syncthreads();
         // the chains (wave 0): groups of 8 keys, the next group's LDS reads issued before the
-        // current group's fmas
+        // current group's fmas, into the other of two register sets (two groups per iteration, so
+        // that no copy between the sets is needed)
         if (wave == 0) {
-            float xa[8], va[8];
-            int ga;
+            float xa[8], va[8], xb[8], vbn[8];
+            int ga, gb;
             auto group = [&](int t0, float (&xs)[8], float (&vs8)[8], int & g) {
 #pragma unroll
                 for (int i = 0; i < 8; i++) xs[i] = L.x[t0 + i][dl];
@@ -178,30 +179,33 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
                 vs8[4] = v1.x; vs8[5] = v1.y; vs8[6] = v1.z; vs8[7] = v1.w;
                 g = L.nm[t0 >> 3];
             };
-            group(0, xa, va, ga);
-            int t = 0;
-            for (; t + 8 <= n; t += 8) {
-                float xb[8], vbn[8];
-                int gb;
-                group(t + 8, xb, vbn, gb);
-                if (__builtin_amdgcn_readfirstlane(ga) == 0) {   // no new maximum: ms = 1
+            auto chain = [&](const float (&xs)[8], const float (&vs8)[8], int g, int t0) {
+                if (__builtin_amdgcn_readfirstlane(g) == 0) {   // no new maximum: ms = 1
 #pragma unroll
-                    for (int i = 0; i < 8; i++) acc = __builtin_fmaf(xa[i], va[i], acc);
+                    for (int i = 0; i < 8; i++) acc = __builtin_fmaf(xs[i], vs8[i], acc);
                 } else {
 #pragma unroll
                     for (int i = 0; i < 8; i++) {
-                        const float m1 = L.ms[t + i];
-                        const float lo = __builtin_fmaf(xa[i], va[i], acc * m1);
-                        const float hs = __builtin_fmaf(acc, m1, va[i]);
+                        const float m1 = L.ms[t0 + i];
+                        const float lo = __builtin_fmaf(xs[i], vs8[i], acc * m1);
+                        const float hs = __builtin_fmaf(acc, m1, vs8[i]);
                         acc = lane >= 32 ? hs : lo;
                     }
                 }
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    xa[i] = xb[i];
-                    va[i] = vbn[i];
-                }
-                ga = gb;
+            };
+            // (a group read ahead may start at t0 <= n: LDS rows up to QX_C + 8 hold no key and
+            // are not used)
+            group(0, xa, va, ga);
+            int t = 0;
+            for (; t + 16 <= n; t += 16) {
+                group(t + 8, xb, vbn, gb);
+                chain(xa, va, ga, t);
+                group(t + 16, xa, va, ga);
+                chain(xb, vbn, gb, t + 8);
+            }
+            if (t + 8 <= n) {
+                chain(xa, va, ga, t);
+                t += 8;
             }
             for (; t < n; t++) {
                 const float x1 = L.x[t][dl], v1 = L.vs[t], m1 = L.ms[t];
