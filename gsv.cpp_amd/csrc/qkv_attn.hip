@@ -43,14 +43,20 @@ constexpr int QA_NB4 = QA_K / 128;       // int4 weight loads per slice lane
 constexpr int QA_ROWS = 3 * ATT_HD;      // rows of one head: q, k, v
 
 constexpr int QX_C = 256;    // keys per chunk of the exact attention: one per thread of 4 waves
-constexpr int QX_XS = 36;    // floats per key row in LDS: 32 V values, 1.0 (S's chain), padding
+constexpr int QX_G = 16;     // keys per group of the chain (one bit of the new-maximum mask)
+constexpr int QX_RA = 3 * QX_G;   // entries past the chunk that the chain reads ahead (never used)
+constexpr int QX_TS = 324;   // floats per dimension row of the transposed V: >= QX_C + QX_RA, and
+                             // 4 more than a multiple of 32 so that 8 lanes' 16-byte reads of
+                             // consecutive rows fall in distinct banks
 
 struct QxLds {
-    float x[QX_C + 8][QX_XS];    // (8 rows past the chunk: read ahead by the chain, never used)
-    float vs[QX_C + 8];
+    // V transposed: row d < 32 holds dimension d of the chunk's keys, row 32 holds 1.0 (S's
+    // chain); keys past the chunk's end hold -0.0 (a product of -0.0 added to any value leaves it)
+    float xt[ATT_HD + 1][QX_TS];
+    float vs[QX_C + QX_RA];      // the key's weight exp(s - max before it); 0 past the chunk's end
     float ms[QX_C];
     float wmax[QX_C / 64];
-    uint8_t nm[QX_C / 8 + 8];    // per group of 8 keys: the bits of the keys that set a new maximum
+    uint8_t gm[QX_C / 64];       // per wave, one bit per group of QX_G keys that holds a new maximum
 };
 
 __constant__ uint64_t qx_exp2_tab[32] = GSVK_EXP2_TAB32;
@@ -128,10 +134,12 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
             }
             const float t0 = s0[0] + s0[4], t1 = s0[1] + s0[5], t2 = s0[2] + s0[6], t3 = s0[3] + s0[7];
             s = ((t0 + t1) + (t2 + t3)) * scale;
-            float4 * xr = reinterpret_cast<float4 *>(&L.x[tid][0]);
 #pragma unroll
-            for (int c = 0; c < 8; c++) xr[c] = make_float4(vf[4 * c], vf[4 * c + 1], vf[4 * c + 2], vf[4 * c + 3]);
-            xr[8] = make_float4(1.0f, 0.0f, 0.0f, 0.0f);
+            for (int d = 0; d < ATT_HD; d++) L.xt[d][tid] = vf[d];
+            L.xt[ATT_HD][tid] = 1.0f;
+        } else {
+#pragma unroll
+            for (int d = 0; d <= ATT_HD; d++) L.xt[d][tid] = -0.0f;
         }
         // the maximum before each key: inclusive scan within the wave, the waves' maxima, seeded
         // with the running maximum (max is exact in any order)
@@ -153,66 +161,76 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
             mn = fmaxf(mn, wm);
         }
         before = fmaxf(before, excl);
-        float ms = 1.0f, vs = 1.0f;
+        float ms = 1.0f, vs = 0.0f;   // past the chunk's end: weight 0, maximum unchanged
         if (tid < n) {
+            vs = 1.0f;
             if (s > before) ms = expf_glibc(before - s, qx_exp2_tab);
             else vs = expf_glibc(s - before, qx_exp2_tab);
         }
         L.ms[tid] = ms;
         L.vs[tid] = vs;
         const uint64_t nm = __ballot(ms != 1.0f);
-        if (lane == 0) *reinterpret_cast<uint64_t *>(&L.nm[8 * wave]) = nm;
+        const uint64_t gz = __ballot(lane < 64 / QX_G && ((nm >> (QX_G * lane)) & ((1ull << QX_G) - 1)) != 0);
+        if (lane == 0) L.gm[wave] = (uint8_t) gz;
         M = mn;
         __syncthreads();
-        // the chains (wave 0): groups of 8 keys, the next group's LDS reads issued before the
-        // current group's fmas, into the other of two register sets (two groups per iteration, so
-        // that no copy between the sets is needed)
+        // the chains (wave 0): groups of QX_G keys, the last one completed by keys of weight 0 and
+        // value -0.0 (acc * 1 + -0.0 * 0 is acc, and so is fma(-0.0, 0, acc)); each group's LDS
+        // reads are issued three groups ahead into a ring of four register sets (four groups per
+        // iteration, so that no copy between the sets is needed)
         if (wave == 0) {
-            float xa[8], va[8], xb[8], vbn[8];
-            int ga, gb;
-            auto group = [&](int t0, float (&xs)[8], float (&vs8)[8], int & g) {
+            constexpr int G = QX_G, GPW = 64 / QX_G;
+            // group g's bit is bit g % GPW of byte g / GPW (uniform, a scalar register)
+            const uint32_t gmask = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(L.gm));
+            const int ng = (n + G - 1) / G;
+            float x0[G], v0[G], x1[G], v1[G], x2[G], v2[G], x3[G], v3[G];
+            auto group = [&](int g, float (&xs)[G], float (&vs8)[G]) {
 #pragma unroll
-                for (int i = 0; i < 8; i++) xs[i] = L.x[t0 + i][dl];
-                const float4 v0 = *reinterpret_cast<const float4 *>(&L.vs[t0]);
-                const float4 v1 = *reinterpret_cast<const float4 *>(&L.vs[t0 + 4]);
-                vs8[0] = v0.x; vs8[1] = v0.y; vs8[2] = v0.z; vs8[3] = v0.w;
-                vs8[4] = v1.x; vs8[5] = v1.y; vs8[6] = v1.z; vs8[7] = v1.w;
-                g = L.nm[t0 >> 3];
+                for (int i = 0; i < G / 4; i++) {
+                    const float4 a = *reinterpret_cast<const float4 *>(&L.xt[dl][G * g + 4 * i]);
+                    const float4 c = *reinterpret_cast<const float4 *>(&L.vs[G * g + 4 * i]);
+                    xs[4 * i] = a.x; xs[4 * i + 1] = a.y; xs[4 * i + 2] = a.z; xs[4 * i + 3] = a.w;
+                    vs8[4 * i] = c.x; vs8[4 * i + 1] = c.y; vs8[4 * i + 2] = c.z; vs8[4 * i + 3] = c.w;
+                }
             };
-            auto chain = [&](const float (&xs)[8], const float (&vs8)[8], int g, int t0) {
-                if (__builtin_amdgcn_readfirstlane(g) == 0) {   // no new maximum: ms = 1
+            auto chain = [&](const float (&xs)[G], const float (&vs8)[G], int g) {
+                const int bit = 8 * (g / GPW) + g % GPW;
+                if (__builtin_expect(((gmask >> bit) & 1u) == 0, 1)) {   // no new maximum: ms = 1 (the
+                                                                          // fall-through path)
 #pragma unroll
-                    for (int i = 0; i < 8; i++) acc = __builtin_fmaf(xs[i], vs8[i], acc);
+                    for (int i = 0; i < G; i++) acc = __builtin_fmaf(xs[i], vs8[i], acc);
                 } else {
 #pragma unroll
-                    for (int i = 0; i < 8; i++) {
-                        const float m1 = L.ms[t0 + i];
-                        const float lo = __builtin_fmaf(xs[i], vs8[i], acc * m1);
-                        const float hs = __builtin_fmaf(acc, m1, vs8[i]);
-                        acc = lane >= 32 ? hs : lo;
+                    for (int i4 = 0; i4 < G / 4; i4++) {
+                        const float4 m4 = *reinterpret_cast<const float4 *>(&L.ms[G * g + 4 * i4]);
+                        const float m[4] = {m4.x, m4.y, m4.z, m4.w};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const float lo = __builtin_fmaf(xs[4 * i4 + i], vs8[4 * i4 + i], acc * m[i]);
+                            const float hs = __builtin_fmaf(acc, m[i], vs8[4 * i4 + i]);
+                            acc = lane >= 32 ? hs : lo;
+                        }
                     }
                 }
             };
-            // (a group read ahead may start at t0 <= n: LDS rows up to QX_C + 8 hold no key and
-            // are not used)
-            group(0, xa, va, ga);
-            int t = 0;
-            for (; t + 16 <= n; t += 16) {
-                group(t + 8, xb, vbn, gb);
-                chain(xa, va, ga, t);
-                group(t + 16, xa, va, ga);
-                chain(xb, vbn, gb, t + 8);
+            // (groups up to ng + 2 are read: entries up to QX_C + QX_RA - 1)
+            group(0, x0, v0);
+            group(1, x1, v1);
+            group(2, x2, v2);
+            int g = 0;
+            for (; g + 4 <= ng; g += 4) {
+                group(g + 3, x3, v3);
+                chain(x0, v0, g);
+                group(g + 4, x0, v0);
+                chain(x1, v1, g + 1);
+                group(g + 5, x1, v1);
+                chain(x2, v2, g + 2);
+                group(g + 6, x2, v2);
+                chain(x3, v3, g + 3);
             }
-            if (t + 8 <= n) {
-                chain(xa, va, ga, t);
-                t += 8;
-            }
-            for (; t < n; t++) {
-                const float x1 = L.x[t][dl], v1 = L.vs[t], m1 = L.ms[t];
-                const float lo = __builtin_fmaf(x1, v1, acc * m1);
-                const float hs = __builtin_fmaf(acc, m1, v1);
-                acc = lane >= 32 ? hs : lo;
-            }
+            if (g < ng) chain(x0, v0, g);
+            if (g + 1 < ng) chain(x1, v1, g + 1);
+            if (g + 2 < ng) chain(x2, v2, g + 2);
         }
         __syncthreads();
     }
