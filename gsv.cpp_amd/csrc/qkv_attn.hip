@@ -57,9 +57,29 @@ struct QxLds {
     float ms[QX_C];
     float wmax[QX_C / 64];
     uint8_t gm[QX_C / 64];       // per wave, one bit per group of QX_G keys that holds a new maximum
+    uint64_t etab[32];           // the exponential's table
 };
 
 __constant__ uint64_t qx_exp2_tab[32] = GSVK_EXP2_TAB32;
+
+// v moved across lanes by the DPP control CTRL; lanes with no source lane, or outside the rows
+// of ROW_MASK, read -inf
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float qx_dpp_ninf(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp((int) 0xff800000u, __float_as_int(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// inclusive maximum scan over the 64 lanes: row shifts by 1, 2, 4 and 8 within each row of 16,
+// then row 0's last lane into row 1 (and row 2's into row 3), then lane 31 into rows 2 and 3
+__device__ __forceinline__ float qx_wave_incl_max(float v) {
+    v = fmaxf(v, qx_dpp_ninf<0x111, 0xf>(v));
+    v = fmaxf(v, qx_dpp_ninf<0x112, 0xf>(v));
+    v = fmaxf(v, qx_dpp_ninf<0x114, 0xf>(v));
+    v = fmaxf(v, qx_dpp_ninf<0x118, 0xf>(v));
+    v = fmaxf(v, qx_dpp_ninf<0x142, 0xa>(v));
+    v = fmaxf(v, qx_dpp_ninf<0x143, 0xc>(v));
+    return v;
+}
 
 // the K and V rows (64 bytes each) of key j of one (sequence, head); a key past `last` reads key
 // `last` (in the buffer; not used)
@@ -76,12 +96,12 @@ __device__ __forceinline__ void qx_load(const uint16_t * __restrict__ kb, const 
 }
 
 // Exact attention of one (sequence, head) over keys [beg, end), end - 1 == col (the new key, in
-// s_kv); 256 threads; r holds the rows of key beg + tid on entry. Returns dimension `lane` of the
-// output in wave 0's lanes 0..31.
+// s_kv); 256 threads; r holds the rows of key beg + tid on entry; etab_v: entry lane % 32 of the
+// exponential's table. Returns dimension `lane` of the output in wave 0's lanes 0..31.
 __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * __restrict__ kb,
                                            const uint16_t * __restrict__ vb, int beg, int end, int col,
                                            int last_old, const float * s_q, const uint16_t (*s_kv)[ATT_HD],
-                                           float scale, int tid) {
+                                           uint64_t etab_v, float scale, int tid) {
     __shared__ __align__(16) QxLds L;
     const int lane = tid & 63, wave = tid >> 6;
     float qv[32];
@@ -90,6 +110,7 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
         const float4 q4 = *reinterpret_cast<const float4 *>(&s_q[4 * c]);
         qv[4 * c] = q4.x; qv[4 * c + 1] = q4.y; qv[4 * c + 2] = q4.z; qv[4 * c + 3] = q4.w;
     }
+    if (tid < 32) L.etab[tid] = etab_v;   // (read after the first chunk's first barrier)
     const int dl = lane < 32 ? lane : 32;
     float M = -INFINITY;   // running maximum, uniform
     float acc = 0.0f;      // wave 0: lanes 0..31 the output dimensions, lane 32 (and above) S
@@ -143,14 +164,8 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
         }
         // the maximum before each key: inclusive scan within the wave, the waves' maxima, seeded
         // with the running maximum (max is exact in any order)
-        float incl = s;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const float o = __shfl_up(incl, off, 64);
-            if (lane >= off) incl = fmaxf(incl, o);
-        }
-        float excl = __shfl_up(incl, 1, 64);
-        if (lane == 0) excl = -INFINITY;
+        const float incl = qx_wave_incl_max(s);
+        const float excl = qx_dpp_ninf<0x138, 0xf>(incl);   // wave_shr:1 (lane 0: -inf)
         if (lane == 63) L.wmax[wave] = incl;
         __syncthreads();
         float before = M, mn = M;
@@ -164,8 +179,8 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
         float ms = 1.0f, vs = 0.0f;   // past the chunk's end: weight 0, maximum unchanged
         if (tid < n) {
             vs = 1.0f;
-            if (s > before) ms = expf_glibc(before - s, qx_exp2_tab);
-            else vs = expf_glibc(s - before, qx_exp2_tab);
+            if (s > before) ms = expf_glibc(before - s, L.etab);
+            else vs = expf_glibc(s - before, L.etab);
         }
         L.ms[tid] = ms;
         L.vs[tid] = vs;
@@ -343,6 +358,11 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     KV8 cur;
     if constexpr (EXACT)   // the rows of key beg + tid (the first chunk)
         qx_load(a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg + tid, last_old, cur);
+    // exact mode: the exponential's table, for LDS (a lookup in constant memory per lane would be a
+    // memory round trip inside each chunk's scan); loaded after the first chunk's keys, which the
+    // scan waits for first
+    uint64_t etab_v = 0;
+    if constexpr (EXACT) etab_v = qx_exp2_tab[lane & 31];
     else
         load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
     __syncthreads();
@@ -392,7 +412,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     }
     if constexpr (EXACT) {
         const float val = qx_attend(cur, a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg,
-                                    end, col, last_old, s_q, s_kv, a.scale, tid);
+                                    end, col, last_old, s_q, s_kv, etab_v, a.scale, tid);
         if (wave == 0) attn_store_out(val, lane, pair, nh, a.out, nullptr, a.oq, a.od);
         return;
     }

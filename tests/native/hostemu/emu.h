@@ -137,8 +137,11 @@ inline int dpp_src(int ctrl, int l) {
     if (ctrl >= 0x101 && ctrl <= 0x10f) { const int n = ctrl - 0x100; return r + n <= 15 ? l + n : -1; }
     if (ctrl >= 0x111 && ctrl <= 0x11f) { const int n = ctrl - 0x110; return r - n >= 0 ? l - n : -1; }
     if (ctrl >= 0x121 && ctrl <= 0x12f) { const int n = ctrl - 0x120; return base | ((r - n + 16) & 15); }
+    if (ctrl == 0x138) return l >= 1 ? l - 1 : -1;                  // wave_shr:1
     if (ctrl == 0x140) return base | (15 - r);
     if (ctrl == 0x141) return (l & ~7) | (7 - (l & 7));
+    if (ctrl == 0x142) return base >= 16 ? base - 1 : -1;           // row_bcast:15
+    if (ctrl == 0x143) return base >= 32 ? 31 : -1;                 // row_bcast:31
     std::fprintf(stderr, "emu: DPP control 0x%x not emulated\n", ctrl);
     std::abort();
 }
