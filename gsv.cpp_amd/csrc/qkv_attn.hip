@@ -42,21 +42,26 @@ constexpr int QA_NBLK = QA_K / 32;
 constexpr int QA_NB4 = QA_K / 128;       // int4 weight loads per slice lane
 constexpr int QA_ROWS = 3 * ATT_HD;      // rows of one head: q, k, v
 
-constexpr int QX_C = 256;    // keys per chunk of the exact attention: one per thread of 4 waves
+constexpr int QX_C = 384;    // keys per chunk of the exact attention: one per producer thread
+constexpr int QX_NP = QX_C / 64;   // producer waves
+constexpr int QX_CW = 3;     // the chain's wave: with 7 waves dealt to a CU's 4 SIMDs in turn, the
+                             // only one with a SIMD of its own
 constexpr int QX_G = 16;     // keys per group of the chain (one bit of the new-maximum mask)
 constexpr int QX_RA = 3 * QX_G;   // entries past the chunk that the chain reads ahead (never used)
-constexpr int QX_TS = 324;   // floats per dimension row of the transposed V: >= QX_C + QX_RA, and
+constexpr int QX_TS = 452;   // floats per dimension row of the transposed V: >= QX_C + QX_RA, and
                              // 4 more than a multiple of 32 so that 8 lanes' 16-byte reads of
                              // consecutive rows fall in distinct banks
 
 struct QxLds {
-    // V transposed: row d < 32 holds dimension d of the chunk's keys, row 32 holds 1.0 (S's
-    // chain); keys past the chunk's end hold -0.0 (a product of -0.0 added to any value leaves it)
-    float xt[ATT_HD + 1][QX_TS];
-    float vs[QX_C + QX_RA];      // the key's weight exp(s - max before it); 0 past the chunk's end
-    float ms[QX_C];
+    // V transposed: row d < 32 holds dimension d of the chunk's keys, row 32 holds 1.0 (S's chain;
+    // written once); keys past the chunk's end hold -0.0 (a product of -0.0 added to any value
+    // leaves it) and weight 0 (S + 1 * 0 is S)
+    // (two of each: the chunk the producers fill, the chunk the chain reads)
+    float xt[2][ATT_HD + 1][QX_TS];
+    float vs[2][QX_C + QX_RA];   // the key's weight exp(s - max before it); 0 past the chunk's end
+    float ms[2][QX_C];
     float wmax[QX_C / 64];
-    uint8_t gm[QX_C / 64];       // per wave, one bit per group of QX_G keys that holds a new maximum
+    uint8_t gm[2][8];            // per producer wave, one bit per group of QX_G keys that holds a new maximum
     uint64_t etab[32];           // the exponential's table
 };
 
@@ -95,158 +100,190 @@ __device__ __forceinline__ void qx_load(const uint16_t * __restrict__ kb, const 
     }
 }
 
+// producer index of a thread of the exact attention's producer waves (every wave but QX_CW)
+__device__ __forceinline__ int qx_ptid(int wave, int lane) { return (wave < QX_CW ? wave : wave - 1) * 64 + lane; }
+
 // Exact attention of one (sequence, head) over keys [beg, end), end - 1 == col (the new key, in
-// s_kv); 256 threads; r holds the rows of key beg + tid on entry; etab_v: entry lane % 32 of the
-// exponential's table. Returns dimension `lane` of the output in wave 0's lanes 0..31.
+// s_kv); (QX_NP + 1) * 64 threads. The producer waves (producer thread p holding key c0 + p of a
+// chunk of QX_C) compute each chunk's scores, maxima and weights into one of two LDS buffers; wave
+// QX_CW runs the sequential chain over the chunk before, from the other buffer, in two parts
+// around the producers' barrier. `first` holds the rows of key beg + p on entry (producers);
+// etab_v: entry lane % 32 of the exponential's table. Returns dimension `lane` of the output in
+// wave QX_CW's lanes 0..31.
 __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * __restrict__ kb,
                                            const uint16_t * __restrict__ vb, int beg, int end, int col,
                                            int last_old, const float * s_q, const uint16_t (*s_kv)[ATT_HD],
                                            uint64_t etab_v, float scale, int tid) {
     __shared__ __align__(16) QxLds L;
     const int lane = tid & 63, wave = tid >> 6;
-    float qv[32];
-#pragma unroll
-    for (int c = 0; c < 8; c++) {
-        const float4 q4 = *reinterpret_cast<const float4 *>(&s_q[4 * c]);
-        qv[4 * c] = q4.x; qv[4 * c + 1] = q4.y; qv[4 * c + 2] = q4.z; qv[4 * c + 3] = q4.w;
-    }
+    const bool prod = wave != QX_CW;             // uniform per wave
+    const int pwave = wave < QX_CW ? wave : wave - 1, ptid = qx_ptid(wave, lane);   // producers
     if (tid < 32) L.etab[tid] = etab_v;   // (read after the first chunk's first barrier)
+    for (int i = tid; i < 2 * (QX_C + QX_RA); i += (QX_NP + 1) * 64)   // S's rows (read after a barrier too)
+        L.xt[i / (QX_C + QX_RA)][ATT_HD][i % (QX_C + QX_RA)] = 1.0f;
     const int dl = lane < 32 ? lane : 32;
-    float M = -INFINITY;   // running maximum, uniform
+    float M = -INFINITY;   // producers: running maximum (uniform)
     float acc = 0.0f;      // wave 0: lanes 0..31 the output dimensions, lane 32 (and above) S
     uint4 rk0 = first.k[0], rk1 = first.k[1], rk2 = first.k[2], rk3 = first.k[3];
     uint4 rv0 = first.v[0], rv1 = first.v[1], rv2 = first.v[2], rv3 = first.v[3];
-    for (int c0 = beg; c0 < end; c0 += QX_C) {   // uniform
-        const int n = min(QX_C, end - c0);
-        const int j = c0 + tid;
-        // the new key from LDS (the loaded slot holds the old contents)
-        const bool nw = j == col;
-        const uint4 * nk = reinterpret_cast<const uint4 *>(&s_kv[0][0]);
-        const uint4 * nv = reinterpret_cast<const uint4 *>(&s_kv[1][0]);
-        const uint4 kw[4] = {nw ? nk[0] : rk0, nw ? nk[1] : rk1, nw ? nk[2] : rk2, nw ? nk[3] : rk3};
-        const uint4 vw[4] = {nw ? nv[0] : rv0, nw ? nv[1] : rv1, nw ? nv[2] : rv2, nw ? nv[3] : rv3};
-        if (c0 + QX_C < end) {   // the next chunk's rows (uniform)
-            const int key = j + QX_C < last_old ? j + QX_C : last_old;
-            const uint4 * kp = reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
-            const uint4 * vp = reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
-            rk0 = kp[0]; rk1 = kp[1]; rk2 = kp[2]; rk3 = kp[3];
-            rv0 = vp[0]; rv1 = vp[1]; rv2 = vp[2]; rv3 = vp[3];
-        }
-        float s = -INFINITY;
-        if (tid < n) {
-            float kf[32], vf[32];
+    float s = -INFINITY, excl = -INFINITY;   // producers: the key's score, the maximum before it in the wave
+
+    // the chain over groups [g0, g1) of the chunk in buffer `bf` (wave 0): groups of QX_G keys,
+    // the last one completed by keys of weight 0 and value -0.0 (acc * 1 + -0.0 * 0 is acc, and so
+    // is fma(-0.0, 0, acc)); each group's LDS reads are issued three groups ahead into a ring of
+    // four register sets (four groups per iteration, so that no copy between the sets is needed)
+    auto chain_range = [&](int bf, int g0, int g1) {
+        if (g0 >= g1) return;   // (uniform)
+        constexpr int G = QX_G, GPW = 64 / QX_G;
+        // group g's bit is bit g % GPW of byte g / GPW (uniform, a scalar register)
+        const uint32_t glo = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(&L.gm[bf][0]));
+        const uint32_t ghi = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(&L.gm[bf][4]));
+        const uint64_t gmask = (uint64_t) glo | ((uint64_t) ghi << 32);
+        float x0[G], v0[G], x1[G], v1[G], x2[G], v2[G], x3[G], v3[G];
+        auto group = [&](int g, float (&xs)[G], float (&vs8)[G]) {
 #pragma unroll
-            for (int p = 0; p < 4; p++) {
-                float t8[8];
-                h8_to_f(kw[p], t8);
-#pragma unroll
-                for (int i = 0; i < 8; i++) kf[8 * p + i] = t8[i];
-                h8_to_f(vw[p], t8);
-#pragma unroll
-                for (int i = 0; i < 8; i++) vf[8 * p + i] = t8[i];
+            for (int i = 0; i < G / 4; i++) {
+                const float4 a = *reinterpret_cast<const float4 *>(&L.xt[bf][dl][G * g + 4 * i]);
+                const float4 c = *reinterpret_cast<const float4 *>(&L.vs[bf][G * g + 4 * i]);
+                xs[4 * i] = a.x; xs[4 * i + 1] = a.y; xs[4 * i + 2] = a.z; xs[4 * i + 3] = a.w;
+                vs8[4 * i] = c.x; vs8[4 * i + 1] = c.y; vs8[4 * i + 2] = c.z; vs8[4 * i + 3] = c.w;
             }
-            // ggml_vec_dot_f32 (32 elements): 4 x 8 partial products, (0 + 2) + (1 + 3), hsum
-            float s0[8];
+        };
+        auto chain = [&](const float (&xs)[G], const float (&vs8)[G], int g) {
+            const int bit = 8 * (g / GPW) + g % GPW;
+            if (__builtin_expect(((gmask >> bit) & 1ull) == 0, 1)) {   // no new maximum: ms = 1 (the
+                                                                      // fall-through path)
 #pragma unroll
-            for (int l = 0; l < 8; l++) {
-                const float p0 = __builtin_fmaf(kf[l], qv[l], 0.0f), p1 = __builtin_fmaf(kf[8 + l], qv[8 + l], 0.0f);
-                const float p2 = __builtin_fmaf(kf[16 + l], qv[16 + l], 0.0f), p3 = __builtin_fmaf(kf[24 + l], qv[24 + l], 0.0f);
-                s0[l] = (p0 + p2) + (p1 + p3);
-            }
-            const float t0 = s0[0] + s0[4], t1 = s0[1] + s0[5], t2 = s0[2] + s0[6], t3 = s0[3] + s0[7];
-            s = ((t0 + t1) + (t2 + t3)) * scale;
+                for (int i = 0; i < G; i++) acc = __builtin_fmaf(xs[i], vs8[i], acc);
+            } else {
 #pragma unroll
-            for (int d = 0; d < ATT_HD; d++) L.xt[d][tid] = vf[d];
-            L.xt[ATT_HD][tid] = 1.0f;
-        } else {
+                for (int i4 = 0; i4 < G / 4; i4++) {
+                    const float4 m4 = *reinterpret_cast<const float4 *>(&L.ms[bf][G * g + 4 * i4]);
+                    const float m[4] = {m4.x, m4.y, m4.z, m4.w};
 #pragma unroll
-            for (int d = 0; d <= ATT_HD; d++) L.xt[d][tid] = -0.0f;
-        }
-        // the maximum before each key: inclusive scan within the wave, the waves' maxima, seeded
-        // with the running maximum (max is exact in any order)
-        const float incl = qx_wave_incl_max(s);
-        const float excl = qx_dpp_ninf<0x138, 0xf>(incl);   // wave_shr:1 (lane 0: -inf)
-        if (lane == 63) L.wmax[wave] = incl;
-        __syncthreads();
-        float before = M, mn = M;
-#pragma unroll
-        for (int w = 0; w < QX_C / 64; w++) {
-            const float wm = L.wmax[w];
-            if (w < wave) before = fmaxf(before, wm);
-            mn = fmaxf(mn, wm);
-        }
-        before = fmaxf(before, excl);
-        float ms = 1.0f, vs = 0.0f;   // past the chunk's end: weight 0, maximum unchanged
-        if (tid < n) {
-            vs = 1.0f;
-            if (s > before) ms = expf_glibc(before - s, L.etab);
-            else vs = expf_glibc(s - before, L.etab);
-        }
-        L.ms[tid] = ms;
-        L.vs[tid] = vs;
-        const uint64_t nm = __ballot(ms != 1.0f);
-        const uint64_t gz = __ballot(lane < 64 / QX_G && ((nm >> (QX_G * lane)) & ((1ull << QX_G) - 1)) != 0);
-        if (lane == 0) L.gm[wave] = (uint8_t) gz;
-        M = mn;
-        __syncthreads();
-        // the chains (wave 0): groups of QX_G keys, the last one completed by keys of weight 0 and
-        // value -0.0 (acc * 1 + -0.0 * 0 is acc, and so is fma(-0.0, 0, acc)); each group's LDS
-        // reads are issued three groups ahead into a ring of four register sets (four groups per
-        // iteration, so that no copy between the sets is needed)
-        if (wave == 0) {
-            constexpr int G = QX_G, GPW = 64 / QX_G;
-            // group g's bit is bit g % GPW of byte g / GPW (uniform, a scalar register)
-            const uint32_t gmask = __builtin_amdgcn_readfirstlane(*reinterpret_cast<const uint32_t *>(L.gm));
-            const int ng = (n + G - 1) / G;
-            float x0[G], v0[G], x1[G], v1[G], x2[G], v2[G], x3[G], v3[G];
-            auto group = [&](int g, float (&xs)[G], float (&vs8)[G]) {
-#pragma unroll
-                for (int i = 0; i < G / 4; i++) {
-                    const float4 a = *reinterpret_cast<const float4 *>(&L.xt[dl][G * g + 4 * i]);
-                    const float4 c = *reinterpret_cast<const float4 *>(&L.vs[G * g + 4 * i]);
-                    xs[4 * i] = a.x; xs[4 * i + 1] = a.y; xs[4 * i + 2] = a.z; xs[4 * i + 3] = a.w;
-                    vs8[4 * i] = c.x; vs8[4 * i + 1] = c.y; vs8[4 * i + 2] = c.z; vs8[4 * i + 3] = c.w;
-                }
-            };
-            auto chain = [&](const float (&xs)[G], const float (&vs8)[G], int g) {
-                const int bit = 8 * (g / GPW) + g % GPW;
-                if (__builtin_expect(((gmask >> bit) & 1u) == 0, 1)) {   // no new maximum: ms = 1 (the
-                                                                          // fall-through path)
-#pragma unroll
-                    for (int i = 0; i < G; i++) acc = __builtin_fmaf(xs[i], vs8[i], acc);
-                } else {
-#pragma unroll
-                    for (int i4 = 0; i4 < G / 4; i4++) {
-                        const float4 m4 = *reinterpret_cast<const float4 *>(&L.ms[G * g + 4 * i4]);
-                        const float m[4] = {m4.x, m4.y, m4.z, m4.w};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const float lo = __builtin_fmaf(xs[4 * i4 + i], vs8[4 * i4 + i], acc * m[i]);
-                            const float hs = __builtin_fmaf(acc, m[i], vs8[4 * i4 + i]);
-                            acc = lane >= 32 ? hs : lo;
-                        }
+                    for (int i = 0; i < 4; i++) {
+                        const float lo = __builtin_fmaf(xs[4 * i4 + i], vs8[4 * i4 + i], acc * m[i]);
+                        const float hs = __builtin_fmaf(acc, m[i], vs8[4 * i4 + i]);
+                        acc = lane >= 32 ? hs : lo;
                     }
                 }
-            };
-            // (groups up to ng + 2 are read: entries up to QX_C + QX_RA - 1)
-            group(0, x0, v0);
-            group(1, x1, v1);
-            group(2, x2, v2);
-            int g = 0;
-            for (; g + 4 <= ng; g += 4) {
-                group(g + 3, x3, v3);
-                chain(x0, v0, g);
-                group(g + 4, x0, v0);
-                chain(x1, v1, g + 1);
-                group(g + 5, x1, v1);
-                chain(x2, v2, g + 2);
-                group(g + 6, x2, v2);
-                chain(x3, v3, g + 3);
             }
-            if (g < ng) chain(x0, v0, g);
-            if (g + 1 < ng) chain(x1, v1, g + 1);
-            if (g + 2 < ng) chain(x2, v2, g + 2);
+        };
+        // (groups up to g1 + 2 <= QX_C / G + 2 are read: entries up to QX_C + QX_RA - 1)
+        group(g0, x0, v0);
+        group(g0 + 1, x1, v1);
+        group(g0 + 2, x2, v2);
+        int g = g0;
+        for (; g + 4 <= g1; g += 4) {
+            group(g + 3, x3, v3);
+            chain(x0, v0, g);
+            group(g + 4, x0, v0);
+            chain(x1, v1, g + 1);
+            group(g + 5, x1, v1);
+            chain(x2, v2, g + 2);
+            group(g + 6, x2, v2);
+            chain(x3, v3, g + 3);
         }
+        if (g < g1) chain(x0, v0, g);
+        if (g + 1 < g1) chain(x1, v1, g + 1);
+        if (g + 2 < g1) chain(x2, v2, g + 2);
+    };
+
+    const int nchunks = (end - beg + QX_C - 1) / QX_C;
+    for (int it = 0; it <= nchunks; it++) {   // uniform: chunk it's scan, chunk it - 1's chain
+        const int bf = it & 1;
+        const int c0 = beg + it * QX_C;
+        const int n = min(QX_C, end - c0);   // (<= 0 in the last iteration)
+        const int np = min(QX_C, end - (c0 - QX_C));   // keys of chunk it - 1
+        const int ngp = (np + QX_G - 1) / QX_G;
+        // the chain's part before the producers' barrier (all of it when no chunk is being scanned)
+        const int gsplit = it == nchunks ? ngp : (ngp * 5 + 4) / 8;
+        if (prod && it < nchunks) {
+            const int j = c0 + ptid;
+            // the new key from LDS (the loaded slot holds the old contents)
+            uint4 kw[4] = {rk0, rk1, rk2, rk3}, vw[4] = {rv0, rv1, rv2, rv3};
+            if (j == col) {   // (one thread)
+                const uint4 * nk = reinterpret_cast<const uint4 *>(&s_kv[0][0]);
+                const uint4 * nv = reinterpret_cast<const uint4 *>(&s_kv[1][0]);
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    kw[p] = nk[p];
+                    vw[p] = nv[p];
+                }
+            }
+            if (c0 + QX_C < end) {   // the next chunk's rows (uniform)
+                const int key = j + QX_C < last_old ? j + QX_C : last_old;
+                const uint4 * kp = reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
+                const uint4 * vp = reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+                rk0 = kp[0]; rk1 = kp[1]; rk2 = kp[2]; rk3 = kp[3];
+                rv0 = vp[0]; rv1 = vp[1]; rv2 = vp[2]; rv3 = vp[3];
+            }
+            s = -INFINITY;
+            if (ptid < n) {
+                float qv[32];
+#pragma unroll
+                for (int c = 0; c < 8; c++) {
+                    const float4 q4 = *reinterpret_cast<const float4 *>(&s_q[4 * c]);
+                    qv[4 * c] = q4.x; qv[4 * c + 1] = q4.y; qv[4 * c + 2] = q4.z; qv[4 * c + 3] = q4.w;
+                }
+                float kf[32], vf[32];
+#pragma unroll
+                for (int p = 0; p < 4; p++) {
+                    float t8[8];
+                    h8_to_f(kw[p], t8);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) kf[8 * p + i] = t8[i];
+                    h8_to_f(vw[p], t8);
+#pragma unroll
+                    for (int i = 0; i < 8; i++) vf[8 * p + i] = t8[i];
+                }
+                // ggml_vec_dot_f32 (32 elements): 4 x 8 partial products, (0 + 2) + (1 + 3), hsum
+                float s0[8];
+#pragma unroll
+                for (int l = 0; l < 8; l++) {
+                    const float p0 = __builtin_fmaf(kf[l], qv[l], 0.0f), p1 = __builtin_fmaf(kf[8 + l], qv[8 + l], 0.0f);
+                    const float p2 = __builtin_fmaf(kf[16 + l], qv[16 + l], 0.0f), p3 = __builtin_fmaf(kf[24 + l], qv[24 + l], 0.0f);
+                    s0[l] = (p0 + p2) + (p1 + p3);
+                }
+                const float t0 = s0[0] + s0[4], t1 = s0[1] + s0[5], t2 = s0[2] + s0[6], t3 = s0[3] + s0[7];
+                s = ((t0 + t1) + (t2 + t3)) * scale;
+#pragma unroll
+                for (int d = 0; d < ATT_HD; d++) L.xt[bf][d][ptid] = vf[d];
+            } else {
+#pragma unroll
+                for (int d = 0; d < ATT_HD; d++) L.xt[bf][d][ptid] = -0.0f;
+            }
+            // the maximum before each key: inclusive scan within the wave, the waves' maxima,
+            // seeded with the running maximum (max is exact in any order)
+            const float incl = qx_wave_incl_max(s);
+            excl = qx_dpp_ninf<0x138, 0xf>(incl);   // wave_shr:1 (lane 0: -inf)
+            if (lane == 63) L.wmax[pwave] = incl;
+        }
+        if (!prod && it >= 1) chain_range(bf ^ 1, 0, gsplit);
+        if (it < nchunks) __syncthreads();   // (uniform)
+        if (prod && it < nchunks) {
+            float before = M, mn = M;
+#pragma unroll
+            for (int w = 0; w < QX_C / 64; w++) {
+                const float wm = L.wmax[w];
+                if (w < pwave) before = fmaxf(before, wm);
+                mn = fmaxf(mn, wm);
+            }
+            before = fmaxf(before, excl);
+            float ms = 1.0f, vs = 0.0f;   // past the chunk's end: weight 0, maximum unchanged
+            if (ptid < n) {
+                vs = 1.0f;
+                if (s > before) ms = expf_glibc(before - s, L.etab);
+                else vs = expf_glibc(s - before, L.etab);
+            }
+            L.ms[bf][ptid] = ms;
+            L.vs[bf][ptid] = vs;
+            const uint64_t nm = __ballot(ms != 1.0f);
+            const uint64_t gz = __ballot(lane < 64 / QX_G && ((nm >> (QX_G * lane)) & ((1ull << QX_G) - 1)) != 0);
+            if (lane == 0) L.gm[bf][pwave] = (uint8_t) gz;
+            M = mn;
+        }
+        if (!prod && it >= 1) chain_range(bf ^ 1, gsplit, ngp);
         __syncthreads();
     }
     const float S = __shfl(acc, 32, 64);
@@ -256,7 +293,7 @@ __device__ __forceinline__ float qx_attend(const KV8 & first, const uint16_t * _
 
 template <int NW, int MODE, bool EXACT>
 __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
-    static_assert(!EXACT || NW * 64 == QX_C, "exact mode: one key of a chunk per thread");
+    static_assert(!EXACT || (NW - 1) * 64 == QX_C, "exact mode: one key of a chunk per producer thread");
     constexpr int PASSES = (QA_ROWS / 8 + NW - 1) / NW;   // 8 rows per wave and pass
     const int nh = a.n_head;
     const int bh = blockIdx.x;
@@ -356,8 +393,9 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     last_old = last_old < a.lstride ? last_old : (int) a.lstride - 1;
     int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
     KV8 cur;
-    if constexpr (EXACT)   // the rows of key beg + tid (the first chunk)
-        qx_load(a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg + tid, last_old, cur);
+    if constexpr (EXACT)   // producer p: the rows of key beg + p (the first chunk); the chain's wave: unused
+        qx_load(a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD,
+                wave != QX_CW ? beg + qx_ptid(wave, lane) : beg, last_old, cur);
     // exact mode: the exponential's table, for LDS (a lookup in constant memory per lane would be a
     // memory round trip inside each chunk's scan); loaded after the first chunk's keys, which the
     // scan waits for first
@@ -413,7 +451,7 @@ __global__ void __launch_bounds__(NW * 64) k_qkv_attn(QkvAttnArgs a) {
     if constexpr (EXACT) {
         const float val = qx_attend(cur, a.kc + pair * a.lstride * ATT_HD, a.vc + pair * a.lstride * ATT_HD, beg,
                                     end, col, last_old, s_q, s_kv, etab_v, a.scale, tid);
-        if (wave == 0) attn_store_out(val, lane, pair, nh, a.out, nullptr, a.oq, a.od);
+        if (wave == QX_CW) attn_store_out(val, lane, pair, nh, a.out, nullptr, a.oq, a.od);
         return;
     }
     float qv[8];
@@ -490,9 +528,9 @@ int launch_qkv_attn(const QkvAttnArgs & a, int B, int64_t max_keys, hipStream_t 
     if (exact) {   // any row length: the chunks cover it
         GSVK_REQUIRE(B <= 65535 * 16 && a.scale > 0.0f, "qkv_attn: bad exact-mode arguments");
         if (a.in.mode == IN_LN)
-            hipLaunchKernelGGL((k_qkv_attn<4, IN_LN, true>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_qkv_attn<QX_NP + 1, IN_LN, true>), grid, dim3((QX_NP + 1) * 64), 0, stream, a);
         else
-            hipLaunchKernelGGL((k_qkv_attn<4, IN_EMB, true>), grid, dim3(256), 0, stream, a);
+            hipLaunchKernelGGL((k_qkv_attn<QX_NP + 1, IN_EMB, true>), grid, dim3((QX_NP + 1) * 64), 0, stream, a);
         GSVK_LAUNCH_CHECK();
         return GSVK_OK;
     }
