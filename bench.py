@@ -12,12 +12,13 @@ launch). The timed region covers exactly --steps steps with the inputs and the p
 resident on the device (the prefill runs before it and is reported separately).
 
     python bench.py [--gpus 1] [--steps 500] [--warmup 16] [--no-cpu]
+    python bench.py --exact-only [--steps 20]      (exact mode alone, for a kernel trace)
 
-Prints one JSON line. The roofline object times the dominant decode kernel (the attention launch
-of the two-launch layer at batch <= 16) alone with HIP events on the stream it runs on, at the
-mid-run shape of the line's own steps, rotating through buffers larger than the 256 MB MALL; its
-traffic is the HBM-counter ratio of profiles/decode_layer_b16_hbm.md times those algorithmic
-bytes. cpu_baseline times the oracle (the CPU restatement of the reference path) on this host's
+Prints one JSON line. The roofline object times the dominant decode kernel (the persistent decode
+kernel, all 24 layers of a step in one launch, at batch <= 32) alone with HIP events on the
+model's stream (gsvk_model_time_decode_kernel), at the mid-run state of the line's own steps; its
+traffic is the HBM-counter ratio of profiles/decode_persist_b16_hbm.md at that shape times those
+algorithmic bytes. cpu_baseline times the oracle (the CPU restatement of the reference path) on this host's
 cores on the same requests and the same steps, repeated to at least 10 s of decode; with the
 oracle as the checker it also counts, under teacher forcing, the steps whose device choice differs
 from the oracle's (default path and exact mode, batch 16 and batch 1). extra.exact_mode times
@@ -442,6 +443,31 @@ def bert_line(torch):
     return res
 
 
+def exact_line(g, B, steps, warmup, cfg, flags):
+    """Exact mode (gsvk_model_set_exact) on the batch-B workload over `steps` steps and on the batch-1
+    workload (128 phones + 64 prompt codes, 300 greedy steps, repetition penalty 1.35)."""
+    import synth_model as sm
+    if B > 16:
+        raise SystemExit("exact mode decodes at most 16 sequences")
+    reqs = workload_requests(B)
+    r1 = sm.synth_requests(0x6A5E0001, 1, 64, [128])
+    cfg1 = (1, 1.0, 1.0, 1.35)
+    g.set_exact(True)
+    try:
+        g.generate(r1, sampler=cfg1, max_steps=8, seeds=[1], flags=flags)
+        rx1 = g.generate(r1, sampler=cfg1, max_steps=300, seeds=[1], flags=flags)
+        g.generate(reqs, sampler=cfg, max_steps=max(warmup, 1), seeds=list(range(1, B + 1)), flags=flags)
+        rx = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=list(range(1, B + 1)), flags=flags)
+    finally:
+        g.set_exact(False)
+    return {"tok_s": round(B * steps / (rx["decode_ms"] / 1e3), 1),
+            "ms_per_step": round(rx["decode_ms"] / steps, 4),
+            "tok_s_b1": round(300 / (rx1["decode_ms"] / 1e3), 1),
+            "ms_per_step_b1": round(rx1["decode_ms"] / 300, 4),
+            "what": "gsvk_model_set_exact: the same workloads with ggml-cpu's arithmetic "
+                    "order throughout (logits equal to the oracle's to the bit)"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -455,6 +481,8 @@ def main():
     ap.add_argument("--b128-only", action="store_true", help="time only the batch-128 long-context decode")
     ap.add_argument("--bert-only", action="store_true", help="time only the BERT text encoder")
     ap.add_argument("--no-bert", action="store_true", help="skip the BERT text encoder line")
+    ap.add_argument("--exact-only", action="store_true",
+                    help="time only exact mode (the batch's workload and batch 1) and print it")
     ap.add_argument("--kernels-only", action="store_true",
                     help="time only the per-kernel roofline launches (for counter runs) and print them")
     args = ap.parse_args()
@@ -500,6 +528,10 @@ def main():
         return
     cfg = (15, 1.0, 1.0, 1.35)
     flags = gsvk.GSVK_GEN_EOS_MASK_ALL
+    if args.exact_only:
+        print(json.dumps({"exact_mode": exact_line(g, args.batch, args.steps, args.warmup, cfg, flags)}))
+        g.close()
+        return
 
     def run(B, steps, warmup):
         reqs = workload_requests(B)
@@ -537,22 +569,7 @@ def main():
     extra["b1_workload"] = "1 sequence, 128 phones + 64 prompt codes, 300 greedy steps, repetition penalty 1.35"
     # exact mode (ggml-cpu's arithmetic order throughout: the oracle's logits to the bit) on the same
     # two workloads
-    g.set_exact(True)
-    try:
-        if B > 16:
-            raise SystemExit("exact mode decodes at most 16 sequences")
-        g.generate(r1, sampler=cfg1, max_steps=8, seeds=[1], flags=flags)
-        rx1 = g.generate(r1, sampler=cfg1, max_steps=300, seeds=[1], flags=flags)
-        g.generate(reqs, sampler=cfg, max_steps=max(args.warmup, 1), seeds=list(range(1, B + 1)), flags=flags)
-        rx = g.generate(reqs, sampler=cfg, max_steps=args.steps, seeds=list(range(1, B + 1)), flags=flags)
-    finally:
-        g.set_exact(False)
-    extra["exact_mode"] = {"tok_s": round(B * args.steps / (rx["decode_ms"] / 1e3), 1),
-                           "ms_per_step": round(rx["decode_ms"] / args.steps, 4),
-                           "tok_s_b1": round(300 / (rx1["decode_ms"] / 1e3), 1),
-                           "ms_per_step_b1": round(rx1["decode_ms"] / 300, 4),
-                           "what": "gsvk_model_set_exact: the same workloads with ggml-cpu's arithmetic "
-                                   "order throughout (logits equal to the oracle's to the bit)"}
+    extra["exact_mode"] = exact_line(g, B, args.steps, args.warmup, cfg, flags)
     # the decode's dominant kernel alone at the timed run's mid-run state (batch <= 16)
     pk = persist_kernel(g, reqs, args.steps) if (not args.no_kernels and B <= 32) else None
     # batch 64: the batch-16 workload's request shape at 64 sequences, 200 steps
