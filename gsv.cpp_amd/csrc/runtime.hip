@@ -923,14 +923,17 @@ int enqueue_decode_body(gsvk_model * m) {
     if (m->generic) {
         GSVK_REQUIRE(m->decode_path == GSVK_DECODE_AUTO, "decode path %d: not available for a model with F16 / "
                      "F32 projections (it has its own per-op path)", m->decode_path);
-        GSVK_REQUIRE(!m->exact || m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences (got %d)",
-                     DECODE_GEMM_MIN_BATCH - 1, m->B);
+        GSVK_REQUIRE(!m->exact || m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences of a model "
+                     "with F16 / F32 projections (got %d)", DECODE_GEMM_MIN_BATCH - 1, m->B);
         return enqueue_decode_generic(m);
     }
     if (m->exact) {
-        GSVK_REQUIRE(m->B < DECODE_GEMM_MIN_BATCH, "exact mode decodes up to %d sequences (got %d)",
-                     DECODE_GEMM_MIN_BATCH - 1, m->B);
-        return enqueue_decode_rows(m, 0, m->B, m->stream);
+        // the GEMV chain in groups of at most GEMV_DECODE_MAX_BATCH rows, one group after another
+        // (every kernel of it computes each row on its own, so a row's arithmetic is the same in
+        // any group; each launch holds at most the rows the chain is tested at)
+        for (int r0 = 0; r0 < m->B; r0 += GEMV_DECODE_MAX_BATCH)
+            GSVK_TRY(enqueue_decode_rows(m, r0, std::min(GEMV_DECODE_MAX_BATCH, m->B - r0), m->stream));
+        return GSVK_OK;
     }
     // an explicit choice runs as asked or fails: it never falls back to another path
     switch (m->decode_path) {

@@ -197,8 +197,9 @@ int gsvk_model_set_decode_path(gsvk_model * m, int path);
  * prefill and the decode in ggml-cpu's x86 arithmetic order, so that logits and tokens are those
  * of the CPU reference bit for bit: the GEMV chain at every row count (no matrix-core GEMM) and
  * the attention of each (row, head) as flash_attn_ext's sequential online softmax with glibc's
- * expf (gsvk_op_attn_exact). Slower than the default kernels; decodes up to 16 sequences. No
- * counterpart in the reference (whose one CPU path is this arithmetic); for callers that need
+ * expf (gsvk_op_attn_exact). Slower than the default kernels; above 16 sequences the decode runs
+ * the chain in groups of 16 rows one after another (a model with F16 / F32 projections: at most
+ * 16 sequences). No counterpart in the reference (whose one CPU path is this arithmetic); for callers that need
  * its exact tokens and for tests. */
 int gsvk_model_set_exact(gsvk_model * m, int on);
 

@@ -193,15 +193,35 @@ def test_exact_mode_prefill_and_decode_bitexact(gpu, model4_path):
             assert np.array_equal(dv[b, :, sl].view(np.float16).astype(np.float32), rv[b, :, sl]), b
 
 
-def test_exact_mode_refuses_17_sequences(gpu, model4_path):
-    reqs = sm.synth_requests(412, 17, 8, [6] * 17)
+def test_exact_mode_decodes_past_16_sequences_in_row_groups(gpu, model4_path):
+    """Exact mode at 20 sequences: the GEMV chain in row groups of 16 and 4, one after another;
+    logits and the K/V of rows in both groups equal the oracle's to the bit."""
+    rng = np.random.default_rng(412)
+    B = 20
+    reqs = sm.synth_requests(412, B, 8, list(rng.integers(3, 25, B)))
+    steps = 6
+    forced = rng.integers(0, 1024, steps).astype(np.int32)
     g = gpu.Model(model4_path)
+    o = O.Model(model4_path)
     try:
         g.set_exact(True)
-        with pytest.raises(gpu.GsvkError, match="exact mode decodes up to 16"):
-            g.generate(reqs, sampler=GREEDY, max_steps=3, flags=1)
-        g.set_exact(False)
-        res = g.generate(reqs, sampler=GREEDY, max_steps=3, flags=1)   # the default path still runs
-        assert res["n_steps"] == 3
+        print("exact mode: generate, 4 layers, batch 20", flush=True)
+        res = g.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced, flags=1)
+        assert res["n_steps"] == steps
+        k3, v3 = g.kv_read(3)
+        print("exact mode: step logits, batch 20", flush=True)
+        dev = _forced_logits(g, reqs, forced, steps)
+        ref = o.generate(reqs, sampler=GREEDY, max_steps=steps, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, kv_layer=3, want_logits=True)
     finally:
         g.close()
+        o.close()
+    assert np.array_equal(dev.view(np.uint32), ref["logits"][:steps].view(np.uint32)), \
+        np.abs(dev - ref["logits"][:steps]).max()
+    rk, rv = ref["kv"]
+    S = max(len(r["phones"]) for r in reqs) + 8
+    for b in (0, 15, 16, 19):   # rows of both groups
+        pad = S - 8 - len(reqs[b]["phones"])
+        sl = slice(pad, S + steps)
+        assert np.array_equal(k3[b, :, sl].view(np.float16).astype(np.float32), rk[b, :, sl]), b
+        assert np.array_equal(v3[b, :, sl].view(np.float16).astype(np.float32), rv[b, :, sl]), b

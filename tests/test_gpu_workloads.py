@@ -94,3 +94,38 @@ def test_batch16_500_sampled_steps(gpu, model24_path):
     P_b = rng.integers(100, 401, 16)
     reqs = sm.synth_requests(0x6A5E0002, 16, 64, P_b - 64)
     _check_workload(gpu, model24_path, reqs, (15, 1.0, 1.0, 1.35), 500, list(range(1, 17)))
+
+
+def test_batch32_exact_mode_100_sampled_steps(gpu, model24_path):
+    """Exact mode past 16 sequences (row groups of 16): 32 sequences of the batch-16 workload's
+    request shape, 100 top-k steps; the free run's tokens are the oracle's and the teacher-forced
+    step logits equal its logits to the bit."""
+    rng = np.random.Generator(np.random.PCG64(0x6A5E0005))
+    P_b = rng.integers(100, 401, 32)
+    reqs = sm.synth_requests(0x6A5E0005, 32, 64, P_b - 64)
+    cfg, steps, seeds = (15, 1.0, 1.0, 1.35), 100, list(range(1, 33))
+    o = O.Model(model24_path)
+    try:
+        print("oracle: batch 32, 100 steps, free run", flush=True)
+        free = o.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL)
+        forced = free["sampled"][:, 0].astype(np.int32)
+        print("oracle: forced run", flush=True)
+        ref = o.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, oracle=forced,
+                         flags=O.ORC_KV_F16 | O.ORC_EOS_MASK_ALL, want_logits=True)
+    finally:
+        o.close()
+    g = gpu.Model(model24_path)
+    try:
+        g.set_exact(True)
+        print("device, exact mode: free run and step logits, batch 32", flush=True)
+        res = g.generate(reqs, sampler=cfg, max_steps=steps, seeds=seeds, flags=1, want_sampled=True)
+        dev = FR.device_step_logits(g, reqs, forced, steps)
+    finally:
+        g.close()
+    assert res["n_steps"] == free["n_steps"] == steps
+    assert np.array_equal(res["sampled"], free["sampled"])
+    for b in range(32):
+        assert np.array_equal(res["tokens"][b], free["tokens"][b]), b
+    assert np.array_equal(dev.view(np.uint32), ref["logits"][:steps].view(np.uint32)), \
+        np.abs(dev - ref["logits"][:steps]).max()
+    print("batch 32, exact mode: 3200 choices, every one the oracle's; logits equal to the bit", flush=True)
