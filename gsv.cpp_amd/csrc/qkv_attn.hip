@@ -18,15 +18,16 @@
 // XCD, so the 52 KB of weights of head h are read from HBM once per XCD L2.
 //
 // Exact mode (EXACT): step 4 is flash_attn_ext's sequential online softmax in ggml-cpu's order
-// (src/gsv_ar.cpp:404; the oracle's orc_attn_row), bit for bit, in chunks of 256 keys:
-//   a. thread t of the 4 waves takes key c0 + t: its score q.k in ggml_vec_dot_f32's order times
-//      the scale, and its V row into LDS as fp32 (plus 1.0 for S's chain); the next chunk's K/V
-//      rows are loaded now;
+// (src/gsv_ar.cpp:404; the oracle's orc_attn_row), bit for bit, in chunks of 384 keys, 7 waves:
+//   a. producer thread p of the 6 producer waves takes key c0 + p: its score q.k in
+//      ggml_vec_dot_f32's order times the scale, and its V row into LDS as fp32, transposed; the
+//      next chunk's K/V rows are loaded now;
 //   b. the maximum before each key (an exclusive prefix max over the chunk, seeded with the
 //      running maximum) gives each key's ms and vs (glibc's expf): ms = expf(before - s), vs = 1
 //      for a new maximum, else ms = 1, vs = expf(s - before);
-//   c. wave 0 runs the chains, one dependent fma per key: lanes 0..31 acc_d = fma(v_d, vs,
-//      acc_d * ms), lane 32 S = fma(S, ms, vs); with ms = 1 (no new maximum among 8 keys, a
+//   c. the chain wave runs the chains over the chunk before (a and b fill one of two LDS buffers
+//      while c reads the other), one dependent fma per key: lanes 0..31 acc_d = fma(v_d, vs,
+//      acc_d * ms), lane 32 S = fma(S, ms, vs); with ms = 1 (no new maximum among 16 keys, a
 //      ballot per key) both are fma(x, vs, acc) with x = v_d or 1.
 #include "attn_dev.h"
 #include "expf_exact.h"

@@ -386,7 +386,7 @@ int gsvk_op_qkv_attn(const int8_t * wq, const uint16_t * wd, const float * bias,
                      float * ln_out, void * stream);
 /* The same launch with the attention in ggml-cpu's order (flash_attn_ext's sequential online
  * softmax, src/gsv_ar.cpp:404, with glibc's expf), bit for bit with the CPU reference: exact mode's
- * decode kernel (gsvk_model_set_exact). Any row length (the keys are taken in chunks of 256). */
+ * decode kernel (gsvk_model_set_exact). Any row length (the keys are taken in chunks of 384). */
 int gsvk_op_qkv_attn_exact(const int8_t * wq, const uint16_t * wd, const float * bias, const float * res,
                            const float * r, const float * ln_bias, const float * wb, int B, int nh,
                            uint16_t * k, uint16_t * v, int64_t lstride, const int32_t * kv_begin,
