@@ -106,6 +106,8 @@ struct DecPersistArgs {
                                 // one step is launched repeatedly, every launch's words above the last)
     int * flags;                // [8][32] barrier words (zero before the first step of a run)
     int * err;                  // 0, or 1 (a wait gave up) / 2 (an XCC id outside 0..7)
+    const int * active;         // or null: 0 there (no row took part in this step, as the step's
+                                // sampler records) makes the launch return at once
 };
 constexpr int DEC_PERSIST_WGS = 256;
 constexpr int DEC_PERSIST_MAX_BATCH = 32;   // 4 sequences per XCD

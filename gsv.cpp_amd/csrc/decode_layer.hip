@@ -680,7 +680,8 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     if (tid == 0) {
         const bool placed = (xcc & 0xf) < 8;
         if (!placed) __hip_atomic_store(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        s_go = placed && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+        const bool active = !p.active || __hip_atomic_load(p.active, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+        s_go = placed && __hip_atomic_load(p.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0 && active;
     }
     __syncthreads();
     if (!s_go) return;

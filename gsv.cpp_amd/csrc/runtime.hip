@@ -48,6 +48,8 @@ int launch_attn_exact_prefill(const float * qkv, int B, int S, int max_len, cons
                               int d_model, float scale, float * out, int8_t * oq, float * od, hipStream_t stream);
 
 constexpr int PE_MAX = 4096;   // Y_PE_MAX, src/gsv_ar.cpp:44
+// decode steps per graph launch of generate on the persistent decode (no launch passes max_steps)
+constexpr int GEN_STEPS_PER_LAUNCH = 4;
 
 // ---- device allocation helpers ------------------------------------------------------------
 
@@ -188,10 +190,14 @@ struct gsvk_model {
     // sequence state
     int prompt_len = 0, S = 0, max_len = 0, B = 0, host_step = 0;
     bool prefilled = false;
-    // graph of one decode step
-    hipGraphExec_t gexec = nullptr;
-    hipGraph_t graph = nullptr;
+    // graph of one decode step; generate on the persistent decode also captures GEN_STEPS_PER_LAUNCH
+    // steps in one graph (gexec_k), and its steps' sampler records whether any row took part, which
+    // the persistent kernel checks (persist_gate) so that the steps run after the last row finished
+    // return at once
+    hipGraphExec_t gexec = nullptr, gexec_k = nullptr;
+    hipGraph_t graph = nullptr, graph_k = nullptr;
     bool use_graph = true;
+    bool persist_gate = false;
     // a batch that sequences join and leave while it decodes (gsvk_cb_*): per-row loop index at
     // which the row joined and its step limit (both non-null only while a session is open), the
     // session's shape and its host-side slot table
@@ -206,6 +212,8 @@ struct gsvk_model {
         if (pf_pool) (void) hipFree(pf_pool);
         if (gexec) (void) hipGraphExecDestroy(gexec);
         if (graph) (void) hipGraphDestroy(graph);
+        if (gexec_k) (void) hipGraphExecDestroy(gexec_k);
+        if (graph_k) (void) hipGraphDestroy(graph_k);
         if (h_pinned) (void) hipHostFree(h_pinned);
         if (h_unfinished) (void) hipHostFree(h_unfinished);
         for (hipEvent_t & e : step_ev)
@@ -232,8 +240,10 @@ struct DeviceGuard {
 void drop_graph(gsvk_model * m) {
     if (m->gexec) (void) hipGraphExecDestroy(m->gexec);
     if (m->graph) (void) hipGraphDestroy(m->graph);
-    m->gexec = nullptr;
-    m->graph = nullptr;
+    if (m->gexec_k) (void) hipGraphExecDestroy(m->gexec_k);
+    if (m->graph_k) (void) hipGraphDestroy(m->graph_k);
+    m->gexec = m->gexec_k = nullptr;
+    m->graph = m->graph_k = nullptr;
 }
 
 // Close an open batch session (its graph and per-row arrays); the cache and state stay allocated.
@@ -794,6 +804,7 @@ DecPersistArgs persist_args(const gsvk_model * m) {
     pa.step = m->d_step;
     pa.flags = m->d_pflags;
     pa.err = m->d_pflags + 8 * 32;
+    pa.active = m->persist_gate ? m->d_pflags + 8 * 32 + 1 : nullptr;
     return pa;
 }
 
@@ -889,14 +900,14 @@ int prepare_persist(gsvk_model * m) {
     if (!m->d_pattn) {
         GSVK_TRY(m->wmem.alloc(m->d_pattn, (size_t) m->NL));
         GSVK_TRY(m->wmem.alloc(m->d_pffn, (size_t) m->NL));
-        GSVK_TRY(m->wmem.alloc(m->d_pflags, 8 * 32 + 1));
+        GSVK_TRY(m->wmem.alloc(m->d_pflags, 8 * 32 + 2));   // flags, error word, step-active word
     }
     std::vector<DecAttnArgs> aa((size_t) m->NL);
     std::vector<DecFfnArgs> fa((size_t) m->NL);
     for (int li = 0; li < m->NL; li++) dec_layer_args(m, li, aa[(size_t) li], fa[(size_t) li]);
     GSVK_HIP(hipMemcpy(m->d_pattn, aa.data(), aa.size() * sizeof(DecAttnArgs), hipMemcpyHostToDevice));
     GSVK_HIP(hipMemcpy(m->d_pffn, fa.data(), fa.size() * sizeof(DecFfnArgs), hipMemcpyHostToDevice));
-    GSVK_HIP(hipMemsetAsync(m->d_pflags, 0, (8 * 32 + 1) * sizeof(int), m->stream));
+    GSVK_HIP(hipMemsetAsync(m->d_pflags, 0, (8 * 32 + 2) * sizeof(int), m->stream));
     GSVK_HIP(hipStreamSynchronize(m->stream));
     m->persist_now = true;
     return GSVK_OK;
@@ -2021,22 +2032,44 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     };
     drop_graph(m);
     GSVK_TRY(prepare_persist(m));
-    if (m->use_graph && max_steps > 1) {
+    // On the persistent decode a launch holds GEN_STEPS_PER_LAUNCH steps (a graph launch after
+    // another costs ~13 us of idle GPU, a kernel boundary inside a graph ~1.5 us), and the steps
+    // that run after the last row finished skip the persistent kernel: each step's sampler records
+    // whether any row took part (the count before it was nonzero) and the kernel reads that.
+    struct GateReset {
+        gsvk_model * m;
+        ~GateReset() { m->persist_gate = false; }
+    } gate_reset{m};
+    m->persist_gate = m->persist_now;
+    sa.active = m->persist_gate ? m->d_pflags + 8 * 32 + 1 : nullptr;
+    const int K = (m->use_graph && m->persist_now && max_steps >= GEN_STEPS_PER_LAUNCH) ? GEN_STEPS_PER_LAUNCH : 1;
+    auto capture = [&](int nsteps, hipGraph_t & graph, hipGraphExec_t & gexec) -> int {
         GSVK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-        const int rc = enqueue_step();
+        int rc = GSVK_OK;
+        for (int k = 0; k < nsteps && rc == GSVK_OK; k++) rc = enqueue_step();
         hipGraph_t g = nullptr;
         const hipError_t e = hipStreamEndCapture(st, &g);
         if (rc != GSVK_OK) { if (g) (void) hipGraphDestroy(g); return rc; }
         GSVK_HIP(e);
-        m->graph = g;
-        GSVK_HIP(hipGraphInstantiate(&m->gexec, g, nullptr, nullptr, 0));
+        graph = g;
+        GSVK_HIP(hipGraphInstantiate(&gexec, g, nullptr, nullptr, 0));
+        return GSVK_OK;
+    };
+    if (m->use_graph && max_steps > 1) {
+        GSVK_TRY(capture(1, m->graph, m->gexec));
+        if (K > 1) GSVK_TRY(capture(K, m->graph_k, m->gexec_k));
     }
-    // Completion: STEPS_IN_FLIGHT steps are queued ahead of the one whose count the host reads.
-    // Before launching step idx the host waits for step idx - STEPS_IN_FLIGHT to end (the GPU
-    // still has the steps after it queued) and reads the unfinished count its sampler stored in
-    // pinned memory; 0 ends the loop. At most STEPS_IN_FLIGHT - 1 steps run after the one where
-    // the last sequence finished (they sample nothing: every row is closed).
+    // the count before the first step: every row
+    GSVK_HIP(hipMemcpyAsync(m->n_unfinished, &B, sizeof(int32_t), hipMemcpyHostToDevice, st));
+    // Completion: STEPS_IN_FLIGHT launches are queued ahead of the one whose count the host reads.
+    // Before a launch the host waits for the launch STEPS_IN_FLIGHT before it to end (the GPU
+    // still has the ones after it queued) and reads the unfinished count its last sampler stored
+    // in pinned memory; 0 ends the loop. At most STEPS_IN_FLIGHT * K - 1 steps run after the one
+    // where the last sequence finished (they sample nothing: every row is closed; on the
+    // persistent decode their decoder kernel returns at once). The steps of a launch never pass
+    // max_steps (the last max_steps % K go one per launch).
     constexpr int STEPS_IN_FLIGHT = 2;
+    int launch_steps[STEPS_IN_FLIGHT] = {0, 0};
     *(volatile int32_t *) m->h_unfinished = B;
     int ticked = 0;   // progress callbacks so far: one per step known to have run for a sequence
     auto tick = [&]() {
@@ -2046,16 +2079,21 @@ extern "C" int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B,
     GSVK_HIP(hipStreamSynchronize(st));
     const auto t_dec = std::chrono::steady_clock::now();
     m->prof.dec_build_ms = std::chrono::duration<double, std::milli>(t_dec - t_graph).count();
-    for (int idx = 0; idx < max_steps; idx++) {
-        hipEvent_t & ev = m->step_ev[idx % STEPS_IN_FLIGHT];
-        if (idx >= STEPS_IN_FLIGHT) {
+    for (int idx = 0, li = 0; idx < max_steps; li++) {
+        hipEvent_t & ev = m->step_ev[li % STEPS_IN_FLIGHT];
+        if (li >= STEPS_IN_FLIGHT) {
             GSVK_HIP(hipEventSynchronize(ev));
-            tick();   // step idx - STEPS_IN_FLIGHT ran with sequences still open
             if (*(volatile int32_t *) m->h_unfinished == 0) break;
+            // the steps of launch li - STEPS_IN_FLIGHT ran with sequences still open
+            for (int k = 0; k < launch_steps[li % STEPS_IN_FLIGHT]; k++) tick();
         }
-        if (m->gexec) GSVK_HIP(hipGraphLaunch(m->gexec, st));
+        const int ks = (m->gexec_k && max_steps - idx >= K) ? K : 1;
+        if (ks > 1) GSVK_HIP(hipGraphLaunch(m->gexec_k, st));
+        else if (m->gexec) GSVK_HIP(hipGraphLaunch(m->gexec, st));
         else GSVK_TRY(enqueue_step());
         GSVK_HIP(hipEventRecord(ev, st));
+        launch_steps[li % STEPS_IN_FLIGHT] = ks;
+        idx += ks;
     }
     GSVK_HIP(hipStreamSynchronize(st));
     out->decode_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t_dec).count();

@@ -34,6 +34,9 @@ struct SampleArgs {
     int32_t * n_unfinished;    // written by the last workgroup
     int32_t * n_unfinished_host;   // the same count in mapped pinned host memory (or null): the
                                    // host reads it once the step's event has completed
+    int32_t * active;          // or null: set by the last workgroup to whether any row took part
+                               // in this step (the count before it, *n_unfinished, was nonzero);
+                               // a decode kernel after the sampler may skip a step that is not
     int early_stop;            // -1 = off
     // a batch that sequences join while it decodes: row b takes part from loop index
     // row_start[b] on, for at most row_max[b] steps, its EOS-mask window, oracle, dumps and

@@ -439,6 +439,7 @@ __global__ void __launch_bounds__(SMP_THREADS) k_sample(SampleArgs a) {
         if (unfinished) atomicAdd(&s_unfinished, unfinished);
         __syncthreads();
         if (tid == 0) {
+            if (a.active) *a.active = *a.n_unfinished > 0 ? 1 : 0;   // (the count before this step)
             *a.n_unfinished = s_unfinished;
             if (a.n_unfinished_host)
                 __hip_atomic_store(a.n_unfinished_host, s_unfinished, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);

@@ -381,6 +381,35 @@ def test_persistent_decode_equals_two_launch_layer(gpu, model4_path, B):
             assert np.array_equal(r["tokens"][i], ra["tokens"][i]), i
 
 
+@pytest.mark.parametrize("B, early_stop, max_steps, flags", [(5, 9, 23, 0), (3, -1, 23, 1), (9, 13, 30, 1)])
+def test_persistent_generate_steps_per_launch(gpu, model4_path, B, early_stop, max_steps, flags):
+    """generate on the persistent decode launches 4 steps per graph (the last max_steps % 4 one by
+    one) and its kernel returns at once in steps after the last row finished: the tokens, lengths,
+    finish order and step count equal the two-launch layer's (one step per launch), with a
+    batch-wide early stop in the middle of a launch and without one."""
+    rng = np.random.default_rng(900 + B)
+    reqs = _reqs(901 + B, rng.integers(3, 60, B), 16)
+    cfg = (15, 1.0, 1.0, 1.35)
+    seeds = list(range(1, B + 1))
+    g = gpu.Model(model4_path)
+    try:
+        print(f"generate: batch {B}, early stop {early_stop}, {max_steps} steps", flush=True)
+        res = {}
+        for path in ("FUSED", "PERSIST", "FUSED"):
+            g.set_decode_path(getattr(gpu, "GSVK_DECODE_" + path))
+            r = g.generate(reqs, sampler=cfg, early_stop=early_stop, max_steps=max_steps, seeds=seeds, flags=flags)
+            res.setdefault(path, r)
+    finally:
+        g.close()
+    a, b = res["FUSED"], res["PERSIST"]
+    if early_stop >= 0:
+        assert a["n_steps"] < max_steps
+    assert b["n_steps"] == a["n_steps"]
+    assert np.array_equal(b["lens"], a["lens"]) and np.array_equal(b["finish_seq"], a["finish_seq"])
+    for i in range(B):
+        assert np.array_equal(b["tokens"][i], a["tokens"][i]), i
+
+
 def test_decode_kernel_timing_leaves_the_state(gpu, model4_path):
     """gsvk_model_time_decode_kernel (the bench's timing of the persistent kernel alone) repeats the
     current step's kernel: a positive duration, and a generate afterwards gives the tokens it gave
