@@ -1738,6 +1738,7 @@ extern "C" int gsvk_cb_open(gsvk_model * m, int capacity, int max_prefill, int m
                  "positional table (%d)", prompt_len + max_steps, PE_MAX);
     DeviceGuard guard(m->device);
     cb_drop(m);
+    drop_graph(m);   // a generate's graphs (the session captures its own)
     const int hist_len = prompt_len + max_steps;
     GSVK_TRY(alloc_kv(m, capacity, max_prefill + max_steps + 8));
     GSVK_TRY(ensure_state(m, capacity, hist_len, max_steps));
