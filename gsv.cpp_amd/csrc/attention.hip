@@ -49,7 +49,7 @@ __device__ __forceinline__ void attn_merge_parts(const float * p0, int nact, int
     attn_store_out(Ot * (1.0f / Lt), lane, bh, nh, out, out16, oq, od, oq_layout);
 }
 
-template <int NW>
+template <int NW, bool NT>
 __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     const float * __restrict__ q, int64_t q_stride, const uint16_t * __restrict__ kc,
     const uint16_t * __restrict__ vc, int nh, int64_t lstride, const int32_t * __restrict__ kv_begin,
@@ -116,12 +116,12 @@ __global__ void __launch_bounds__(NW * 64) k_attn_decode(
     const int nb = blk1 - blk0;
     int blk = blk0 + (wave < nb ? wave : nb - 1);
     KV8 cur;
-    load_block(kb, vb, beg + blk * ATT_BLK, last_key, ks, cur);
+    load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_key, ks, cur);
     const uint4 z4 = make_uint4(0, 0, 0, 0);
     if (wave < nb) {
         while (blk + NW < blk1) {
             KV8 pre;
-            load_block(kb, vb, beg + (blk + NW) * ATT_BLK, last_key, ks, pre);
+            load_block<NT>(kb, vb, beg + (blk + NW) * ATT_BLK, last_key, ks, pre);
             attn_block_step<false>(cur, beg + blk * ATT_BLK, end, ks, qv, scale_log2, -1, z4, z4, m, l, o);
             cur = pre;
             blk += NW;
@@ -241,6 +241,7 @@ int attn_waves(int B, int nh, int64_t max_keys) {
 // of attention per layer -> 121 us + 5 us of merge. Rows of at most 2 chunks lose more to the
 // extra launch than the balance returns (batch 64 x 16 heads, rows U[256, 2048]: 31 -> 37 us).
 constexpr int ATT_CHUNK = 16;
+constexpr int64_t ATT_NT_BYTES = (int64_t) 16 << 20;
 
 AttnPlan attn_plan(int B, int nh, int64_t max_keys) {
     const int64_t pairs = (int64_t) B * nh;
@@ -294,12 +295,21 @@ int launch_attn_decode(const float * q, int64_t q_stride, const uint16_t * k, co
     int32_t * counters = (int32_t *) ((char *) ws + ((part_bytes + 255) / 256) * 256);
     const dim3 grid((unsigned) ns, (unsigned) nh, (unsigned) B);
     const int nw = attn_waves(B, nh, max_keys);
-#define GSVK_ATTN_LAUNCH(W)                                                                      \
-    hipLaunchKernelGGL(k_attn_decode<W>, grid, dim3(W * 64), 0, stream, q, q_stride, k, v, nh,    \
+#define GSVK_ATTN_LAUNCH(W, NT)                                                                  \
+    hipLaunchKernelGGL((k_attn_decode<W, NT>), grid, dim3(W * 64), 0, stream, q, q_stride, k, v, nh, \
                        lstride, kv_begin, kv_end, ns, plan.chunk, scale * LOG2E, out, out16, oq, \
                        od, oq_layout, part, counters)
-    if (nw == 8) GSVK_ATTN_LAUNCH(8);
-    else GSVK_ATTN_LAUNCH(4);
+    // streaming loads for a launch of at least ATT_NT_BYTES of K/V rows: a decode of that many
+    // per layer reads far more than the MALL holds per step (batch 64 x 16 heads, rows U[256, 2048],
+    // 146 MB: 30.4 -> 27.1 us)
+    const bool nt = (int64_t) B * nh * max_keys * ATT_HD * 2 * 2 >= ATT_NT_BYTES;
+    if (nw == 8) {
+        if (nt) GSVK_ATTN_LAUNCH(8, true);
+        else GSVK_ATTN_LAUNCH(8, false);
+    } else {
+        if (nt) GSVK_ATTN_LAUNCH(4, true);
+        else GSVK_ATTN_LAUNCH(4, false);
+    }
 #undef GSVK_ATTN_LAUNCH
     GSVK_LAUNCH_CHECK();
     if (plan.chunk > 0) {

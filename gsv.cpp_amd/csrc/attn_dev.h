@@ -65,16 +65,26 @@ struct KV8 {
 // load is issued (no branch, so all 8 are in flight together); a key past `last` reads key
 // `last` instead (an index inside the buffer, on the same cache lines), and the caller masks
 // such keys at use: score -inf and V replaced by zero (a select, so whatever the slot holds
-// cannot reach the result).
+// cannot reach the result). NT: non-temporal (streaming) loads, for a cache whose step reads far
+// exceed the 256 MB MALL, where keeping the rows only evicts what is reused (the weights).
+template <bool NT = false>
 __device__ __forceinline__ void load_block(const uint16_t * __restrict__ kb,
                                            const uint16_t * __restrict__ vb, int key0, int last,
                                            int ks, KV8 & r) {
+    typedef unsigned int u4v __attribute__((ext_vector_type(4)));
 #pragma unroll
     for (int p = 0; p < 4; p++) {
         int key = key0 + p * 16 + ks;
         key = key < last ? key : last;
-        r.k[p] = *reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
-        r.v[p] = *reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+        if constexpr (NT) {
+            const u4v kk = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(kb + (int64_t) key * ATT_HD));
+            const u4v vv = __builtin_nontemporal_load(reinterpret_cast<const u4v *>(vb + (int64_t) key * ATT_HD));
+            r.k[p] = make_uint4(kk.x, kk.y, kk.z, kk.w);
+            r.v[p] = make_uint4(vv.x, vv.y, vv.z, vv.w);
+        } else {
+            r.k[p] = *reinterpret_cast<const uint4 *>(kb + (int64_t) key * ATT_HD);
+            r.v[p] = *reinterpret_cast<const uint4 *>(vb + (int64_t) key * ATT_HD);
+        }
     }
 }
 

@@ -108,6 +108,8 @@ struct DecPersistArgs {
     int * err;                  // 0, or 1 (a wait gave up) / 2 (an XCC id outside 0..7)
     const int * active;         // or null: 0 there (no row took part in this step, as the step's
                                 // sampler records) makes the launch return at once
+    int nt;                     // 1: the cached keys by non-temporal (streaming) loads, for a cache
+                                // whose per-step reads far exceed the 256 MB MALL
 };
 constexpr int DEC_PERSIST_WGS = 256;
 constexpr int DEC_PERSIST_MAX_BATCH = 32;   // 4 sequences per XCD

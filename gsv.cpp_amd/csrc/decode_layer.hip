@@ -201,7 +201,7 @@ __device__ __forceinline__ float ld_row(const float * p) {
 // recomputed for each item instead of being hoisted out of the persistent decode's layer loop and
 // kept live across it (which the loop form spilled: 28 VGPRs; without spills it is 0.60 instead of
 // 0.67 ms per step at batch 17-24; the one-item form is faster without it).
-template <int MODE, int NP, bool PERSIST, bool OPAQUE = false>
+template <int MODE, int NP, bool PERSIST, bool OPAQUE = false, bool NT = false>
 __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h, const int b, const XBar & bar,
                                               const int col_pre = 0, const int beg_pre = 0) {
     constexpr int NW = DL_WAVES;
@@ -323,14 +323,14 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     int blk = nblk > 0 ? (wave < nblk ? wave : nblk - 1) : 0;
     KV8 cur;
     if constexpr (!PERSIST) {
-        load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+        load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
     } else {
         if (!xbar_wait(bar, tid, &s_ok)) return false;
         if constexpr (MODE == IN_LN) {
             load_ln_rows();
             load_ln_params();
         }
-        load_block(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
+        load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
         load_out_weights();
     }
 
@@ -385,7 +385,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
         if (wave < nblk) {
             while (blk + NW < nblk) {
                 KV8 pre;
-                load_block(kb, vb, beg + (blk + NW) * ATT_BLK, last_old, ks, pre);
+                load_block<NT>(kb, vb, beg + (blk + NW) * ATT_BLK, last_old, ks, pre);
                 attn_block_step<true>(cur, beg + blk * ATT_BLK, end, ks, qv, a.scale_log2, col, knew, vnew, m, l, o);
                 cur = pre;
                 blk += NW;
@@ -626,7 +626,7 @@ __device__ __forceinline__ DecFfnArgs persist_ffn_args(const DecFfnArgs * all, i
 // without the item loops; the loop form (batch 17-32) runs its bodies OPAQUE.
 static_assert(DEC_PERSIST_MAX_BATCH / 8 * DL_NH <= 2 * 32, "two attention items per workgroup at most");
 
-template <int MODE, int G, bool ONE>
+template <int MODE, int G, bool ONE, bool NT>
 __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int li, int x, int w, int ns, int epoch,
                                                   const XBar & bar, int * my, int tid, int col, const int (&beg)[2]) {
     const DecAttnArgs aa = persist_attn_args(p.attn, li);
@@ -634,14 +634,15 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
         if (w < ns * DL_NH) {   // uniform over the workgroup
             XBar bw = bar;
             bw.target = MODE == IN_LN ? epoch + 2 * li : 0;
-            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true>(aa, w % DL_NH, x + 8 * (w / DL_NH), bw, col, beg[0]))
+            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, false, NT>(aa, w % DL_NH, x + 8 * (w / DL_NH), bw, col,
+                                                                               beg[0]))
                 return false;
         }
     } else {
         for (int it = w, k = 0; it < ns * DL_NH; it += 32, k++) {
             XBar bw = bar;
             bw.target = (MODE == IN_LN && k == 0) ? epoch + 2 * li : 0;
-            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, true>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw,
+            if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, true, NT>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw,
                                                                           col, k == 0 ? beg[0] : beg[1]))
                 return false;
         }
@@ -670,7 +671,7 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
 // (the XCD, blockIdx / 8) numbers them 0..31 within it. The XCD comes from the hardware (XCC_ID),
 // so the workgroups that exchange a sequence's rows share an L2 whatever the placement; a
 // placement other than 32 per XCD leaves some flag word unwritten and the waits give up.
-template <int G, bool ONE>
+template <int G, bool ONE, bool NT>
 __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     const int tid = threadIdx.x;
     int xcc;
@@ -697,9 +698,9 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
         const int it = w + 32 * k;
         if (it < ns * DL_NH) beg[k] = __builtin_amdgcn_readfirstlane(a0.kv_begin[x + 8 * (it / DL_NH)]);
     }
-    if (!dec_persist_layer<IN_EMB, G, ONE>(p, 0, x, w, ns, epoch, bar, my, tid, col, beg)) return;
+    if (!dec_persist_layer<IN_EMB, G, ONE, NT>(p, 0, x, w, ns, epoch, bar, my, tid, col, beg)) return;
     for (int li = 1; li < p.n_layer; li++)
-        if (!dec_persist_layer<IN_LN, G, ONE>(p, li, x, w, ns, epoch, bar, my, tid, col, beg)) return;
+        if (!dec_persist_layer<IN_LN, G, ONE, NT>(p, li, x, w, ns, epoch, bar, my, tid, col, beg)) return;
 }
 
 int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
@@ -707,12 +708,17 @@ int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
                      a.attn && a.ffn && a.flags && a.err && a.step,
                  "dec_persist: bad arguments (batch %d, %d layers)", a.B, a.n_layer);
     // one item per workgroup and phase while the XCD holds at most 2 sequences (32 groups: 1)
-    if (a.groups == 32)
-        hipLaunchKernelGGL((k_dec_persist<32, true>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
-    else if (a.B <= 16)
-        hipLaunchKernelGGL((k_dec_persist<16, true>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
-    else
-        hipLaunchKernelGGL((k_dec_persist<16, false>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, stream, a);
+#define GSVK_DP(G, ONE)                                                                                     \
+    do {                                                                                                    \
+        if (a.nt) hipLaunchKernelGGL((k_dec_persist<G, ONE, true>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0, \
+                                     stream, a);                                                            \
+        else hipLaunchKernelGGL((k_dec_persist<G, ONE, false>), dim3(DEC_PERSIST_WGS), dim3(DL_THREADS), 0,    \
+                                stream, a);                                                                 \
+    } while (0)
+    if (a.groups == 32) GSVK_DP(32, true);
+    else if (a.B <= 16) GSVK_DP(16, true);
+    else GSVK_DP(16, false);
+#undef GSVK_DP
     GSVK_LAUNCH_CHECK();
     return GSVK_OK;
 }
@@ -720,15 +726,17 @@ int launch_dec_persist(const DecPersistArgs & a, hipStream_t stream) {
 bool dec_persist_device_ok(int device) {
     hipDeviceProp_t prop;
     if (hipGetDeviceProperties(&prop, device) != hipSuccess) return false;
-    int occ16 = 0, occ32 = 0, occ16m = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16, k_dec_persist<16, true>, DL_THREADS, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ16m, k_dec_persist<16, false>, DL_THREADS, 0) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ32, k_dec_persist<32, true>, DL_THREADS, 0) != hipSuccess) {
-        (void) hipGetLastError();
-        return false;
+    int occ[6] = {};
+    const void * kern[6] = {(const void *) k_dec_persist<16, true, false>, (const void *) k_dec_persist<16, false, false>,
+                            (const void *) k_dec_persist<32, true, false>, (const void *) k_dec_persist<16, true, true>,
+                            (const void *) k_dec_persist<16, false, true>, (const void *) k_dec_persist<32, true, true>};
+    for (int i = 0; i < 6; i++) {
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ[i], kern[i], DL_THREADS, 0) != hipSuccess || occ[i] < 1) {
+            (void) hipGetLastError();
+            return false;
+        }
     }
-    return prop.multiProcessorCount == DEC_PERSIST_WGS && occ16 >= 1 && occ16m >= 1 && occ32 >= 1 &&
-           std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
+    return prop.multiProcessorCount == DEC_PERSIST_WGS && std::string(prop.gcnArchName).rfind("gfx950", 0) == 0;
 }
 
 bool dec_layer_supported(int B, int nh, int d_model, int ffn, int64_t max_keys) {
