@@ -152,7 +152,30 @@ struct XBar {
     int * flags;    // the XCD's 32 flag words
     int * err;      // error word (0: none)
     int target;     // wait until every word >= target (0: no wait)
+    int li = -1;    // the persistent decode's layer (its phase stamps); -1 outside it
 };
+
+// Phase stamps of the persistent decode, in a library built with GSVK_PHASE_STAMPS only (build.py
+// --phase-stamps): thread 0 of every workgroup records s_memrealtime (100 MHz) at each step of
+// each layer's two phases into slot [workgroup][layer * 16 + event] (the last launch's values
+// remain): 0 barrier seen, 1 input row quantised, 2 QKV and K/V append done, 3 attention merged,
+// 4 out-projection partial row stored, 5 flag stored; 8 barrier seen, 9 LN1 row quantised, 10
+// FFN1 blocks quantised, 11 FFN2 partial row stored, 12 flag stored; slot 63 * 16: the launch's
+// start, 63 * 16 + 1: the workgroup's XCD. gsvk_phase_stamps reads them.
+constexpr int DL_STAMP_SLOTS = 64 * 16;
+#if defined(GSVK_PHASE_STAMPS)
+__device__ long long g_phase_stamps[DEC_PERSIST_WGS][DL_STAMP_SLOTS];
+#define DL_STAMP_AT(li, ev, v)                                                                         \
+    do {                                                                                               \
+        if ((li) >= 0 && threadIdx.x == 0 && blockIdx.x < DEC_PERSIST_WGS)                              \
+            g_phase_stamps[blockIdx.x][((li) & 63) * 16 + (ev)] = (long long) (v);                     \
+    } while (0)
+#else
+#define DL_STAMP_AT(li, ev, v) \
+    do {                      \
+    } while (0)
+#endif
+#define DL_STAMP(li, ev) DL_STAMP_AT(li, ev, __builtin_amdgcn_s_memrealtime())
 
 __device__ __forceinline__ bool xbar_wait(const XBar & x, int tid, int * s_ok) {
     if (x.target == 0) return true;
@@ -326,6 +349,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
         load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
     } else {
         if (!xbar_wait(bar, tid, &s_ok)) return false;
+        DL_STAMP(bar.li, 0);
         if constexpr (MODE == IN_LN) {
             load_ln_rows();
             load_ln_params();
@@ -348,6 +372,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     if (h == 0 && a.x_out) a.x_out[(int64_t) b * DL_K + tid] = x;
     wg_quantize_row(x, tid, s_x, s_d);
     __syncthreads();
+    DL_STAMP(bar.li, 1);
 
     // ---- q, k, v of head h; the new K/V appended at column col ----
 #pragma unroll
@@ -368,6 +393,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
         }
     }
     __syncthreads();
+    DL_STAMP(bar.li, 2);
 
     // ---- attention over [beg, col] (the block loop of attention.hip) ----
     float m = -INFINITY, l = 0.0f;
@@ -405,6 +431,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
         }
     }
     __syncthreads();
+    DL_STAMP(bar.li, 3);
     // every wave merges the waves' partials (the same arithmetic in each) into the head's output,
     // lane d < 32 holding dimension d, quantised to one Q8_0 block (no valid key: 0, as ggml) and
     // kept in the wave's own LDS slot: no further barrier
@@ -437,6 +464,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
         const float y = (h2f(wos[u]) * da) * (float) isum;
         if (lane < 32) prow[t * 32 + lane] = y;
     }
+    DL_STAMP(bar.li, 4);
     return true;
 }
 
@@ -529,6 +557,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
         load_ffn2_weights();
     } else {
         if (!xbar_wait(bar, tid, &s_ok)) return false;
+        DL_STAMP(bar.li, 8);
         load_ln_rows();
         load_ln_params();
         load_ffn2_weights();
@@ -542,6 +571,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
     if (g == 0) a.n1_out[(int64_t) b * DL_K + tid] = y;
     wg_quantize_row(y, tid, s_x, s_d);
     __syncthreads();
+    DL_STAMP(bar.li, 9);
 
     // ---- FFN1 + b_1 + ReLU of the group's units ----
 #pragma unroll
@@ -562,6 +592,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
         if (lane == 0) s_hd[wave] = d;
     }
     __syncthreads();
+    DL_STAMP(bar.li, 10);
 
     // ---- FFN2 over the group's blocks: partial row p2[g][b] ----
     float * prow = a.p2 + ((int64_t) g * B + b) * DL_K;
@@ -576,6 +607,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
         }
         if (lane < 32) prow[t * 32 + lane] = acc;
     }
+    DL_STAMP(bar.li, 11);
     return true;
 }
 
@@ -634,6 +666,7 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
         if (w < ns * DL_NH) {   // uniform over the workgroup
             XBar bw = bar;
             bw.target = MODE == IN_LN ? epoch + 2 * li : 0;
+            bw.li = li;
             if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, false, NT>(aa, w % DL_NH, x + 8 * (w / DL_NH), bw, col,
                                                                                beg[0]))
                 return false;
@@ -642,27 +675,32 @@ __device__ __forceinline__ bool dec_persist_layer(const DecPersistArgs & p, int 
         for (int it = w, k = 0; it < ns * DL_NH; it += 32, k++) {
             XBar bw = bar;
             bw.target = (MODE == IN_LN && k == 0) ? epoch + 2 * li : 0;
+            bw.li = li;
             if (!dec_attn_body<MODE, MODE == IN_LN ? G : 16, true, true, NT>(aa, it % DL_NH, x + 8 * (it / DL_NH), bw,
                                                                           col, k == 0 ? beg[0] : beg[1]))
                 return false;
         }
     }
     xbar_signal(my, epoch + 2 * li + 1, tid);
+    DL_STAMP(li, 5);
     const DecFfnArgs fa = persist_ffn_args(p.ffn, li);
     if constexpr (ONE) {
         if (w < ns * G) {
             XBar bw = bar;
             bw.target = epoch + 2 * li + 1;
+            bw.li = li;
             if (!dec_ffn_body<G, true>(fa, w % G, x + 8 * (w / G), bw)) return false;
         }
     } else {
         for (int it = w; it < ns * G; it += 32) {
             XBar bw = bar;
             bw.target = it == w ? epoch + 2 * li + 1 : 0;
+            bw.li = li;
             if (!dec_ffn_body<G, true, true>(fa, it % G, x + 8 * (it / G), bw)) return false;
         }
     }
     xbar_signal(my, epoch + 2 * li + 2, tid);
+    DL_STAMP(li, 12);
     return true;
 }
 
@@ -686,6 +724,8 @@ __global__ void __launch_bounds__(DL_THREADS) k_dec_persist(DecPersistArgs p) {
     }
     __syncthreads();
     if (!s_go) return;
+    DL_STAMP(63, 0);
+    DL_STAMP_AT(63, 1, x);
     const int ns = x < p.B ? (p.B - 1 - x) / 8 + 1 : 0;   // sequences x, x + 8, ...
     const int epoch = (__builtin_amdgcn_readfirstlane(*p.step) + p.epoch_add) * 64;   // 2 phases per layer, < 64
     const XBar bar{p.flags + x * 32, p.err, 0};
@@ -779,6 +819,19 @@ int launch_dec_ffn(const DecFfnArgs & a, hipStream_t stream) {
 }
 
 }  // namespace gsvk
+
+extern "C" int gsvk_phase_stamps(int64_t * out, size_t n) {
+    using namespace gsvk;
+    GSVK_REQUIRE(out && n >= (size_t) DEC_PERSIST_WGS * DL_STAMP_SLOTS, "phase_stamps: need %d values",
+                 DEC_PERSIST_WGS * DL_STAMP_SLOTS);
+#if defined(GSVK_PHASE_STAMPS)
+    GSVK_HIP(hipMemcpyFromSymbol(out, HIP_SYMBOL(g_phase_stamps), sizeof(g_phase_stamps), 0, hipMemcpyDeviceToHost));
+    return GSVK_OK;
+#else
+    set_error("phase_stamps: this library was built without phase stamps (build.py --phase-stamps)");
+    return GSVK_ERR_STATE;
+#endif
+}
 
 extern "C" int gsvk_op_dec_attn(int B, const float * res, const float * parts, const float * ln_bias,
                                 const float * ln_wb, const float * emb, const float * pe, const int32_t * tok,

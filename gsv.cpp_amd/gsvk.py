@@ -32,7 +32,7 @@ EXPORTS = [
     "gsvk_op_attn_decode_noalloc", "gsvk_model_set_decode_path", "gsvk_op_dec_attn", "gsvk_op_dec_ffn",
     "gsvk_model_set_exact", "gsvk_op_attn_exact", "gsvk_op_expf_exact", "gsvk_model_set_prefill_f16",
     "gsvk_op_q8_dequant_f16", "gsvk_op_q8h_gemm", "gsvk_op_qkv_attn_exact", "gsvk_model_get_profile",
-    "gsvk_model_time_decode_kernel",
+    "gsvk_model_time_decode_kernel", "gsvk_phase_stamps",
 ]
 
 GSVK_DECODE_AUTO, GSVK_DECODE_GEMV, GSVK_DECODE_FUSED, GSVK_DECODE_MFMA, GSVK_DECODE_PERSIST = 0, 1, 2, 3, 4

@@ -155,6 +155,16 @@ int gsvk_model_get_profile(gsvk_model * m, gsvk_profile * out);
  * No counterpart in the reference; for benchmarks (the decode's dominant kernel, timed alone). */
 int gsvk_model_time_decode_kernel(gsvk_model * m, int launches, float * ms_per_launch);
 
+/* The persistent decode's phase stamps, in a library built with `build.py --phase-stamps` only
+ * (lib/libgsvk_stamps.so; otherwise GSVK_ERR_STATE): for each of the 256 workgroups, 1024 int64
+ * values, [layer * 16 + event] = the 100 MHz s_memrealtime counter when thread 0 reached the event
+ * in the last persistent launch (0 barrier seen, 1 input row quantised, 2 QKV and K/V append done,
+ * 3 attention merged, 4 out-projection partial row stored, 5 flag stored; 8 barrier seen, 9 LN1
+ * row quantised, 10 FFN1 blocks quantised, 11 FFN2 partial row stored, 12 flag stored), and at
+ * [63 * 16] the launch's start, [63 * 16 + 1] the workgroup's XCD. `n` must be at least 256 * 1024.
+ * No counterpart in the reference; for profiling. */
+int gsvk_phase_stamps(int64_t * out, size_t n);
+
 /* Full batched generation: replaces gsv_ar::generate (src/gsv_ar.cpp:719-824).
  * oracle (teacher forcing) may be NULL; seeds may be NULL (then seed_base + 0x9E3779B9*b). */
 int gsvk_generate(gsvk_model * m, const gsvk_request * reqs, int B, const gsvk_sampler_cfg * cfg,

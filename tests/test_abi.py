@@ -132,3 +132,14 @@ def test_attn_noalloc_rejects_shapes_beyond_its_scratch():
     rc = L.gsvk_op_attn_decode_noalloc(None, None, None, 4096, 16, 32, 4096, None, None, 4096, 1.0, None,
                                        None, None, None, None)
     assert rc == 1 and "scratch" in gsvk.last_error()
+
+
+def test_phase_stamps_need_the_stamps_build():
+    """gsvk_phase_stamps: the default library is built without the persistent decode's phase stamps
+    and says so (GSVK_ERR_STATE, no device call); a buffer below 256 x 1024 values is refused."""
+    import ctypes as C
+    L = gsvk.lib()
+    buf = np.zeros(256 * 1024, np.int64)
+    assert L.gsvk_phase_stamps(C.c_void_p(buf.ctypes.data), C.c_size_t(buf.size)) == 6
+    assert b"phase stamps" in L.gsvk_last_error()
+    assert L.gsvk_phase_stamps(C.c_void_p(buf.ctypes.data), C.c_size_t(100)) == 1
