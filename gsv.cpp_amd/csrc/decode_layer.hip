@@ -323,8 +323,10 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
             wos[u] = a.wod[(((int64_t) t * DL_NBLK + h) << 5) + (lane & 31)];
         }
     };
-    // PERSIST: the QKV weights go out ahead of the barrier's poll; the loads that are needed
-    // later (cached keys, out projection) after the input row's, behind the wait
+    // PERSIST: the QKV weights go out ahead of the barrier's poll, the cached keys after the input
+    // row's, behind the wait, and the out projection's once the input row is quantised (issued
+    // with the row's loads, they delayed the LayerNorm: batch 16 0.332 -> 0.325 ms per step over
+    // 20 steps, 0.348 -> 0.342 over 500)
     load_qkv_weights();
     if constexpr (!PERSIST) load_out_weights();
     // (the key range arrived first: its loads were issued first and retire in order)
@@ -355,7 +357,6 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
             load_ln_params();
         }
         load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
-        load_out_weights();
     }
 
     // ---- the input row: LN2 of the previous layer (or the embedding), quantised into LDS ----
@@ -371,6 +372,7 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     }
     if (h == 0 && a.x_out) a.x_out[(int64_t) b * DL_K + tid] = x;
     wg_quantize_row(x, tid, s_x, s_d);
+    if constexpr (PERSIST) load_out_weights();
     __syncthreads();
     DL_STAMP(bar.li, 1);
 
@@ -550,8 +552,9 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
             }
         }
     };
-    // PERSIST: FFN1's weights ahead of the barrier's poll, FFN2's after the input row's (as in
-    // dec_attn_body)
+    // PERSIST: FFN1's weights ahead of the barrier's poll, FFN2's after the input row's; with 32
+    // groups (batch <= 8) FFN2's once LN1 is quantised (batch 1 0.293 -> 0.283 ms per step; with
+    // 16 groups, twice the FFN2 bytes per workgroup, that was slower: 0.3169 -> 0.3208 at batch 16)
     load_ffn1_weights();
     if constexpr (!PERSIST) {
         load_ffn2_weights();
@@ -560,7 +563,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
         DL_STAMP(bar.li, 8);
         load_ln_rows();
         load_ln_params();
-        load_ffn2_weights();
+        if constexpr (G != 32) load_ffn2_weights();
     }
 
     // ---- n1 = LN1((x + o) + b_o), quantised into LDS ----
@@ -570,6 +573,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
     const float y = wg_layernorm((xr + r) + xb, xw, xc, lane, wave, s_red);
     if (g == 0) a.n1_out[(int64_t) b * DL_K + tid] = y;
     wg_quantize_row(y, tid, s_x, s_d);
+    if constexpr (PERSIST && G == 32) load_ffn2_weights();
     __syncthreads();
     DL_STAMP(bar.li, 9);
 
