@@ -540,9 +540,10 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
             rb1[p] = a.b1[row];
         }
     };
-    auto load_ffn2_weights = [&]() {
+    auto load_ffn2_weights = [&](int u0 = 0, int u1 = W2_T) {
 #pragma unroll
         for (int u = 0; u < W2_T; u++) {
+            if (u < u0 || u >= u1) continue;
             const int t = wave + NW * u;
 #pragma unroll
             for (int k = 0; k < UB; k++) {
@@ -552,9 +553,10 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
             }
         }
     };
-    // PERSIST: FFN1's weights ahead of the barrier's poll, FFN2's after the input row's; with 32
-    // groups (batch <= 8) FFN2's once LN1 is quantised (batch 1 0.293 -> 0.283 ms per step; with
-    // 16 groups, twice the FFN2 bytes per workgroup, that was slower: 0.3169 -> 0.3208 at batch 16)
+    // PERSIST: FFN1's weights ahead of the barrier's poll; FFN2's once LN1 is quantised with 32
+    // groups (batch <= 8: batch 1 0.293 -> 0.283 ms per step, against after the input row's), with
+    // 16 groups (twice the FFN2 bytes per workgroup) half after the input row's and half after LN1
+    // (batch 16 0.3158 -> 0.3124; all after LN1: 0.3169 -> 0.3208)
     load_ffn1_weights();
     if constexpr (!PERSIST) {
         load_ffn2_weights();
@@ -563,7 +565,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
         DL_STAMP(bar.li, 8);
         load_ln_rows();
         load_ln_params();
-        if constexpr (G != 32) load_ffn2_weights();
+        if constexpr (G != 32) load_ffn2_weights(0, 1);
     }
 
     // ---- n1 = LN1((x + o) + b_o), quantised into LDS ----
@@ -574,6 +576,7 @@ __device__ __forceinline__ bool dec_ffn_body(const DecFfnArgs & a, const int g, 
     if (g == 0) a.n1_out[(int64_t) b * DL_K + tid] = y;
     wg_quantize_row(y, tid, s_x, s_d);
     if constexpr (PERSIST && G == 32) load_ffn2_weights();
+    if constexpr (PERSIST && G != 32) load_ffn2_weights(1, W2_T);
     __syncthreads();
     DL_STAMP(bar.li, 9);
 
