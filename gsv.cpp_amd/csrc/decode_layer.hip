@@ -177,13 +177,16 @@ __device__ long long g_phase_stamps[DEC_PERSIST_WGS][DL_STAMP_SLOTS];
 #endif
 #define DL_STAMP(li, ev) DL_STAMP_AT(li, ev, __builtin_amdgcn_s_memrealtime())
 
+// PW: the wave that polls (its loads issued before the poll return ahead of the poll's)
+template <int PW = 0>
 __device__ __forceinline__ bool xbar_wait(const XBar & x, int tid, int * s_ok) {
     if (x.target == 0) return true;
-    if (tid < 64) {
+    if ((tid >> 6) == PW) {
+        const int ln = tid & 63;
         bool ok = false;
         for (int spins = 0; spins < XBAR_SPIN_MAX; spins++) {
-            const int v = tid < 32 ? __hip_atomic_load(&x.flags[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                   : x.target;
+            const int v = ln < 32 ? __hip_atomic_load(&x.flags[ln], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                  : x.target;
             if (__all(v >= x.target)) {
                 ok = true;
                 break;
@@ -192,7 +195,7 @@ __device__ __forceinline__ bool xbar_wait(const XBar & x, int tid, int * s_ok) {
                 __hip_atomic_load(x.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0)
                 break;
         }
-        if (tid == 0) {
+        if (ln == 0) {
             *s_ok = ok;
             if (!ok) __hip_atomic_store(x.err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -302,6 +305,8 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     auto load_qkv_weights = [&]() {
 #pragma unroll
         for (int p = 0; p < PASSES; p++) {
+            // (the persistent decode: waves past the 96 rows in the second pass load nothing)
+            if (PERSIST && (p * NW + wave) * 8 >= DL_QKV_ROWS) break;   // (uniform per wave)
             const int rl = (p * NW + wave) * 8 + rsub;
             const int rlc = rl < DL_QKV_ROWS ? rl : DL_QKV_ROWS - 1;
             const int row = (rlc >> 5) * DL_K + h * ATT_HD + (rlc & 31);
@@ -350,7 +355,9 @@ __device__ __forceinline__ bool dec_attn_body(const DecAttnArgs & a, const int h
     if constexpr (!PERSIST) {
         load_block<NT>(kb, vb, beg + blk * ATT_BLK, last_old, ks, cur);
     } else {
-        if (!xbar_wait(bar, tid, &s_ok)) return false;
+        // polled by wave 4 with 32 FFN groups (batch <= 8), one pass of QKV weights ahead of its
+        // poll instead of wave 0's two (batch 1 0.309 -> 0.306 ms per step; at batch 16 no gain)
+        if (!xbar_wait<NP == 32 ? 4 : 0>(bar, tid, &s_ok)) return false;
         DL_STAMP(bar.li, 0);
         if constexpr (MODE == IN_LN) {
             load_ln_rows();
